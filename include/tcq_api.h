@@ -1,0 +1,124 @@
+/* C ABI of the MI355X (gfx950) TCQ W2A8 deploy path: trellis-coded 2-bit weights (bitshift trellis L = 16, K = 2, V = 2,
+ * 16 x 16 tiles, 512 x 2 table per layer, per-row scales, two-sided randomized block-Walsh rotation) with 8-bit per-token
+ * activations, and the W8A8 INT8 GEMM.
+ *
+ * Every entry point takes device pointers, sizes and a stream (a hipStream_t passed as void*; NULL = the default stream),
+ * launches asynchronously on that stream, allocates nothing and copies nothing between host and device, so calls can be
+ * captured into HIP graphs. Return value: TCQ_OK, a negative TCQ_ERR_* for an argument the call rejects before launching, or
+ * a positive hipError_t reported by the launch.
+ *
+ * Each declaration names the reference interface it replaces (paths relative to the reference repository). The reference
+ * launched NVRTC-compiled CUDA kernels through ctypes (deploy/tcq_kernels/cuda_rt.py:87-108) from Python helpers with
+ * caller-allocated outputs (deploy/tcq_kernels/kernels.py:602-696); these functions are that boundary as a C ABI.
+ *
+ * Layouts (all row-major, C order):
+ *   bits       (m/16 * n/16, 32) uint16: the packed stream, 32 words per tile, tiles row-major (tcq_format.py:3-4)
+ *   wdev       device layout of the same words made by tcq_repack (see there); required by the fused products
+ *   tlut       (512, 2) FP16 table; t8: (512, 2) INT8 table (tcq_format.py:74-77)
+ *   row_scale  (m,) FP16; rs: (m,) FP32; su: (n,) int8 +-1; sv: (m,) int8 +-1
+ *   q          (M, K) int8 row-major; q4: (K/4, ldq) int32, 4 consecutive inputs per word, token = column
+ */
+#ifndef TCQ_API_H
+#define TCQ_API_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* tcq_stream_t;
+
+enum tcq_status {
+    TCQ_OK = 0,
+    TCQ_ERR_ARG = -1,         /* null pointer where one is required, or a non-positive size */
+    TCQ_ERR_SHAPE = -2,       /* sizes violate the format (m, n multiples of 16; K multiple of 4; widths too large) */
+    TCQ_ERR_DTYPE = -3,       /* unsupported dtype code for this entry point */
+    TCQ_ERR_UNSUPPORTED = -4, /* a size the kernel has no variant for (e.g. more tokens than the small-M products take) */
+    TCQ_ERR_ALIGN = -5        /* a pointer the kernel reads or writes in 16-byte vectors is not 16-byte aligned */
+};
+
+enum tcq_dtype { TCQ_F32 = 0, TCQ_BF16 = 1, TCQ_F16 = 2, TCQ_I32 = 3, TCQ_I8 = 4 };
+
+/* Library version string and the widest row the block-Walsh kernels take (16384). */
+const char* tcq_version(void);
+int tcq_max_width(void);
+
+/* ---------------------------------------------------------------------------------------------------------- load time */
+
+/* INT8 table and row scale of one layer: t8 = clamp(round(tlut * g), +-127), g = float(1/max|tlut|) * 127,
+ * rs = float(row_scale) / g; gain (1 float, may be NULL) receives g.
+ * Replaces tcq_format.snap (deploy/tcq_kernels/tcq_format.py:74-77), called by tcq_format.Layer.__init__ (:90). */
+int tcq_snap(const void* tlut, const void* row_scale, int m, int8_t* t8, float* rs, float* gain, tcq_stream_t stream);
+
+/* Reference word layout -> device layout for the fused products (tcq_gemv_f16, tcq_gemm_tcq). For tile row I and chunk c of
+ * 16 tiles (columns 256 c .. 256 c + 255) the device layout holds 1 KiB: dword 4 l + j of lane l = 16 g + r is the 32-bit
+ * window (word[2r] << 16) | word[2r + 1] of tile 16 c + 4 j + g. n is padded to a multiple of 256 with zero words.
+ * wdev holds (m/16) * ceil(n/256) * 256 uint32. No reference counterpart: the reference streams the words as stored
+ * (kernels.py:403-427); this is a load-time permutation of the same 2 bits per weight. */
+int tcq_repack(const void* bits, void* wdev, int m, int n, tcq_stream_t stream);
+int64_t tcq_repack_words(int m, int n);
+
+/* ------------------------------------------------------------------------------------------------------------- decode */
+
+/* Dense INT8 decode: out (m, n) int8 = sign * t8[hash(state)]. Replaces kernels.decode / k_decode
+ * (deploy/tcq_kernels/kernels.py:339-349, 653-656); definition tcq_format.Layer.w8_reference (tcq_format.py:97-98). */
+int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream);
+
+/* Dense decode through the FP16 table: out (m, n) FP16 = sign * tlut[hash(state)] (exact). Counterpart of
+ * tcq_format.lookup(states, tlut.float()) (tcq_format.py:66-71, 103, 139) and of kernels.decode_bf16 (kernels.py:320-337). */
+int tcq_decode_f16(const void* bits, const void* tlut, void* out, int m, int n, tcq_stream_t stream);
+
+/* ----------------------------------------------------------------------------------------------------------- rotation */
+
+/* Randomized block-Walsh transform of M rows: y = fwht(x * su) (su may be NULL: no sign flip), FP32 butterflies in stage
+ * order h = 1, 2, 4, ..., normalised per power-of-two block. x_dtype in {F32, BF16, F16}, y_dtype in {F32, BF16, F16}.
+ * Leading dimensions in elements. Replaces tcq_format.fwht (deploy/tcq_kernels/tcq_format.py:44-55) applied to x * su
+ * (tcq_format.py:130). */
+int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, void* y, int y_dtype, int ldy, int M, int n,
+            tcq_stream_t stream);
+
+/* Rotate + quantize: sign, block Walsh, per-token absmax, INT8. q (M, K) row-major and / or q4 (K/4, ldq) int32 (either may
+ * be NULL), scale (M,) FP32. Replaces kernels.pre / k_pre_bf16 / k_pre_f32 (deploy/tcq_kernels/kernels.py:208-219, 602-606);
+ * definition quantize_tokens(fwht(x * su)) (tcq_format.py:119-122, 130-134). */
+int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
+            tcq_stream_t stream);
+
+/* Rotate for the float (W2) path: h16 (M, K) FP16 = fwht(x * su) / hscale[t], hscale[t] (M,) FP32 a power of two that puts
+ * the row's absmax in [2^14, 2^15) (1 for a zero row), so the division is exact and FP16 cannot overflow. Counterpart of
+ * kernels.pre_h (kernels.py:309-317, 677-680), which rounds to BF16 instead. */
+int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h16, float* hscale, int M, int K, tcq_stream_t stream);
+
+/* Per-row symmetric INT8 without rotation (tcq_format.quantize_tokens, tcq_format.py:119-122): activations per token, or a
+ * dense weight per output channel. q (M, K) int8, scale (M,) FP32. */
+int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q, float* scale, int M, int K, tcq_stream_t stream);
+
+/* Scale + rotate epilogue: z = SCALE(acc[t, col0 + i]) -> block Walsh -> * sv -> + bias -> y (M, N).
+ * acc_dtype I32: SCALE = (float(a) * s[t]) * rs[i]; F32: SCALE = a (s, rs ignored); BF16: SCALE = bf16(a) * rs[i].
+ * bias FP32 (N,) or NULL. y_dtype in {BF16, F16, F32}. lda = leading dimension of acc in elements.
+ * Replaces kernels.post / k_post_{i32,f32,bf16} (deploy/tcq_kernels/kernels.py:221-230, 545, 612-615). */
+int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
+             const float* bias, void* y, int y_dtype, int M, int N, tcq_stream_t stream);
+
+/* -------------------------------------------------------------------------------------------------------- products */
+
+/* One layer of a batched FP16-table decode-GEMV / small-M GEMM (M <= 16 tokens): z[t, i] = (sum_k h16[t, k] *
+ * Q[i, k]) * hscale[t] * row_scale[i], Q = FP16 table values decoded from wdev on the fly, FP32 accumulation (MFMA).
+ * All layers of a batch share m, n, M, h16 and hscale. */
+typedef struct tcq_gemv_layer {
+    const void* wdev;       /* tcq_repack layout */
+    const void* tlut;       /* (512, 2) FP16 */
+    const void* row_scale;  /* (m,) FP16 */
+    float* z;               /* (M, m) FP32 out */
+} tcq_gemv_layer;
+
+/* layers: a DEVICE array of nlayers descriptors. The FP16-table product of tcq_format.reference_linear(table='fp16',
+ * a8=False) (tcq_format.py:139-144), which the reference computes only in PyTorch (FP64 matmul); its INT8-table kernel
+ * counterpart is kernels.gemmf_tcq / k_gemmf_tcq (kernels.py:465-489). */
+int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
+                 tcq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,254 @@
+"""GPU parity of the HIP kernels against the CPU oracle (and, through it, the reference's own arithmetic): integer and
+bit-pattern outputs bit-exact, the FP16-table float path within relative L2 2e-3 of the FP32/FP64 reference."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tcq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+@pytest.fixture(scope='module', autouse=True)
+def _lib():
+    from yanlongvla_amd import _lib
+    _lib.lib()
+    torch.cuda.init()
+
+
+def T(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(DEV)
+
+
+def layer_from(golden, tag):
+    t = {k: golden[f'{tag}_{k}'] for k in ('bits', 'tlut', 'row_scale', 'su', 'sv')}
+    bias = golden[f'{tag}_bias'] if f'{tag}_bias' in golden.files else None
+    return O.Layer(tag, t, bias=bias)
+
+
+def dev_layer(L):
+    return dict(bits=T(L.bits), tlut=T(L.tlut.view(np.int16)), row_scale=T(L.row_scale.view(np.int16)), su=T(L.su), sv=T(L.sv))
+
+
+def bits_of(t):
+    return t.cpu().numpy().view(np.uint32 if t.element_size() == 4 else np.uint16)
+
+
+# -------------------------------------------------------------------------------------------------------------------- snap
+@pytest.mark.parametrize('tag', ['l0', 'l1', 'l2', 'l3', 'snap_neg', 'snap_tiny'])
+def test_snap_bitexact(golden, tag):
+    from yanlongvla_amd import kernels as K
+    tl, rsc = golden[f'{tag}_tlut'], golden[f'{tag}_row_scale']
+    t8, rs, g = K.snap(T(tl.view(np.int16)), T(rsc.view(np.int16)))
+    assert np.array_equal(t8.cpu().numpy(), golden[f'{tag}_t8'])
+    assert np.array_equal(bits_of(rs), golden[f'{tag}_rs'].view(np.uint32))
+    assert bits_of(g)[0] == golden[f'{tag}_gain'].view(np.uint32)
+
+
+# ------------------------------------------------------------------------------------------------------------------ decode
+@pytest.mark.parametrize('m,n,seed', [(32, 48, 0), (48, 80, 1), (256, 1024, 2), (2048, 2048, 3), (1024, 4096, 4)])
+def test_decode_i8_and_f16_bitexact(m, n, seed):
+    from yanlongvla_amd import kernels as K
+    L = O.random_layer(m, n, seed)
+    d = dev_layer(L)
+    t8, rs, _ = K.snap(d['tlut'], d['row_scale'])
+    assert np.array_equal(t8.cpu().numpy(), L.t8)
+    out = torch.empty(m, n, dtype=torch.int8, device=DEV)
+    K.decode(d['bits'], t8, out)
+    st = L.states()
+    assert np.array_equal(out.cpu().numpy(), O.lookup(st, L.t8.astype(np.int16)).astype(np.int8))
+    out16 = torch.empty(m, n, dtype=torch.int16, device=DEV)
+    K.decode_f16(d['bits'], d['tlut'], out16)
+    ref16 = O.lookup(st, L.tlut.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), ref16.view(np.uint16))
+
+
+@pytest.mark.parametrize('tag', ['l0', 'l1', 'l2', 'l3'])
+def test_decode_golden(golden, tag):
+    from yanlongvla_amd import kernels as K
+    L = layer_from(golden, tag)
+    d = dev_layer(L)
+    t8 = T(golden[f'{tag}_t8'])
+    out = torch.empty(L.m, L.n, dtype=torch.int8, device=DEV)
+    K.decode(d['bits'], t8, out)
+    assert np.array_equal(out.cpu().numpy(), golden[f'{tag}_w8'])
+
+
+# -------------------------------------------------------------------------------------------------------------------- RHT
+RHT_CASES = [(1, 1), (3, 16), (2, 48), (5, 80), (1, 1024), (16, 2048), (50, 4096), (16, 16384), (4, 1152), (3, 4304),
+             (800, 1024), (800, 16384)]
+
+
+@pytest.mark.parametrize('M,n', RHT_CASES)
+@pytest.mark.parametrize('xdt', [torch.bfloat16, torch.float32, torch.float16])
+def test_rht_bitexact(M, n, xdt):
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M * 7 + n)
+    x = torch.from_numpy(rng.standard_normal((M, n)).astype(np.float32)).to(xdt)
+    su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.int8)
+    y = torch.empty(M, n, dtype=torch.float32, device=DEV)
+    K.rht(x.to(DEV), T(su), y)
+    ref = O.fwht(x.float().numpy() * su.astype(np.float32))
+    assert np.array_equal(bits_of(y), ref.view(np.uint32))
+    yb = torch.empty(M, n, dtype=torch.bfloat16, device=DEV)
+    K.rht(x.to(DEV), T(su), yb)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
+
+
+@pytest.mark.parametrize('M,n', [(1, 1024), (16, 2048), (50, 4096)])
+def test_rht_vs_dense_hadamard(M, n):
+    """C1 contract: FP32 result within 1e-3 relative of a dense-Hadamard FP64 reference (closed form, not the oracle)."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(n)
+    x = torch.from_numpy(rng.standard_normal((M, n)).astype(np.float32)).bfloat16()
+    su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.int8)
+    y = torch.empty(M, n, dtype=torch.float32, device=DEV)
+    K.rht(x.to(DEV), T(su), y)
+    H = torch.ones(1, 1, dtype=torch.float64)
+    while H.shape[0] < n:
+        H = torch.cat((torch.cat((H, H), 1), torch.cat((H, -H), 1)), 0)
+    ref = (x.double() * torch.from_numpy(su).double()) @ H / np.sqrt(n)
+    err = (y.cpu().double() - ref).norm() / ref.norm()
+    assert err < 1e-3
+
+
+@pytest.mark.parametrize('M,n', [(800, 16384), (800, 4096), (16, 4304)])
+def test_rht_involution_full_size(M, n):
+    """Size-independent property at the full C1 size: the normalised transform is its own inverse, and it preserves norms."""
+    from yanlongvla_amd import kernels as K
+    x = torch.randn(M, n, device=DEV)
+    y = torch.empty_like(x)
+    z = torch.empty_like(x)
+    K.rht(x, None, y)
+    K.rht(y, None, z)
+    assert (z - x).norm() / x.norm() < 1e-5
+    assert torch.allclose(y.norm(dim=1), x.norm(dim=1), rtol=1e-4)
+
+
+# ------------------------------------------------------------------------------------------------------------ pre / post
+@pytest.mark.parametrize('M,K', [(1, 48), (3, 80), (10, 1024), (16, 2048), (50, 4096), (7, 16384), (300, 2048), (4, 1152)])
+@pytest.mark.parametrize('xdt', [torch.bfloat16, torch.float32])
+def test_pre_bitexact(M, K, xdt):
+    from yanlongvla_amd import kernels as Kk
+    rng = np.random.default_rng(M + K)
+    x = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).to(xdt)
+    if M > 2:
+        x[2] = 0                                  # all-zero token -> scale 1
+    su = np.where(rng.integers(0, 2, K) > 0, 1, -1).astype(np.int8)
+    q = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    q4 = torch.empty(K // 4, M, dtype=torch.int32, device=DEV)
+    s = torch.empty(M, dtype=torch.float32, device=DEV)
+    Kk.pre(x.to(DEV), T(su), q=q, q4=q4, scale=s)
+    qr, sr = O.quantize_tokens(O.fwht(x.float().numpy() * su.astype(np.float32)))
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(bits_of(s), sr[:, 0].view(np.uint32))
+    assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
+
+
+@pytest.mark.parametrize('M,N', [(1, 16), (3, 48), (10, 256), (16, 2048), (50, 4096), (5, 16384), (300, 1024), (2, 4304)])
+def test_post_bitexact(M, N):
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M * N)
+    acc = rng.integers(-2 ** 20, 2 ** 20, size=(M, N + 8)).astype(np.int32)
+    s = (rng.random(M) + 0.5).astype(np.float32)
+    rs = (rng.random(N + 8) * 1e-3).astype(np.float32)
+    sv = np.where(rng.integers(0, 2, N + 8) > 0, 1, -1).astype(np.int8)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    col0 = 8 if M % 2 else 0
+    for with_bias in (False, True):
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        K.post(T(acc), T(s), T(rs[col0:col0 + N].copy()), T(sv[col0:col0 + N].copy()), T(bias) if with_bias else None, y, col0=col0)
+        z = (acc[:, col0:col0 + N].astype(np.float32) * s[:, None]) * rs[None, col0:col0 + N]
+        ref = O.post_bf16(z, sv[col0:col0 + N], bias if with_bias else None)
+        assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+    # FP32 accumulators (already scaled), FP32 and FP16 outputs
+    zf = (rng.standard_normal((M, N)) * 0.3).astype(np.float32)
+    for ydt in (torch.float32, torch.float16):
+        y = torch.empty(M, N, dtype=ydt, device=DEV)
+        K.post(T(zf), None, None, T(sv[:N].copy()), None, y)
+        ref = O.fwht(zf) * sv[:N].astype(np.float32)
+        if ydt == torch.float32:
+            assert np.array_equal(bits_of(y), ref.view(np.uint32))
+        else:
+            assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize('tag', ['l0', 'l1', 'l2', 'l3'])
+@pytest.mark.parametrize('dt', ['f32', 'bf16'])
+def test_w2a8_layer_golden(golden, tag, dt):
+    """pre -> decode -> exact INT32 product -> post against the reference's own W2A8 outputs, bit for bit."""
+    from yanlongvla_amd import kernels as K
+    L = layer_from(golden, tag)
+    d = dev_layer(L)
+    t8, rs, _ = K.snap(d['tlut'], d['row_scale'])
+    x = golden[f'{tag}_x_{dt}']
+    xt = torch.from_numpy(x).view(torch.bfloat16) if dt == 'bf16' else torch.from_numpy(x)
+    M = xt.shape[0]
+    q = torch.empty(M, L.n, dtype=torch.int8, device=DEV)
+    s = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.pre(xt.to(DEV), d['su'], q=q, scale=s)
+    w8 = torch.empty(L.m, L.n, dtype=torch.int8, device=DEV)
+    K.decode(d['bits'], t8, w8)
+    acc = O.int_matmul(q.cpu().numpy(), w8.cpu().numpy())       # exact products; the INT8 GEMM kernel is tested on its own
+    y = torch.empty(M, L.m, dtype=torch.bfloat16, device=DEV)
+    bias = None if L.bias is None else T(L.bias)
+    K.post(T(acc), s, rs, d['sv'], bias, y)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy(), golden[f'{tag}_y_{dt}_a8_int8'])
+
+
+# ------------------------------------------------------------------------------------------------------ FP16-table GEMV
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize('m,n,M,nl', [(2048, 2048, 1, 1), (2048, 2048, 4, 3), (48, 80, 1, 2), (256, 1024, 16, 1),
+                                      (1024, 4096, 1, 2), (4096, 1024, 2, 1), (64, 1152, 3, 2)])
+def test_gemv_f16_layer(m, n, M, nl):
+    """C0 layer: pre_h16 -> fused decode-GEMV -> post, against reference_linear(table='fp16', a8=False), rel L2 <= 2e-3."""
+    from yanlongvla_amd import kernels as K
+    layers = [O.random_layer(m, n, 100 + i) for i in range(nl)]
+    for L in layers[1:]:
+        L.su = layers[0].su                              # a batch shares the input rotation (su depends only on n)
+    rng = np.random.default_rng(m + n + M)
+    x = rng.standard_normal((M, n)).astype(np.float16)
+    xd = T(x.view(np.int16)).view(torch.float16)
+    h16 = torch.empty(M, n, dtype=torch.float16, device=DEV)
+    hs = torch.empty(M, dtype=torch.float32, device=DEV)
+    dl = [dev_layer(L) for L in layers]
+    K.pre_h16(xd, dl[0]['su'], h16, hs)
+    zs = [torch.empty(M, m, dtype=torch.float32, device=DEV) for _ in layers]
+    wdevs = [K.repack(d['bits'], m, n) for d in dl]
+    desc = K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z) for w, d, z in zip(wdevs, dl, zs)])
+    K.gemv_f16(desc, h16, hs, m, n)
+    for L, d, z in zip(layers, dl, zs):
+        y = torch.empty(M, m, dtype=torch.float32, device=DEV)
+        K.post(z, None, None, d['sv'], None, y)
+        ref = O.reference_linear(x.astype(np.float32), L, a8=False, table='fp16', out_dtype='f32')
+        assert rel_l2(y.cpu().numpy(), ref) < 2e-3
+        # accumulator before the output rotation
+        h = O.fwht(x.astype(np.float32) * L.su.astype(np.float32))
+        zr = (h.astype(np.float64) @ O.lookup(L.states(), L.tlut.astype(np.float32)).astype(np.float64).T) * \
+            L.row_scale.astype(np.float64)[None, :]
+        assert rel_l2(z.cpu().numpy(), zr) < 2e-3
+        y16 = torch.empty(M, m, dtype=torch.float16, device=DEV)
+        K.post(z, None, None, d['sv'], None, y16)
+        assert rel_l2(y16.cpu().float().numpy(), ref) < 2e-3
+
+
+def test_gemv_f16_deterministic():
+    from yanlongvla_amd import kernels as K
+    L = O.random_layer(512, 2048, 7)
+    d = dev_layer(L)
+    h16 = torch.randn(1, 2048, device=DEV).half()
+    hs = torch.ones(1, device=DEV)
+    w = K.repack(d['bits'], 512, 2048)
+    z1, z2 = torch.empty(1, 512, device=DEV), torch.empty(1, 512, device=DEV)
+    K.gemv_f16(K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z1)]), h16, hs, 512, 2048)
+    K.gemv_f16(K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z2)]), h16, hs, 512, 2048)
+    assert torch.equal(z1, z2)

@@ -1,0 +1,86 @@
+"""ctypes binding of libtcq.so (the C ABI declared in include/tcq_api.h).
+
+Mirrors the reference's kernel runtime (deploy/tcq_kernels/cuda_rt.py:79-108): tensors travel as raw device pointers,
+ints as c_int, None as NULL, and every call is issued on torch.cuda.current_stream() so HIP graph captures record it. There is
+no fallback: if the library is missing or was built for another architecture, loading fails loudly.
+"""
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / 'libtcq.so'
+
+F32, BF16, F16, I32, I8 = 0, 1, 2, 3, 4
+DTYPE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int8: I8}
+STATUS = {-1: 'invalid argument', -2: 'shape violates the format', -3: 'unsupported dtype', -4: 'unsupported size',
+          -5: 'pointer not 16-byte aligned'}
+
+_P, _I, _L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+# name -> argument types (restype int unless listed in _RESTYPE)
+SIGNATURES = {
+    'tcq_version': [],
+    'tcq_max_width': [],
+    'tcq_snap': [_P, _P, _I, _P, _P, _P, _P],
+    'tcq_repack': [_P, _P, _I, _I, _P],
+    'tcq_repack_words': [_I, _I],
+    'tcq_decode_i8': [_P, _P, _P, _I, _I, _P],
+    'tcq_decode_f16': [_P, _P, _P, _I, _I, _P],
+    'tcq_rht': [_P, _I, _I, _P, _P, _I, _I, _I, _I, _P],
+    'tcq_pre': [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_pre_h16': [_P, _I, _P, _P, _P, _I, _I, _P],
+    'tcq_quantize_rows': [_P, _I, _I, _P, _P, _I, _I, _P],
+    'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_gemv_f16': [_P, _I, _P, _P, _I, _I, _I, _P],
+}
+_RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L}
+
+_state = {}
+_lock = threading.Lock()
+
+
+class TcqError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (loaded once). Raises if libtcq.so has not been built."""
+    if 'lib' not in _state:
+        with _lock:
+            if 'lib' not in _state:
+                if not LIB_PATH.exists():
+                    raise TcqError(f'{LIB_PATH} is missing: build it with `python -m yanlongvla_amd.build` '
+                                   '(there is no CPU fallback)')
+                L = ctypes.CDLL(str(LIB_PATH))
+                for name, args in SIGNATURES.items():
+                    f = getattr(L, name)
+                    f.argtypes = args
+                    f.restype = _RESTYPE.get(name, ctypes.c_int)
+                _state['lib'] = L
+    return _state['lib']
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL). Refuses CPU tensors: the library only takes device memory."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise TcqError('libtcq takes device tensors only (got a CPU tensor)')
+    return t.data_ptr()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        what = STATUS.get(rc, f'HIP error {rc}')
+        raise TcqError(f'{name} failed: {what} (status {rc})')
+    return rc
+
+
+def version():
+    return lib().tcq_version().decode()

@@ -1,0 +1,196 @@
+// Device helpers shared by the TCQ kernels (gfx950, wave64).
+//
+// Number formats follow the reference arithmetic of deploy/tcq_kernels/tcq_format.py: BF16 round-to-nearest-even with the
+// canonical NaN 0x7fc0 (c10::BFloat16; reference kernels.py:19-25), FP16 round-to-nearest-even (_Float16 conversion),
+// IEEE FP32 division, round-half-even (v_rndne_f32). Every translation unit is built with -ffp-contract=off so that no
+// a * b + c is contracted into an FMA (the reference compiles with --fmad=false, cuda_rt.py:53).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tcq_api.h"
+
+typedef uint16_t u16;
+typedef uint32_t u32;
+typedef uint64_t u64;
+typedef int8_t i8;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef int int4_t __attribute__((ext_vector_type(4)));
+typedef u32 uint4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------------------------ conversions
+__device__ __forceinline__ float bf16_to_f32(u16 b) { return __uint_as_float(((u32)b) << 16); }
+__device__ __forceinline__ u16 f32_to_bf16(float f) {
+    u32 u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (u16)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
+
+// load element i of a row of dtype `dt` as FP32 (exact for every supported input type)
+__device__ __forceinline__ float load_as_f32(const void* p, size_t i, int dt) {
+    switch (dt) {
+        case TCQ_F32: return ((const float*)p)[i];
+        case TCQ_BF16: return bf16_to_f32(((const u16*)p)[i]);
+        case TCQ_F16: return f16_to_f32(((const u16*)p)[i]);
+        case TCQ_I32: return (float)((const int*)p)[i];
+        default: return 0.f;
+    }
+}
+__device__ __forceinline__ void store_from_f32(void* p, size_t i, float v, int dt) {
+    switch (dt) {
+        case TCQ_F32: ((float*)p)[i] = v; break;
+        case TCQ_BF16: ((u16*)p)[i] = f32_to_bf16(v); break;
+        case TCQ_F16: ((u16*)p)[i] = f32_to_f16(v); break;
+        default: break;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- wave / block reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// max over the workgroup; red: >= 16 floats of LDS. Ends with a barrier (red may be reused after it).
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float m = 0.f;
+    for (int i = 0; i < nw; ++i) m = fmaxf(m, red[i]);
+    __syncthreads();
+    return m;
+}
+
+// --------------------------------------------------------------------------------------------------- block Walsh in LDS
+// A row of K FP32 values lives in LDS at logical index i -> physical slot lds_slot(i) (one padding word per 32: strided
+// groups of up to 32 contiguous elements and unit-stride lanes both spread over all banks).
+__device__ __forceinline__ int lds_slot(int i) { return i + (i >> 5); }
+__host__ __device__ __forceinline__ int lds_words(int K) { return K + (K >> 5) + 1; }
+
+// R radix-2 stages on 2^R register values: pairs (k, k + h) for h = 1, 2, ..., 2^(R-1); the lower slot gets a + b, the upper
+// a - b, exactly the butterfly of tcq_format.fwht (reference tcq_format.py:48-52), so any distribution of the pairs over lanes
+// that keeps the stage order reproduces its sums bit for bit.
+template <int R>
+__device__ __forceinline__ void butterflies(float* v) {
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+        const int h = 1 << s;
+#pragma unroll
+        for (int k = 0; k < (1 << R); ++k)
+            if (!(k & h)) {
+                const float a = v[k], b = v[k + h];
+                v[k] = a + b;
+                v[k + h] = a - b;
+            }
+    }
+}
+
+// One pass of R consecutive stages (index bits b0 .. b0 + R - 1) over the segment [off, off + w) of the LDS row. Each thread
+// takes groups g = tid, tid + T, ...; group g covers the 2^R indices that differ only in those bits. On the last pass each
+// finished value goes to out(i, v) (i relative to the segment) instead of back to LDS.
+template <int R, bool LAST, class Out>
+__device__ __forceinline__ void walsh_pass(float* lds, int off, int w, int b0, Out&& out) {
+    const int T = blockDim.x, G = w >> R, lowmask = (1 << b0) - 1;
+    for (int g = threadIdx.x; g < G; g += T) {
+        const int i0 = ((g & ~lowmask) << R) | (g & lowmask);
+        float v[1 << R];
+#pragma unroll
+        for (int k = 0; k < (1 << R); ++k) v[k] = lds[lds_slot(off + i0 + (k << b0))];
+        butterflies<R>(v);
+#pragma unroll
+        for (int k = 0; k < (1 << R); ++k) {
+            if (LAST) out(i0 + (k << b0), v[k]);
+            else lds[lds_slot(off + i0 + (k << b0))] = v[k];
+        }
+    }
+}
+
+template <bool LAST, class Out>
+__device__ __forceinline__ void walsh_pass_r(int r, float* lds, int off, int w, int b0, Out&& out) {
+    switch (r) {
+        case 1: walsh_pass<1, LAST>(lds, off, w, b0, out); break;
+        case 2: walsh_pass<2, LAST>(lds, off, w, b0, out); break;
+        case 3: walsh_pass<3, LAST>(lds, off, w, b0, out); break;
+        case 4: walsh_pass<4, LAST>(lds, off, w, b0, out); break;
+        default: walsh_pass<5, LAST>(lds, off, w, b0, out); break;
+    }
+}
+
+// Unnormalised Walsh transform of one power-of-two segment (the LDS row must be complete and synchronised on entry). The
+// log2(w) stages are split into passes of at most 5 bits, balanced (14 = 5 + 5 + 4, 11 = 4 + 4 + 3); a barrier separates
+// passes. out(i, v) receives every finished value once. Ends without a barrier.
+template <class Out>
+__device__ __forceinline__ void walsh_segment(float* lds, int off, int w, Out&& out) {
+    const int L = 31 - __clz(w);
+    if (L == 0) {
+        if (threadIdx.x == 0) out(0, lds[lds_slot(off)]);
+        return;
+    }
+    const int passes = (L + 4) / 5;
+    int b0 = 0;
+    for (int p = 0; p < passes; ++p) {
+        const int r = (L - b0) / (passes - p);
+        if (p == passes - 1) {
+            walsh_pass_r<true>(L - b0, lds, off, w, b0, out);
+        } else {
+            walsh_pass_r<false>(r, lds, off, w, b0, out);
+            __syncthreads();
+        }
+        b0 += r;
+    }
+}
+
+// Block Walsh over the binary decomposition of K (descending powers of two, reference tcq_format.py:26-30, 44-55): every value
+// is multiplied by the FP32 constant float(1 / sqrt(w)) of its block (computed in FP64 then rounded, as
+// np.float32(1.0 / math.sqrt(w)) in tcq_format.py:40). out(i, v) gets the normalised value at row index i. Blocks touch
+// disjoint LDS so they need no barrier between them; the caller synchronises after the call.
+template <class Out>
+__device__ __forceinline__ void block_walsh(float* lds, int K, Out&& out) {
+    int off = 0, rem = K;
+    while (rem) {
+        const int w = 1 << (31 - __clz(rem));
+        const float c = (float)(1.0 / __builtin_sqrt((double)w));
+        const int o = off;
+        walsh_segment(lds, o, w, [&](int i, float v) { out(o + i, v * c); });
+        off += w;
+        rem -= w;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------- activation quantizer
+// Per-token symmetric INT8 of tcq_format.quantize_tokens (reference tcq_format.py:119-122): IEEE division, half-even, clamp.
+__device__ __forceinline__ int q8(float v, float s) {
+    float r = __builtin_rintf(v / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return (int)r;
+}
+__device__ __forceinline__ float token_scale(float amax) { return amax > 0.f ? amax / 127.f : 1.f; }
+
+// Quantize an LDS row (logical indices 0..K-1, K % 4 == 0) with scale s: q (K bytes, row-major) and / or the q4 layout
+// (K/4, ldq) int32 words (4 consecutive inputs per word, token = column), as reference kernels.py:170-184.
+__device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, int* q4, int tok, int K, int ldq) {
+    for (int j = threadIdx.x; j < (K >> 2); j += blockDim.x) {
+        const u32 word = (u32)(q8(lds[lds_slot(4 * j)], s) & 0xff) | ((u32)(q8(lds[lds_slot(4 * j + 1)], s) & 0xff) << 8) |
+                         ((u32)(q8(lds[lds_slot(4 * j + 2)], s) & 0xff) << 16) | ((u32)(q8(lds[lds_slot(4 * j + 3)], s) & 0xff) << 24);
+        if (q) ((u32*)q)[j] = word;
+        if (q4) q4[(size_t)j * ldq + tok] = (int)word;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------- trellis code
+// One 16 x 16 tile = 32 uint16 words, 512 bits, most significant bit first; state t = bits [4t, 4t + 16) (tail-biting).
+// Tile row r, weight pair p (columns 2p, 2p + 1) has state t = 8 r + p (reference tcq_format.py:58-63).
+// Code: x = (s + 1) s; table row (x >> 6) & 511; first coordinate negated when bit 15 of x is set (tcq_format.py:66-71).
+// Only bits 6..15 of x are used and they depend only on s mod 2^16, so x may be computed modulo 2^16 (two states per
+// v_pk_mad_u16) from any value congruent to s.
+//
+// Sign-folded table: entry e in 0..1023 = (e >> 9 ? -t[e & 511][0] : t[e & 511][0], t[e & 511][1]), index e = (x >> 6) & 1023.
+__device__ __forceinline__ u32 code_index(u32 x) { return (x >> 6) & 1023u; }

@@ -1,0 +1,120 @@
+"""Op-level helpers over the HIP library: caller-allocated outputs, dtype dispatch on the tensor dtype, launches on the current
+stream. Names and argument meaning follow the reference's launch helpers (deploy/tcq_kernels/kernels.py:572-696); the
+functions added here (rht, pre_h16, quantize_rows, repack, decode_f16, gemv_f16, ...) have no reference counterpart and say so.
+"""
+import torch
+
+from . import _lib
+from ._lib import DTYPE, call, ptr, stream
+
+
+def _dt(t, allowed, what):
+    d = DTYPE.get(t.dtype)
+    if d not in allowed:
+        raise TypeError(f'{what}: unsupported dtype {t.dtype}')
+    return d
+
+
+def _contig(*ts):
+    for t in ts:
+        if t is not None and not t.is_contiguous():
+            raise ValueError('tensors passed to the TCQ kernels must be contiguous')
+
+
+# ------------------------------------------------------------------------------------------------------------- load time
+def snap(tlut, row_scale, t8=None, rs=None, gain=None):
+    """INT8 table / row scale / gain of tcq_format.snap (reference tcq_format.py:74-77), computed on the device."""
+    dev = tlut.device
+    t8 = torch.empty(512, 2, dtype=torch.int8, device=dev) if t8 is None else t8
+    rs = torch.empty(row_scale.numel(), dtype=torch.float32, device=dev) if rs is None else rs
+    gain = torch.empty(1, dtype=torch.float32, device=dev) if gain is None else gain
+    _contig(tlut, row_scale, t8, rs)
+    call('tcq_snap', ptr(tlut), ptr(row_scale), row_scale.numel(), ptr(t8), ptr(rs), ptr(gain), stream())
+    return t8, rs, gain
+
+
+def repack_words(m, n):
+    return int(_lib.lib().tcq_repack_words(m, n))
+
+
+def repack(bits, m, n, out=None):
+    """Reference word layout -> device layout of the fused products (no reference counterpart; a load-time permutation)."""
+    out = torch.empty(repack_words(m, n), dtype=torch.int32, device=bits.device) if out is None else out
+    _contig(bits, out)
+    call('tcq_repack', ptr(bits), ptr(out), m, n, stream())
+    return out
+
+
+# ---------------------------------------------------------------------------------------------------------------- decode
+def decode(bits, t8, out):
+    """Dense INT8 decode, out (m, n) int8 (reference kernels.py:653-656)."""
+    m, n = out.shape
+    _contig(bits, t8, out)
+    call('tcq_decode_i8', ptr(bits), ptr(t8), ptr(out), m, n, stream())
+
+
+def decode_f16(bits, tlut, out):
+    """Dense decode through the FP16 table, out (m, n) float16 (exact lookup(states, tlut))."""
+    m, n = out.shape
+    _contig(bits, tlut, out)
+    call('tcq_decode_f16', ptr(bits), ptr(tlut), ptr(out), m, n, stream())
+
+
+# -------------------------------------------------------------------------------------------------------------- rotation
+def rht(x, su, y):
+    """y = fwht(x * su) row by row (su may be None). x, y (M, n); dtypes float32 / bfloat16 / float16."""
+    M, n = x.shape
+    call('tcq_rht', ptr(x), _dt(x, (0, 1, 2), 'rht x'), x.stride(0), ptr(su), ptr(y), _dt(y, (0, 1, 2), 'rht y'), y.stride(0),
+         M, n, stream())
+    return y
+
+
+def pre(x, su, q=None, q4=None, scale=None):
+    """x (M, K) BF16 / FP32 / FP16 contiguous -> q (M, K) int8 and / or q4 (K/4, ld) int32, scale (M,) FP32
+    (reference kernels.py:602-606)."""
+    M, K = x.shape
+    _contig(x, su, q, q4, scale)
+    call('tcq_pre', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(q), ptr(q4), 0 if q4 is None else q4.shape[1], ptr(scale),
+         M, K, stream())
+
+
+def pre_h16(x, su, h16, hscale):
+    """Float path: h16 (M, K) float16 = fwht(x * su) / hscale, hscale (M,) FP32 powers of two."""
+    M, K = x.shape
+    _contig(x, su, h16, hscale)
+    call('tcq_pre_h16', ptr(x), _dt(x, (0, 1, 2), 'pre_h16 x'), ptr(su), ptr(h16), ptr(hscale), M, K, stream())
+
+
+def quantize_rows(x, q, scale):
+    """Per-row symmetric INT8 without rotation (tcq_format.quantize_tokens): q (M, K) int8, scale (M,) FP32."""
+    M, K = x.shape
+    _contig(q, scale)
+    call('tcq_quantize_rows', ptr(x), _dt(x, (0, 1, 2), 'quantize_rows x'), x.stride(0), ptr(q), ptr(scale), M, K, stream())
+
+
+def post(acc, s, rs, sv, bias, y, col0=0):
+    """acc (M, lda) int32 (scaled here by s, rs), FP32 (already scaled) or BF16 (scaled by rs); columns col0 .. col0 + N -> y
+    (M, N) BF16 / FP16 / FP32 (reference kernels.py:612-615)."""
+    M, N = y.shape
+    _contig(acc, s, rs, sv, bias, y)
+    call('tcq_post', ptr(acc), _dt(acc, (0, 1, 3), 'post acc'), acc.shape[1], col0, ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(y),
+         _dt(y, (0, 1, 2), 'post y'), M, N, stream())
+
+
+# -------------------------------------------------------------------------------------------------------------- products
+def gemv_descriptors(layers):
+    """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers each). Keep the tensors alive."""
+    flat = []
+    for wdev, tlut, row_scale, z in layers:
+        _contig(wdev, tlut, row_scale, z)
+        flat += [ptr(wdev), ptr(tlut), ptr(row_scale), ptr(z)]
+    dev = layers[0][0].device
+    return torch.tensor(flat, dtype=torch.int64).to(dev)
+
+
+def gemv_f16(desc, h16, hscale, m, n):
+    """Batched FP16-table decode-GEMV: for every layer in desc, z (M, m) = (h16 Q^T) * hscale * row_scale (M <= 16)."""
+    M = h16.shape[0]
+    _contig(h16, hscale)
+    call('tcq_gemv_f16', ptr(desc), desc.shape[0] // 4 if desc.dim() == 1 else desc.shape[0], ptr(h16), ptr(hscale), M, m, n,
+         stream())
