@@ -1,0 +1,240 @@
+"""Benchmark of the TCQ 2-bit deploy path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--layers 1024] [--cpu-seconds 10]
+
+Headline workload (one JSON line on stdout): the 2-bit TCQ decode-GEMV of a 2048 x 2048 layer at batch 1 with FP16
+activations and the FP16 512 x 2 codebook (bitshift trellis L = 16, K = 2, V = 2), streamed over `--layers` distinct layers
+(1 MiB of packed words each; 1024 layers = 1 GiB, four times the 256 MB Infinity Cache, so the words come from HBM). One
+step = the complete layer forward of every layer on the same input token:
+    input rotation h = fwht(x * su) -> FP16 (tcq_pre_h16, once: the layers share the input signs, as a q/k/v group does)
+    fused decode-GEMV z_l = (h Q_l^T) * r_l for all layers (tcq_gemv_f16, one launch)
+    output rotation y_l = fwht(z_l) * sv_l (tcq_postg, one launch over all layers).
+value = packed-weight bytes per step / step time (GB/s). roofline = the decode-GEMV kernel alone, timed with HIP events on
+the stream it runs on. cpu_baseline = the oracle's restatement of the reference layer (reference_linear, FP16 table,
+unquantized activations) timed on the host over a bounded sample of the same layers.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published peak
+M_DIM = N_DIM = 2048           # config: one 2048 x 2048 layer, batch 1
+PACKED_BYTES = M_DIM * N_DIM * 2 // 8
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=200)
+    p.add_argument('--warmup', type=int, default=20)
+    p.add_argument('--layers', type=int, default=1024)
+    p.add_argument('--cpu-seconds', type=float, default=10.0)
+    p.add_argument('--no-cpu', action='store_true')
+    p.add_argument('--seed', type=int, default=0)
+    return p.parse_args()
+
+
+def make_stream(nl, seed, dev):
+    """nl synthetic C0 layers: uniform-random packed words, N(0,1) FP16 tables, one FP16 scale per layer drawn U[0.5, 1.5]
+    broadcast over rows, random +-1 signs (one shared input sign vector)."""
+    import torch
+    from yanlongvla_amd import kernels as K
+    g = torch.Generator(device=dev).manual_seed(seed)
+    tiles = (M_DIM // 16) * (N_DIM // 16)
+    bits = torch.randint(-32768, 32768, (nl * tiles, 32), generator=g, device=dev, dtype=torch.int32).to(torch.int16)
+    wdev = K.repack(bits, nl * M_DIM, N_DIM)                 # stacked layers repack as one tall layer
+    per = K.repack_words(M_DIM, N_DIM)
+    tlut = torch.randn(nl, 512, 2, generator=g, device=dev).half()
+    scale = torch.rand(nl, 1, generator=g, device=dev) + 0.5
+    row_scale = scale.expand(nl, M_DIM).half().contiguous()
+    su = (torch.randint(0, 2, (N_DIM,), generator=g, device=dev) * 2 - 1).to(torch.int8)
+    sv = (torch.randint(0, 2, (nl, M_DIM), generator=g, device=dev) * 2 - 1).to(torch.int8)
+    return dict(bits=bits, wdev=wdev, per=per, tlut=tlut, row_scale=row_scale, su=su, sv=sv)
+
+
+class Stream:
+    """Buffers and launch descriptors of one pass over the layer stream (allocated once; the pass allocates nothing)."""
+
+    def __init__(self, L, x, M=1):
+        import torch
+        from yanlongvla_amd import kernels as K
+        dev = x.device
+        nl = L['tlut'].shape[0]
+        self.K, self.L, self.x, self.nl, self.M = K, L, x, nl, M
+        self.h16 = torch.empty(M, N_DIM, dtype=torch.float16, device=dev)
+        self.hs = torch.empty(M, dtype=torch.float32, device=dev)
+        self.z = torch.empty(nl, M, M_DIM, dtype=torch.float32, device=dev)
+        self.y = torch.empty(nl, M, M_DIM, dtype=torch.float16, device=dev)
+        w = L['wdev'].view(nl, L['per'])
+        self.gdesc = K.gemv_descriptors([(w[i], L['tlut'][i], L['row_scale'][i], self.z[i]) for i in range(nl)])
+        self.pdesc = K.post_segments([(self.z[i], 0, None, L['sv'][i], None, self.y[i], False) for i in range(nl)], dev)
+
+    def rotate_in(self):
+        self.K.pre_h16(self.x, self.L['su'], self.h16, self.hs)
+
+    def gemv(self):
+        self.K.gemv_f16(self.gdesc, self.h16, self.hs, M_DIM, N_DIM)
+
+    def rotate_out(self):
+        import torch
+        self.K.postg(self.pdesc, self.nl, torch.float32, torch.float16, None, self.M, M_DIM)
+
+    def step(self):
+        self.rotate_in()
+        self.gemv()
+        self.rotate_out()
+
+
+def timed(fn, steps, warmup):
+    """Average ms of fn over `steps` calls after `warmup` untimed calls, HIP events on the current stream (where the library
+    launches), bracketed by device synchronisation."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def graph_latency(fn, replays=200, warmup=20):
+    """Median / p95 ms of one HIP-graph replay of fn (the reference's timing protocol: 20 warm-up + 200 timed replays)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2], ts[int(len(ts) * 0.95)]
+
+
+def check_against_oracle(L, S, n_check=2):
+    """Spot check of the timed pass: the first layers' outputs against the oracle (relative L2 <= 2e-3)."""
+    import numpy as np
+    from oracle import tcq_oracle as O
+    x = S.x.float().cpu().numpy()
+    errs = []
+    for i in range(n_check):
+        OL = oracle_layer(L, i)
+        ref = O.reference_linear(x, OL, a8=False, table='fp16', out_dtype='f32')
+        y = S.y[i].float().cpu().numpy()
+        errs.append(float(np.linalg.norm(y - ref) / np.linalg.norm(ref)))
+    return max(errs)
+
+
+def oracle_layer(L, i):
+    from oracle import tcq_oracle as O
+    tiles = (M_DIM // 16) * (N_DIM // 16)
+    t = dict(bits=L['bits'][i * tiles:(i + 1) * tiles].cpu().numpy(), tlut=L['tlut'][i].cpu().numpy(),
+             row_scale=L['row_scale'][i].cpu().numpy(), su=L['su'].cpu().numpy(), sv=L['sv'][i].cpu().numpy())
+    return O.Layer(f'layer{i}', t)
+
+
+def cpu_baseline(L, x, seconds):
+    """The oracle's reference layer (FP16 table, a8=False: windowed read, table lookup, FP64 product, two rotations) on the
+    host cores, over as many of the stream's layers as fit in about `seconds` (at least 2)."""
+    import numpy as np
+    from oracle import tcq_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        blas = max([d.get('num_threads', 1) for d in threadpool_info() if d.get('user_api') == 'blas'] or [1])
+    except Exception:
+        blas = 1
+    xs = x.float().cpu().numpy()
+    layers = [oracle_layer(L, 0)]
+    O.reference_linear(xs, layers[0], a8=False, table='fp16', out_dtype='f32')      # warm-up
+    el, done = 0.0, 0          # compute time only: the device -> host copy of each layer is outside the timing
+    while done < 2 or (el < seconds and done < L['tlut'].shape[0]):
+        OL = oracle_layer(L, done)
+        t1 = time.perf_counter()
+        O.reference_linear(xs, OL, a8=False, table='fp16', out_dtype='f32')
+        el += time.perf_counter() - t1
+        done += 1
+    return dict(value=round(done * PACKED_BYTES / el / 1e9, 4), unit='GB/s', cores=int(blas), kind='port',
+                sample=f'{done} of the stream\'s 2048x2048 layers at batch 1 through the numpy oracle '
+                       f'(reference_linear, FP16 table, a8=False), {el:.1f} s; host affinity {len(os.sched_getaffinity(0))} cores')
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({'error': f'--gpus {args.gpus}: this benchmark runs on one GPU only; the path has no multi-GPU '
+                                   'implementation (row-split sharding is described in the design notes)'}))
+        sys.exit(2)
+    import torch
+    from yanlongvla_amd import _lib
+    _lib.lib()
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    nl = args.layers
+    L = make_stream(nl, args.seed, dev)
+    gx = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    x = torch.randn(1, N_DIM, generator=gx, device=dev).half()
+    S = Stream(L, x)
+    S.step()
+    torch.cuda.synchronize()
+    err = check_against_oracle(L, S)
+    if not err < 2e-3:
+        raise SystemExit(f'decode-GEMV output differs from the oracle: relative L2 {err}')
+
+    ms_step = timed(S.step, args.steps, args.warmup)
+    ms_gemv = timed(S.gemv, args.steps, args.warmup)
+    byts = nl * PACKED_BYTES
+    achieved = byts / (ms_gemv * 1e-3) / 1e9
+    # single-layer latency (one layer, one token: rotation, decode-GEMV, rotation), HIP graph replays
+    L1 = dict(L, tlut=L['tlut'][:1], row_scale=L['row_scale'][:1], sv=L['sv'][:1], wdev=L['wdev'][:L['per']])
+    S1 = Stream(L1, x)
+    lat_med, lat_p95 = graph_latency(S1.step)
+    cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
+    out = {
+        'metric': 'TCQ-2bit decode-GEMV GB/s (% HBM peak) + ms per action chunk, 1 GPU',
+        'value': round(byts / (ms_step * 1e-3) / 1e9, 2),
+        'unit': 'GB/s',
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'ms_per_step': round(ms_step, 5),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'fp16',
+        'data': 'synthetic (seeded uniform-random packed trellis words, N(0,1) FP16 tables, random signs, N(0,1) FP16 input)',
+        'config': {'workload': f'tcq2 decode-GEMV layer stream: {nl} distinct 2048x2048 layers, batch 1, FP16 activations, '
+                               'FP16 512x2 codebook, L=16 K=2 V=2, input and output block-Walsh rotations',
+                   'layers': nl, 'm': M_DIM, 'n': N_DIM, 'tokens': 1, 'packed_bytes_per_step': byts},
+        'hbm_frac': round(byts / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
+                     'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
+        'single_layer_ms': {'median': round(lat_med, 5), 'p95': round(lat_p95, 5)},
+        'max_rel_l2_vs_oracle': err,
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

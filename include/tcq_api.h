@@ -100,6 +100,26 @@ int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q, float* sca
 int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
              const float* bias, void* y, int y_dtype, int M, int N, tcq_stream_t stream);
 
+/* One segment of a batched epilogue: columns col0 .. col0 + N of M accumulator rows (stride lda elements) -> y (M, N). */
+typedef struct tcq_post_seg {
+    const void* acc;     /* accumulator base */
+    const float* rs;     /* (N,) FP32 row scale (I32 / BF16 accumulators), else NULL */
+    const int8_t* sv;    /* (N,) output signs */
+    const float* bias;   /* (N,) FP32 or NULL */
+    void* y;             /* (M, N) output, row stride N */
+    int lda, col0, N;
+    int gelu;            /* nonzero: BF16 output goes through the GELU table (gelu_lut must then be given) */
+} tcq_post_seg;
+
+/* Batched epilogue: one workgroup per (token, segment), each segment as tcq_post with its own columns, row scale, signs, bias,
+ * output and optional GELU. segs is a DEVICE array of nseg descriptors; every segment's N must be <= maxN (a segment with
+ * N > maxN or N <= 0 is skipped). acc_dtype and y_dtype apply to all segments; s (M,) FP32 per-token scales for I32
+ * accumulators. gelu_lut: 65536 BF16 values, GELU (tanh) of every BF16 bit pattern, or NULL.
+ * Replaces kernels.post3 / k_post3_* and kernels.postg / k_postg_* (deploy/tcq_kernels/kernels.py:232-261, 618-628), which
+ * hold at most three segments sharing one accumulator row; here the count is free and each segment may have its own base. */
+int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype, int M,
+              int maxN, tcq_stream_t stream);
+
 /* -------------------------------------------------------------------------------------------------------- products */
 
 /* One layer of a batched FP16-table decode-GEMV / small-M GEMM (M <= 16 tokens): z[t, i] = (sum_k h16[t, k] *

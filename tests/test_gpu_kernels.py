@@ -252,3 +252,60 @@ def test_gemv_f16_deterministic():
     K.gemv_f16(K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z1)]), h16, hs, 512, 2048)
     K.gemv_f16(K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z2)]), h16, hs, 512, 2048)
     assert torch.equal(z1, z2)
+
+
+# ------------------------------------------------------------------------------------------------------ batched epilogue
+@pytest.mark.parametrize('M', [1, 10, 50])
+def test_postg_matches_post_and_oracle(M):
+    """q / k / v style segments sharing one INT32 accumulator row, plus separate FP32 accumulators, with bias and GELU."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M)
+    widths = [2048, 256, 256]
+    lda = sum(widths)
+    acc = rng.integers(-2 ** 20, 2 ** 20, size=(M, lda)).astype(np.int32)
+    s = (rng.random(M) + 0.5).astype(np.float32)
+    rs = (rng.random(lda) * 1e-3).astype(np.float32)
+    sv = np.where(rng.integers(0, 2, lda) > 0, 1, -1).astype(np.int8)
+    bias = (rng.standard_normal(lda) * 0.1).astype(np.float32)
+    accd, sd = T(acc), T(s)
+    ys, segs, c0 = [], [], 0
+    for i, w in enumerate(widths):
+        y = torch.empty(M, w, dtype=torch.bfloat16, device=DEV)
+        segs.append((accd, c0, T(rs[c0:c0 + w].copy()), T(sv[c0:c0 + w].copy()), T(bias[c0:c0 + w].copy()) if i else None, y, i == 0))
+        ys.append(y)
+        c0 += w
+    lut = K.gelu_table(DEV)
+    desc = K.post_segments(segs, DEV)
+    K.postg(desc, len(segs), torch.int32, torch.bfloat16, sd, M, max(widths), gelu_lut=lut)
+    lut_np = lut.view(torch.int16).cpu().numpy().view(np.uint16)
+    c0 = 0
+    for i, (w, y) in enumerate(zip(widths, ys)):
+        z = (acc[:, c0:c0 + w].astype(np.float32) * s[:, None]) * rs[None, c0:c0 + w]
+        ref = O.post_bf16(z, sv[c0:c0 + w], bias[c0:c0 + w] if i else None)
+        if i == 0:
+            ref = lut_np[ref]
+        assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+        c0 += w
+    # FP32 accumulators of separate layers (the decode-GEMV outputs), FP32 outputs
+    zs = [T((rng.standard_normal((M, 512)) * 0.2).astype(np.float32)) for _ in range(5)]
+    svs = [np.where(rng.integers(0, 2, 512) > 0, 1, -1).astype(np.int8) for _ in range(5)]
+    outs = [torch.empty(M, 512, dtype=torch.float32, device=DEV) for _ in range(5)]
+    desc = K.post_segments([(z, 0, None, T(v), None, y, False) for z, v, y in zip(zs, svs, outs)], DEV)
+    K.postg(desc, 5, torch.float32, torch.float32, None, M, 512)
+    for z, v, y in zip(zs, svs, outs):
+        ref = O.fwht(z.cpu().numpy()) * v.astype(np.float32)
+        assert np.array_equal(bits_of(y), ref.view(np.uint32))
+
+
+def test_gelu_table_vs_cpu():
+    """The device GELU table against PyTorch's CPU routine over all 65,536 BF16 inputs (NaN inputs: both NaN). Records the
+    number of differing finite entries; the fused kernels use the device table, as the reference does."""
+    from yanlongvla_amd import kernels as K
+    dev = K.gelu_table(DEV).cpu()
+    allb = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    cpu = torch.nn.functional.gelu(allb, approximate='tanh')
+    nan = torch.isnan(allb)
+    assert bool((torch.isnan(dev) == torch.isnan(cpu))[nan].all())
+    diff = (dev.view(torch.int16) != cpu.view(torch.int16)) & ~nan
+    print(f'GELU table: {int(diff.sum())} of {int((~nan).sum())} finite BF16 inputs differ between device and CPU')
+    assert int(diff.sum()) < 65536 // 100

@@ -32,6 +32,7 @@ SIGNATURES = {
     'tcq_pre_h16': [_P, _I, _P, _P, _P, _I, _I, _P],
     'tcq_quantize_rows': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_postg': [_P, _I, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemv_f16': [_P, _I, _P, _P, _I, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L}

@@ -110,6 +110,27 @@ __global__ void k_post(const void* acc, int lda, int col0, const float* s, const
     });
 }
 
+// Batched epilogue: workgroup (token, segment). Segments with N outside (0, maxN] are skipped (LDS is sized for maxN).
+template <int ADT, int YDT>
+__global__ void k_postg(const tcq_post_seg* segs, const float* s, const u16* gelu_lut, int maxN) {
+    extern __shared__ float lds[];
+    const tcq_post_seg S = segs[blockIdx.y];
+    const int tok = blockIdx.x, N = S.N;
+    if (N <= 0 || N > maxN) return;
+    const size_t base = (size_t)tok * S.lda + S.col0;
+    const float st = (ADT == TCQ_I32) ? s[tok] : 1.f;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) lds[lds_slot(i)] = scaled_acc<ADT>(S.acc, base + i, st, S.rs, i);
+    __syncthreads();
+    const size_t yb = (size_t)tok * N;
+    const bool gl = YDT == TCQ_BF16 && S.gelu && gelu_lut;
+    block_walsh(lds, N, [&](int i, float v) {
+        v = v * (float)S.sv[i];
+        if (S.bias) v = v + S.bias[i];
+        if (gl) ((u16*)S.y)[yb + i] = gelu_lut[f32_to_bf16(v)];
+        else Elem<YDT>::st(S.y, yb + i, v);
+    });
+}
+
 // =========================================================================================================== C ABI
 static int row_threads(int K) {
     const int top = 1 << (31 - __builtin_clz(K));
@@ -201,6 +222,32 @@ extern "C" int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const
         case TCQ_I32: POST_A(TCQ_I32); break;
         case TCQ_F32: POST_A(TCQ_F32); break;
         case TCQ_BF16: POST_A(TCQ_BF16); break;
+        default: return TCQ_ERR_DTYPE;
+    }
+    return launch_status();
+}
+
+extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype,
+                         int M, int maxN, tcq_stream_t stream) {
+    if (!segs || nseg <= 0 || M <= 0 || maxN <= 0) return TCQ_ERR_ARG;
+    if (acc_dtype == TCQ_I32 && !s) return TCQ_ERR_ARG;
+    if (maxN > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (nseg > 65535) return TCQ_ERR_UNSUPPORTED;
+    const dim3 grid(M, nseg), block(row_threads(maxN));
+    const size_t sh = row_lds(maxN);
+    hipStream_t st = (hipStream_t)stream;
+#define POSTG_Y(AD, YD) launch_k(k_postg<AD, YD>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN)
+#define POSTG_A(AD)                                          \
+    switch (y_dtype) {                                       \
+        case TCQ_F32: POSTG_Y(AD, TCQ_F32); break;           \
+        case TCQ_BF16: POSTG_Y(AD, TCQ_BF16); break;         \
+        case TCQ_F16: POSTG_Y(AD, TCQ_F16); break;           \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+    switch (acc_dtype) {
+        case TCQ_I32: POSTG_A(TCQ_I32); break;
+        case TCQ_F32: POSTG_A(TCQ_F32); break;
+        case TCQ_BF16: POSTG_A(TCQ_BF16); break;
         default: return TCQ_ERR_DTYPE;
     }
     return launch_status();

@@ -118,3 +118,50 @@ def gemv_f16(desc, h16, hscale, m, n):
     _contig(h16, hscale)
     call('tcq_gemv_f16', ptr(desc), desc.shape[0] // 4 if desc.dim() == 1 else desc.shape[0], ptr(h16), ptr(hscale), M, m, n,
          stream())
+
+
+# ------------------------------------------------------------------------------------------------------ batched epilogue
+_SEG = None
+
+
+def _seg_dtype():
+    global _SEG
+    if _SEG is None:
+        import numpy as np
+        _SEG = np.dtype([('acc', '<u8'), ('rs', '<u8'), ('sv', '<u8'), ('bias', '<u8'), ('y', '<u8'), ('lda', '<i4'),
+                         ('col0', '<i4'), ('N', '<i4'), ('gelu', '<i4')])
+        assert _SEG.itemsize == 56
+    return _SEG
+
+
+def post_segments(segs, device):
+    """[(acc, col0, rs, sv, bias, y, gelu), ...] -> device array of tcq_post_seg. acc: (M, lda) tensor; y: (M, N) tensor.
+    Keep the tensors alive while the array is in use (its pointers are baked in, as in a captured graph)."""
+    import numpy as np
+    a = np.zeros(len(segs), dtype=_seg_dtype())
+    for i, (acc, col0, rs, sv, bias, y, gelu) in enumerate(segs):
+        _contig(acc, rs, sv, bias, y)
+        N = y.shape[1]
+        if col0 < 0 or col0 + N > acc.shape[1] or sv.numel() != N or (rs is not None and rs.numel() != N):
+            raise ValueError(f'segment {i}: columns {col0}..{col0 + N} do not fit the accumulator / scales')
+        a[i] = (ptr(acc), ptr(rs) or 0, ptr(sv), ptr(bias) or 0, ptr(y), acc.shape[1], col0, N, int(bool(gelu)))
+    return torch.from_numpy(a.view(np.uint8).copy()).to(device)
+
+
+def postg(desc, nseg, acc_dtype, y_dtype, s, M, maxN, gelu_lut=None):
+    """Batched epilogue over nseg segments of post_segments (reference kernels.postg / post3, kernels.py:618-628): one
+    workgroup per (token, segment). acc_dtype / y_dtype: torch dtypes shared by all segments."""
+    call('tcq_postg', ptr(desc), nseg, DTYPE[acc_dtype], ptr(s), ptr(gelu_lut), DTYPE[y_dtype], M, maxN, stream())
+
+
+_GELU = {}
+
+
+def gelu_table(device):
+    """BF16 GELU (tanh approximation) of every BF16 bit pattern, computed by PyTorch on `device` (reference
+    kernels.gelu_table, kernels.py:563-569): the fused kernels look the activation up instead of re-implementing it."""
+    key = str(device)
+    if key not in _GELU:
+        x = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+        _GELU[key] = torch.nn.functional.gelu(x, approximate='tanh').contiguous()
+    return _GELU[key]
