@@ -80,7 +80,7 @@ def test_decode_golden(golden, tag):
 
 
 # -------------------------------------------------------------------------------------------------------------------- RHT
-RHT_CASES = [(1, 1), (3, 16), (2, 48), (5, 80), (1, 1024), (16, 2048), (50, 4096), (16, 16384), (4, 1152), (3, 4304),
+RHT_CASES = [(1, 1), (3, 16), (2, 48), (5, 80), (2, 20), (1, 1024), (16, 2048), (50, 4096), (16, 16384), (4, 1152), (3, 4304),
              (800, 1024), (800, 16384)]
 
 
@@ -131,7 +131,8 @@ def test_rht_involution_full_size(M, n):
 
 
 # ------------------------------------------------------------------------------------------------------------ pre / post
-@pytest.mark.parametrize('M,K', [(1, 48), (3, 80), (10, 1024), (16, 2048), (50, 4096), (7, 16384), (300, 2048), (4, 1152)])
+@pytest.mark.parametrize('M,K', [(1, 48), (3, 80), (2, 20), (10, 1024), (16, 2048), (50, 4096), (7, 16384), (300, 2048),
+                                 (4, 1152), (800, 4096)])
 @pytest.mark.parametrize('xdt', [torch.bfloat16, torch.float32])
 def test_pre_bitexact(M, K, xdt):
     from yanlongvla_amd import kernels as Kk
@@ -150,7 +151,8 @@ def test_pre_bitexact(M, K, xdt):
     assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
 
 
-@pytest.mark.parametrize('M,N', [(1, 16), (3, 48), (10, 256), (16, 2048), (50, 4096), (5, 16384), (300, 1024), (2, 4304)])
+@pytest.mark.parametrize('M,N', [(1, 16), (3, 48), (2, 20), (10, 256), (16, 2048), (50, 4096), (5, 16384), (300, 1024),
+                                 (2, 4304), (800, 2048)])
 def test_post_bitexact(M, N):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * N)

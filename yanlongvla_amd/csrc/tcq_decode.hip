@@ -1,16 +1,6 @@
-// Trellis decode kernels: load-time table snap and word repack, dense INT8 / FP16 decode, and the fused FP16-table
-// decode-GEMV (small-M GEMM on MFMA) that streams the packed words from HBM.
+// Trellis decode kernels: load-time table snap and word repack, dense INT8 / FP16 decode.
 #include "tcq_device.h"
 #include "tcq_launch.h"
-
-typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
-
-// x = (s + 1) s modulo 2^16 for the two 16-bit states held in w (one v_pk_mad_u16)
-__device__ __forceinline__ u32 pk_code(u32 w) {
-    const ushort2_t s = __builtin_bit_cast(ushort2_t, w);
-    const ushort2_t x = s * s + s;
-    return __builtin_bit_cast(u32, x);
-}
 
 // 48-bit window of tile row r: hi = (word[2r] << 16) | word[2r + 1], lo = word[(2r + 2) & 31]. State p (0..7) =
 // bits [4p, 4p + 16) of hi:lo from the top (reference tcq_format.py:58-63; kernels.py:186-205).
@@ -105,86 +95,6 @@ __global__ void k_decode_f16(const u16* bits, const u16* tlut, u16* out, int m, 
     o[1] = w1;
 }
 
-// ------------------------------------------------------------------------------------------- fused FP16-table decode-GEMV
-// Work: one wave = TRW tile rows (16 output rows each) over the whole input width; a workgroup of 8 waves covers
-// rows_per_wg tile rows of one layer (blockIdx.y = layer). Per chunk of 16 tiles (1 KiB of words in the device layout) each
-// lane loads one dwordx4: the windows hi_r of 4 tiles (tile 16 c + 4 j + g, lane = 16 g + r). The neighbour window hi_{r+1}
-// (tail-biting within the tile) comes from lane (r + 1) % 16 of the same 16-lane row by DPP row_ror:15. The 32-bit window
-// starting at state p (p = 0..3) holds state p in its high half and state p + 4 in its low half, so one v_pk_mad_u16 gives
-// both codes; each code indexes the sign-folded FP16-pair table in LDS. The 8 pairs of the lane's tile row are the
-// A operands of two v_mfma_f32_16x16x32_f16 (k slots = the tile's columns 0..7 and 8..15, any k order works as long as the
-// activations use the same one); B = activations of tokens j = lane % 16 (zero for j >= M).
-template <int NCOPY, int TRW>
-__global__ __launch_bounds__(512) void k_gemv_f16(const tcq_gemv_layer* layers, const u16* h16, const float* hscale, int M,
-                                                  int m, int n, int rows_per_wg) {
-    extern __shared__ u32 tab[];  // 1024 * NCOPY entries: entry e, copy c at e * NCOPY + c
-    const tcq_gemv_layer L = layers[blockIdx.y];
-    const u16* tl = (const u16*)L.tlut;
-    for (int i = threadIdx.x; i < 1024 * NCOPY; i += blockDim.x) {
-        const int e = i / NCOPY, h = e & 511;
-        tab[i] = ((u32)tl[2 * h] ^ ((u32)(e >> 9) << 15)) | ((u32)tl[2 * h + 1] << 16);
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int lr = lane & 15, lg = lane >> 4, cp = lane & (NCOPY - 1);
-    const int tiles_m = m >> 4, nch = (n + 255) >> 8;
-    const int I0 = blockIdx.x * rows_per_wg, I1 = min(I0 + rows_per_wg, tiles_m);
-    const uint4_t* W = (const uint4_t*)L.wdev;
-    const u16* rsc = (const u16*)L.row_scale;
-    for (int I = I0 + wave * TRW; I < I1; I += nwaves * TRW) {
-        float4_t acc[TRW];
-#pragma unroll
-        for (int t = 0; t < TRW; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < nch; ++c) {
-            half8_t B[4][2];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k0 = 16 * (16 * c + 4 * j + lg);
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const int k = k0 + 8 * hf;
-                    if (lr < M && k < n) B[j][hf] = *(const half8_t*)(h16 + (size_t)lr * n + k);
-                    else B[j][hf] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < TRW; ++t) {
-                if (I + t >= I1) break;
-                const uint4_t d = W[((size_t)(I + t) * nch + c) * 64 + lane];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const u32 hi = d[j];
-                    const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
-                    u32 a0[4], a1[4];
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        const u32 wp = p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p);
-                        const u32 x = pk_code(wp);
-                        a0[p] = tab[code_index(x >> 16) * NCOPY + cp];
-                        a1[p] = tab[code_index(x & 0xffffu) * NCOPY + cp];
-                    }
-                    const uint4_t A0 = {a0[0], a0[1], a0[2], a0[3]}, A1 = {a1[0], a1[1], a1[2], a1[3]};
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A0), B[j][0], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A1), B[j][1], acc[t], 0, 0, 0);
-                }
-            }
-        }
-        // D layout: lane = 16 g + j holds rows 4 g .. 4 g + 3 of token j
-        if (lr < M) {
-            const float hs = hscale[lr];
-#pragma unroll
-            for (int t = 0; t < TRW; ++t) {
-                if (I + t >= I1) break;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int row = 16 * (I + t) + 4 * lg + e;
-                    L.z[(size_t)lr * m + row] = (acc[t][e] * hs) * f16_to_f32(rsc[row]);
-                }
-            }
-        }
-    }
-}
-
 // =========================================================================================================== C ABI
 extern "C" const char* tcq_version(void) { return "tcq-mi355x 0.1 (gfx950)"; }
 extern "C" int tcq_max_width(void) { return TCQ_MAX_WIDTH; }
@@ -226,23 +136,5 @@ extern "C" int tcq_decode_f16(const void* bits, const void* tlut, void* out, int
     const size_t total = (size_t)m * (n / 16);
     launch_k(k_decode_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
              (const u16*)tlut, (u16*)out, m, n);
-    return launch_status();
-}
-
-extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
-                            tcq_stream_t stream) {
-    if (!layers || !h16 || !hscale || nlayers <= 0 || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
-    if (m % 16 || n % 16) return TCQ_ERR_SHAPE;
-    if (M > 16 || nlayers > 65535) return TCQ_ERR_UNSUPPORTED;
-    if ((uintptr_t)h16 % 16) return TCQ_ERR_ALIGN;
-    constexpr int NCOPY = 1, TRW = 1, WAVES = 8;
-    const int tiles_m = m / 16;
-    // enough workgroups to fill the chip: about 1024 in total, at least one wave-row per wave
-    int per_layer = (1024 + nlayers - 1) / nlayers;
-    int rows_per_wg = (tiles_m + per_layer - 1) / per_layer;
-    if (rows_per_wg < WAVES * TRW) rows_per_wg = WAVES * TRW < tiles_m ? WAVES * TRW : tiles_m;
-    const int wgs = (tiles_m + rows_per_wg - 1) / rows_per_wg;
-    launch_k(k_gemv_f16<NCOPY, TRW>, dim3(wgs, nlayers), dim3(64 * WAVES), 1024 * NCOPY * sizeof(u32), (hipStream_t)stream,
-             layers, (const u16*)h16, hscale, M, m, n, rows_per_wg);
     return launch_status();
 }

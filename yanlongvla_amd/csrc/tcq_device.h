@@ -194,3 +194,31 @@ __device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, i
 //
 // Sign-folded table: entry e in 0..1023 = (e >> 9 ? -t[e & 511][0] : t[e & 511][0], t[e & 511][1]), index e = (x >> 6) & 1023.
 __device__ __forceinline__ u32 code_index(u32 x) { return (x >> 6) & 1023u; }
+
+// x = s * s + s = (s + 1) s modulo 2^16 for both 16-bit states held in w: one v_pk_mad_u16 (the compiler splits the
+// vector expression into an add and a multiply)
+__device__ __forceinline__ u32 pk_code(u32 w) {
+    u32 x;
+    asm("v_pk_mad_u16 %0, %1, %1, %1" : "=v"(x) : "v"(w));
+    return x;
+}
+
+// ------------------------------------------------------------------------------------------------------- buffer loads
+// Raw buffer resource over [p, p + bytes): loads address it with a 32-bit per-lane offset plus a wave-uniform offset, and a
+// lane whose offset lies at or beyond `bytes` reads zeros. Word 3 = 0x00020000: 32-bit data format, no swizzle (gfx9 family).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, u32 bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr u32 RSRC_OOB = 0x80000000u;   // a lane offset that always reads zeros (buffers stay below 2 GiB)
+
+// Global-address-space view of a generic pointer: loads and stores through it are global_* instructions, which count only
+// on vmcnt (flat ones also count on lgkmcnt and make the compiler wait for every LDS read as well).
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gptr(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}

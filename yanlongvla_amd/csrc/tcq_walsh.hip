@@ -1,46 +1,136 @@
 // Row kernels built on the LDS block-Walsh engine: randomized Hadamard (RHT), rotate + quantize, rotate for the float path,
-// plain per-row quantizer, and the scale + rotate epilogue. One workgroup per token row; every butterfly is the FP32
-// (a + b, a - b) of tcq_format.fwht in stage order h = 1, 2, 4, ... so the results equal the reference bit for bit.
+// plain per-row quantizer, and the scale + rotate epilogues. One workgroup per (token row[, segment]); every butterfly is
+// the FP32 (a + b, a - b) of tcq_format.fwht in stage order h = 1, 2, 4, ... so the results equal the reference bit for bit.
+//
+// A row moves HBM -> LDS -> HBM in 16-byte vectors (8 elements per thread-step) whenever the row length is a multiple of 8
+// and the rows are 16-byte aligned, else element by element; the Walsh passes run in LDS between the two.
 #include "tcq_device.h"
 #include "tcq_launch.h"
 
-template <int DT> struct Elem;
-template <> struct Elem<TCQ_F32> { static __device__ __forceinline__ float ld(const void* p, size_t i) { return ((const float*)p)[i]; }
-                                  static __device__ __forceinline__ void st(void* p, size_t i, float v) { ((float*)p)[i] = v; } };
-template <> struct Elem<TCQ_BF16> { static __device__ __forceinline__ float ld(const void* p, size_t i) { return bf16_to_f32(((const u16*)p)[i]); }
-                                   static __device__ __forceinline__ void st(void* p, size_t i, float v) { ((u16*)p)[i] = f32_to_bf16(v); } };
-template <> struct Elem<TCQ_F16> { static __device__ __forceinline__ float ld(const void* p, size_t i) { return f16_to_f32(((const u16*)p)[i]); }
-                                  static __device__ __forceinline__ void st(void* p, size_t i, float v) { ((u16*)p)[i] = f32_to_f16(v); } };
-template <> struct Elem<TCQ_I32> { static __device__ __forceinline__ float ld(const void* p, size_t i) { return (float)((const int*)p)[i]; }
-                                  static __device__ __forceinline__ void st(void*, size_t, float) {} };
+namespace {
 
-// x (rows at stride ldx) * su -> LDS row
+// ---------------------------------------------------------------------------------------------------- element access
+template <int DT> struct Elem;
+template <> struct Elem<TCQ_F32> {
+    static __device__ __forceinline__ float ld(const void* p, size_t i) { return gptr((const float*)p)[i]; }
+    static __device__ __forceinline__ void st(void* p, size_t i, float v) { gptr((float*)p)[i] = v; }
+    static __device__ __forceinline__ void ld8(const void* p, size_t i, float (&v)[8]) {
+        const uint4_t a = gptr((const uint4_t*)((const float*)p + i))[0], b = gptr((const uint4_t*)((const float*)p + i))[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { v[k] = __uint_as_float(a[k]); v[4 + k] = __uint_as_float(b[k]); }
+    }
+    static __device__ __forceinline__ void st8(void* p, size_t i, const float (&v)[8]) {
+        uint4_t a, b;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { a[k] = __float_as_uint(v[k]); b[k] = __float_as_uint(v[4 + k]); }
+        gptr((uint4_t*)((float*)p + i))[0] = a;
+        gptr((uint4_t*)((float*)p + i))[1] = b;
+    }
+};
+template <int DT> struct Elem16 {
+    static __device__ __forceinline__ float cv(u16 h) { return DT == TCQ_BF16 ? bf16_to_f32(h) : f16_to_f32(h); }
+    static __device__ __forceinline__ u16 cv(float f) { return DT == TCQ_BF16 ? f32_to_bf16(f) : f32_to_f16(f); }
+    static __device__ __forceinline__ float ld(const void* p, size_t i) { return cv(gptr((const u16*)p)[i]); }
+    static __device__ __forceinline__ void st(void* p, size_t i, float v) { gptr((u16*)p)[i] = cv(v); }
+    static __device__ __forceinline__ void ld8(const void* p, size_t i, float (&v)[8]) {
+        const uint4_t a = gptr((const uint4_t*)((const u16*)p + i))[0];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { v[2 * k] = cv((u16)(a[k] & 0xffffu)); v[2 * k + 1] = cv((u16)(a[k] >> 16)); }
+    }
+    static __device__ __forceinline__ void st8(void* p, size_t i, const float (&v)[8]) {
+        uint4_t a;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a[k] = (u32)cv(v[2 * k]) | ((u32)cv(v[2 * k + 1]) << 16);
+        gptr((uint4_t*)((u16*)p + i))[0] = a;
+    }
+};
+template <> struct Elem<TCQ_BF16> : Elem16<TCQ_BF16> {};
+template <> struct Elem<TCQ_F16> : Elem16<TCQ_F16> {};
+template <> struct Elem<TCQ_I32> {
+    static __device__ __forceinline__ float ld(const void* p, size_t i) { return (float)gptr((const int*)p)[i]; }
+    static __device__ __forceinline__ void ld8i(const void* p, size_t i, int (&v)[8]) {
+        const int4_t a = gptr((const int4_t*)((const int*)p + i))[0], b = gptr((const int4_t*)((const int*)p + i))[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { v[k] = a[k]; v[4 + k] = b[k]; }
+    }
+};
+
+__device__ __forceinline__ void ld8_i8(const i8* p, int i, float (&v)[8]) {
+    const u64 w = *gptr((const u64*)(p + i));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (float)(i8)(w >> (8 * k));
+}
+__device__ __forceinline__ void ld8_f32(const float* p, int i, float (&v)[8]) { Elem<TCQ_F32>::ld8(p, i, v); }
+
+// ------------------------------------------------------------------------------------------------------ row movement
+// x[base + i] (* su[i]) -> LDS slot of i, for i < K. vec: 8-element vectors (K % 8 == 0, x + base and su 16 / 8-byte aligned).
 template <int XDT>
-__device__ __forceinline__ void load_signed_row(float* lds, const void* x, size_t base, const i8* su, int K) {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        float v = Elem<XDT>::ld(x, base + i);
-        if (su) v = v * (float)su[i];
-        lds[lds_slot(i)] = v;
+__device__ __forceinline__ void load_row(float* lds, const void* x, size_t base, const i8* su, int K, bool vec) {
+    if (vec) {
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * blockDim.x) {
+            float v[8], s[8];
+            Elem<XDT>::ld8(x, base + i, v);
+            if (su) {
+                ld8_i8(su, i, s);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = v[k] * s[k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) lds[lds_slot(i + k)] = v[k];
+        }
+    } else {
+        for (int i = threadIdx.x; i < K; i += blockDim.x) {
+            float v = Elem<XDT>::ld(x, base + i);
+            if (su) v = v * (float)gptr(su)[i];
+            lds[lds_slot(i)] = v;
+        }
     }
     __syncthreads();
 }
 
+// LDS row -> y[base + i] = f(i, v) for i < K (vec: as load_row). f8(i, v[8]) transforms 8 consecutive values in place.
+template <int YDT, class F8, class F1>
+__device__ __forceinline__ void store_row(const float* lds, void* y, size_t base, int K, bool vec, F8&& f8, F1&& f1) {
+    if (vec) {
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * blockDim.x) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = lds[lds_slot(i + k)];
+            f8(i, v);
+            Elem<YDT>::st8(y, base + i, v);
+        }
+    } else {
+        for (int i = threadIdx.x; i < K; i += blockDim.x) Elem<YDT>::st(y, base + i, f1(i, lds[lds_slot(i)]));
+    }
+}
+
+// In-place normalised block Walsh of the LDS row (values stay in LDS); ends with a barrier.
+__device__ __forceinline__ void walsh_inplace(float* lds, int K) {
+    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; });
+    __syncthreads();
+}
+
+__device__ __forceinline__ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
 // ------------------------------------------------------------------------------------------------------------------- RHT
 template <int XDT, int YDT>
-__global__ void k_rht(const void* x, int ldx, const i8* su, void* y, int ldy, int K) {
+__global__ void k_rht(const void* x, int ldx, const i8* su, void* y, int ldy, int K, int vec) {
     extern __shared__ float lds[];
     const size_t tok = blockIdx.x;
-    load_signed_row<XDT>(lds, x, tok * ldx, su, K);
-    block_walsh(lds, K, [&](int i, float v) { Elem<YDT>::st(y, tok * ldy + i, v); });
+    load_row<XDT>(lds, x, tok * ldx, su, K, vec);
+    walsh_inplace(lds, K);
+    store_row<YDT>(lds, y, tok * ldy, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
 }
 
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
 template <int XDT>
-__global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K) {
+__global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     const int tok = blockIdx.x;
-    load_signed_row<XDT>(lds, x, (size_t)tok * K, su, K);
+    load_row<XDT>(lds, x, (size_t)tok * K, su, K, vec);
     float mx = 0.f;
     block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
     const float s = token_scale(block_max(mx, red));
@@ -50,11 +140,11 @@ __global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, floa
 
 // -------------------------------------------------------------------------------------------- rotate for the float path
 template <int XDT>
-__global__ void k_pre_h16(const void* x, const i8* su, u16* h16, float* hscale, int K) {
+__global__ void k_pre_h16(const void* x, const i8* su, u16* h16, float* hscale, int K, int vec) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     const int tok = blockIdx.x;
-    load_signed_row<XDT>(lds, x, (size_t)tok * K, su, K);
+    load_row<XDT>(lds, x, (size_t)tok * K, su, K, vec);
     float mx = 0.f;
     block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
     const float amax = block_max(mx, red);
@@ -64,81 +154,132 @@ __global__ void k_pre_h16(const void* x, const i8* su, u16* h16, float* hscale, 
         e -= 15;                     // amax / 2^e in [2^14, 2^15)
     }
     if (threadIdx.x == 0) hscale[tok] = ldexpf(1.f, e);
-    u16* out = h16 + (size_t)tok * K;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) out[i] = f32_to_f16(ldexpf(lds[lds_slot(i)], -e));
+    store_row<TCQ_F16>(lds, h16, (size_t)tok * K, K, vec, [&](int, float(&v)[8]) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = ldexpf(v[k], -e);
+    }, [&](int, float v) { return ldexpf(v, -e); });
 }
 
 // ------------------------------------------------------------------------------------------------- per-row INT8 (no RHT)
 template <int XDT>
-__global__ void k_quantize_rows(const void* x, int ldx, i8* q, float* scale, int K) {
+__global__ void k_quantize_rows(const void* x, int ldx, i8* q, float* scale, int K, int vec) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     const int row = blockIdx.x;
+    load_row<XDT>(lds, x, (size_t)row * ldx, nullptr, K, vec);
     float mx = 0.f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        const float v = Elem<XDT>::ld(x, (size_t)row * ldx + i);
-        lds[lds_slot(i)] = v;
-        mx = fmaxf(mx, fabsf(v));
-    }
+    for (int i = threadIdx.x; i < K; i += blockDim.x) mx = fmaxf(mx, fabsf(lds[lds_slot(i)]));
     const float s = token_scale(block_max(mx, red));
     if (threadIdx.x == 0) scale[row] = s;
     quantize_row(lds, s, q + (size_t)row * K, nullptr, row, K, 0);
 }
 
 // ------------------------------------------------------------------------------------------------- scale + rotate epilogue
+// Accumulator column i of a row -> FP32: I32 (float(a) * s) * rs[i]; BF16 bf16(a) * rs[i]; F32 a (already scaled).
 template <int ADT>
-__device__ __forceinline__ float scaled_acc(const void* acc, size_t idx, float s, const float* rs, int i) {
-    if (ADT == TCQ_I32) return ((float)((const int*)acc)[idx] * s) * rs[i];
-    if (ADT == TCQ_BF16) return bf16_to_f32(((const u16*)acc)[idx]) * rs[i];
-    return ((const float*)acc)[idx];
+__device__ __forceinline__ void load_acc_row(float* lds, const void* acc, size_t base, float s, const float* rs, int N, bool vec) {
+    if (vec) {
+        for (int i = 8 * threadIdx.x; i < N; i += 8 * blockDim.x) {
+            float v[8];
+            if (ADT == TCQ_I32) {
+                int a[8];
+                float r[8];
+                Elem<TCQ_I32>::ld8i(acc, base + i, a);
+                ld8_f32(rs, i, r);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = ((float)a[k] * s) * r[k];
+            } else if (ADT == TCQ_BF16) {
+                float r[8];
+                Elem<TCQ_BF16>::ld8(acc, base + i, v);
+                ld8_f32(rs, i, r);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = v[k] * r[k];
+            } else {
+                Elem<TCQ_F32>::ld8(acc, base + i, v);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) lds[lds_slot(i + k)] = v[k];
+        }
+    } else {
+        for (int i = threadIdx.x; i < N; i += blockDim.x) {
+            float v;
+            if (ADT == TCQ_I32) v = (Elem<TCQ_I32>::ld(acc, base + i) * s) * gptr(rs)[i];
+            else if (ADT == TCQ_BF16) v = Elem<TCQ_BF16>::ld(acc, base + i) * gptr(rs)[i];
+            else v = Elem<TCQ_F32>::ld(acc, base + i);
+            lds[lds_slot(i)] = v;
+        }
+    }
+    __syncthreads();
+}
+
+// y = walsh(row) * sv (+ bias) [-> GELU table for BF16 outputs]
+template <int YDT>
+__device__ __forceinline__ void store_post_row(const float* lds, void* y, size_t base, const i8* sv, const float* bias,
+                                               const u16* gelu, int N, bool vec) {
+    store_row<YDT>(lds, y, base, N, vec, [&](int i, float(&v)[8]) {
+        float s[8];
+        ld8_i8(sv, i, s);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = v[k] * s[k];
+        if (bias) {
+            float b[8];
+            ld8_f32(bias, i, b);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = v[k] + b[k];
+        }
+        if (YDT == TCQ_BF16 && gelu) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = bf16_to_f32(gptr(gelu)[f32_to_bf16(v[k])]);
+        }
+    }, [&](int i, float v) {
+        v = v * (float)gptr(sv)[i];
+        if (bias) v = v + gptr(bias)[i];
+        if (YDT == TCQ_BF16 && gelu) v = bf16_to_f32(gptr(gelu)[f32_to_bf16(v)]);
+        return v;
+    });
 }
 
 template <int ADT, int YDT>
 __global__ void k_post(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv, const float* bias,
-                       void* y, int N) {
+                       void* y, int N, int vec) {
     extern __shared__ float lds[];
     const int tok = blockIdx.x;
-    const size_t base = (size_t)tok * lda + col0;
-    const float st = (ADT == TCQ_I32) ? s[tok] : 1.f;
-    for (int i = threadIdx.x; i < N; i += blockDim.x) lds[lds_slot(i)] = scaled_acc<ADT>(acc, base + i, st, rs, i);
-    __syncthreads();
-    const size_t yb = (size_t)tok * N;
-    block_walsh(lds, N, [&](int i, float v) {
-        v = v * (float)sv[i];
-        if (bias) v = v + bias[i];
-        Elem<YDT>::st(y, yb + i, v);
-    });
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + col0, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
+    walsh_inplace(lds, N);
+    store_post_row<YDT>(lds, y, (size_t)tok * N, sv, bias, nullptr, N, vec);
 }
 
-// Batched epilogue: workgroup (token, segment). Segments with N outside (0, maxN] are skipped (LDS is sized for maxN).
+// Batched epilogue: workgroup (token, segment). Segments with N outside (0, maxN], or without the row scale their
+// accumulator type needs, are skipped (the host wrapper rejects them before they get here).
+// Vectors are used for a segment when its N is a multiple of 8 and its pointers and strides are 16-byte aligned.
 template <int ADT, int YDT>
 __global__ void k_postg(const tcq_post_seg* segs, const float* s, const u16* gelu_lut, int maxN) {
     extern __shared__ float lds[];
     const tcq_post_seg S = segs[blockIdx.y];
     const int tok = blockIdx.x, N = S.N;
-    if (N <= 0 || N > maxN) return;
-    const size_t base = (size_t)tok * S.lda + S.col0;
-    const float st = (ADT == TCQ_I32) ? s[tok] : 1.f;
-    for (int i = threadIdx.x; i < N; i += blockDim.x) lds[lds_slot(i)] = scaled_acc<ADT>(S.acc, base + i, st, S.rs, i);
-    __syncthreads();
-    const size_t yb = (size_t)tok * N;
-    const bool gl = YDT == TCQ_BF16 && S.gelu && gelu_lut;
-    block_walsh(lds, N, [&](int i, float v) {
-        v = v * (float)S.sv[i];
-        if (S.bias) v = v + S.bias[i];
-        if (gl) ((u16*)S.y)[yb + i] = gelu_lut[f32_to_bf16(v)];
-        else Elem<YDT>::st(S.y, yb + i, v);
-    });
+    if (N <= 0 || N > maxN || (ADT != TCQ_F32 && !S.rs)) return;
+    const int esz = ADT == TCQ_BF16 ? 2 : 4, ysz = YDT == TCQ_F32 ? 4 : 2;
+    const bool vec = N % 8 == 0 && aligned16(S.acc) && ((size_t)S.lda * esz) % 16 == 0 && ((size_t)S.col0 * esz) % 16 == 0 &&
+                     aligned16(S.y) && ((size_t)N * ysz) % 16 == 0 && ((uintptr_t)S.sv & 7) == 0 && (!S.rs || aligned16(S.rs)) &&
+                     (!S.bias || aligned16(S.bias));
+    load_acc_row<ADT>(lds, S.acc, (size_t)tok * S.lda + S.col0, ADT == TCQ_I32 ? s[tok] : 1.f, S.rs, N, vec);
+    walsh_inplace(lds, N);
+    store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec);
 }
 
 // =========================================================================================================== C ABI
-static int row_threads(int K) {
-    const int top = 1 << (31 - __builtin_clz(K));
+// Threads per row: few rows (latency) -> about one 8-element vector per thread; many rows (throughput) -> four vectors per
+// thread so more rows share a CU.
+static int row_threads(int M, int K) {
+    const int per = M <= 256 ? 8 : 32;
     int t = 64;
-    while (t < 512 && t * 32 < top) t <<= 1;
+    while (t < 512 && t * per < K) t <<= 1;
     return t;
 }
 static size_t row_lds(int K) { return (size_t)lds_words(K) * sizeof(float); }
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
+static int dsize(int dt) { return dt == TCQ_F32 || dt == TCQ_I32 ? 4 : dt == TCQ_I8 ? 1 : 2; }
 
 #define DISPATCH_X(dt, KERNEL, ...)                                                             \
     switch (dt) {                                                                               \
@@ -152,10 +293,12 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
                        tcq_stream_t stream) {
     if (!x || !y || M <= 0 || n <= 0 || ldx < n || ldy < n) return TCQ_ERR_ARG;
     if (n > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const dim3 grid(M), block(row_threads(n));
+    const dim3 grid(M), block(row_threads(M, n));
     const size_t sh = row_lds(n);
+    const int vec = n % 8 == 0 && al16(x) && al16(y) && ((size_t)ldx * dsize(x_dtype)) % 16 == 0 &&
+                    ((size_t)ldy * dsize(y_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
-#define RHT_Y(XD, YD) launch_k(k_rht<XD, YD>, grid, block, sh, st, x, ldx, (const i8*)su, y, ldy, n)
+#define RHT_Y(XD, YD) launch_k(k_rht<XD, YD>, grid, block, sh, st, x, ldx, (const i8*)su, y, ldy, n, vec)
 #define RHT_X(XD, _)                                          \
     switch (y_dtype) {                                        \
         case TCQ_F32: RHT_Y(XD, TCQ_F32); break;              \
@@ -171,10 +314,11 @@ extern "C" int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, 
                        tcq_stream_t stream) {
     if (!x || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const dim3 grid(M), block(row_threads(K));
+    const dim3 grid(M), block(row_threads(M, K));
     const size_t sh = row_lds(K);
+    const int vec = K % 8 == 0 && al16(x) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
-#define PRE(XD, _) launch_k(k_pre<XD>, grid, block, sh, st, x, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K)
+#define PRE(XD, _) launch_k(k_pre<XD>, grid, block, sh, st, x, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec)
     DISPATCH_X(x_dtype, PRE, 0)
     return launch_status();
 }
@@ -183,10 +327,11 @@ extern "C" int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h
                            tcq_stream_t stream) {
     if (!x || !h16 || !hscale || M <= 0 || K <= 0) return TCQ_ERR_ARG;
     if (K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const dim3 grid(M), block(row_threads(K));
+    const dim3 grid(M), block(row_threads(M, K));
     const size_t sh = row_lds(K);
+    const int vec = K % 8 == 0 && al16(x) && al16(h16) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
-#define PREH(XD, _) launch_k(k_pre_h16<XD>, grid, block, sh, st, x, (const i8*)su, (u16*)h16, hscale, K)
+#define PREH(XD, _) launch_k(k_pre_h16<XD>, grid, block, sh, st, x, (const i8*)su, (u16*)h16, hscale, K, vec)
     DISPATCH_X(x_dtype, PREH, 0)
     return launch_status();
 }
@@ -194,10 +339,11 @@ extern "C" int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h
 extern "C" int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q, float* scale, int M, int K, tcq_stream_t stream) {
     if (!x || !q || !scale || M <= 0 || K <= 0 || ldx < K) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const dim3 grid(M), block(row_threads(K));
+    const dim3 grid(M), block(row_threads(M, K));
     const size_t sh = row_lds(K);
+    const int vec = K % 8 == 0 && al16(x) && ((size_t)ldx * dsize(x_dtype)) % 16 == 0;
     hipStream_t st = (hipStream_t)stream;
-#define QROWS(XD, _) launch_k(k_quantize_rows<XD>, grid, block, sh, st, x, ldx, (i8*)q, scale, K)
+#define QROWS(XD, _) launch_k(k_quantize_rows<XD>, grid, block, sh, st, x, ldx, (i8*)q, scale, K, vec)
     DISPATCH_X(x_dtype, QROWS, 0)
     return launch_status();
 }
@@ -207,10 +353,13 @@ extern "C" int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const
     if (!acc || !sv || !y || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
     if (N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const dim3 grid(M), block(row_threads(N));
+    const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N);
+    const int asz = dsize(acc_dtype);
+    const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && al16(y) &&
+                    ((size_t)N * dsize(y_dtype)) % 16 == 0 && al8(sv) && (!rs || al16(rs)) && (!bias || al16(bias));
     hipStream_t st = (hipStream_t)stream;
-#define POST_Y(AD, YD) launch_k(k_post<AD, YD>, grid, block, sh, st, acc, lda, col0, s, rs, (const i8*)sv, bias, y, N)
+#define POST_Y(AD, YD) launch_k(k_post<AD, YD>, grid, block, sh, st, acc, lda, col0, s, rs, (const i8*)sv, bias, y, N, vec)
 #define POST_A(AD)                                           \
     switch (y_dtype) {                                       \
         case TCQ_F32: POST_Y(AD, TCQ_F32); break;            \
@@ -233,7 +382,7 @@ extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, cons
     if (acc_dtype == TCQ_I32 && !s) return TCQ_ERR_ARG;
     if (maxN > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     if (nseg > 65535) return TCQ_ERR_UNSUPPORTED;
-    const dim3 grid(M, nseg), block(row_threads(maxN));
+    const dim3 grid(M, nseg), block(row_threads(M * nseg, maxN));
     const size_t sh = row_lds(maxN);
     hipStream_t st = (hipStream_t)stream;
 #define POSTG_Y(AD, YD) launch_k(k_postg<AD, YD>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN)

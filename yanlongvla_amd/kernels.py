@@ -144,6 +144,8 @@ def post_segments(segs, device):
         N = y.shape[1]
         if col0 < 0 or col0 + N > acc.shape[1] or sv.numel() != N or (rs is not None and rs.numel() != N):
             raise ValueError(f'segment {i}: columns {col0}..{col0 + N} do not fit the accumulator / scales')
+        if rs is None and acc.dtype != torch.float32:
+            raise ValueError(f'segment {i}: an {acc.dtype} accumulator needs its row scale')
         a[i] = (ptr(acc), ptr(rs) or 0, ptr(sv), ptr(bias) or 0, ptr(y), acc.shape[1], col0, N, int(bool(gelu)))
     return torch.from_numpy(a.view(np.uint8).copy()).to(device)
 
