@@ -138,6 +138,29 @@ typedef struct tcq_gemv_layer {
 int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                  tcq_stream_t stream);
 
+/* One layer (segment) of a small-M INT8 product. The output z of the segment starts at its first column: z[t * ldz + i] for
+ * token t and output row i < m (several layers of a group write side by side into one (M, ldz) buffer). */
+typedef struct tcq_gemm_seg {
+    const void* w;       /* tcq_gemm_tcq: tcq_repack words of an (m, K) layer; tcq_gemm_w8: (m, K) int8 row-major weights */
+    const int8_t* t8;    /* (512, 2) INT8 table (tcq_gemm_tcq only) */
+    const float* rs;     /* (m,) FP32 row scale */
+    float* z;            /* FP32 output, first column of the segment */
+    int m;               /* output rows, a multiple of 16 */
+} tcq_gemm_seg;
+
+/* W2A8 fused decode + product for M <= 64 tokens: z[t, i] = (float(sum_k q[t, k] * w8[i, k]) * s[t]) * rs[i] with w8 = sign *
+ * t8[hash(state)] decoded from the words on the fly and the sum exact in int32. q (M, K) int8 row-major, s (M,) FP32.
+ * segs: DEVICE array of nseg descriptors, max_m = the largest m among them. K a multiple of 16.
+ * Replaces kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673), which takes at most three
+ * concatenated layers (q/k/v or gate/up, table chosen by tile-row bounds) and MT <= 10 tokens in shared memory. */
+int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+                 tcq_stream_t stream);
+
+/* INT8-resident product, same contract with w = decoded (m, K) int8 weights (tcq_decode_i8). Replaces kernels.gemm_w8 /
+ * k_gemm_w8 / k_gemm_w8d (deploy/tcq_kernels/kernels.py:365-399, 662-668). */
+int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+                tcq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -311,3 +311,64 @@ def test_gelu_table_vs_cpu():
     diff = (dev.view(torch.int16) != cpu.view(torch.int16)) & ~nan
     print(f'GELU table: {int(diff.sum())} of {int((~nan).sum())} finite BF16 inputs differ between device and CPU')
     assert int(diff.sum()) < 65536 // 100
+
+
+# ------------------------------------------------------------------------------------------------- small-M INT8 products
+def _small_product_case(shapes, M, seed):
+    """Layers of one group (same n, shared input signs), INT8 activations, expected z from the exact integer product."""
+    from yanlongvla_amd import kernels as K
+    n = shapes[0][1]
+    layers = [O.random_layer(m, n, seed + i) for i, (m, _) in enumerate(shapes)]
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-127, 128, size=(M, n)).astype(np.int8)
+    if M > 3:
+        q[3] = 0
+    s = (rng.random(M) * 0.02 + 1e-3).astype(np.float32)
+    ldz = sum(L.m for L in layers)
+    ref = np.concatenate([(O.int_matmul(q, L.w8_reference()).astype(np.float32) * s[:, None]) * L.rs[None, :] for L in layers], 1)
+    dev = [dev_layer(L) for L in layers]
+    t8s = [K.snap(d['tlut'], d['row_scale'])[:2] for d in dev]
+    return layers, dev, t8s, q, s, ldz, ref
+
+
+@pytest.mark.parametrize('shapes,M', [([(2048, 1024)], 1), ([(2048, 1024), (256, 1024), (256, 1024)], 50),
+                                      ([(1024, 2048)], 16), ([(4096, 1024), (4096, 1024)], 17), ([(1024, 4096)], 64),
+                                      ([(64, 1152)], 33), ([(48, 80), (32, 80)], 5), ([(256, 16384)], 10)])
+def test_gemm_tcq_and_w8_bitexact(shapes, M):
+    """Fused decode + INT8 product and the INT8-resident product against the oracle, FP32 bits equal (exact int32 sums)."""
+    from yanlongvla_amd import kernels as K
+    layers, dev, t8s, q, s, ldz, ref = _small_product_case(shapes, M, 31 * M + len(shapes))
+    n = layers[0].n
+    qd, sd = T(q), T(s)
+    z = torch.full((M, ldz), float('nan'), device=DEV)
+    z2 = torch.full((M, ldz), float('nan'), device=DEV)
+    wdevs = [K.repack(d['bits'], L.m, n) for L, d in zip(layers, dev)]
+    w8s = []
+    for L, d, (t8, _) in zip(layers, dev, t8s):
+        w = torch.empty(L.m, n, dtype=torch.int8, device=DEV)
+        K.decode(d['bits'], t8, w)
+        w8s.append(w)
+    cols, c0 = [], 0
+    for L in layers:
+        cols.append(c0)
+        c0 += L.m
+    max_m = max(L.m for L in layers)
+    desc = K.gemm_segments([(w, t8, rs, z[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], DEV)
+    K.gemm_tcq(desc, len(layers), max_m, qd, sd, ldz)
+    desc2 = K.gemm_segments([(w, None, rs, z2[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], DEV)
+    K.gemm_w8(desc2, len(layers), max_m, qd, sd, ldz)
+    assert np.array_equal(bits_of(z), ref.view(np.uint32))
+    assert np.array_equal(bits_of(z2), ref.view(np.uint32))
+
+
+def test_gemm_small_rejects_bad_sizes():
+    from yanlongvla_amd import kernels as K, _lib
+    L = O.random_layer(32, 64, 1)
+    d = dev_layer(L)
+    t8, rs, _ = K.snap(d['tlut'], d['row_scale'])
+    q = torch.zeros(65, 64, dtype=torch.int8, device=DEV)
+    s = torch.ones(65, device=DEV)
+    z = torch.empty(65, 32, device=DEV)
+    desc = K.gemm_segments([(K.repack(d['bits'], 32, 64), t8, rs, z)], DEV)
+    with pytest.raises(_lib.TcqError):
+        K.gemm_tcq(desc, 1, 32, q, s, 32)             # 65 tokens: more than the small-M product takes

@@ -167,3 +167,48 @@ def gelu_table(device):
         x = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
         _GELU[key] = torch.nn.functional.gelu(x, approximate='tanh').contiguous()
     return _GELU[key]
+
+
+# ------------------------------------------------------------------------------------------------- small-M INT8 products
+_GSEG = None
+
+
+def _gseg_dtype():
+    global _GSEG
+    if _GSEG is None:
+        import numpy as np
+        _GSEG = np.dtype([('w', '<u8'), ('t8', '<u8'), ('rs', '<u8'), ('z', '<u8'), ('m', '<i4'), ('pad', '<i4')])
+        assert _GSEG.itemsize == 40
+    return _GSEG
+
+
+def gemm_segments(segs, device):
+    """[(w, t8, rs, z), ...] -> device array of tcq_gemm_seg. w: tcq_repack words (fused decode) or (m, K) int8 weights
+    (resident); t8 (512, 2) int8 or None; rs (m,) FP32; z: a view whose first element is the segment's first output column
+    of an (M, ldz) FP32 buffer. Keep the tensors alive while the array is in use."""
+    import numpy as np
+    a = np.zeros(len(segs), dtype=_gseg_dtype())
+    for i, (w, t8, rs, z) in enumerate(segs):
+        _contig(w, t8, rs)
+        m = rs.numel()
+        if m % 16:
+            raise ValueError(f'segment {i}: {m} output rows is not a multiple of 16')
+        a[i] = (ptr(w), ptr(t8) or 0, ptr(rs), ptr(z), m, 0)
+    return torch.from_numpy(a.view(np.uint8).copy()).to(device)
+
+
+def _gemm_small(name, desc, nseg, max_m, q, s, ldz):
+    M, K = q.shape
+    _contig(q, s)
+    call(name, ptr(desc), nseg, max_m, ptr(q), ptr(s), M, K, ldz, stream())
+
+
+def gemm_tcq(desc, nseg, max_m, q, s, ldz):
+    """W2A8 fused decode + product (reference kernels.gemm_tcq, kernels.py:671-673): for every segment, z = (float(q w8^T) * s)
+    * rs with w8 decoded on the fly. q (M <= 64, K) int8, s (M,) FP32, ldz = row stride of the shared FP32 output."""
+    _gemm_small('tcq_gemm_tcq', desc, nseg, max_m, q, s, ldz)
+
+
+def gemm_w8(desc, nseg, max_m, q, s, ldz):
+    """Same product on resident INT8 weights (reference kernels.gemm_w8, kernels.py:662-668)."""
+    _gemm_small('tcq_gemm_w8', desc, nseg, max_m, q, s, ldz)
