@@ -161,6 +161,15 @@ int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q,
 int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
                 tcq_stream_t stream);
 
+/* W8A8 INT8 GEMM: acc[m, n] = sum_k a[m, k] w[n, k], exact int32. a (M, K) int8 per-token quantized activations, w (N, K)
+ * int8 per-output-channel quantized weights (both row-major, K a multiple of 16), out (M, ldo) of out_dtype: I32 the
+ * accumulators; F32 (float(acc) * sa[m]) * sw[n]; BF16 the BF16 rounding of that (sa, sw FP32 scales, unused for I32).
+ * Replaces the prefill product torch._int_mm(q, W.t()) of Group.product (deploy/tcq_kernels/modules.py:81-86;
+ * tcq_format.int_matmul, tcq_format.py:110-116) followed by the (acc * s) * rs scaling of tcq_format.reference_linear
+ * (tcq_format.py:135). */
+int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
+                int K, tcq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -372,3 +372,52 @@ def test_gemm_small_rejects_bad_sizes():
     desc = K.gemm_segments([(K.repack(d['bits'], 32, 64), t8, rs, z)], DEV)
     with pytest.raises(_lib.TcqError):
         K.gemm_tcq(desc, 1, 32, q, s, 32)             # 65 tokens: more than the small-M product takes
+
+
+# ----------------------------------------------------------------------------------------------------------- W8A8 GEMM
+@pytest.mark.parametrize('M,K,N', [(800, 2048, 16384), (50, 2048, 16384), (1, 2048, 16384), (33, 80, 48), (130, 1152, 260),
+                                   (17, 16, 4)])
+def test_gemm_i8_bitexact(M, K, N):
+    """INT32 accumulators equal the exact integer product; FP32 / BF16 epilogues equal (acc * sa) * sw bit for bit."""
+    from yanlongvla_amd import kernels as Kk
+    rng = np.random.default_rng(M + K + N)
+    a = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    sa = (rng.random(M) * 0.03 + 1e-3).astype(np.float32)
+    sw = (rng.random(N) * 1e-3 + 1e-5).astype(np.float32)
+    ref = O.int_matmul(a, w)
+    ad, wd = T(a), T(w)
+    acc = torch.empty(M, N, dtype=torch.int32, device=DEV)
+    Kk.gemm_i8(ad, wd, acc)
+    assert np.array_equal(acc.cpu().numpy(), ref)
+    zf = (ref.astype(np.float32) * sa[:, None]) * sw[None, :]
+    z = torch.empty(M, N, dtype=torch.float32, device=DEV)
+    Kk.gemm_i8(ad, wd, z, T(sa), T(sw))
+    assert np.array_equal(bits_of(z), zf.view(np.uint32))
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    Kk.gemm_i8(ad, wd, y, T(sa), T(sw))
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(zf))
+
+
+def test_w8a8_pipeline_matches_oracle():
+    """C2 contract end to end: per-token INT8 of bf16 activations, per-channel INT8 of N(0, 0.02) weights, GEMM, BF16."""
+    from yanlongvla_amd import kernels as Kk
+    M, K, N = 50, 2048, 4096
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wt = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    ref = O.w8a8_reference(x.float().numpy(), wt.float().numpy())
+    qa = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    sa = torch.empty(M, device=DEV)
+    Kk.quantize_rows(x.to(DEV), qa, sa)
+    qw = torch.empty(N, K, dtype=torch.int8, device=DEV)
+    sw = torch.empty(N, device=DEV)
+    Kk.quantize_rows(wt.to(DEV), qw, sw)
+    assert np.array_equal(qa.cpu().numpy(), ref['qa']) and np.array_equal(qw.cpu().numpy(), ref['qw'])
+    assert np.array_equal(bits_of(sa), ref['sa'].view(np.uint32)) and np.array_equal(bits_of(sw), ref['sw'].view(np.uint32))
+    acc = torch.empty(M, N, dtype=torch.int32, device=DEV)
+    Kk.gemm_i8(qa, qw, acc)
+    assert np.array_equal(acc.cpu().numpy(), ref['acc'])
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    Kk.gemm_i8(qa, qw, y, sa, sw)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), ref['y'])

@@ -8,15 +8,18 @@
 // A from the trellis words: the window layout of tcq_repack (one dwordx4 per lane per tile row and chunk), 8 lookups of
 // INT8 pairs in a sign-folded LDS table (1024 entries x 16 copies, one 4-byte slot each, lane l reads copy l mod 16), packed
 // into the 16 A bytes. A from resident INT8 weights: one 16-byte load per lane per (tile row, j).
-// The activations of a chunk (16 NB tokens x 256 bytes, zero for tokens >= M and columns >= K) are staged in LDS, double
-// buffered, with an XOR swizzle of the 16-byte granules by token so that the 16 tokens of a B read hit different banks.
+// Work split (few tokens = little work per layer, so the launch is latency-bound): a workgroup takes one tile row (16 output
+// rows) of one segment and its waves split K, one 256-column chunk each (up to 16 waves; wave w takes chunks w, w + NW, ...
+// beyond 16 chunks). Every wave issues the loads of its words / weights and of its activation fragments (16 bytes of each
+// token per lane and j, straight into registers; zero for tokens >= M and columns >= K) before the table fill, so a
+// workgroup costs one memory round trip. The partial int32 sums of the waves are added in LDS at the end (exact).
 #include "tcq_device.h"
 #include "tcq_launch.h"
 
 namespace {
 
-constexpr int SM_C = 16;               // table copies
-constexpr int SM_THREADS = 512;
+constexpr int SM_C = 4;                // table copies (a workgroup streams little: the fill must stay cheap)
+constexpr int SM_MAXW = 16;            // waves per workgroup at most
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 
@@ -33,145 +36,101 @@ __device__ __forceinline__ void fill_table_i8(u32* tab, const i8* t8) {
     }
 }
 
-// stage the activations of chunk c: buffer (16 NB tokens) x 256 bytes, granule (t, g16) at t * 256 + 16 * (g16 ^ (t & 15))
-template <int NB>
-__device__ __forceinline__ void stage_load(const i8* q, int M, int K, int c, uint4_t (&v)[NB / 2 > 0 ? NB / 2 : 1]) {
-    constexpr int G = NB * 16 * 16, PER = (G + SM_THREADS - 1) / SM_THREADS;
-    static_assert(PER <= (NB / 2 > 0 ? NB / 2 : 1), "staging registers");
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int gi = threadIdx.x + p * SM_THREADS;
-        const int t = gi >> 4, k = 256 * c + 16 * (gi & 15);
-        v[p] = (gi < G && t < M && k < K) ? gptr((const uint4_t*)(q + (size_t)t * K + k))[0] : uint4_t{0, 0, 0, 0};
-    }
-}
-template <int NB>
-__device__ __forceinline__ void stage_store(char* buf, const uint4_t (&v)[NB / 2 > 0 ? NB / 2 : 1]) {
-    constexpr int G = NB * 16 * 16, PER = (G + SM_THREADS - 1) / SM_THREADS;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int gi = threadIdx.x + p * SM_THREADS;
-        if (gi < G) {
-            const int t = gi >> 4, g16 = gi & 15;
-            *(uint4_t*)(buf + t * 256 + 16 * (g16 ^ (t & 15))) = v[p];
-        }
-    }
-}
-
 }  // namespace
 
-// grid (workgroups per segment, segments). A workgroup covers 8 R tile rows of its segment (wave w: rows w R .. w R + R - 1)
-// for all chunks; the words / weights of chunk c + 1 and the activations of chunk c + 1 are loaded while chunk c is
-// multiplied. MODE 0: decode from tcq_repack words; MODE 1: resident INT8 weights.
-template <int MODE, int NB, int R>
-__global__ __launch_bounds__(SM_THREADS) void k_gemm_small(const tcq_gemm_seg* segs, const i8* q, const float* s, int M, int K,
-                                                          int ldz) {
+// grid (tile rows of the largest segment, segments), NW = blockDim.x / 64 waves. MODE 0: decode from tcq_repack words;
+// MODE 1: resident INT8 weights.
+template <int MODE, int NB>
+__global__ __launch_bounds__(1024) void k_gemm_small(const tcq_gemm_seg* segs, const i8* q, const float* s, int M, int K, int ldz) {
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
-    __shared__ __attribute__((aligned(16))) char bq[2][NB * 16 * 256];
+    __shared__ __attribute__((aligned(16))) int4v red[(SM_MAXW - 1) * NB * 64];
     const tcq_gemm_seg S = segs[blockIdx.y];
     const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
+    const int I = blockIdx.x;
+    if (I >= tiles_m) return;                                             // uniform
+    const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int lr = lane & 15, lg = lane >> 4;
-    const int I0 = (blockIdx.x * (SM_THREADS / 64) + wave) * R;           // first tile row of this wave
-    if (blockIdx.x * (SM_THREADS / 64) * R >= tiles_m) return;           // whole workgroup past the segment (uniform)
-    if (MODE == 0) fill_table_i8(tab, S.t8);
-
-    uint4_t st[NB / 2 > 0 ? NB / 2 : 1];
-    stage_load<NB>(q, M, K, 0, st);
-    stage_store<NB>(bq[0], st);
-    const bool active = I0 < tiles_m;
-    const int lastI = tiles_m - 1;
     const u32 cp4 = (u32)(lane & (SM_C - 1)) << 2;
-
-    // A sources
-    uint4_t wa[2][R][MODE == 0 ? 1 : 4];
+    constexpr int ESH = SM_C == 16 ? 6 : SM_C == 8 ? 5 : SM_C == 4 ? 4 : 2;
     rsrc_t Wr;
     if (MODE == 0) Wr = make_rsrc(S.w, (u32)(tiles_m * nch) << 10);
     else Wr = make_rsrc(S.w, (u32)S.m * (u32)K);
-    auto loadA = [&](uint4_t(&dst)[R][MODE == 0 ? 1 : 4], int c) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int I = min(I0 + r, lastI);
-            if (MODE == 0) {
-                dst[r][0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4,
-                                                                                              (u32)(I * nch + c) << 10, 2));
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k0 = 256 * c + 64 * j + 16 * lg;
-                    const u32 off = (u32)(16 * I + lr) * (u32)K + (u32)k0;
-                    dst[r][j] = k0 < K ? __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, off, 0, 2))
-                                       : uint4_t{0, 0, 0, 0};
-                }
-            }
-        }
-    };
+    const rsrc_t Q = make_rsrc(q, (u32)M * (u32)K);
 
-    int4v acc[R][NB];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
-
-    if (active) loadA(wa[0], 0);
-    __syncthreads();
-
-    for (int c = 0; c < nch; ++c) {
-        const int cur = c & 1;
-        if (c + 1 < nch) stage_load<NB>(q, M, K, c + 1, st);
-        if (active && c + 1 < nch) loadA(wa[cur ^ 1], c + 1);
-        if (active) {
-            const char* bb = bq[cur];
+    uint4_t wa[MODE == 0 ? 1 : 4];
+    int4v B[4][NB];
+    auto load = [&](int c) {                                              // words / weights and activations of chunk c
+        if (MODE == 0) {
+            wa[0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
+        } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int4v B[NB];
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const int t = 16 * b + lr;
-                    B[b] = *(const int4v*)(bb + t * 256 + 16 * ((4 * j + lg) ^ (t & 15)));
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    int4v A;
-                    if (MODE == 0) {
-                        const u32 hi = wa[cur][r][0][j];
-                        const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
-                        u32 e0[4], e1[4];
-#pragma unroll
-                        for (int p = 0; p < 4; ++p) {
-                            const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
-                            e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << 6) | cp4));           // pair p
-                            e1[p] = *(const u16*)((const char*)tab + (((x >> 6) & 1023u) << 6 | cp4));     // pair p + 4
-                        }
-                        A = int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
-                                  (int)(e1[2] | (e1[3] << 16))};
-                    } else {
-                        A = __builtin_bit_cast(int4v, wa[cur][r][j]);
-                    }
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[b], acc[r][b], 0, 0, 0);
-                }
+                const int k0 = 256 * c + 64 * j + 16 * lg;
+                const u32 off = k0 < K ? (u32)(16 * I + lr) * (u32)K + (u32)k0 : RSRC_OOB;
+                wa[j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, off, 0, 2));
             }
         }
-        if (c + 1 < nch) stage_store<NB>(bq[cur ^ 1], st);
-        __syncthreads();
-    }
-    if (!active) return;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int I = I0 + r;
-        if (I >= tiles_m) continue;
-        const float4_t rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int t = 16 * b + lr;
-            if (t < M) {
-                const float st_ = gptr(s)[t];
-                float4_t o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = ((float)acc[r][b][e] * st_) * rsv[e];
-                *gptr((float4_t*)(S.z + (size_t)t * ldz + 16 * I + 4 * lg)) = o;
+            for (int b = 0; b < NB; ++b) {
+                const int t = 16 * b + lr, k = 256 * c + 64 * j + 16 * lg;
+                const u32 off = (t < M && k < K) ? (u32)t * (u32)K + (u32)k : RSRC_OOB;
+                B[j][b] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
             }
+    };
+
+    int4v acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = int4v{0, 0, 0, 0};
+    if (wave < nch) load(wave);
+    if (MODE == 0) fill_table_i8(tab, S.t8);
+    __syncthreads();
+    for (int c = wave; c < nch; c += nw) {
+        if (c != wave) load(c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int4v A;
+            if (MODE == 0) {
+                const u32 hi = wa[0][j];
+                const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+                u32 e0[4], e1[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                    e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << ESH) | cp4));             // pair p
+                    e1[p] = *(const u16*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));    // pair p + 4
+                }
+                A = int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
+                          (int)(e1[2] | (e1[3] << 16))};
+            } else {
+                A = __builtin_bit_cast(int4v, wa[j]);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[b], 0, 0, 0);
+        }
+    }
+    // sum the waves' partial accumulators (exact int32) through LDS, then scale and store
+    if (wave > 0) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) red[((wave - 1) * NB + b) * 64 + lane] = acc[b];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 0; w < nw - 1; ++w)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] += red[(w * NB + b) * 64 + lane];
+    const float4_t rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int t = 16 * b + lr;
+        if (t < M) {
+            const float st = gptr(s)[t];
+            float4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = ((float)acc[b][e] * st) * rsv[e];
+            *gptr((float4_t*)(S.z + (size_t)t * ldz + 16 * I + 4 * lg)) = o;
         }
     }
 }
@@ -183,15 +142,15 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_
     if (!segs || !q || !s || nseg <= 0 || max_m <= 0 || M <= 0 || K <= 0 || ldz <= 0) return TCQ_ERR_ARG;
     if (max_m % 16 || K % 16) return TCQ_ERR_SHAPE;
     if (M > 64 || nseg > 65535) return TCQ_ERR_UNSUPPORTED;
-    if ((uintptr_t)q % 16 || ldz % 4) return TCQ_ERR_ALIGN;
-    if ((size_t)max_m * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
-    constexpr int R = 2, WROWS = (SM_THREADS / 64) * R;
-    const dim3 grid((max_m / 16 + WROWS - 1) / WROWS, nseg), block(SM_THREADS);
+    if (ldz % 4 || (uintptr_t)q % 16) return TCQ_ERR_ALIGN;
+    if ((size_t)max_m * K >= ((size_t)1 << 31) || (size_t)M * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
+    const dim3 grid(max_m / 16, nseg), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
     const i8* qq = (const i8*)q;
-    if (M <= 16) launch_k(k_gemm_small<MODE, 1, R>, grid, block, 0, st, segs, qq, s, M, K, ldz);
-    else if (M <= 32) launch_k(k_gemm_small<MODE, 2, R>, grid, block, 0, st, segs, qq, s, M, K, ldz);
-    else launch_k(k_gemm_small<MODE, 4, R>, grid, block, 0, st, segs, qq, s, M, K, ldz);
+    if (M <= 16) launch_k(k_gemm_small<MODE, 1>, grid, block, 0, st, segs, qq, s, M, K, ldz);
+    else if (M <= 32) launch_k(k_gemm_small<MODE, 2>, grid, block, 0, st, segs, qq, s, M, K, ldz);
+    else launch_k(k_gemm_small<MODE, 4>, grid, block, 0, st, segs, qq, s, M, K, ldz);
     return launch_status();
 }
 

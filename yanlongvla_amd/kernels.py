@@ -212,3 +212,18 @@ def gemm_tcq(desc, nseg, max_m, q, s, ldz):
 def gemm_w8(desc, nseg, max_m, q, s, ldz):
     """Same product on resident INT8 weights (reference kernels.gemm_w8, kernels.py:662-668)."""
     _gemm_small('tcq_gemm_w8', desc, nseg, max_m, q, s, ldz)
+
+
+
+# ----------------------------------------------------------------------------------------------------------- W8A8 GEMM
+def gemm_i8(a, w, out, sa=None, sw=None):
+    """acc = a w^T exact in int32; out (M, ldo) int32 (acc), FP32 ((acc * sa) * sw) or BF16 of that. a (M, K), w (N, K) int8.
+    The prefill product of the reference (torch._int_mm in Group.product, deploy/tcq_kernels/modules.py:86)."""
+    M, K = a.shape
+    N = w.shape[0]
+    _contig(a, w, sa, sw)
+    if w.shape[1] != K or out.shape[0] != M or out.stride(1) != 1:
+        raise ValueError('gemm_i8: shapes do not match')
+    call('tcq_gemm_i8', ptr(a), ptr(w), ptr(sa), ptr(sw), ptr(out), _dt(out, (0, 1, 3), 'gemm_i8 out'), out.stride(0), M, N, K,
+         stream())
+    return out
