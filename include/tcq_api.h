@@ -138,27 +138,28 @@ typedef struct tcq_gemv_layer {
 int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                  tcq_stream_t stream);
 
-/* One layer (segment) of a small-M INT8 product. The output z of the segment starts at its first column: z[t * ldz + i] for
- * token t and output row i < m (several layers of a group write side by side into one (M, ldz) buffer). */
+/* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
+ * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
+#define TCQ_MAX_SEGS 4
 typedef struct tcq_gemm_seg {
     const void* w;       /* tcq_gemm_tcq: tcq_repack words of an (m, K) layer; tcq_gemm_w8: (m, K) int8 row-major weights */
     const int8_t* t8;    /* (512, 2) INT8 table (tcq_gemm_tcq only) */
-    const float* rs;     /* (m,) FP32 row scale */
-    float* z;            /* FP32 output, first column of the segment */
+    const float* rs;     /* (m,) FP32 row scale (unused for I32 output) */
+    void* out;           /* output, first column of the segment */
     int m;               /* output rows, a multiple of 16 */
 } tcq_gemm_seg;
 
-/* W2A8 fused decode + product for M <= 64 tokens: z[t, i] = (float(sum_k q[t, k] * w8[i, k]) * s[t]) * rs[i] with w8 = sign *
- * t8[hash(state)] decoded from the words on the fly and the sum exact in int32. q (M, K) int8 row-major, s (M,) FP32.
- * segs: DEVICE array of nseg descriptors, max_m = the largest m among them. K a multiple of 16.
- * Replaces kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673), which takes at most three
- * concatenated layers (q/k/v or gate/up, table chosen by tile-row bounds) and MT <= 10 tokens in shared memory. */
-int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+/* W2A8 fused decode + product for M <= 64 tokens: acc[t, i] = sum_k q[t, k] * w8[i, k], exact in int32, with w8 = sign *
+ * t8[hash(state)] decoded from the words on the fly. out_dtype F32: z = (float(acc) * s[t]) * rs[i]; BF16: its rounding;
+ * I32: acc. q (M, K) int8 row-major, s (M,) FP32, K a multiple of 16. segs: HOST array of nseg <= TCQ_MAX_SEGS descriptors
+ * (copied into the launch). Replaces kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673),
+ * which takes at most three concatenated layers (q/k/v or gate/up, table chosen by tile-row bounds) and MT <= 10 tokens. */
+int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                  tcq_stream_t stream);
 
 /* INT8-resident product, same contract with w = decoded (m, K) int8 weights (tcq_decode_i8). Replaces kernels.gemm_w8 /
  * k_gemm_w8 / k_gemm_w8d (deploy/tcq_kernels/kernels.py:365-399, 662-668). */
-int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                 tcq_stream_t stream);
 
 /* W8A8 INT8 GEMM: acc[m, n] = sum_k a[m, k] w[n, k], exact int32. a (M, K) int8 per-token quantized activations, w (N, K)
@@ -166,7 +167,8 @@ int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, 
  * accumulators; F32 (float(acc) * sa[m]) * sw[n]; BF16 the BF16 rounding of that (sa, sw FP32 scales, unused for I32).
  * Replaces the prefill product torch._int_mm(q, W.t()) of Group.product (deploy/tcq_kernels/modules.py:81-86;
  * tcq_format.int_matmul, tcq_format.py:110-116) followed by the (acc * s) * rs scaling of tcq_format.reference_linear
- * (tcq_format.py:135). */
+ * (tcq_format.py:135). Few tokens (M <= 16, or M <= 64 with N <= 8192) run the small-M product of tcq_gemm_w8 (one K chunk per wave), the
+ * rest the tiled GEMM. */
 int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
                 int K, tcq_stream_t stream);
 

@@ -352,13 +352,18 @@ def test_gemm_tcq_and_w8_bitexact(shapes, M):
     for L in layers:
         cols.append(c0)
         c0 += L.m
-    max_m = max(L.m for L in layers)
-    desc = K.gemm_segments([(w, t8, rs, z[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], DEV)
-    K.gemm_tcq(desc, len(layers), max_m, qd, sd, ldz)
-    desc2 = K.gemm_segments([(w, None, rs, z2[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], DEV)
-    K.gemm_w8(desc2, len(layers), max_m, qd, sd, ldz)
+    K.gemm_tcq([(w, t8, rs, z[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
+    K.gemm_w8([(w, None, rs, z2[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(bits_of(z), ref.view(np.uint32))
     assert np.array_equal(bits_of(z2), ref.view(np.uint32))
+    # the int32 accumulators and the BF16 output of the same products
+    exact = np.concatenate([O.int_matmul(q, L.w8_reference()) for L in layers], 1)
+    acc = torch.empty(M, ldz, dtype=torch.int32, device=DEV)
+    K.gemm_tcq([(w, t8, rs, acc[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, None, ldz)
+    assert np.array_equal(acc.cpu().numpy(), exact)
+    yb = torch.empty(M, ldz, dtype=torch.bfloat16, device=DEV)
+    K.gemm_w8([(w, None, rs, yb[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
 
 
 def test_gemm_small_rejects_bad_sizes():
@@ -369,9 +374,10 @@ def test_gemm_small_rejects_bad_sizes():
     q = torch.zeros(65, 64, dtype=torch.int8, device=DEV)
     s = torch.ones(65, device=DEV)
     z = torch.empty(65, 32, device=DEV)
-    desc = K.gemm_segments([(K.repack(d['bits'], 32, 64), t8, rs, z)], DEV)
     with pytest.raises(_lib.TcqError):
-        K.gemm_tcq(desc, 1, 32, q, s, 32)             # 65 tokens: more than the small-M product takes
+        K.gemm_tcq([(K.repack(d['bits'], 32, 64), t8, rs, z)], q, s, 32)      # 65 tokens: more than the small-M product takes
+    with pytest.raises(ValueError):
+        K.gemm_tcq([(K.repack(d['bits'], 32, 64), t8, rs, z)] * 5, q[:4], s[:4], 32)   # more segments than a launch takes
 
 
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM

@@ -34,11 +34,20 @@ SIGNATURES = {
     'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     'tcq_postg': [_P, _I, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemv_f16': [_P, _I, _P, _P, _I, _I, _I, _P],
-    'tcq_gemm_tcq': [_P, _I, _I, _P, _P, _I, _I, _I, _P],
-    'tcq_gemm_w8': [_P, _I, _I, _P, _P, _I, _I, _I, _P],
+    'tcq_gemm_tcq': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
+    'tcq_gemm_w8': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_i8': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L}
+
+MAX_SEGS = 4
+
+
+class GemmSeg(ctypes.Structure):
+    """tcq_gemm_seg (include/tcq_api.h)."""
+    _fields_ = [('w', ctypes.c_void_p), ('t8', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('out', ctypes.c_void_p),
+                ('m', ctypes.c_int)]
+
 
 _state = {}
 _lock = threading.Lock()

@@ -38,13 +38,17 @@ __device__ __forceinline__ void fill_table_i8(u32* tab, const i8* t8) {
 
 }  // namespace
 
+struct SegPack {
+    tcq_gemm_seg s[TCQ_MAX_SEGS];
+};
+
 // grid (tile rows of the largest segment, segments), NW = blockDim.x / 64 waves. MODE 0: decode from tcq_repack words;
-// MODE 1: resident INT8 weights.
-template <int MODE, int NB>
-__global__ __launch_bounds__(1024) void k_gemm_small(const tcq_gemm_seg* segs, const i8* q, const float* s, int M, int K, int ldz) {
+// MODE 1: resident INT8 weights. ODT: output dtype (F32 scaled, BF16 scaled, I32 accumulators).
+template <int MODE, int NB, int ODT>
+__global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(SM_MAXW - 1) * NB * 64];
-    const tcq_gemm_seg S = segs[blockIdx.y];
+    const tcq_gemm_seg S = P.s[blockIdx.y];
     const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
     const int I = blockIdx.x;
     if (I >= tiles_m) return;                                             // uniform
@@ -85,6 +89,16 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const tcq_gemm_seg* segs, c
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = int4v{0, 0, 0, 0};
     if (wave < nch) load(wave);
+    // epilogue scales, loaded with the operands (wave 0 stores)
+    float4_t rsv = {0.f, 0.f, 0.f, 0.f};
+    float sv[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) sv[b] = 0.f;
+    if (ODT != TCQ_I32 && wave == 0) {
+        rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
+    }
     if (MODE == 0) fill_table_i8(tab, S.t8);
     __syncthreads();
     for (int c = wave; c < nch; c += nw) {
@@ -121,45 +135,79 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const tcq_gemm_seg* segs, c
     for (int w = 0; w < nw - 1; ++w)
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[b] += red[(w * NB + b) * 64 + lane];
-    const float4_t rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int t = 16 * b + lr;
         if (t < M) {
-            const float st = gptr(s)[t];
-            float4_t o;
+            const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
+            if (ODT == TCQ_I32) {
+                *gptr((int4v*)((int*)S.out + o)) = acc[b];
+            } else {
+                const float st = sv[b];
+                float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = ((float)acc[b][e] * st) * rsv[e];
-            *gptr((float4_t*)(S.z + (size_t)t * ldz + 16 * I + 4 * lg)) = o;
+                for (int e = 0; e < 4; ++e) v[e] = ((float)acc[b][e] * st) * rsv[e];
+                if (ODT == TCQ_F32) {
+                    *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
+                } else {
+                    const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
+                    const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
+                    *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
+                }
+            }
         }
     }
 }
 
 // =========================================================================================================== C ABI
+template <int MODE, int NB>
+static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                            int ldo, int odt) {
+    switch (odt) {
+        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+    }
+}
+
 template <int MODE>
-static int gemm_small(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int odt, int ldo,
                       tcq_stream_t stream) {
-    if (!segs || !q || !s || nseg <= 0 || max_m <= 0 || M <= 0 || K <= 0 || ldz <= 0) return TCQ_ERR_ARG;
-    if (max_m % 16 || K % 16) return TCQ_ERR_SHAPE;
-    if (M > 64 || nseg > 65535) return TCQ_ERR_UNSUPPORTED;
-    if (ldz % 4 || (uintptr_t)q % 16) return TCQ_ERR_ALIGN;
-    if ((size_t)max_m * K >= ((size_t)1 << 31) || (size_t)M * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if (!segs || !q || nseg <= 0 || M <= 0 || K <= 0 || ldo <= 0) return TCQ_ERR_ARG;
+    if (odt != TCQ_F32 && odt != TCQ_BF16 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
+    if (odt != TCQ_I32 && !s) return TCQ_ERR_ARG;
+    if (nseg > TCQ_MAX_SEGS || M > 64) return TCQ_ERR_UNSUPPORTED;
+    if (K % 16) return TCQ_ERR_SHAPE;
+    if (ldo % 4 || (uintptr_t)q % 16) return TCQ_ERR_ALIGN;
+    SegPack P = {};
+    int max_m = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const tcq_gemm_seg& g = segs[i];
+        if (!g.w || !g.out || (MODE == 0 && !g.t8) || (odt != TCQ_I32 && !g.rs) || g.m <= 0) return TCQ_ERR_ARG;
+        if (g.m % 16) return TCQ_ERR_SHAPE;
+        if ((size_t)g.m * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+        const size_t osz = odt == TCQ_BF16 ? 2 : 4;
+        if ((uintptr_t)g.out % (4 * osz) || (g.rs && (uintptr_t)g.rs % 16)) return TCQ_ERR_ALIGN;
+        P.s[i] = g;
+        if (g.m > max_m) max_m = g.m;
+    }
+    if ((size_t)M * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
     const dim3 grid(max_m / 16, nseg), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
     const i8* qq = (const i8*)q;
-    if (M <= 16) launch_k(k_gemm_small<MODE, 1>, grid, block, 0, st, segs, qq, s, M, K, ldz);
-    else if (M <= 32) launch_k(k_gemm_small<MODE, 2>, grid, block, 0, st, segs, qq, s, M, K, ldz);
-    else launch_k(k_gemm_small<MODE, 4>, grid, block, 0, st, segs, qq, s, M, K, ldz);
+    if (M <= 16) launch_small_nb<MODE, 1>(grid, block, st, P, qq, s, M, K, ldo, odt);
+    else if (M <= 32) launch_small_nb<MODE, 2>(grid, block, st, P, qq, s, M, K, ldo, odt);
+    else launch_small_nb<MODE, 4>(grid, block, st, P, qq, s, M, K, ldo, odt);
     return launch_status();
 }
 
-extern "C" int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
-                            tcq_stream_t stream) {
-    return gemm_small<0>(segs, nseg, max_m, q, s, M, K, ldz, stream);
+extern "C" int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype,
+                            int ldo, tcq_stream_t stream) {
+    return gemm_small<0>(segs, nseg, q, s, M, K, out_dtype, ldo, stream);
 }
 
-extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, int max_m, const int8_t* q, const float* s, int M, int K, int ldz,
+extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                            tcq_stream_t stream) {
-    return gemm_small<1>(segs, nseg, max_m, q, s, M, K, ldz, stream);
+    return gemm_small<1>(segs, nseg, q, s, M, K, out_dtype, ldo, stream);
 }

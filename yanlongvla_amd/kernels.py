@@ -170,49 +170,47 @@ def gelu_table(device):
 
 
 # ------------------------------------------------------------------------------------------------- small-M INT8 products
-_GSEG = None
+class SmallProduct:
+    """A prepared small-M product over 1..4 segments [(w, t8, rs, out), ...]: out is a view whose first element is the
+    segment's first output column of an (M, ldo) buffer (FP32 / BF16 scaled, or int32 sums); rs (m,) FP32 gives m. The
+    descriptor array is built once (keep the tensors alive); __call__(q, s) launches on the current stream.
+    resident False: w = tcq_repack words + t8 (fused decode, reference kernels.gemm_tcq, kernels.py:671-673);
+    resident True: w = (m, K) int8 weights (reference kernels.gemm_w8, kernels.py:662-668)."""
+
+    def __init__(self, segs, ldo, resident=False):
+        if not 1 <= len(segs) <= _lib.MAX_SEGS:
+            raise ValueError(f'1 to {_lib.MAX_SEGS} segments')
+        self.name = 'tcq_gemm_w8' if resident else 'tcq_gemm_tcq'
+        self.arr = (_lib.GemmSeg * len(segs))()
+        self.keep = segs
+        self.odt = None
+        for i, (w, t8, rs, out) in enumerate(segs):
+            _contig(w, t8, rs)
+            d = _dt(out, (0, 1, 3), f'{self.name} out')
+            if self.odt is not None and d != self.odt:
+                raise TypeError('all segments need one output dtype')
+            self.odt = d
+            self.arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(out), rs.numel())
+        self.n, self.ldo = len(segs), ldo
+        self.fn = getattr(_lib.lib(), self.name)
+
+    def __call__(self, q, s):
+        M, K = q.shape
+        rc = self.fn(self.arr, self.n, q.data_ptr(), None if s is None else s.data_ptr(), M, K, self.odt, self.ldo, stream())
+        if rc:
+            raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
 
-def _gseg_dtype():
-    global _GSEG
-    if _GSEG is None:
-        import numpy as np
-        _GSEG = np.dtype([('w', '<u8'), ('t8', '<u8'), ('rs', '<u8'), ('z', '<u8'), ('m', '<i4'), ('pad', '<i4')])
-        assert _GSEG.itemsize == 40
-    return _GSEG
-
-
-def gemm_segments(segs, device):
-    """[(w, t8, rs, z), ...] -> device array of tcq_gemm_seg. w: tcq_repack words (fused decode) or (m, K) int8 weights
-    (resident); t8 (512, 2) int8 or None; rs (m,) FP32; z: a view whose first element is the segment's first output column
-    of an (M, ldz) FP32 buffer. Keep the tensors alive while the array is in use."""
-    import numpy as np
-    a = np.zeros(len(segs), dtype=_gseg_dtype())
-    for i, (w, t8, rs, z) in enumerate(segs):
-        _contig(w, t8, rs)
-        m = rs.numel()
-        if m % 16:
-            raise ValueError(f'segment {i}: {m} output rows is not a multiple of 16')
-        a[i] = (ptr(w), ptr(t8) or 0, ptr(rs), ptr(z), m, 0)
-    return torch.from_numpy(a.view(np.uint8).copy()).to(device)
-
-
-def _gemm_small(name, desc, nseg, max_m, q, s, ldz):
-    M, K = q.shape
+def gemm_tcq(segs, q, s, ldo):
+    """One-shot fused decode + product over segments (see SmallProduct)."""
     _contig(q, s)
-    call(name, ptr(desc), nseg, max_m, ptr(q), ptr(s), M, K, ldz, stream())
+    SmallProduct(segs, ldo)(q, s)
 
 
-def gemm_tcq(desc, nseg, max_m, q, s, ldz):
-    """W2A8 fused decode + product (reference kernels.gemm_tcq, kernels.py:671-673): for every segment, z = (float(q w8^T) * s)
-    * rs with w8 decoded on the fly. q (M <= 64, K) int8, s (M,) FP32, ldz = row stride of the shared FP32 output."""
-    _gemm_small('tcq_gemm_tcq', desc, nseg, max_m, q, s, ldz)
-
-
-def gemm_w8(desc, nseg, max_m, q, s, ldz):
-    """Same product on resident INT8 weights (reference kernels.gemm_w8, kernels.py:662-668)."""
-    _gemm_small('tcq_gemm_w8', desc, nseg, max_m, q, s, ldz)
-
+def gemm_w8(segs, q, s, ldo):
+    """One-shot INT8-resident product over segments (see SmallProduct)."""
+    _contig(q, s)
+    SmallProduct(segs, ldo, resident=True)(q, s)
 
 
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM
