@@ -38,7 +38,35 @@ def parse():
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu', action='store_true')
     p.add_argument('--seed', type=int, default=0)
+    p.add_argument('--copy-calibration', action='store_true',
+                   help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
+                        'FETCH_SIZE / WRITE_SIZE counters into bytes)')
     return p.parse_args()
+
+
+# HBM bytes per launch of the stream's decode-GEMV kernel, from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over
+# this benchmark at its default 1024 layers, each scaled by what the counter reads for a plain copy of known size
+TRAFFIC_SUMMARY = ROOT / 'profiles' / 'k_gemv_f16_stream1024_traffic.txt'
+
+
+def traffic_from_profile(nl):
+    if nl != 1024 or not TRAFFIC_SUMMARY.exists():
+        return None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith('traffic_bytes_per_launch:'):
+            return int(line.split(':', 1)[1].strip())
+    return None
+
+
+def copy_calibration():
+    import torch
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.int8, device='cuda:0')
+    dst = torch.empty_like(src)
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_bytes_read': n, 'copy_bytes_written': n, 'copies': 8}), flush=True)
 
 
 def make_stream(nl, seed, dev):
@@ -108,8 +136,10 @@ def timed(fn, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
-def graph_latency(fn, replays=200, warmup=20):
-    """Median / p95 ms of one HIP-graph replay of fn (the reference's timing protocol: 20 warm-up + 200 timed replays)."""
+def graph_latency(fn, replays=200, warmup=20, per_graph=1):
+    """Median / p95 ms per call of fn from HIP-graph replays (the reference's timing protocol: 20 warm-up + 200 timed
+    replays, each bracketed by events). With per_graph > 1 the graph holds that many calls back to back and the replay time
+    is divided by it: the device time per call without the graph's own submission latency."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -119,7 +149,8 @@ def graph_latency(fn, replays=200, warmup=20):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for _ in range(per_graph):
+            fn()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -130,7 +161,7 @@ def graph_latency(fn, replays=200, warmup=20):
         g.replay()
         b.record()
         b.synchronize()
-        ts.append(a.elapsed_time(b))
+        ts.append(a.elapsed_time(b) / per_graph)
     ts.sort()
     return ts[len(ts) // 2], ts[int(len(ts) * 0.95)]
 
@@ -188,6 +219,9 @@ def main():
         print(json.dumps({'error': f'--gpus {args.gpus}: this benchmark runs on one GPU only; the path has no multi-GPU '
                                    'implementation (row-split sharding is described in the design notes)'}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
     from yanlongvla_amd import _lib
     _lib.lib()
@@ -212,6 +246,7 @@ def main():
     L1 = dict(L, tlut=L['tlut'][:1], row_scale=L['row_scale'][:1], sv=L['sv'][:1], wdev=L['wdev'][:L['per']])
     S1 = Stream(L1, x)
     lat_med, lat_p95 = graph_latency(S1.step)
+    am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
     out = {
         'metric': 'TCQ-2bit decode-GEMV GB/s (% HBM peak) + ms per action chunk, 1 GPU',
@@ -226,10 +261,12 @@ def main():
                                'FP16 512x2 codebook, L=16 K=2 V=2, input and output block-Walsh rotations',
                    'layers': nl, 'm': M_DIM, 'n': N_DIM, 'tokens': 1, 'packed_bytes_per_step': byts},
         'hbm_frac': round(byts / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
+        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1> (layer-stream plan)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_from_profile(nl),
                      'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
-        'single_layer_ms': {'median': round(lat_med, 5), 'p95': round(lat_p95, 5)},
+        'single_layer_ms': {'graph_replay_median': round(lat_med, 5), 'graph_replay_p95': round(lat_p95, 5),
+                            'per_step_in_100_step_graph_median': round(am_med, 5),
+                            'per_step_in_100_step_graph_p95': round(am_p95, 5)},
         'max_rel_l2_vs_oracle': err,
         'cpu_baseline': cpu,
     }

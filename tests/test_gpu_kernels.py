@@ -209,10 +209,14 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
+# latency plan (<= 2048 tile rows per batch: one tile row per workgroup, 4 / 8 / 16 waves splitting the chunks) and the
+# stream plan (row groups per wave; one workgroup per layer from 256 layers on)
 @pytest.mark.parametrize('m,n,M,nl', [(2048, 2048, 1, 1), (2048, 2048, 4, 3), (48, 80, 1, 2), (256, 1024, 16, 1),
-                                      (1024, 4096, 1, 2), (4096, 1024, 2, 1), (64, 1152, 3, 2)])
+                                      (1024, 4096, 1, 2), (4096, 1024, 2, 1), (64, 1152, 3, 2), (512, 512, 2, 1),
+                                      (1024, 16384, 1, 1), (2048, 2048, 1, 17), (128, 256, 1, 300), (64, 1152, 3, 600)])
 def test_gemv_f16_layer(m, n, M, nl):
-    """C0 layer: pre_h16 -> fused decode-GEMV -> post, against reference_linear(table='fp16', a8=False), rel L2 <= 2e-3."""
+    """Dense-table layer: pre_h16 -> fused decode-GEMV -> post, against reference_linear(table='fp16', a8=False),
+    rel L2 <= 2e-3."""
     from yanlongvla_amd import kernels as K
     layers = [O.random_layer(m, n, 100 + i) for i in range(nl)]
     for L in layers[1:]:

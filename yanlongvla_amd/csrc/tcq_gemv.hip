@@ -39,12 +39,16 @@ __device__ __forceinline__ void fill_table(u32* tab, const u16* tl) {
 
 }  // namespace
 
-// grid (workgroups per layer, layers); workgroup x covers tile rows [x rows_per_wg, (x + 1) rows_per_wg) of its layer. Each
-// wave takes groups of R tile rows round-robin and walks their nch chunks; the words of iteration it + D are loaded while
-// iteration it is decoded (D + 1 register buffers, the only vector-memory loads of the loop, so in-order vmcnt waits never
-// stall on the prefetch). Dynamic LDS: h16 (M, 256 nch) FP16 with zero columns from n on, then the FP32 row scales of the
-// workgroup's rows. Two accumulators per tile row (pairs 0..3 and 4..7) halve the MFMA dependency chain.
-template <int C, int R, int D, int AUX>
+// grid (workgroups per layer, layers); workgroup x covers tile rows [x rows_per_wg, (x + 1) rows_per_wg) of its layer.
+// KS = 1 (layer streams): each wave takes groups of R tile rows round-robin and walks their nch chunks. KS > 1 (a few layers,
+// latency): the waves form nw / KS groups of KS, wave group g owns row group g (rows_per_wg = R nw / KS) and wave k of the
+// group the chunks k, k + KS, ...; the KS partial sums meet in LDS after the loop. The words of iteration it + D are loaded
+// while iteration it is decoded (D + 1 register buffers, the only vector-memory loads of the loop, so in-order vmcnt waits
+// never stall on the prefetch); the first D loads are issued before the codebook fill, hiding their latency behind it.
+// Dynamic LDS: h16 (M, 256 nch) FP16 with zero columns from n on, the FP32 row scales of the workgroup's rows, then for
+// KS > 1 the partial sums (nw R 64 float4). Two accumulators per tile row (pairs 0..3 and 4..7) halve the MFMA dependency
+// chain.
+template <int C, int R, int D, int AUX, int KS>
 __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers, const u16* h16, const float* hscale, int M,
                                                    int m, int n, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * C];
@@ -52,29 +56,17 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
     const tcq_gemv_layer L = layers[blockIdx.y];
     const int tiles_m = m >> 4, nch = (n + 255) >> 8, np = nch << 8;
     const int I0 = blockIdx.x * rows_per_wg, I1 = min(I0 + rows_per_wg, tiles_m);
-    u16* hl = (u16*)dyn;
-    float* sl = (float*)(dyn + (M * np >> 1));
-    fill_table<C>(tab, (const u16*)L.tlut);
-    for (int i = threadIdx.x; i < (M * np) >> 3; i += blockDim.x) {      // 8 FP16 per thread-step, rows padded to np
-        const int t = i / (np >> 3), k = (i - t * (np >> 3)) << 3;
-        ((uint4_t*)hl)[i] = k < n ? gptr((const uint4_t*)(h16 + (size_t)t * n + k))[0] : uint4_t{0, 0, 0, 0};
-    }
-    const u16* rsc = (const u16*)L.row_scale;
-    for (int i = threadIdx.x; i < (I1 - I0) * 16; i += blockDim.x) sl[i] = f16_to_f32(gptr(rsc)[I0 * 16 + i]);
-    __syncthreads();
-
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const int gw = wave / KS, kw = wave % KS, ngw = nw / KS;            // row-group wave index, chunk phase
     const int lr = lane & 15, lg = lane >> 4;
     const bool tok = lr < M;
     const u32 cp4 = (u32)(lane & (C - 1)) << 2;
     constexpr int ESH = 2 + ilog2(C);                     // byte shift of an entry index
     const int ngroups = (I1 - I0 + R - 1) / R;
-    const int iters = wave < ngroups ? ((ngroups - 1 - wave) / nw + 1) * nch : 0;
-    if (iters == 0) return;
+    const int nchw = kw < nch ? (nch - 1 - kw) / KS + 1 : 0;          // chunks of this wave per row group
+    const int iters = gw < ngroups ? ((ngroups - 1 - gw) / ngw + 1) * nchw : 0;
     const rsrc_t W = make_rsrc(L.wdev, (u32)(tiles_m * nch) << 10);
     const u32 wv = (u32)lane << 4;
-    const float hs = gptr(hscale)[tok ? lr : 0];
-    const char* hb = (const char*)hl + (size_t)(lr * np + 16 * lg) * 2;
 
     float4_t acc[R][2];
     uint4_t buf[D + 1][R];
@@ -85,23 +77,52 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
     for (int j = 0; j < 4; ++j) B[j][0] = B[j][1] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
 
     // iteration counters (chunk c, group k) of the next load and the next product, advanced without divisions
-    int lc = 0, lk = 0, pc = 0, pk = 0, nload = 0;
+    int lc = kw, lk = 0, pc = kw, pk = 0, nload = 0;
     const int lastI = tiles_m - 1;
     auto load = [&](uint4_t(&dst)[R]) {
-        const int Ig = I0 + (wave + lk * nw) * R;
+        const int Ig = I0 + (gw + lk * ngw) * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int I = min(Ig + r, lastI);
-            dst[r] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, wv, (u32)(I * nch + lc) << 10, AUX));
+            dst[r] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, wv, (u32)(I * nch + min(lc, nch - 1)) << 10, AUX));
         }
         if (++nload < iters) {                   // past the end the last chunk is loaded again (never used)
-            if (++lc == nch) { lc = 0; ++lk; }
+            lc += KS;
+            if (lc >= nch) { lc = kw; ++lk; }
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < D; ++u) load(buf[u]);
+
+    u16* hl = (u16*)dyn;
+    float* sl = (float*)(dyn + (M * np >> 1));
+    fill_table<C>(tab, (const u16*)L.tlut);
+    for (int i = threadIdx.x; i < (M * np) >> 3; i += blockDim.x) {      // 8 FP16 per thread-step, rows padded to np
+        const int t = i / (np >> 3), k = (i - t * (np >> 3)) << 3;
+        ((uint4_t*)hl)[i] = k < n ? gptr((const uint4_t*)(h16 + (size_t)t * n + k))[0] : uint4_t{0, 0, 0, 0};
+    }
+    const u16* rsc = (const u16*)L.row_scale;
+    for (int i = threadIdx.x; i < (I1 - I0) * 16; i += blockDim.x) sl[i] = f16_to_f32(gptr(rsc)[I0 * 16 + i]);
+    __syncthreads();
+    if (KS == 1 && iters == 0) return;
+    const float hs = gptr(hscale)[tok ? lr : 0];
+    const char* hb = (const char*)hl + (size_t)(lr * np + 16 * lg) * 2;
+
+    auto epilogue = [&](int r, int Ig, const float4_t& a) {
+        const int I = Ig + r;
+        if (I < I1 && tok) {
+            const float* s = sl + (I - I0) * 16 + 4 * lg;
+            float4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (a[e] * hs) * s[e];
+            *gptr((float4_t*)(L.z + (size_t)lr * m + 16 * I + 4 * lg)) = o;
         }
     };
 
     auto process = [&](const uint4_t(&w)[R]) {
-        const int c = pc, Ig = I0 + (wave + pk * nw) * R;
-        if (++pc == nch) { pc = 0; ++pk; }
+        const int c = pc, Ig = I0 + (gw + pk * ngw) * R;
+        pc += KS;
+        if (pc >= nch) { pc = kw; ++pk; }
         if (tok) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -134,24 +155,15 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
             consume(q - 1, va[(q - 1) & 1]);
         }
         consume(4 * R - 1, va[(4 * R - 1) & 1]);
-        if (c == nch - 1) {
+        if (KS == 1 && c == nch - 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const int I = Ig + r;
-                if (I < I1 && tok) {
-                    const float* s = sl + (I - I0) * 16 + 4 * lg;
-                    float4_t o;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = ((acc[r][0][e] + acc[r][1][e]) * hs) * s[e];
-                    *gptr((float4_t*)(L.z + (size_t)lr * m + 16 * I + 4 * lg)) = o;
-                }
+                epilogue(r, Ig, acc[r][0] + acc[r][1]);
                 acc[r][0] = acc[r][1] = float4_t{0.f, 0.f, 0.f, 0.f};
             }
         }
     };
 
-#pragma unroll
-    for (int u = 0; u < D; ++u) load(buf[u]);
     for (int it0 = 0; it0 < iters; it0 += D + 1) {
 #pragma unroll
         for (int u = 0; u <= D; ++u) {
@@ -161,23 +173,53 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
             }
         }
     }
+    if constexpr (KS > 1) {                  // every wave owns at most one row group: sum the KS chunk phases in LDS
+        float4_t* part = (float4_t*)(sl + rows_per_wg * 16);
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[(wave * R + r) * 64 + lane] = acc[r][0] + acc[r][1];
+        __syncthreads();
+        if (kw == 0 && gw < ngroups) {
+            const int Ig = I0 + gw * R;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float4_t a = part[(wave * R + r) * 64 + lane];
+                for (int k = 1; k < KS; ++k) a += part[((wave + k) * R + r) * 64 + lane];
+                epilogue(r, Ig, a);
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------------ plan
-// Launch shape of a batch (measured on MI355X, 1024 layers of 2048 x 2048: 16 table copies, 4 tile rows per wave, one
-// iteration of prefetch and 512-thread workgroups beat 32 copies / 1024 threads and the shallower / deeper pipelines).
-// Big layers get one workgroup per layer when there are enough layers to fill the chip (the table is then filled once
-// per layer), else the rows are split so that every wave of a workgroup has at least one group of rows.
+// Launch shapes (measured on MI355X).
+// Stream (many tile rows, KS = 1): 16 table copies, 4 tile rows per wave, one iteration of prefetch and 512-thread
+// workgroups beat 32 copies / 1024 threads and the shallower / deeper pipelines on 1024 layers of 2048 x 2048. Big layer
+// counts get one workgroup per layer (the table is then filled once per layer), else the rows are split so that every
+// wave of a workgroup has at least one group of rows.
+// Latency (at most LAT_ROWS tile rows in the batch): one tile row per workgroup and KS = 4 / 8 / 16 waves splitting its
+// chunks, so a single 2048 x 2048 layer runs as 128 workgroups of 8 waves with one 1 KiB chunk each instead of 4 workgroups
+// walking 32 rows.
 constexpr int GEMV_C = 16, GEMV_R = 4, GEMV_D = 1, GEMV_THREADS = 512;
+constexpr int LAT_C = 8, LAT_ROWS = 2048;
 
 struct GemvPlan {
-    int rows_per_wg, wgs;
+    int rows_per_wg, wgs, threads, ks;
     size_t dyn;
 };
 
 static GemvPlan gemv_plan(int nlayers, int M, int m, int n) {
-    const int tiles_m = m / 16, nch = (n + 255) / 256, waves = GEMV_THREADS / 64;
+    const int tiles_m = m / 16, nch = (n + 255) / 256;
     const size_t hbytes = (size_t)M * nch * 256 * 2;
+    GemvPlan p;
+    if ((size_t)nlayers * tiles_m <= LAT_ROWS) {
+        p.ks = nch >= 16 ? 16 : nch >= 8 ? 8 : 4;
+        p.rows_per_wg = 1;
+        p.wgs = tiles_m;
+        p.threads = 64 * p.ks;
+        p.dyn = hbytes + 64 + (size_t)p.ks * 1024;
+        return p;
+    }
+    const int waves = GEMV_THREADS / 64;
     int rows;
     if (nlayers >= 256) {
         rows = tiles_m;
@@ -188,9 +230,10 @@ static GemvPlan gemv_plan(int nlayers, int M, int m, int n) {
     }
     rows = (rows + GEMV_R - 1) / GEMV_R * GEMV_R;
     while (hbytes + (size_t)rows * 64 + 4096 * GEMV_C > 160 * 1024 && rows > GEMV_R) rows = (rows / 2 + GEMV_R - 1) / GEMV_R * GEMV_R;
-    GemvPlan p;
+    p.ks = 1;
     p.rows_per_wg = rows;
     p.wgs = (tiles_m + rows - 1) / rows;
+    p.threads = GEMV_THREADS;
     p.dyn = hbytes + (size_t)rows * 64;
     return p;
 }
@@ -203,9 +246,17 @@ extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const voi
     if ((uintptr_t)h16 % 16) return TCQ_ERR_ALIGN;
     if ((size_t)(m / 16) * ((n + 255) / 256) * 1024 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;   // one layer's words < 2 GiB
     const GemvPlan p = gemv_plan(nlayers, M, m, n);
-    if (p.dyn + 4096 * GEMV_C > 160 * 1024) return TCQ_ERR_UNSUPPORTED;                          // activations do not fit LDS
+    const int C = p.ks == 1 ? GEMV_C : LAT_C;
+    if (p.dyn + 4096 * C > 160 * 1024) return TCQ_ERR_UNSUPPORTED;                                // activations do not fit LDS
     constexpr int NT = 2;   // non-temporal loads: every packed word is read once
-    launch_k(k_gemv_f16<GEMV_C, GEMV_R, GEMV_D, NT>, dim3(p.wgs, nlayers), dim3(GEMV_THREADS), p.dyn, (hipStream_t)stream, layers,
-             (const u16*)h16, hscale, M, m, n, p.rows_per_wg);
+    const dim3 grid(p.wgs, nlayers), block(p.threads);
+    const hipStream_t st = (hipStream_t)stream;
+    const u16* h = (const u16*)h16;
+    switch (p.ks) {
+        case 1: launch_k(k_gemv_f16<GEMV_C, GEMV_R, GEMV_D, NT, 1>, grid, block, p.dyn, st, layers, h, hscale, M, m, n, p.rows_per_wg); break;
+        case 4: launch_k(k_gemv_f16<LAT_C, 1, 1, NT, 4>, grid, block, p.dyn, st, layers, h, hscale, M, m, n, p.rows_per_wg); break;
+        case 8: launch_k(k_gemv_f16<LAT_C, 1, 1, NT, 8>, grid, block, p.dyn, st, layers, h, hscale, M, m, n, p.rows_per_wg); break;
+        default: launch_k(k_gemv_f16<LAT_C, 1, 1, NT, 16>, grid, block, p.dyn, st, layers, h, hscale, M, m, n, p.rows_per_wg); break;
+    }
     return launch_status();
 }
