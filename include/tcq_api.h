@@ -120,6 +120,28 @@ typedef struct tcq_post_seg {
 int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype, int M,
               int maxN, tcq_stream_t stream);
 
+/* ----------------------------------------------------------------------------------------------------- MLP middles */
+
+/* Gated-MLP middle (down(gelu(gate(x)) * up(x))): acc (M, lda >= 2N) holds gate columns [0, N) and up columns [N, 2N),
+ * scaled as tcq_post (rs, sv: concatenated (2N,) vectors; rs unused for F32). g = GELU(BF16(walsh(gate) * sv)) by the table,
+ * u = BF16(walsh(up) * sv), x = BF16(g * u) * su (su: the down projection's input signs, (N,)) -> block Walsh -> per-token
+ * INT8: q (M, N) and / or q4 (N/4, ldq), scale (M,). N % 4 == 0, N <= tcq_max_width().
+ * Replaces kernels.mid2 / k_mid2_{i32,f32,bf16} (deploy/tcq_kernels/kernels.py:263-278, 640-643). */
+int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const uint16_t* gelu_lut,
+             const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N, tcq_stream_t stream);
+
+/* Plain-MLP middle (fc2(gelu(fc1(x)))): acc (M, lda >= N) -> walsh -> * sv -> + bias (FP32 (N,) or NULL) -> BF16 -> GELU table
+ * -> * su -> walsh -> per-token INT8 (q / q4, scale). Replaces kernels.mid1 / k_mid1_* (deploy/tcq_kernels/kernels.py:280-292,
+ * 646-650). */
+int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const float* bias,
+             const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
+             tcq_stream_t stream);
+
+/* Second half of a split gated-MLP middle: g, u (M, K) BF16 -> x = BF16(g * u) * su -> walsh -> per-token INT8 (q / q4, scale).
+ * Replaces kernels.pre2 / k_pre2 (deploy/tcq_kernels/kernels.py:295-307, 631-633). */
+int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
+             tcq_stream_t stream);
+
 /* -------------------------------------------------------------------------------------------------------- products */
 
 /* One layer of a batched FP16-table decode-GEMV / small-M GEMM (M <= 16 tokens): z[t, i] = (sum_k h16[t, k] *

@@ -18,7 +18,7 @@ How each function is pinned (tests/test_oracle.py):
          dense Sylvester Hadamard (fwht), bit-by-bit window read of the u16 stream (states_from_bits), the state recurrence
          s[t+1] = ((s[t] << 4) | next nibble) & 0xffff with tail-biting, exact int64 products (int_matmul).
   gelu_tanh_bf16 -> PyTorch's own torch.nn.functional.gelu(approximate='tanh') (the library routine the reference tabulates).
-  mlp_middle, pre2, quantize_channels, w8a8_reference -> compositions of the pinned functions with the rounding points written in
+  mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference -> compositions of the pinned functions with the rounding points written in
          deploy/tcq_kernels/kernels.py:272-277, 303 (checked against the unfused chain in the tests).
 """
 import math
@@ -26,7 +26,7 @@ import math
 import numpy as np
 
 __all__ = ['block_widths', 'fwht', 'states_from_bits', 'lookup', 'snap', 'quantize_tokens', 'int_matmul', 'Layer',
-           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'pre2', 'quantize_channels',
+           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'plain_middle', 'pre2', 'quantize_channels',
            'w8a8_reference', 'q4_layout', 'random_layer']
 
 
@@ -228,6 +228,14 @@ def mlp_middle(z_gate, z_up, sv_gate, sv_up, su_down, gelu=gelu_tanh_bf16):
     u = post_bf16(z_up, sv_up)
     q, s = pre2(g, u, su_down)
     return q, s, g, u
+
+
+def plain_middle(z, sv, bias, su, gelu=gelu_tanh_bf16):
+    """Plain-MLP middle on a scaled FP32 accumulator (deploy/tcq_kernels/kernels.py:280-292): Walsh -> sign -> bias -> BF16 ->
+    GELU -> sign flip of the next layer -> Walsh -> per-token INT8. Returns (q, s, g_bits)."""
+    g = gelu(post_bf16(z, sv, bias))
+    q, s = quantize_tokens(fwht(bf16_to_f32(g) * np.asarray(su).astype(np.float32)))
+    return q, s, g
 
 
 def w8a8_reference(a, w):

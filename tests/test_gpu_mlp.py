@@ -1,0 +1,140 @@
+"""GPU parity of the fused MLP middles (gated GeGLU middle, plain GELU middle, split second half) against the oracle:
+INT8 activations and per-token scales bit-exact, for int32 / FP32 / BF16 accumulators and Walsh widths made of one or
+several power-of-two blocks."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tcq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+@pytest.fixture(scope='module', autouse=True)
+def _lib():
+    from yanlongvla_amd import _lib
+    _lib.lib()
+    torch.cuda.init()
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def signs(rng, n):
+    return np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.int8)
+
+
+def lut_np():
+    from yanlongvla_amd import kernels as K
+    return K.gelu_table(DEV).view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def accumulators(rng, M, width, kind):
+    """Random accumulators of one kind and the scaled FP32 rows the kernels see: int32 -> (float(a) * s) * rs,
+    BF16 -> bf16(a) * rs, FP32 -> a."""
+    if kind == 'i32':
+        acc = rng.integers(-2 ** 18, 2 ** 18, size=(M, width)).astype(np.int32)
+        s = (rng.random(M) * 1e-3 + 1e-4).astype(np.float32)
+        rs = (rng.random(width) * 1e-2 + 1e-3).astype(np.float32)
+        z = (acc.astype(np.float32) * s[:, None]) * rs[None, :]
+        return T(acc), T(s), T(rs), z
+    if kind == 'bf16':
+        a = O.bf16_bits(rng.standard_normal((M, width)).astype(np.float32))
+        rs = (rng.random(width) + 0.5).astype(np.float32)
+        z = O.bf16_to_f32(a) * rs[None, :]
+        return T(a.view(np.int16)).view(torch.bfloat16), None, T(rs), z
+    acc = rng.standard_normal((M, width)).astype(np.float32)
+    return T(acc), None, None, acc
+
+
+@pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
+@pytest.mark.parametrize('M,N', [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 20)])
+def test_mid2_bitexact(kind, M, N):
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M * 7 + N)
+    acc, s, rs, z = accumulators(rng, M, 2 * N, kind)
+    sv, su = signs(rng, 2 * N), signs(rng, N)
+    q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    q4 = torch.empty(N // 4, M, dtype=torch.int32, device=DEV)
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(acc, s, rs, T(sv), T(su), q=q, q4=q4, scale=sc)
+    lut = lut_np()
+    qr, sr, _, _ = O.mlp_middle(z[:, :N], z[:, N:], sv[:N], sv[N:], su, gelu=lambda b: lut[b])
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0])
+    assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
+
+
+def test_mid2_strided_accumulator():
+    """Gate | up columns inside a wider accumulator row (lda > 2N), as when more layers share the product."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(11)
+    M, N, lda = 5, 1024, 2 * 1024 + 256
+    full = rng.integers(-2 ** 18, 2 ** 18, size=(M, lda)).astype(np.int32)
+    s = (rng.random(M) * 1e-3 + 1e-4).astype(np.float32)
+    rs = (rng.random(2 * N) * 1e-2).astype(np.float32)
+    sv, su = signs(rng, 2 * N), signs(rng, N)
+    q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(T(full), T(s), T(rs), T(sv), T(su), q=q, scale=sc)
+    z = (full[:, :2 * N].astype(np.float32) * s[:, None]) * rs[None, :]
+    lut = lut_np()
+    qr, sr, _, _ = O.mlp_middle(z[:, :N], z[:, N:], sv[:N], sv[N:], su, gelu=lambda b: lut[b])
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(sc.cpu().numpy(), sr[:, 0])
+
+
+@pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
+@pytest.mark.parametrize('M,N,with_bias', [(1, 4304, True), (50, 4096, False), (10, 1152, True), (4, 12, True)])
+def test_mid1_bitexact(kind, M, N, with_bias):
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M * 13 + N)
+    acc, s, rs, z = accumulators(rng, M, N, kind)
+    sv, su = signs(rng, N), signs(rng, N)
+    bias = (rng.standard_normal(N) * 0.2).astype(np.float32) if with_bias else None
+    q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid1(acc, s, rs, T(sv), None if bias is None else T(bias), T(su), q=q, scale=sc)
+    lut = lut_np()
+    qr, sr, _ = O.plain_middle(z, sv, bias, su, gelu=lambda b: lut[b])
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0])
+
+
+@pytest.mark.parametrize('M,K', [(1, 16384), (50, 4096), (9, 1152), (3, 8)])
+def test_pre2_bitexact(M, K):
+    from yanlongvla_amd import kernels as Kn
+    rng = np.random.default_rng(M + K)
+    g = O.bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    u = O.bf16_bits(rng.standard_normal((M, K)).astype(np.float32) * 3)
+    su = signs(rng, K)
+    q = torch.empty(M, K, dtype=torch.int8, device=DEV)
+    q4 = torch.empty(K // 4, M + 3, dtype=torch.int32, device=DEV)          # ldq > M
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    Kn.pre2(T(g.view(np.int16)).view(torch.bfloat16), T(u.view(np.int16)).view(torch.bfloat16), T(su), q=q, q4=q4, scale=sc)
+    qr, sr = O.pre2(g, u, su)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0])
+    assert np.array_equal(q4.cpu().numpy()[:, :M], O.q4_layout(qr))
+
+
+def test_mid2_equals_split_middle():
+    """mid2 == postg(gate with GELU, up) followed by pre2: the fused kernel changes no rounding point."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(5)
+    M, N = 50, 4096
+    acc, s, rs, _ = accumulators(rng, M, 2 * N, 'i32')
+    sv, su = T(signs(rng, 2 * N)), T(signs(rng, N))
+    q1 = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    s1 = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(acc, s, rs, sv, su, q=q1, scale=s1)
+    g = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    u = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    desc = K.post_segments([(acc, 0, rs[:N], sv[:N], None, g, True), (acc, N, rs[N:], sv[N:], None, u, False)], DEV)
+    K.postg(desc, 2, torch.int32, torch.bfloat16, s, M, N, gelu_lut=K.gelu_table(DEV))
+    q2 = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    s2 = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.pre2(g, u, su, q=q2, scale=s2)
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)

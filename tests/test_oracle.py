@@ -249,6 +249,24 @@ def test_mlp_middle_is_the_unfused_chain():
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
 
 
+def test_plain_middle_is_the_unfused_chain():
+    """mid1's definition through PyTorch's own BF16 cast and GELU; the bias enters before the BF16 rounding."""
+    import torch
+    rng = np.random.default_rng(3)
+    N = 96                                                   # 64 + 32: two Walsh blocks
+    z = rng.standard_normal((4, N)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.3).astype(np.float32)
+    sv, su = [np.where(rng.integers(0, 2, N) > 0, 1, -1).astype(np.int8) for _ in range(2)]
+    q, s, g = O.plain_middle(z, sv, bias, su)
+    y = torch.from_numpy(O.fwht(z) * sv.astype(np.float32) + bias).bfloat16()
+    act = torch.nn.functional.gelu(y, approximate='tanh').float().numpy()
+    assert np.array_equal(g, torch.from_numpy(act).bfloat16().view(torch.int16).numpy().astype(np.uint16))
+    q2, s2 = O.quantize_tokens(O.fwht(act * su.astype(np.float32)))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    qb, _, _ = O.plain_middle(z, sv, None, su)               # the bias matters
+    assert not np.array_equal(q, qb)
+
+
 def test_q4_layout():
     q = np.arange(2 * 8, dtype=np.int8).reshape(2, 8)
     q4 = O.q4_layout(q)

@@ -32,6 +32,9 @@ SIGNATURES = {
     'tcq_pre_h16': [_P, _I, _P, _P, _P, _I, _I, _P],
     'tcq_quantize_rows': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_mid1': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_pre2': [_P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_postg': [_P, _I, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemv_f16': [_P, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemm_tcq': [_P, _I, _P, _P, _I, _I, _I, _I, _P],

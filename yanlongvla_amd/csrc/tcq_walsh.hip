@@ -267,6 +267,76 @@ __global__ void k_postg(const tcq_post_seg* segs, const float* s, const u16* gel
     store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec);
 }
 
+// ------------------------------------------------------------------------------------------------------------ MLP middles
+// Rounding points of the fused MLP middles (each stage is the unfused chain's): GELU and the gate / up products round to
+// BF16 exactly where the separate epilogue + prologue kernels would store BF16 tensors.
+__device__ __forceinline__ u16 gelu_of(const u16* lut, u16 b) { return gptr(lut)[b]; }
+
+// Gated MLP (down(gelu(gate(x)) * up(x))): accumulator row = gate columns [0, N) | up columns [N, 2N), scaled like tcq_post
+// (rs and sv are the concatenated 2N vectors). g = GELU(BF16(walsh(gate) * sv)) is kept in LDS as BF16, then
+// x = BF16(g * BF16(walsh(up) * sv)) * su -> walsh -> per-token INT8 of the down projection's input.
+template <int ADT>
+__global__ void k_mid2(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const u16* lut, const i8* su,
+                       i8* q, int* q4, int ldq, float* scale, int N, int vec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    u16* g = (u16*)(lds + lds_words(N));
+    const int tok = blockIdx.x;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, st, rs, N, vec);
+    block_walsh(lds, N, [&](int i, float v) { g[i] = gelu_of(lut, f32_to_bf16(v * (float)gptr(sv)[i])); });
+    __syncthreads();
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + N, st, rs + (ADT == TCQ_F32 ? 0 : N), N, vec);
+    block_walsh(lds, N, [&](int i, float v) {
+        const u16 u = f32_to_bf16(v * (float)gptr(sv)[N + i]);
+        lds[lds_slot(i)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(g[i]) * bf16_to_f32(u))) * (float)gptr(su)[i];
+    });
+    __syncthreads();
+    float mx = 0.f;
+    block_walsh(lds, N, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    const float sc = token_scale(block_max(mx, red));
+    if (threadIdx.x == 0) scale[tok] = sc;
+    quantize_row(lds, sc, q ? q + (size_t)tok * N : nullptr, q4, tok, N, ldq);
+}
+
+// Plain MLP (fc2(gelu(fc1(x)))): x = GELU(BF16(walsh(acc) * sv + bias)) * su -> walsh -> per-token INT8 of fc2's input.
+template <int ADT>
+__global__ void k_mid1(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const float* bias, const u16* lut,
+                       const i8* su, i8* q, int* q4, int ldq, float* scale, int N, int vec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x;
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
+    block_walsh(lds, N, [&](int i, float v) {
+        v = v * (float)gptr(sv)[i];
+        if (bias) v = v + gptr(bias)[i];
+        lds[lds_slot(i)] = bf16_to_f32(gelu_of(lut, f32_to_bf16(v))) * (float)gptr(su)[i];
+    });
+    __syncthreads();
+    float mx = 0.f;
+    block_walsh(lds, N, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    const float sc = token_scale(block_max(mx, red));
+    if (threadIdx.x == 0) scale[tok] = sc;
+    quantize_row(lds, sc, q ? q + (size_t)tok * N : nullptr, q4, tok, N, ldq);
+}
+
+// Second half of a split gated-MLP middle: x = BF16(g * u) * su (g = GELU(gate), u = up, both BF16 (M, K)) -> walsh -> INT8.
+__global__ void k_pre2(const u16* g, const u16* u, const i8* su, i8* q, int* q4, int ldq, float* scale, int K) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x;
+    const size_t base = (size_t)tok * K;
+    for (int i = threadIdx.x; i < K; i += blockDim.x)
+        lds[lds_slot(i)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gptr(g)[base + i]) * bf16_to_f32(gptr(u)[base + i]))) *
+                           (float)gptr(su)[i];
+    __syncthreads();
+    float mx = 0.f;
+    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    const float sc = token_scale(block_max(mx, red));
+    if (threadIdx.x == 0) scale[tok] = sc;
+    quantize_row(lds, sc, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
+}
+
 // =========================================================================================================== C ABI
 // Threads per row: few rows (latency) -> about one 8-element vector per thread; many rows (throughput) -> four vectors per
 // thread so more rows share a CU.
@@ -399,5 +469,59 @@ extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, cons
         case TCQ_BF16: POSTG_A(TCQ_BF16); break;
         default: return TCQ_ERR_DTYPE;
     }
+    return launch_status();
+}
+
+extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv,
+                        const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
+                        tcq_stream_t stream) {
+    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < 2 * N || (q4 && ldq < M))
+        return TCQ_ERR_ARG;
+    if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
+    if (N % 4 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const dim3 grid(M), block(row_threads(M, N));
+    const size_t sh = row_lds(N) + (size_t)N * 2;
+    const int asz = dsize(acc_dtype);
+    const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)N * asz) % 16 == 0 &&
+                    (!rs || (al16(rs) && (N * 4) % 16 == 0));
+    hipStream_t st = (hipStream_t)stream;
+    const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
+    switch (acc_dtype) {
+        case TCQ_I32: launch_k(k_mid2<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_F32: launch_k(k_mid2<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_BF16: launch_k(k_mid2<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        default: return TCQ_ERR_DTYPE;
+    }
+    return launch_status();
+}
+
+extern "C" int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const float* bias,
+                        const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
+                        tcq_stream_t stream) {
+    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < N || (q4 && ldq < M))
+        return TCQ_ERR_ARG;
+    if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
+    if (N % 4 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const dim3 grid(M), block(row_threads(M, N));
+    const size_t sh = row_lds(N);
+    const int asz = dsize(acc_dtype);
+    const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && (!rs || al16(rs));
+    hipStream_t st = (hipStream_t)stream;
+    const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
+    switch (acc_dtype) {
+        case TCQ_I32: launch_k(k_mid1<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_F32: launch_k(k_mid1<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_BF16: launch_k(k_mid1<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        default: return TCQ_ERR_DTYPE;
+    }
+    return launch_status();
+}
+
+extern "C" int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
+                        tcq_stream_t stream) {
+    if (!g || !u || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
+    if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    launch_k(k_pre2, dim3(M), dim3(row_threads(M, K)), row_lds(K), (hipStream_t)stream, (const u16*)g, (const u16*)u, (const i8*)su,
+             (i8*)q, (int*)q4, ldq, scale, K);
     return launch_status();
 }

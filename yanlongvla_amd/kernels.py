@@ -101,6 +101,39 @@ def post(acc, s, rs, sv, bias, y, col0=0):
          _dt(y, (0, 1, 2), 'post y'), M, N, stream())
 
 
+# ----------------------------------------------------------------------------------------------------------- MLP middles
+def _ldq(q4):
+    return 0 if q4 is None else q4.shape[1]
+
+
+def mid2(acc, s, rs, sv, su, q=None, q4=None, scale=None, gelu_lut=None):
+    """Gated-MLP middle: acc (M, lda >= 2N) gate | up (int32 scaled by s, rs; FP32 already scaled; BF16 scaled by rs); rs, sv
+    concatenated (2N); su = input signs of the down projection (N) -> q / q4, scale (reference kernels.py:640-643)."""
+    M, N = acc.shape[0], su.numel()
+    _contig(acc, s, rs, sv, su, q, q4, scale)
+    lut = gelu_table(acc.device) if gelu_lut is None else gelu_lut
+    call('tcq_mid2', ptr(acc), _dt(acc, (0, 1, 3), 'mid2 acc'), acc.shape[1], ptr(s), ptr(rs), ptr(sv), ptr(lut), ptr(su), ptr(q),
+         ptr(q4), _ldq(q4), ptr(scale), M, N, stream())
+
+
+def mid1(acc, s, rs, sv, bias, su, q=None, q4=None, scale=None, gelu_lut=None):
+    """Plain-MLP middle: acc (M, N) of the first layer; su = input signs of the second layer (reference kernels.py:646-650)."""
+    M, N = acc.shape[0], su.numel()
+    _contig(acc, s, rs, sv, bias, su, q, q4, scale)
+    lut = gelu_table(acc.device) if gelu_lut is None else gelu_lut
+    call('tcq_mid1', ptr(acc), _dt(acc, (0, 1, 3), 'mid1 acc'), acc.shape[1], ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(lut),
+         ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, N, stream())
+
+
+def pre2(g, u, su, q=None, q4=None, scale=None):
+    """x = BF16(g * u) * su -> block Walsh -> per-token INT8; g, u (M, K) BF16 (reference kernels.py:631-633)."""
+    M, K = g.shape
+    if g.dtype != torch.bfloat16 or u.dtype != torch.bfloat16:
+        raise TypeError('pre2: g and u must be bfloat16')
+    _contig(g, u, su, q, q4, scale)
+    call('tcq_pre2', ptr(g), ptr(u), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, K, stream())
+
+
 # -------------------------------------------------------------------------------------------------------------- products
 def gemv_descriptors(layers):
     """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers each). Keep the tensors alive."""
