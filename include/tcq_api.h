@@ -100,6 +100,9 @@ int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q, float* sca
 int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
              const float* bias, void* y, int y_dtype, int M, int N, tcq_stream_t stream);
 
+/* Most segments (layers) a by-value descriptor pack holds: tcq_post_group, tcq_gemm_tcq, tcq_gemm_w8. */
+#define TCQ_MAX_SEGS 4
+
 /* One segment of a batched epilogue: columns col0 .. col0 + N of M accumulator rows (stride lda elements) -> y (M, N). */
 typedef struct tcq_post_seg {
     const void* acc;     /* accumulator base */
@@ -119,6 +122,14 @@ typedef struct tcq_post_seg {
  * hold at most three segments sharing one accumulator row; here the count is free and each segment may have its own base. */
 int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype, int M,
               int maxN, tcq_stream_t stream);
+
+/* The epilogue of one layer group (q / k / v, gate / up: at most TCQ_MAX_SEGS layers), as tcq_postg, with segs a HOST array
+ * copied into the launch: no device descriptor array, so every call may name new output buffers, also under HIP-graph
+ * capture. A segment with gelu set needs gelu_lut and a BF16 output.
+ * Replaces kernels.post3 / kernels.postg as Group.posts calls them (deploy/tcq_kernels/kernels.py:232-261, 618-628;
+ * modules.py:95-106). */
+int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype,
+                   int M, tcq_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------------------- MLP middles */
 
@@ -162,7 +173,6 @@ int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, con
 
 /* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
  * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
-#define TCQ_MAX_SEGS 4
 typedef struct tcq_gemm_seg {
     const void* w;       /* tcq_gemm_tcq: tcq_repack words of an (m, K) layer; tcq_gemm_w8: (m, K) int8 row-major weights */
     const int8_t* t8;    /* (512, 2) INT8 table (tcq_gemm_tcq only) */

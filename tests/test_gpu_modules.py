@@ -1,0 +1,225 @@
+"""GPU tests of the module layer: Layer / load, RefLinear and the grouped KLinear / KGatedMLP path against the oracle,
+the operating points against each other, install on a Gemma-shaped expert, and HIP-graph replays of an action chunk."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tcq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+@pytest.fixture(scope='module', autouse=True)
+def _lib():
+    from yanlongvla_amd import _lib
+    _lib.lib()
+    torch.cuda.init()
+
+
+def oracle_of(L):
+    """The oracle twin of a device Layer (same packed tensors)."""
+    t = dict(bits=L.bits.cpu().numpy(), tlut=L.tlut.cpu().numpy(), row_scale=L.row_scale.cpu().numpy(),
+             su=L.su.cpu().numpy(), sv=L.sv.cpu().numpy())
+    return O.Layer(L.name, t, bias=None if L.bias is None else L.bias.cpu().numpy())
+
+
+def device_layer(m, n, seed, bias=False, name='layer'):
+    from yanlongvla_amd import tcq_format as F
+    ol = O.random_layer(m, n, seed, name=name, bias=bias, per_layer_scale=False)
+    t = dict(bits=torch.from_numpy(ol.bits), tlut=torch.from_numpy(ol.tlut), row_scale=torch.from_numpy(ol.row_scale),
+             su=torch.from_numpy(ol.su), sv=torch.from_numpy(ol.sv))
+    return F.Layer(name, t, bias=None if ol.bias is None else torch.from_numpy(ol.bias), device=DEV), ol
+
+
+def bits16(y):
+    return y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_layer_derived_tensors_and_dense():
+    L, ol = device_layer(256, 1024, 3)
+    assert np.array_equal(L.t8.cpu().numpy(), ol.t8)
+    assert np.array_equal(L.rs.cpu().numpy().view(np.uint32), ol.rs.view(np.uint32))
+    assert np.array_equal(L.w8_reference().cpu().numpy(), ol.w8_reference())
+    for table in ('fp16', 'int8'):
+        assert np.array_equal(L.dense(table).cpu().numpy(), ol.dense(table))
+
+
+@pytest.mark.parametrize('M', [1, 50, 130])
+@pytest.mark.parametrize('bias', [False, True])
+def test_reflinear_bitexact(M, bias):
+    from yanlongvla_amd.modules import RefLinear
+    L, ol = device_layer(512, 1024, 10 + M, bias=bias)
+    x = torch.randn(M, 1024, device=DEV).bfloat16()
+    ref = O.reference_linear(x.float().cpu().numpy(), ol)
+    for resident in (True, False):
+        y = RefLinear(L, resident=resident)(x)
+        assert y.dtype == torch.bfloat16 and np.array_equal(bits16(y), ref)
+
+
+@pytest.mark.parametrize('table', ['int8', 'fp16'])
+def test_reflinear_float_activations(table):
+    from yanlongvla_amd.modules import RefLinear
+    L, ol = device_layer(256, 512, 21)
+    x = torch.randn(7, 512, device=DEV)
+    ref = O.reference_linear(x.cpu().numpy(), ol, a8=False, table=table, out_dtype='f32')
+    y = RefLinear(L, a8=False, table=table)(x).float().cpu().numpy()
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 4e-3            # BF16 output of an FP32 result
+
+
+def qkv_layers(seed, K=1024, widths=(2048, 256, 256), bias=False):
+    from yanlongvla_amd import tcq_format as F
+    layers, oracles = [], []
+    su = None
+    for i, m in enumerate(widths):
+        L, ol = device_layer(m, K, seed + i, bias=bias, name=f'p.layers.0.self_attn.{("q", "k", "v")[i]}_proj')
+        if su is None:
+            su = L.su
+        L.su = su
+        ol.su = su.cpu().numpy()
+        layers.append(L)
+        oracles.append(ol)
+    return layers, oracles
+
+
+@pytest.mark.parametrize('M', [1, 50, 64, 65, 300])
+@pytest.mark.parametrize('mode', ['fly', 'resident', 'chunk'])
+def test_group_bitexact(M, mode):
+    """q / k / v group: one rotation + quantization, one product (small-M kernels up to 64 tokens, INT8 MFMA GEMM above),
+    one batched epilogue; every member's BF16 output equals the oracle's layer bit for bit."""
+    from yanlongvla_amd.modules import Group, KLinear
+    layers, oracles = qkv_layers(100 + M, bias=M == 50)
+    g = Group(layers, 'expert' if M <= 64 else 'llm', mode)
+    mods = [KLinear(g, i) for i in range(3)]
+    x = torch.randn(M, 1024, device=DEV).bfloat16()
+    xs = x.float().cpu().numpy()
+    for mod, ol in zip(mods, oracles):
+        y = mod(x)
+        assert np.array_equal(bits16(y), O.reference_linear(xs, ol))
+    assert g.x is None                                              # all three members served
+
+
+@pytest.mark.parametrize('M', [10, 50, 200])
+@pytest.mark.parametrize('split', [False, True])
+def test_gated_mlp_bitexact(M, split):
+    """KGatedMLP (fused middle) == the unfused chain: gate / up layers, BF16 GELU(gate) * up in PyTorch, down layer."""
+    from yanlongvla_amd import modules
+    from yanlongvla_amd.modules import Group, KGatedMLP
+    gate, og = device_layer(4096, 1024, 7, name='p.mlp.gate_proj')
+    up, ou = device_layer(4096, 1024, 8, name='p.mlp.up_proj')
+    up.su = gate.su
+    ou.su = og.su
+    down, od = device_layer(1024, 4096, 9, name='p.mlp.down_proj')
+    old = modules.FUSE['split']
+    modules.FUSE['split'] = split
+    try:
+        mlp = KGatedMLP(Group([gate, up], 'expert', 'fly'), Group([down], 'expert', 'fly'))
+        x = torch.randn(M, 1024, device=DEV).bfloat16()
+        y = mlp(x)
+    finally:
+        modules.FUSE['split'] = old
+    xs = x.float().cpu().numpy()
+    gb = O.reference_linear(xs, og)
+    ub = O.reference_linear(xs, ou)
+    prod = O.bf16_bits(O.bf16_to_f32(O.gelu_tanh_bf16(gb)) * O.bf16_to_f32(ub))
+    ref = O.reference_linear(O.bf16_to_f32(prod), od)
+    assert np.array_equal(bits16(y), ref)
+
+
+def small_expert(layers=2, prefix=64, seed=0):
+    from yanlongvla_amd import gemma
+    model = gemma.make_policy(gemma.ExpertPolicy, DEV, seed=seed, layers=layers)
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
+    ks = [torch.randn(prefix, 256, generator=g, device=DEV).bfloat16() for _ in range(layers)]
+    vs = [torch.randn(prefix, 256, generator=g, device=DEV).bfloat16() for _ in range(layers)]
+    model.set_prefix(ks, vs)
+    return model
+
+
+def test_install_operating_points_agree():
+    """The fused groups (fly / resident / hybrid) give the same action chunk as RefLinear layer by layer, bit for bit."""
+    from yanlongvla_amd import gemma, modules
+    outs, infos = {}, {}
+    noise = torch.randn(50, 32, generator=torch.Generator(device=DEV).manual_seed(5), device=DEV)
+    for runtime in ('reference', 'fly', 'resident', 'hybrid'):
+        model = small_expert()
+        layers = gemma.synthetic_layers(model, 11, DEV)
+        infos[runtime] = modules.install(model, runtime=runtime, layers=layers)
+        if runtime == 'hybrid':
+            assert modules.decode_chunk(model) == 14
+        outs[runtime] = model.sample_chunk(noise, steps=3)
+    assert infos['fly']['groups'] == 2 * 4 and infos['fly']['fused_mlps'] == 2
+    assert infos['hybrid']['modes'] == {'resident': 0, 'fly': 0, 'chunk': 8}
+    for r in ('fly', 'resident', 'hybrid'):
+        assert torch.equal(outs[r], outs['reference']), r
+    assert torch.isfinite(outs['fly']).all()
+
+
+def test_load_from_packed_file(tmp_path):
+    from yanlongvla_amd import gemma, modules
+    from yanlongvla_amd import tcq_format as F
+    model = small_expert(layers=1)
+    layers = gemma.synthetic_layers(model, 3, DEV)
+    p = F.save({n: dict(bits=L.bits, tlut=L.tlut, row_scale=L.row_scale, su=L.su, sv=L.sv) for n, L in layers.items()},
+               tmp_path / 'packed.safetensors')
+    info = modules.install(model, row=p, runtime='fly')
+    assert info['layers'] == 7 and info['fused_mlps'] == 1
+    x = torch.randn(50, 32, device=DEV)
+    twin = small_expert(layers=1)
+    modules.install(twin, runtime='fly', layers=layers)
+    assert torch.equal(model.velocity(x), twin.velocity(x))
+
+
+def test_chunk_graph_replays_match_eager():
+    """A captured action chunk (fused groups, small-M kernels, by-value descriptors) replays to the eager result, several
+    times, with eager work in between."""
+    from yanlongvla_amd import gemma, modules
+    model = small_expert()
+    modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 2, DEV))
+    noise = torch.randn(50, 32, device=DEV)
+    eager = model.sample_chunk(noise, steps=2)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        model.sample_chunk(noise, steps=2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = model.sample_chunk(noise, steps=2)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(model.sample_chunk(noise, steps=2), eager)
+
+
+def test_chunk_close_to_cpu_oracle():
+    """One flow step of a 2-layer expert against the same model on the CPU with every quantized Linear computed by the
+    oracle's reference_linear: the quantized layers are bit-exact on equal inputs, the PyTorch ops between them (norms,
+    attention) round differently on CPU and GPU, so the velocity is compared in relative L2."""
+    from yanlongvla_amd import gemma, modules
+    model = small_expert()
+    layers = gemma.synthetic_layers(model, 4, DEV)
+    oracles = {n: oracle_of(L) for n, L in layers.items()}
+    cpu = gemma.ExpertPolicy(layers=2).bfloat16().requires_grad_(False)
+    cpu.load_state_dict({k: v.cpu() for k, v in model.state_dict().items()}, strict=False)
+    cpu.set_prefix([k.cpu() for k in model.prefix_k], [v.cpu() for v in model.prefix_v])
+
+    class OracleLinear(torch.nn.Module):
+        def __init__(self, ol):
+            super().__init__()
+            self.ol, self.w8 = ol, ol.w8_reference()
+
+        def forward(self, x):
+            y = O.reference_linear(x.float().reshape(-1, self.ol.n).numpy(), self.ol, w8=self.w8)
+            return torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).reshape(*x.shape[:-1], self.ol.m)
+
+    for n, ol in oracles.items():
+        modules.set_submodule(cpu, n, OracleLinear(ol))
+    modules.install(model, runtime='fly', layers=layers)
+    x = torch.randn(50, 32)
+    v_gpu = model.velocity(x.to(DEV)).float().cpu()
+    v_cpu = cpu.velocity(x).float()
+    assert (v_gpu - v_cpu).norm() / v_cpu.norm() < 2e-2

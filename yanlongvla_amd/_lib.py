@@ -32,6 +32,7 @@ SIGNATURES = {
     'tcq_pre_h16': [_P, _I, _P, _P, _P, _I, _I, _P],
     'tcq_quantize_rows': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_mid1': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_pre2': [_P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
@@ -44,6 +45,13 @@ SIGNATURES = {
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L}
 
 MAX_SEGS = 4
+
+
+class PostSeg(ctypes.Structure):
+    """tcq_post_seg (include/tcq_api.h)."""
+    _fields_ = [('acc', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('sv', ctypes.c_void_p), ('bias', ctypes.c_void_p),
+                ('y', ctypes.c_void_p), ('lda', ctypes.c_int), ('col0', ctypes.c_int), ('N', ctypes.c_int),
+                ('gelu', ctypes.c_int)]
 
 
 class GemmSeg(ctypes.Structure):

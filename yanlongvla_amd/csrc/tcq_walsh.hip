@@ -250,10 +250,16 @@ __global__ void k_post(const void* acc, int lda, int col0, const float* s, const
 }
 
 // Batched epilogue: workgroup (token, segment). Segments with N outside (0, maxN], or without the row scale their
-// accumulator type needs, are skipped (the host wrapper rejects them before they get here).
+// accumulator type needs, are skipped (the host wrappers reject them before they get here). SEGS is a device array of
+// descriptors (tcq_postg) or a by-value pack of at most TCQ_MAX_SEGS (tcq_post_group), indexed the same way.
 // Vectors are used for a segment when its N is a multiple of 8 and its pointers and strides are 16-byte aligned.
-template <int ADT, int YDT>
-__global__ void k_postg(const tcq_post_seg* segs, const float* s, const u16* gelu_lut, int maxN) {
+struct PostPack {
+    tcq_post_seg s[TCQ_MAX_SEGS];
+    __device__ __forceinline__ const tcq_post_seg& operator[](int i) const { return s[i]; }
+};
+
+template <int ADT, int YDT, class SEGS>
+__global__ void k_postg(SEGS segs, const float* s, const u16* gelu_lut, int maxN) {
     extern __shared__ float lds[];
     const tcq_post_seg S = segs[blockIdx.y];
     const int tok = blockIdx.x, N = S.N;
@@ -455,7 +461,7 @@ extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, cons
     const dim3 grid(M, nseg), block(row_threads(M * nseg, maxN));
     const size_t sh = row_lds(maxN);
     hipStream_t st = (hipStream_t)stream;
-#define POSTG_Y(AD, YD) launch_k(k_postg<AD, YD>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN)
+#define POSTG_Y(AD, YD) launch_k(k_postg<AD, YD, const tcq_post_seg*>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN)
 #define POSTG_A(AD)                                          \
     switch (y_dtype) {                                       \
         case TCQ_F32: POSTG_Y(AD, TCQ_F32); break;           \
@@ -523,5 +529,42 @@ extern "C" int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* 
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     launch_k(k_pre2, dim3(M), dim3(row_threads(M, K)), row_lds(K), (hipStream_t)stream, (const u16*)g, (const u16*)u, (const i8*)su,
              (i8*)q, (int*)q4, ldq, scale, K);
+    return launch_status();
+}
+
+extern "C" int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype,
+                              int M, tcq_stream_t stream) {
+    if (!segs || nseg <= 0 || M <= 0) return TCQ_ERR_ARG;
+    if (nseg > TCQ_MAX_SEGS) return TCQ_ERR_UNSUPPORTED;
+    if (acc_dtype == TCQ_I32 && !s) return TCQ_ERR_ARG;
+    PostPack pk;
+    int maxN = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const tcq_post_seg& g = segs[i];
+        if (!g.acc || !g.sv || !g.y || g.N <= 0 || g.col0 < 0 || g.lda < g.col0 + g.N) return TCQ_ERR_ARG;
+        if (acc_dtype != TCQ_F32 && !g.rs) return TCQ_ERR_ARG;
+        if (g.gelu && (!gelu_lut || y_dtype != TCQ_BF16)) return TCQ_ERR_ARG;
+        pk.s[i] = g;
+        maxN = g.N > maxN ? g.N : maxN;
+    }
+    for (int i = nseg; i < TCQ_MAX_SEGS; ++i) pk.s[i] = tcq_post_seg{};
+    if (maxN > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const dim3 grid(M, nseg), block(row_threads(M * nseg, maxN));
+    const size_t sh = row_lds(maxN);
+    hipStream_t st = (hipStream_t)stream;
+#define POSTV_Y(AD, YD) launch_k(k_postg<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN)
+#define POSTV_A(AD)                                          \
+    switch (y_dtype) {                                       \
+        case TCQ_F32: POSTV_Y(AD, TCQ_F32); break;           \
+        case TCQ_BF16: POSTV_Y(AD, TCQ_BF16); break;         \
+        case TCQ_F16: POSTV_Y(AD, TCQ_F16); break;           \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+    switch (acc_dtype) {
+        case TCQ_I32: POSTV_A(TCQ_I32); break;
+        case TCQ_F32: POSTV_A(TCQ_F32); break;
+        case TCQ_BF16: POSTV_A(TCQ_BF16); break;
+        default: return TCQ_ERR_DTYPE;
+    }
     return launch_status();
 }

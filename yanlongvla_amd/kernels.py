@@ -189,6 +189,27 @@ def postg(desc, nseg, acc_dtype, y_dtype, s, M, maxN, gelu_lut=None):
     call('tcq_postg', ptr(desc), nseg, DTYPE[acc_dtype], ptr(s), ptr(gelu_lut), DTYPE[y_dtype], M, maxN, stream())
 
 
+def post_group(segs, acc_dtype, y_dtype, s, M, gelu_lut=None):
+    """Epilogue of one layer group, at most MAX_SEGS segments [(acc, col0, rs, sv, bias, y, gelu), ...] as in post_segments,
+    passed by value in the launch (reference kernels.post3 / postg as Group.posts calls them, kernels.py:618-628): every call
+    may name new outputs, also under graph capture."""
+    n = len(segs)
+    if not 0 < n <= _lib.MAX_SEGS:
+        raise ValueError(f'post_group takes 1..{_lib.MAX_SEGS} segments, got {n}')
+    arr = (_lib.PostSeg * n)()
+    for i, (acc, col0, rs, sv, bias, y, gelu) in enumerate(segs):
+        _contig(acc, rs, sv, bias, y)
+        N = y.shape[1]
+        if col0 < 0 or col0 + N > acc.shape[1] or sv.numel() != N or (rs is not None and rs.numel() != N):
+            raise ValueError(f'segment {i}: columns {col0}..{col0 + N} do not fit the accumulator / scales')
+        if rs is None and acc.dtype != torch.float32:
+            raise ValueError(f'segment {i}: an {acc.dtype} accumulator needs its row scale')
+        if y.dtype != y_dtype or acc.dtype != acc_dtype:
+            raise TypeError(f'segment {i}: dtypes differ from the group\'s')
+        arr[i] = _lib.PostSeg(ptr(acc), ptr(rs), ptr(sv), ptr(bias), ptr(y), acc.shape[1], col0, N, int(bool(gelu)))
+    call('tcq_post_group', arr, n, DTYPE[acc_dtype], ptr(s), ptr(gelu_lut), DTYPE[y_dtype], M, stream())
+
+
 _GELU = {}
 
 

@@ -1,0 +1,128 @@
+"""The packed TCQ deployment format on the device: one quantized Linear per `Layer`, files in `packed.safetensors`.
+
+Mirrors deploy/tcq_kernels/tcq_format.py (Layer 80-107, load 230-237, the file schema 1-13) with the derived tensors made by
+the HIP library instead of PyTorch ops:
+
+packed.safetensors: per quantized Linear `name`
+  <name>::bits       int16 view of the uint16 words (m/16 * n/16, 32): 512 bits per 16 x 16 tile
+  <name>::tlut       FP16 (512, 2) table
+  <name>::row_scale  FP16 (m,)
+  <name>::su, ::sv   int8 (n,), (m,) input / output signs of the two-sided block-Walsh rotation
+Derived at load (tcq_snap on the device): t8 = clamp(round(tlut * g)), g = float(1 / max|tlut|) * 127; rs = row_scale / g.
+Derived on demand: the repacked words of the fused products (tcq_repack), the INT8 weight (tcq_decode_i8).
+"""
+import os
+from pathlib import Path
+
+import torch
+
+from . import kernels as K
+
+ROOT = Path(os.environ.get('VLA_ROOT', '/projects/yanlongvla'))        # project root holding models/pi05_tcq/<row>/
+ROW = 'tcq_raqft_d1'
+TENSORS = ('bits', 'tlut', 'row_scale', 'su', 'sv')
+
+
+def block_widths(width):
+    """Descending power-of-two Walsh blocks of a width (tcq_format.py:26-30): 4304 -> [4096, 128, 64, 16]."""
+    out = []
+    while width:
+        b = 1 << (width.bit_length() - 1)
+        out.append(b)
+        width -= b
+    return out
+
+
+class Layer:
+    """One quantized Linear on a device: the packed tensors, the INT8 table / FP32 row scale derived at load, and the
+    device word layout of the fused products (made on first use). Same constructor as tcq_format.Layer (tcq_format.py:80-92)."""
+
+    def __init__(self, name, tensors, bias=None, device='cuda'):
+        self.name = name
+        self.bits = tensors['bits'].to(device).view(torch.int16).contiguous()
+        self.tlut = tensors['tlut'].to(device).to(torch.float16).contiguous()
+        self.row_scale = tensors['row_scale'].to(device).to(torch.float16).contiguous()
+        self.su = tensors['su'].to(device).to(torch.int8).contiguous()
+        self.sv = tensors['sv'].to(device).to(torch.int8).contiguous()
+        self.m, self.n = self.sv.numel(), self.su.numel()
+        if not (self.bits.shape == ((self.m // 16) * (self.n // 16), 32) and self.m % 16 == 0 and self.n % 16 == 0):
+            raise ValueError(f'{name}: bits {tuple(self.bits.shape)} do not fit a ({self.m}, {self.n}) layer of 16 x 16 tiles')
+        if self.tlut.shape != (512, 2):
+            raise ValueError(f'{name}: table shape {tuple(self.tlut.shape)} != (512, 2)')
+        self.t8, self.rs, self.gain = K.snap(self.tlut, self.row_scale)
+        self.bias = None if bias is None else bias.float().to(device).contiguous()
+        self._words = None
+        self.bits_resident = True
+
+    def words(self):
+        """The tcq_repack layout of the words (cached)."""
+        if self._words is None:
+            if self.bits is None:
+                raise RuntimeError(f'{self.name}: the bitstream was released at load (resident operating point)')
+            self._words = K.repack(self.bits, self.m, self.n)
+        return self._words
+
+    def w8_reference(self, out=None):
+        """INT8 weight (m, n) in the rotated basis: sign * t8[hash(state)] (tcq_format.py:97-98), decoded on the device."""
+        out = torch.empty(self.m, self.n, dtype=torch.int8, device=self.bits.device) if out is None else out
+        K.decode(self.bits, self.t8, out)
+        return out
+
+    def decode_f16(self, out=None):
+        """FP16-table weight (m, n) in the rotated basis, before the row scale: sign * tlut[hash(state)]."""
+        out = torch.empty(self.m, self.n, dtype=torch.float16, device=self.bits.device) if out is None else out
+        K.decode_f16(self.bits, self.tlut, out)
+        return out
+
+    def dense(self, table='fp16'):
+        """Original-basis FP32 weight S_v H_m diag(r) Q H_n S_u (tcq_format.py:100-107), rotations by tcq_rht."""
+        if table == 'fp16':
+            q = self.decode_f16().float() * self.row_scale.float()[:, None]
+        else:
+            q = self.w8_reference().float() * self.rs[:, None]
+        w = torch.empty_like(q)
+        K.rht(q, None, w)
+        w = (w * self.su.float()[None, :]).t().contiguous()
+        wt = torch.empty_like(w)
+        K.rht(w, None, wt)
+        return (wt * self.sv.float()[None, :]).t().contiguous()
+
+
+def packed_path(row=ROW):
+    """A row name -> ROOT/models/pi05_tcq/<row>/packed.safetensors (tcq_format.py:191-192); a path is taken as is."""
+    p = Path(row)
+    if p.suffix == '.safetensors' or p.exists():
+        return p
+    return ROOT / f'models/pi05_tcq/{row}/packed.safetensors'
+
+
+def layer_names(row=ROW):
+    """Names of the layers stored in a packed file (one per ::bits entry)."""
+    from safetensors import safe_open
+    with safe_open(str(packed_path(row)), framework='pt', device='cpu') as f:
+        return [k[:-len('::bits')] for k in f.keys() if k.endswith('::bits')]
+
+
+def load(row=ROW, device='cuda', names=None, biases=None):
+    """{name: Layer} from a packed file (tcq_format.py:230-237)."""
+    from safetensors import safe_open
+    out = {}
+    with safe_open(str(packed_path(row)), framework='pt', device='cpu') as f:
+        for name in (names or [k[:-len('::bits')] for k in f.keys() if k.endswith('::bits')]):
+            out[name] = Layer(name, {k: f.get_tensor(f'{name}::{k}') for k in TENSORS}, bias=(biases or {}).get(name),
+                              device=device)
+    return out
+
+
+def save(tensors, path):
+    """Write {name: {bits, tlut, row_scale, su, sv}} (CPU or device tensors) as a packed file."""
+    from safetensors.torch import save_file
+    flat = {}
+    for name, t in tensors.items():
+        for k in TENSORS:
+            v = t[k].detach().cpu().clone()                  # members of a group may share one sign tensor
+            flat[f'{name}::{k}'] = (v.view(torch.int16) if k == 'bits' else v).contiguous()
+    path = Path(path)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    save_file(flat, str(path))
+    return path
