@@ -38,6 +38,8 @@ def parse():
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu', action='store_true')
     p.add_argument('--seed', type=int, default=0)
+    p.add_argument('--chunk-replays', type=int, default=100)
+    p.add_argument('--no-chunk', action='store_true', help='skip the action-expert chunk measurement')
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
                         'FETCH_SIZE / WRITE_SIZE counters into bytes)')
@@ -213,6 +215,107 @@ def cpu_baseline(L, x, seconds):
                        f'(reference_linear, FP16 table, a8=False), {el:.1f} s; host affinity {len(os.sched_getaffinity(0))} cores')
 
 
+# ------------------------------------------------------------------------------------------------ action-expert chunk
+CHUNK_TOKENS, CHUNK_STEPS, PREFIX = 50, 10, 800
+EXPERT_PACKED_BYTES = 311_427_072 * 2 // 8      # 2-bit payload of the expert's 126 layers, per flow step
+
+
+def expert_setup(seed, dev):
+    """Prefix KV cache (800 rows of keys / values per layer, N(0,1) BF16) and the chunk's noise, seeded."""
+    import torch
+    from yanlongvla_amd import gemma
+    g = torch.Generator(device=dev).manual_seed(seed + 3)
+    nl = gemma.EXPERT['layers']
+    ks = [torch.randn(PREFIX, 256, generator=g, device=dev).bfloat16() for _ in range(nl)]
+    vs = [torch.randn(PREFIX, 256, generator=g, device=dev).bfloat16() for _ in range(nl)]
+    noise = torch.randn(CHUNK_TOKENS, gemma.EXPERT['action_dim'], generator=g, device=dev)
+    return ks, vs, noise
+
+
+def expert_policy(runtime, seed, dev, ks, vs):
+    from yanlongvla_amd import gemma, modules
+    model = gemma.make_policy(gemma.ExpertPolicy, dev, seed=seed)
+    model.set_prefix(ks, vs)
+    layers = gemma.synthetic_layers(model, seed + 7, dev)        # the same weights for every runtime
+    modules.install(model, runtime=runtime, layers=layers)
+    return model, layers
+
+
+def action_chunk(args, dev):
+    """ms per action chunk of the 2-bit pi0.5-shaped expert: 18 layers, 50 action tokens against an 800-row prefix KV cache,
+    10 Euler steps, captured as one HIP graph per operating point; the fused runtimes are checked bit-exact against the
+    layer-by-layer reference runtime on the same chunk."""
+    import torch
+    from yanlongvla_amd import modules
+    ks, vs, noise = expert_setup(args.seed, dev)
+    out, res, keep = {}, {}, {}
+    with torch.inference_mode():
+        for runtime in ('reference', 'fly', 'resident', 'hybrid'):
+            model, layers = expert_policy(runtime, args.seed, dev, ks, vs)
+
+            def chunk(model=model, runtime=runtime):
+                if runtime == 'hybrid':
+                    modules.decode_chunk(model)
+                return model.sample_chunk(noise, CHUNK_STEPS)
+            out[runtime] = chunk().clone()
+            if runtime != 'reference':
+                med, p95 = graph_latency(chunk, replays=args.chunk_replays, warmup=10)
+                res[runtime] = {'median': round(med, 4), 'p95': round(p95, 4)}
+            if runtime == 'fly':
+                keep = dict(model=model, layers=layers)
+            else:
+                del model, layers
+            torch.cuda.synchronize()
+    exact = {r: bool(torch.equal(out[r], out['reference'])) for r in ('fly', 'resident', 'hybrid')}
+    fly = res['fly']['median']
+    return dict(workload=f'pi0.5-shaped action expert, 18 layers x (q 2048x1024, k/v 256x1024, o 1024x2048, gate/up '
+                         f'4096x1024, down 1024x4096) 2-bit TCQ, {CHUNK_TOKENS} action tokens, {PREFIX}-row prefix KV, '
+                         f'{CHUNK_STEPS} Euler steps, one HIP graph per chunk',
+                ms_per_chunk=fly, ms_per_chunk_p95=res['fly']['p95'], runtime='fly (2-bit stream decoded on every call)',
+                operating_points_ms=res, bitexact_vs_reference_runtime=exact,
+                packed_bytes_per_chunk=EXPERT_PACKED_BYTES * CHUNK_STEPS,
+                effective_packed_GBs=round(EXPERT_PACKED_BYTES * CHUNK_STEPS / (fly * 1e-3) / 1e9, 2)), keep, (ks, vs, noise)
+
+
+def chunk_cpu_baseline(keep, setup, seconds):
+    """One flow step of the same expert on the host: every quantized Linear through the oracle's reference_linear with its
+    INT8 weight decoded once beforehand (as RefLinear(resident=True)); norms, attention and residuals by PyTorch on the
+    CPU. ms per chunk = 10 x the step."""
+    import numpy as np
+    import torch
+    from oracle import tcq_oracle as O
+    from yanlongvla_amd import gemma, modules
+    model, layers = keep['model'], keep['layers']
+    ks, vs, noise = setup
+
+    class OracleLinear(torch.nn.Module):
+        def __init__(self, L):
+            super().__init__()
+            self.ol = O.Layer(L.name, dict(bits=L.bits.cpu().numpy(), tlut=L.tlut.cpu().numpy(),
+                                           row_scale=L.row_scale.cpu().numpy(), su=L.su.cpu().numpy(), sv=L.sv.cpu().numpy()))
+            self.w8 = L.w8_reference().cpu().numpy()             # decoded once (setup, untimed)
+
+        def forward(self, x):
+            y = O.reference_linear(x.float().reshape(-1, self.ol.n).numpy(), self.ol, w8=self.w8)
+            return torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).reshape(*x.shape[:-1], self.ol.m)
+
+    cpu = gemma.ExpertPolicy().bfloat16().requires_grad_(False)
+    state = {k: v.cpu() for k, v in model.state_dict().items()}
+    cpu.load_state_dict(state, strict=False)
+    cpu.set_prefix([k.cpu() for k in ks], [v.cpu() for v in vs])
+    for n, L in layers.items():
+        modules.set_submodule(cpu, n, OracleLinear(L))
+    x = noise.cpu()
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        cpu.velocity(x)
+        el = time.perf_counter() - t0
+    return dict(value=round(el * CHUNK_STEPS * 1e3, 1), unit='ms per chunk', cores=torch.get_num_threads(), kind='port',
+                sample=f'one of the chunk\'s {CHUNK_STEPS} flow steps ({el:.1f} s), times {CHUNK_STEPS}: 126 layers through the '
+                       f'numpy oracle (reference_linear, INT8 weights decoded once), PyTorch CPU for norms and attention; '
+                       f'host affinity {len(os.sched_getaffinity(0))} cores')
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -248,6 +351,13 @@ def main():
     lat_med, lat_p95 = graph_latency(S1.step)
     am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
+    chunk = None
+    if not args.no_chunk:
+        del S1, L1
+        chunk, keep, setup = action_chunk(args, dev)
+        if not all(chunk['bitexact_vs_reference_runtime'].values()):
+            raise SystemExit(f'action chunk differs from the reference runtime: {chunk["bitexact_vs_reference_runtime"]}')
+        chunk['cpu_baseline'] = None if args.no_cpu else chunk_cpu_baseline(keep, setup, args.cpu_seconds)
     out = {
         'metric': 'TCQ-2bit decode-GEMV GB/s (% HBM peak) + ms per action chunk, 1 GPU',
         'value': round(byts / (ms_step * 1e-3) / 1e9, 2),
@@ -269,6 +379,7 @@ def main():
                             'per_step_in_100_step_graph_p95': round(am_p95, 5)},
         'max_rel_l2_vs_oracle': err,
         'cpu_baseline': cpu,
+        'action_chunk': chunk,
     }
     print(json.dumps(out), flush=True)
 
