@@ -40,6 +40,9 @@ def parse():
     p.add_argument('--seed', type=int, default=0)
     p.add_argument('--chunk-replays', type=int, default=100)
     p.add_argument('--no-chunk', action='store_true', help='skip the action-expert chunk measurement')
+    p.add_argument('--no-ops', action='store_true', help='skip the RHT and W8A8 GEMM measurements')
+    p.add_argument('--no-backbone', action='store_true', help='skip the Gemma-2B-shaped backbone measurement')
+    p.add_argument('--backbone-replays', type=int, default=10)
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
                         'FETCH_SIZE / WRITE_SIZE counters into bytes)')
@@ -215,6 +218,76 @@ def cpu_baseline(L, x, seconds):
                        f'(reference_linear, FP16 table, a8=False), {el:.1f} s; host affinity {len(os.sched_getaffinity(0))} cores')
 
 
+# ------------------------------------------------------------------------------------------------ RHT and W8A8 GEMM
+MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense INT8 MFMA, published peak
+
+
+def graph_per_call(fn, calls=20, replays=20):
+    """Device ms per call of fn: a HIP graph of `calls` back-to-back calls, replayed, median replay / calls."""
+    med, _ = graph_latency(fn, replays=replays, warmup=3, per_graph=calls)
+    return med
+
+
+def rht_figures(dev, seed):
+    """Randomized block-Walsh transform of BF16 rows [M, n] (tcq_rht, BF16 in and out), per call; bytes = 4 M n + n."""
+    import torch
+    from yanlongvla_amd import kernels as K
+    g = torch.Generator(device=dev).manual_seed(seed + 5)
+    out = {}
+    for n in (1024, 2048, 4096, 16384):
+        su = (torch.randint(0, 2, (n,), generator=g, device=dev) * 2 - 1).to(torch.int8)
+        for M in (1, 16, 50, 800):
+            x = torch.randn(M, n, generator=g, device=dev).bfloat16()
+            y = torch.empty_like(x)
+            ms = graph_per_call(lambda: K.rht(x, su, y))
+            byts = 4 * M * n + n
+            out[f'{M}x{n}'] = {'us': round(ms * 1e3, 2), 'GBs': round(byts / (ms * 1e-3) / 1e9, 1),
+                               'hbm_frac': round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def gemm_figures(dev, seed):
+    """W8A8 GEMM, K = 2048, N = 16384: A = per-token INT8 of N(0,1) BF16 activations, B = per-channel INT8 of N(0, 0.02)
+    weights (tcq_quantize_rows); timed: the exact int32 product and the BF16 output (acc * s_token) * s_channel. The
+    M = 50 product is checked bit-exact against the oracle's integer matmul."""
+    import numpy as np
+    import torch
+    from oracle import tcq_oracle as O
+    from yanlongvla_amd import kernels as K
+    g = torch.Generator(device=dev).manual_seed(seed + 6)
+    Kd, N = 2048, 16384
+    w = (torch.randn(N, Kd, generator=g, device=dev) * 0.02).bfloat16()
+    qw = torch.empty(N, Kd, dtype=torch.int8, device=dev)
+    sw = torch.empty(N, dtype=torch.float32, device=dev)
+    K.quantize_rows(w, qw, sw)
+    out = {}
+    for M in (800, 50, 1):
+        a = torch.randn(M, Kd, generator=g, device=dev).bfloat16()
+        qa = torch.empty(M, Kd, dtype=torch.int8, device=dev)
+        sa = torch.empty(M, dtype=torch.float32, device=dev)
+        K.quantize_rows(a, qa, sa)
+        acc = torch.empty(M, N, dtype=torch.int32, device=dev)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        t_i32 = graph_per_call(lambda: K.gemm_i8(qa, qw, acc))
+        t_bf16 = graph_per_call(lambda: K.gemm_i8(qa, qw, y, sa, sw))
+        ops = 2 * M * N * Kd
+        byts = M * Kd + N * Kd + 4 * M + 4 * N + 2 * M * N
+        r = {'us_int32': round(t_i32 * 1e3, 2), 'us_bf16': round(t_bf16 * 1e3, 2),
+             'TOPS_bf16': round(ops / (t_bf16 * 1e-3) / 1e12, 1), 'GBs_bf16': round(byts / (t_bf16 * 1e-3) / 1e9, 1)}
+        if M == 800:
+            r['mfma_frac_bf16'] = round(r['TOPS_bf16'] / MFMA_I8_PEAK_TOPS, 4)
+            r['mfma_frac_int32'] = round(ops / (t_i32 * 1e-3) / 1e12 / MFMA_I8_PEAK_TOPS, 4)
+        else:
+            r['hbm_frac_bf16'] = round(r['GBs_bf16'] / HBM_PEAK_GBS, 4)
+        if M == 50:
+            ref = O.int_matmul(qa.cpu().numpy(), qw.cpu().numpy())
+            r['int32_bitexact'] = bool(np.array_equal(acc.cpu().numpy(), ref))
+            yb = O.bf16_bits((ref.astype(np.float32) * sa.cpu().numpy()[:, None]) * sw.cpu().numpy()[None, :])
+            r['bf16_bitexact'] = bool(np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), yb))
+        out[f'M={M}'] = r
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ action-expert chunk
 CHUNK_TOKENS, CHUNK_STEPS, PREFIX = 50, 10, 800
 EXPERT_PACKED_BYTES = 311_427_072 * 2 // 8      # 2-bit payload of the expert's 126 layers, per flow step
@@ -316,6 +389,71 @@ def chunk_cpu_baseline(keep, setup, seconds):
                        f'host affinity {len(os.sched_getaffinity(0))} cores')
 
 
+# ------------------------------------------------------------------------------------------------------ backbone
+BB_IMAGE, BB_TEXT, BB_DECODE = 256, 544, 32
+BACKBONE_WEIGHTS = 1_981_808_640
+
+
+def backbone_setup(seed, dev):
+    import torch
+    from yanlongvla_amd import gemma
+    g = torch.Generator(device=dev).manual_seed(seed + 8)
+    img = torch.randn(BB_IMAGE, gemma.BACKBONE['width'], generator=g, device=dev).bfloat16()
+    ids = torch.randint(0, gemma.BACKBONE['vocab'], (BB_TEXT,), generator=g, device=dev)
+    dec = torch.randint(0, gemma.BACKBONE['vocab'], (BB_DECODE, 1), generator=g, device=dev)
+    return img, ids, dec
+
+
+def backbone(args, dev):
+    """Gemma-2B-shaped language model (18 layers, width 2048, MLP 16384, 8 query heads / 1 KV head of dim 256): prefill over
+    256 image embeddings + 544 token embeddings, then 32 single-token decode steps on the grown KV cache (synthetic token
+    ids). fly = 2-bit TCQ decoded on every call; resident = the W8A8 variant (INT8 weights decoded once at load). Prefill
+    and the 32 decode steps are two HIP graphs; fly and resident are checked bit-exact against the reference runtime."""
+    import torch
+    from yanlongvla_amd import gemma, modules
+    img, ids, dec = backbone_setup(args.seed, dev)
+    res, outs = {}, {}
+    with torch.inference_mode():
+        for runtime in ('reference', 'fly', 'resident'):
+            model = gemma.make_policy(gemma.BackbonePolicy, dev, seed=args.seed + 1)
+            layers = gemma.synthetic_layers(model, args.seed + 9, dev)
+            modules.install(model, runtime=runtime, layers=layers)
+            del layers
+            x = torch.cat([img, model.embed(ids)], 0)
+            state = {}
+
+            def prefill(model=model, x=x, state=state):
+                h, ks, vs = model.prefill(x)
+                state.update(h=h, ks=ks, vs=vs)
+                return h
+
+            def decode(model=model, state=state):
+                ks, vs, hs = state['ks'], state['vs'], []
+                for t in range(BB_DECODE):
+                    h, ks, vs = model.decode_step(model.embed(dec[t]), ks, vs)
+                    hs.append(h)
+                return torch.cat(hs, 0)
+            outs[runtime] = (prefill().clone(), decode().clone())
+            if runtime != 'reference':
+                p_med, p_p95 = graph_latency(prefill, replays=args.backbone_replays, warmup=2)
+                prefill()
+                d_med, d_p95 = graph_latency(decode, replays=args.backbone_replays, warmup=2)
+                res[runtime] = {'prefill_ms': round(p_med, 3), 'decode_ms_32_tokens': round(d_med, 3),
+                                'total_ms': round(p_med + d_med, 3), 'decode_ms_per_token': round(d_med / BB_DECODE, 4)}
+            del model, state
+            torch.cuda.synchronize()
+    exact = {r: bool(torch.equal(outs[r][0], outs['reference'][0]) and torch.equal(outs[r][1], outs['reference'][1]))
+             for r in ('fly', 'resident')}
+    tok_fly = res['fly']['decode_ms_per_token']
+    return dict(workload='Gemma-2B-shaped backbone, 18 layers x (q 2048x2048, k/v 256x2048, o 2048x2048, gate/up 16384x2048, '
+                         'down 2048x16384), 800-token prefill (256 image embeddings + 544 token ids), 32 decode steps',
+                runtimes=res, bitexact_vs_reference_runtime=exact,
+                prefill_int8_TOPS={r: round(2 * 800 * BACKBONE_WEIGHTS / (v['prefill_ms'] * 1e-3) / 1e12, 1) for r, v in res.items()},
+                decode_packed_bytes_per_token=BACKBONE_WEIGHTS // 4,
+                decode_effective_packed_GBs_fly=round(BACKBONE_WEIGHTS / 4 / (tok_fly * 1e-3) / 1e9, 1),
+                decode_effective_int8_GBs_resident=round(BACKBONE_WEIGHTS / (res['resident']['decode_ms_per_token'] * 1e-3) / 1e9, 1))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -351,6 +489,9 @@ def main():
     lat_med, lat_p95 = graph_latency(S1.step)
     am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
+    ops = None
+    if not args.no_ops:
+        ops = {'rht_bf16': rht_figures(dev, args.seed), 'w8a8_gemm_K2048_N16384': gemm_figures(dev, args.seed)}
     chunk = None
     if not args.no_chunk:
         del S1, L1
@@ -380,7 +521,12 @@ def main():
         'max_rel_l2_vs_oracle': err,
         'cpu_baseline': cpu,
         'action_chunk': chunk,
+        'ops': ops,
     }
+    if not args.no_backbone:
+        out['backbone'] = backbone(args, dev)
+        if not all(out['backbone']['bitexact_vs_reference_runtime'].values()):
+            raise SystemExit(f'backbone differs from the reference runtime: {out["backbone"]["bitexact_vs_reference_runtime"]}')
     print(json.dumps(out), flush=True)
 
 
