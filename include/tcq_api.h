@@ -153,6 +153,27 @@ int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s, const floa
 int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
              tcq_stream_t stream);
 
+/* ------------------------------------------------------------------------------------- norms around the projections */
+
+/* Gemma RMSNorm of M rows of BF16 x (M, K) -> y (M, K) BF16: y = bf16((x * r) * (1 + w)), r = 1 / sqrt(sum(x^2) / K + eps) in
+ * FP32, w (K,) BF16. The sum of squares runs in an order fixed by K alone (16-element chunk sums, then a pairwise tree), so
+ * the fused kernels below reproduce this output bit for bit. K % 16 == 0. No reference counterpart: the reference leaves the
+ * policy's norms to PyTorch (modules.py:226-243 only loads their weights); these kernels fuse them into the prologues. */
+int tcq_rmsnorm(const void* x, const void* w, float eps, void* y, int M, int K, tcq_stream_t stream);
+
+/* tcq_rmsnorm followed by tcq_pre with signs su, in one launch: q / q4 / scale of fwht(RMSNorm(x) * su). Extends the
+ * rotate + quantize prologue kernels.pre (deploy/tcq_kernels/kernels.py:208-219) with the decoder layer's input norm. */
+int tcq_norm_pre(const void* x, const void* w, float eps, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M,
+                 int K, tcq_stream_t stream);
+
+/* Epilogue + residual + next prologue of a decoder layer, one launch: a = the tcq_post output of columns col0 .. col0 + N
+ * (BF16 rounding), xout = bf16(x + a) (x, xout (M, N) BF16); then, when w is given, q / q4 / scale of
+ * fwht(RMSNorm(xout) * su) as tcq_norm_pre. Extends kernels.post (deploy/tcq_kernels/kernels.py:221-230) with the residual
+ * add and the following norm. N % 16 == 0. */
+int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
+                          const float* bias, const void* x, void* xout, const void* w, float eps, const int8_t* su, int8_t* q,
+                          int32_t* q4, int ldq, float* scale, int M, int N, tcq_stream_t stream);
+
 /* -------------------------------------------------------------------------------------------------------- products */
 
 /* One layer of a batched FP16-table decode-GEMV / small-M GEMM (M <= 16 tokens): z[t, i] = (sum_k h16[t, k] *

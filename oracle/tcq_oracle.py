@@ -18,6 +18,7 @@ How each function is pinned (tests/test_oracle.py):
          dense Sylvester Hadamard (fwht), bit-by-bit window read of the u16 stream (states_from_bits), the state recurrence
          s[t+1] = ((s[t] << 4) | next nibble) & 0xffff with tail-biting, exact int64 products (int_matmul).
   gelu_tanh_bf16 -> PyTorch's own torch.nn.functional.gelu(approximate='tanh') (the library routine the reference tabulates).
+  rmsnorm_bf16 -> PyTorch's own RMSNorm formula in FP64 (within one BF16 rounding; the summation order is the kernels').
   mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference -> compositions of the pinned functions with the rounding points written in
          deploy/tcq_kernels/kernels.py:272-277, 303 (checked against the unfused chain in the tests).
 """
@@ -26,7 +27,7 @@ import math
 import numpy as np
 
 __all__ = ['block_widths', 'fwht', 'states_from_bits', 'lookup', 'snap', 'quantize_tokens', 'int_matmul', 'Layer',
-           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'plain_middle', 'pre2', 'quantize_channels',
+           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'plain_middle', 'pre2', 'rmsnorm_bf16', 'quantize_channels',
            'w8a8_reference', 'q4_layout', 'random_layer']
 
 
@@ -236,6 +237,27 @@ def plain_middle(z, sv, bias, su, gelu=gelu_tanh_bf16):
     g = gelu(post_bf16(z, sv, bias))
     q, s = quantize_tokens(fwht(bf16_to_f32(g) * np.asarray(su).astype(np.float32)))
     return q, s, g
+
+
+def rmsnorm_bf16(x, w_bits, eps):
+    """Gemma RMSNorm as the device kernels define it (the decoder layers' norm, fused into their prologues; not part of the
+    reference's quantized path): y = bf16((x * r) * (1 + w)), r = 1 / sqrt(ss / K + eps) in FP32, ss summed as 16-element
+    sequential chunk sums followed by a pairwise tree over the chunks (stride 1, 2, 4, ...). x float32 (M, K) of BF16 values,
+    w_bits BF16 bit patterns (K,). Returns BF16 bit patterns."""
+    x = np.asarray(x, dtype=np.float32)
+    M, K = x.shape
+    xs = x.reshape(M, K // 16, 16)
+    a = np.zeros((M, K // 16), dtype=np.float32)
+    for k in range(16):
+        a = a + xs[:, :, k] * xs[:, :, k]
+    C, h = K // 16, 1
+    while h < C:
+        j = np.arange(0, C - h, 2 * h)
+        a[:, j] = a[:, j] + a[:, j + h]
+        h *= 2
+    r = np.float32(1.0) / np.sqrt(a[:, 0] / np.float32(K) + np.float32(eps))
+    one_w = np.float32(1.0) + bf16_to_f32(w_bits)
+    return bf16_bits((x * r[:, None]) * one_w[None, :])
 
 
 def w8a8_reference(a, w):

@@ -273,3 +273,22 @@ def test_q4_layout():
     assert q4.shape == (2, 2)
     assert q4[1, 0] == int.from_bytes(bytes([4, 5, 6, 7]), 'little')
     assert q4[0, 1] == int.from_bytes(bytes([8, 9, 10, 11]), 'little')
+
+
+def test_rmsnorm_close_to_the_formula():
+    """The kernels' RMSNorm (fixed summation order) against the Gemma formula in FP64: at most one BF16 rounding apart, and
+    a wrong term (no +1 on the weight, mean over K-1, eps dropped) moves it far."""
+    rng = np.random.default_rng(4)
+    M, K = 6, 1024
+    x = O.bf16_to_f32(O.bf16_bits(rng.standard_normal((M, K)).astype(np.float32) * 3))
+    x[5] *= 1e-4                                              # eps matters for this row
+    w = O.bf16_bits(rng.standard_normal(K).astype(np.float32) * 0.1)
+    eps = 1e-6
+    y = O.bf16_to_f32(O.rmsnorm_bf16(x, w, eps)).astype(np.float64)
+    x64, w64 = x.astype(np.float64), O.bf16_to_f32(w).astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + eps) * (1 + w64)
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-30)
+    bad = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + eps) * w64
+    assert np.abs(y - bad).max() > 0.1
+    bad_eps = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True)) * (1 + w64)
+    assert np.abs(y[5] - bad_eps[5]).max() > 1e-3 * np.abs(bad_eps[5]).max()

@@ -17,7 +17,7 @@ DTYPE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int
 STATUS = {-1: 'invalid argument', -2: 'shape violates the format', -3: 'unsupported dtype', -4: 'unsupported size',
           -5: 'pointer not 16-byte aligned'}
 
-_P, _I, _L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+_P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 # name -> argument types (restype int unless listed in _RESTYPE)
 SIGNATURES = {
     'tcq_version': [],
@@ -32,6 +32,9 @@ SIGNATURES = {
     'tcq_pre_h16': [_P, _I, _P, _P, _P, _I, _I, _P],
     'tcq_quantize_rows': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_post': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_rmsnorm': [_P, _P, _F, _P, _I, _I, _P],
+    'tcq_norm_pre': [_P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_post_add_norm_pre': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_mid1': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],

@@ -343,6 +343,92 @@ __global__ void k_pre2(const u16* g, const u16* u, const i8* su, i8* q, int* q4,
     quantize_row(lds, sc, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
 }
 
+// --------------------------------------------------------------------------------------------- RMSNorm and its fusions
+// RMSNorm of a row held in LDS (BF16 values as FP32): v <- bf16((v * r) * (1 + w[i])) (* su[i]), r = 1 / sqrt(ss / K + eps),
+// the Gemma norm with FP32 arithmetic and a BF16 result. ss is summed in an order that depends only on K (16-element
+// chunk sums, then a pairwise tree over the chunks), so every kernel that normalises a row of width K gets the same bits
+// whatever its block size. part: K / 16 floats of LDS. K % 16 == 0. Ends with a barrier.
+__device__ __forceinline__ void rmsnorm_row(float* lds, float* part, const u16* w, float eps, const i8* su, int K) {
+    const int C = K >> 4;
+    for (int j = threadIdx.x; j < C; j += blockDim.x) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float v = lds[lds_slot(16 * j + k)];
+            a = a + v * v;
+        }
+        part[j] = a;
+    }
+    __syncthreads();
+    for (int h = 1; h < C; h <<= 1) {
+        for (int j = 2 * h * threadIdx.x; j + h < C; j += 2 * h * blockDim.x) part[j] = part[j] + part[j + h];
+        __syncthreads();
+    }
+    const float r = 1.f / __builtin_sqrtf(part[0] / (float)K + eps);
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        float v = bf16_to_f32(f32_to_bf16((lds[lds_slot(i)] * r) * (1.f + bf16_to_f32(gptr(w)[i]))));
+        if (su) v = v * (float)gptr(su)[i];
+        lds[lds_slot(i)] = v;
+    }
+    __syncthreads();
+}
+
+// Rotate + quantize the LDS row (values already signed): walsh, per-token absmax, INT8 (as k_pre).
+__device__ __forceinline__ void rotate_quantize(float* lds, float* red, i8* q, int* q4, int ldq, float* scale, int tok, int K) {
+    float mx = 0.f;
+    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    const float sc = token_scale(block_max(mx, red));
+    if (threadIdx.x == 0) scale[tok] = sc;
+    quantize_row(lds, sc, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
+}
+
+__global__ void k_rmsnorm(const u16* x, const u16* w, float eps, u16* y, int K, int vec) {
+    extern __shared__ float lds[];
+    float* part = lds + lds_words(K);
+    const size_t base = (size_t)blockIdx.x * K;
+    load_row<TCQ_BF16>(lds, x, base, nullptr, K, vec);
+    rmsnorm_row(lds, part, w, eps, nullptr, K);
+    store_row<TCQ_BF16>(lds, y, base, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
+}
+
+// RMSNorm -> * su -> block Walsh -> per-token INT8: the input norm of a decoder layer fused with the rotate + quantize
+// prologue of the projections that read it.
+__global__ void k_norm_pre(const u16* x, const u16* w, float eps, const i8* su, i8* q, int* q4, int ldq, float* scale, int K,
+                           int vec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    float* part = lds + lds_words(K);
+    const int tok = blockIdx.x;
+    load_row<TCQ_BF16>(lds, x, (size_t)tok * K, nullptr, K, vec);
+    rmsnorm_row(lds, part, w, eps, su, K);
+    rotate_quantize(lds, red, q, q4, ldq, scale, tok, K);
+}
+
+// Epilogue of a projection fused with the residual add and (w != NULL) the next norm + rotate + quantize:
+// a = BF16(walsh(SCALE(acc)) * sv + bias); x_out = BF16(x + a); then, as k_norm_pre, q / scale of RMSNorm(x_out).
+template <int ADT>
+__global__ void k_post_add_norm_pre(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv,
+                                    const float* bias, const u16* x, u16* xout, const u16* w, float eps, const i8* su, i8* q,
+                                    int* q4, int ldq, float* scale, int N, int vec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    float* part = lds + lds_words(N);
+    const int tok = blockIdx.x;
+    const size_t row = (size_t)tok * N;
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + col0, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
+    block_walsh(lds, N, [&](int i, float v) {
+        v = v * (float)gptr(sv)[i];
+        if (bias) v = v + gptr(bias)[i];
+        const u16 xn = f32_to_bf16(bf16_to_f32(gptr(x)[row + i]) + bf16_to_f32(f32_to_bf16(v)));
+        gptr(xout)[row + i] = xn;
+        lds[lds_slot(i)] = bf16_to_f32(xn);
+    });
+    __syncthreads();
+    if (!w) return;
+    rmsnorm_row(lds, part, w, eps, su, N);
+    rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
+}
+
 // =========================================================================================================== C ABI
 // Threads per row: few rows (latency) -> about one 8-element vector per thread; many rows (throughput) -> four vectors per
 // thread so more rows share a CU.
@@ -564,6 +650,52 @@ extern "C" int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype,
         case TCQ_I32: POSTV_A(TCQ_I32); break;
         case TCQ_F32: POSTV_A(TCQ_F32); break;
         case TCQ_BF16: POSTV_A(TCQ_BF16); break;
+        default: return TCQ_ERR_DTYPE;
+    }
+    return launch_status();
+}
+
+static size_t norm_lds(int K) { return row_lds(K) + (size_t)(K / 16) * sizeof(float); }
+
+extern "C" int tcq_rmsnorm(const void* x, const void* w, float eps, void* y, int M, int K, tcq_stream_t stream) {
+    if (!x || !w || !y || M <= 0 || K <= 0) return TCQ_ERR_ARG;
+    if (K % 16 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const int vec = al16(x) && al16(y) && (K * 2) % 16 == 0;
+    launch_k(k_rmsnorm, dim3(M), dim3(row_threads(M, K)), norm_lds(K), (hipStream_t)stream, (const u16*)x, (const u16*)w, eps,
+             (u16*)y, K, vec);
+    return launch_status();
+}
+
+extern "C" int tcq_norm_pre(const void* x, const void* w, float eps, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale,
+                            int M, int K, tcq_stream_t stream) {
+    if (!x || !w || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
+    if (K % 16 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const int vec = al16(x) && (K * 2) % 16 == 0;
+    launch_k(k_norm_pre, dim3(M), dim3(row_threads(M, K)), norm_lds(K), (hipStream_t)stream, (const u16*)x, (const u16*)w, eps,
+             (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec);
+    return launch_status();
+}
+
+extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs,
+                                     const int8_t* sv, const float* bias, const void* x, void* xout, const void* w, float eps,
+                                     const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
+                                     tcq_stream_t stream) {
+    if (!acc || !sv || !x || !xout || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
+    if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
+    if (w && (!su || !scale || (!q && !q4) || (q4 && ldq < M))) return TCQ_ERR_ARG;
+    if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const int asz = dsize(acc_dtype);
+    const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && (!rs || al16(rs));
+    const dim3 grid(M), block(row_threads(M, N));
+    const size_t sh = norm_lds(N);
+    hipStream_t st = (hipStream_t)stream;
+    const u16 *xp = (const u16*)x, *wp = (const u16*)w;
+#define PANP(AD) launch_k(k_post_add_norm_pre<AD>, grid, block, sh, st, acc, lda, col0, s, rs, (const i8*)sv, bias, xp, (u16*)xout, \
+                          wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N, vec)
+    switch (acc_dtype) {
+        case TCQ_I32: PANP(TCQ_I32); break;
+        case TCQ_F32: PANP(TCQ_F32); break;
+        case TCQ_BF16: PANP(TCQ_BF16); break;
         default: return TCQ_ERR_DTYPE;
     }
     return launch_status();

@@ -23,7 +23,11 @@ class GemmaRMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.zeros(dim))
 
     def forward(self, x):
-        xf = x.float()
+        if x.is_cuda and x.dtype == torch.bfloat16 and self.weight.dtype == torch.bfloat16:
+            from . import kernels
+            x2 = x.reshape(-1, x.shape[-1]).contiguous()
+            return kernels.rmsnorm(x2, self.weight, self.eps, torch.empty_like(x2)).reshape(x.shape)
+        xf = x.float()                  # host tensors (CPU twins of a model in tests): the same formula in PyTorch
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * (1.0 + self.weight.float())
         return y.to(x.dtype)
 
@@ -65,13 +69,16 @@ class GemmaAttention(nn.Module):
         self.v_proj = nn.Linear(width, head_dim, bias=False)
         self.o_proj = nn.Linear(heads * head_dim, width, bias=False)
 
-    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
-        """x (M, width). Keys / values: the cache rows (if any) followed by this call's own."""
-        q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+    def core(self, q, k, v, cache_k=None, cache_v=None, causal_offset=None):
+        """Attention of the projected q / k / v (the cache rows, if any, before this call's own keys / values)."""
         kk = k if cache_k is None else torch.cat([cache_k, k.to(cache_k.dtype)], 0)
         vv = v if cache_v is None else torch.cat([cache_v, v.to(cache_v.dtype)], 0)
-        o = attend(q, kk, vv, self.heads, causal_offset).to(x.dtype)
-        return self.o_proj(o), k, v
+        return attend(q, kk, vv, self.heads, causal_offset).to(q.dtype)
+
+    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
+        """x (M, width) -> (o_proj output, this call's k, v)."""
+        q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        return self.o_proj(self.core(q, k, v, cache_k, cache_v, causal_offset)), k, v
 
 
 class GemmaDecoderLayer(nn.Module):

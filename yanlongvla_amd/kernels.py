@@ -134,6 +134,40 @@ def pre2(g, u, su, q=None, q4=None, scale=None):
     call('tcq_pre2', ptr(g), ptr(u), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, K, stream())
 
 
+# ------------------------------------------------------------------------------------------- norms around the projections
+def _bf16(t, what):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f'{what} must be bfloat16')
+
+
+def rmsnorm(x, w, eps, y):
+    """Gemma RMSNorm, BF16 x (M, K) -> y, w (K,) BF16; FP32 arithmetic with a sum order fixed by K."""
+    M, K = x.shape
+    _bf16(x, 'rmsnorm x'), _bf16(w, 'rmsnorm w'), _bf16(y, 'rmsnorm y')
+    _contig(x, w, y)
+    call('tcq_rmsnorm', ptr(x), ptr(w), float(eps), ptr(y), M, K, stream())
+    return y
+
+
+def norm_pre(x, w, eps, su, q=None, q4=None, scale=None):
+    """rmsnorm then pre(., su) in one launch: q / q4 / scale of fwht(RMSNorm(x) * su)."""
+    M, K = x.shape
+    _bf16(x, 'norm_pre x'), _bf16(w, 'norm_pre w')
+    _contig(x, w, su, q, q4, scale)
+    call('tcq_norm_pre', ptr(x), ptr(w), float(eps), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, K, stream())
+
+
+def post_add_norm_pre(acc, s, rs, sv, bias, x, xout, w=None, eps=0.0, su=None, q=None, q4=None, scale=None, col0=0):
+    """xout = bf16(x + post(acc ...)) and, with w, q / q4 / scale of fwht(RMSNorm(xout) * su), one launch. acc as post."""
+    M, N = x.shape
+    _bf16(x, 'post_add_norm_pre x'), _bf16(xout, 'post_add_norm_pre xout')
+    _contig(acc, s, rs, sv, bias, x, xout, w, su, q, q4, scale)
+    call('tcq_post_add_norm_pre', ptr(acc), _dt(acc, (0, 1, 3), 'post_add_norm_pre acc'), acc.shape[1], col0, ptr(s), ptr(rs),
+         ptr(sv), ptr(bias), ptr(x), ptr(xout), ptr(w), float(eps), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, N,
+         stream())
+    return xout
+
+
 # -------------------------------------------------------------------------------------------------------------- products
 def gemv_descriptors(layers):
     """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers each). Keep the tensors alive."""

@@ -25,8 +25,10 @@ from . import tcq_format as F
 
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
-STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0)
-FUSE = dict(post3=True, mlp=True, split=False)      # split: gated-MLP middle as postg + pre2 instead of one mid2 launch
+STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0)
+# mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
+# and residual adds fused into the prologues / epilogues)
+FUSE = dict(post3=True, mlp=True, split=False, layer=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -217,6 +219,50 @@ class KPlainMLP(torch.nn.Module):
         return g2.posts(g2.product(b2), b2, x.shape)[0]
 
 
+class KDecoderLayer(torch.nn.Module):
+    """Gemma decoder layer x + attn(norm1(x)) -> + mlp(norm2(.)) over the layer's groups with the norms and residual adds
+    fused into the TCQ kernels: norm1 + rotate + quantize (tcq_norm_pre), q/k/v product, q/k/v epilogue, attention (the
+    model's own), o rotate + quantize, o product, o epilogue + residual + norm2 + rotate + quantize (tcq_post_add_norm_pre),
+    gate/up product, gated middle (tcq_mid2), down product, down epilogue + residual. Every rounding point is the unfused
+    layer's, so the output equals the module-by-module forward bit for bit. No reference counterpart: it extends the
+    reference's MLP fusion (modules.py:170-189) to the whole layer."""
+
+    def __init__(self, layer, qkv, o, mlp):
+        super().__init__()
+        self.input_layernorm, self.post_attention_layernorm = layer.input_layernorm, layer.post_attention_layernorm
+        self.self_attn, self.mlp = layer.self_attn, mlp
+        self.groups = [qkv, o]
+
+    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
+        qkv, og = self.groups
+        gu, dn = self.mlp.groups
+        n1, n2 = self.input_layernorm, self.post_attention_layernorm
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        M, dev = x2.shape[0], x2.device
+        b = qkv.buffers(M, dev)
+        kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], scale=b['scale'])
+        q, k, v = qkv.posts(qkv.product(b), b, x2.shape)
+        o = self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)
+        b2 = og.quantize(og.prep(o))
+        z = og.product(b2)
+        x3 = torch.empty_like(x2)
+        b3 = gu.buffers(M, dev)
+        sc = z.dtype == torch.float32
+        kernels.post_add_norm_pre(z, None if sc else b2['scale'], None if sc else og.rs, og.sv, og.bias, x2, x3, n2.weight, n2.eps,
+                                  gu.su, q=b3['q'], scale=b3['scale'])
+        acc = gu.product(b3)
+        b4 = dn.buffers(M, dev)
+        sc = acc.dtype == torch.float32
+        kernels.mid2(acc, None if sc else b3['scale'], None if sc else gu.rs, gu.sv, dn.su, q=b4['q'], scale=b4['scale'])
+        z4 = dn.product(b4)
+        x4 = torch.empty_like(x2)
+        sc = z4.dtype == torch.float32
+        kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4)
+        STATS['fused_layers'] += 1
+        return x4.reshape(shape), k, v
+
+
 class RefLinear(torch.nn.Module):
     """The layer by definition, one unfused step per launch (modules.py:209-219 runs tcq_format.reference_linear):
     a8 / INT8 table: h = fwht(x * su) in FP32 -> per-token INT8 -> exact int32 product with the decoded INT8 weight ->
@@ -362,8 +408,23 @@ def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', refere
                     raise TypeError(f'{parent}: expected a SiglipMLP, got {type(model.get_submodule(parent)).__name__}')
                 set_submodule(model, parent, KPlainMLP(g, by_name[f'{parent}.fc2']))
                 fused += 1
+    layers_fused = 0
+    if FUSE['mlp'] and FUSE['layer']:
+        by_name = {g.layers[0].name: g for g in groups}
+        for g in groups:
+            attn, _, leaf = g.layers[0].name.rpartition('.')
+            lname = attn.rpartition('.')[0]
+            if leaf != 'q_proj' or len(g.layers) != 3 or f'{attn}.o_proj' not in by_name:
+                continue
+            layer = model.get_submodule(lname)
+            mlp = getattr(layer, 'mlp', None)
+            if type(layer).__name__ != 'GemmaDecoderLayer' or not isinstance(mlp, KGatedMLP) or not hasattr(layer.self_attn, 'core'):
+                continue
+            set_submodule(model, lname, KDecoderLayer(layer, g, by_name[f'{attn}.o_proj'], mlp))
+            layers_fused += 1
     torch.cuda.synchronize()
     policy._tcq_groups = groups
+    info['fused_layers'] = layers_fused
     info['fused_mlps'] = fused
     info.update(groups=len(groups), shared_rotations=sum(len(g.layers) - 1 for g in groups),
                 modes={m: sum(1 for g in groups if g.mode == m) for m in ('resident', 'fly', 'chunk')})
