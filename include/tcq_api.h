@@ -136,13 +136,13 @@ int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype, const floa
 /* Gated-MLP middle (down(gelu(gate(x)) * up(x))): acc (M, lda >= 2N) holds gate columns [0, N) and up columns [N, 2N),
  * scaled as tcq_post (rs, sv: concatenated (2N,) vectors; rs unused for F32). g = GELU(BF16(walsh(gate) * sv)) by the table,
  * u = BF16(walsh(up) * sv), x = BF16(g * u) * su (su: the down projection's input signs, (N,)) -> block Walsh -> per-token
- * INT8: q (M, N) and / or q4 (N/4, ldq), scale (M,). N % 4 == 0, N <= tcq_max_width().
+ * INT8: q (M, N) and / or q4 (N/4, ldq), scale (M,). N % 16 == 0, N <= tcq_max_width().
  * Replaces kernels.mid2 / k_mid2_{i32,f32,bf16} (deploy/tcq_kernels/kernels.py:263-278, 640-643). */
 int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const uint16_t* gelu_lut,
              const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N, tcq_stream_t stream);
 
 /* Plain-MLP middle (fc2(gelu(fc1(x)))): acc (M, lda >= N) -> walsh -> * sv -> + bias (FP32 (N,) or NULL) -> BF16 -> GELU table
- * -> * su -> walsh -> per-token INT8 (q / q4, scale). Replaces kernels.mid1 / k_mid1_* (deploy/tcq_kernels/kernels.py:280-292,
+ * -> * su -> walsh -> per-token INT8 (q / q4, scale); N % 16 == 0. Replaces kernels.mid1 / k_mid1_* (deploy/tcq_kernels/kernels.py:280-292,
  * 646-650). */
 int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const float* bias,
              const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
@@ -173,6 +173,19 @@ int tcq_norm_pre(const void* x, const void* w, float eps, const int8_t* su, int8
 int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
                           const float* bias, const void* x, void* xout, const void* w, float eps, const int8_t* su, int8_t* q,
                           int32_t* q4, int ldq, float* scale, int M, int N, tcq_stream_t stream);
+
+/* Attention of H <= 8 query heads over one shared key / value head of dim D = 256 (multi-query), BF16 in and out, FP32
+ * arithmetic. q (M, H * D); keys / values = the P cache rows (k_cache, v_cache (P, D); NULL when P = 0) followed by this
+ * call's M rows (k_new, v_new (M, D)); query t sees key j iff causal_offset < 0 or j <= causal_offset + t. Scores
+ * (q . k) / 16, softmax over the visible keys, computed in chunks of 64 keys (chunk maximum, exponentials, sums) merged
+ * per token: the result depends on the number of keys only through that fixed chunking. part: workspace of
+ * M * tcq_attend_chunks(P, M) * H * (D + 2) floats. Outputs: o (M, H * D) BF16 (may be NULL when su is given) and, when su
+ * is given, the rotate + quantize prologue of the next projection applied to the BF16 o row (q8 (M, H * D) int8, scale (M,)).
+ * No reference counterpart: the reference policy's attention is PyTorch; this is the decoder layers' attention between
+ * the TCQ projections, with the o-projection prologue (kernels.pre, deploy/tcq_kernels/kernels.py:208-219) fused in. */
+int tcq_attend_chunks(int P, int M);
+int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
+               int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale, tcq_stream_t stream);
 
 /* -------------------------------------------------------------------------------------------------------- products */
 

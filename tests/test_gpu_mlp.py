@@ -51,7 +51,7 @@ def accumulators(rng, M, width, kind):
 
 
 @pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
-@pytest.mark.parametrize('M,N', [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 20)])
+@pytest.mark.parametrize("M,N", [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 48)])
 def test_mid2_bitexact(kind, M, N):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * 7 + N)
@@ -87,7 +87,7 @@ def test_mid2_strided_accumulator():
 
 
 @pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
-@pytest.mark.parametrize('M,N,with_bias', [(1, 4304, True), (50, 4096, False), (10, 1152, True), (4, 12, True)])
+@pytest.mark.parametrize("M,N,with_bias", [(1, 4304, True), (50, 4096, False), (10, 1152, True), (4, 48, True)])
 def test_mid1_bitexact(kind, M, N, with_bias):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * 13 + N)

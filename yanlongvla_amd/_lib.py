@@ -35,6 +35,8 @@ SIGNATURES = {
     'tcq_rmsnorm': [_P, _P, _F, _P, _I, _I, _P],
     'tcq_norm_pre': [_P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_post_add_norm_pre': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_attend_chunks': [_I, _I],
+    'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_mid1': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],

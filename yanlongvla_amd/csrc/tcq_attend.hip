@@ -1,0 +1,158 @@
+// Attention of H query heads over one shared key / value head (multi-query, head dim 256), BF16 in and out, FP32
+// arithmetic: the attention of the Gemma decoder layers whose projections run on the TCQ kernels. The keys are the cache
+// rows followed by this call's own rows, so no concatenated copy is made.
+//
+// Split over the keys (64 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
+// head, their chunk maximum m, the exponentials e = exp(s - m), l = sum e and the unnormalised outputs o = sum e v; then
+// k_attn_combine merges the chunks of a token (weights exp(m_c - max_c m_c)) and divides by the merged sum. The result
+// depends on the number of keys only through this fixed chunking, never on launch shapes. The combine can feed its BF16
+// output row straight into the rotate + quantize prologue of the output projection.
+#include "tcq_device.h"
+#include "tcq_launch.h"
+
+namespace {
+
+constexpr int AD = 256;          // head dim
+constexpr int AH = 8;            // most query heads
+constexpr int KC = 64;           // keys per chunk
+constexpr int AT = 256;          // threads of k_attn_part
+
+__device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh, int P, int j) {
+    return j < P ? cache + (size_t)j * AD : fresh + (size_t)(j - P) * AD;
+}
+
+}  // namespace
+
+// grid (tokens M, chunks NC), AT threads. part: (M, NC, H, AD + 2) FP32: o[AD], m, l per head.
+__global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, const u16* vc, int P, const u16* kn, const u16* vn,
+                                                  int M, int H, int causal, float* part) {
+    __shared__ float qs[AH][AD];
+    __shared__ float ps[AH][KC + 1];
+    const int t = blockIdx.x, c = blockIdx.y, NC = gridDim.y, tid = threadIdx.x;
+    const int T = P + M, j0 = c * KC;
+    const int jend = min(T, causal >= 0 ? causal + t + 1 : T);        // keys j < jend are visible to this query
+    const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
+    for (int i = tid; i < AH * AD; i += AT) {
+        const int h = i / AD, d = i - h * AD;
+        qs[h][d] = h < H ? bf16_to_f32(gptr(q)[(size_t)t * H * AD + h * AD + d]) : 0.f;
+    }
+    __syncthreads();
+    // scores: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the 4 quarters
+    {
+        const int kk = tid >> 2, p = tid & 3, j = j0 + kk;
+        float a[AH];
+#pragma unroll
+        for (int h = 0; h < AH; ++h) a[h] = 0.f;
+        if (j < jend) {
+            const u16* kr = key_row(kc, kn, P, j) + 64 * p;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint4_t w = gptr((const uint4_t*)kr)[b];
+                float kv[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { kv[2 * e] = bf16_to_f32((u16)(w[e] & 0xffffu)); kv[2 * e + 1] = bf16_to_f32((u16)(w[e] >> 16)); }
+#pragma unroll
+                for (int h = 0; h < AH; ++h)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][64 * p + 8 * b + e] * kv[e];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < AH; ++h) {
+            a[h] = a[h] + __shfl_xor(a[h], 1, 64);
+            a[h] = a[h] + __shfl_xor(a[h], 2, 64);
+        }
+        if (p == 0) {
+#pragma unroll
+            for (int h = 0; h < AH; ++h) ps[h][kk] = j < jend ? a[h] * scl : -__builtin_inff();
+        }
+    }
+    __syncthreads();
+    // chunk softmax statistics: wave w takes heads 2w, 2w + 1, lane = key
+    {
+        const int w = tid >> 6, lane = tid & 63;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int h = 2 * w + hh;
+            const float s = ps[h][lane];
+            const float m = wave_max(s);
+            const float e = m == -__builtin_inff() ? 0.f : expf(s - m);
+            float l = e;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
+            ps[h][lane] = e;
+            if (lane == 0 && h < H) {
+                float* base = part + (((size_t)t * NC + c) * H + h) * (AD + 2);
+                base[AD] = m;
+                base[AD + 1] = l;
+            }
+        }
+    }
+    __syncthreads();
+    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order
+    {
+        const int d = tid;
+        float o[AH];
+#pragma unroll
+        for (int h = 0; h < AH; ++h) o[h] = 0.f;
+        const int kn_end = min(KC, jend - j0);
+        for (int kk = 0; kk < kn_end; ++kk) {
+            const float v = bf16_to_f32(gptr(key_row(vc, vn, P, j0 + kk))[d]);
+#pragma unroll
+            for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][kk] * v;
+        }
+        for (int h = 0; h < H; ++h) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = o[h];
+    }
+}
+
+// grid M, block 256 (one thread per dim). o (M, H * AD) BF16 (or NULL); with su, the row also goes through the rotate +
+// quantize prologue (q8 row-major (M, H * AD), scale (M,)).
+__global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int t = blockIdx.x, d = threadIdx.x, K = H * AD;
+    for (int h = 0; h < H; ++h) {
+        const float* base = part + ((size_t)t * NC * H + h) * (AD + 2);
+        const size_t cs = (size_t)H * (AD + 2);                      // stride between chunks
+        float mx = -__builtin_inff();
+        for (int c = 0; c < NC; ++c) mx = fmaxf(mx, base[c * cs + AD]);
+        float L = 0.f, acc = 0.f;
+        for (int c = 0; c < NC; ++c) {
+            const float m = base[c * cs + AD];
+            const float wgt = m == -__builtin_inff() ? 0.f : expf(m - mx);
+            L = L + wgt * base[c * cs + AD + 1];
+            acc = acc + wgt * base[c * cs + d];
+        }
+        const u16 b = f32_to_bf16(acc / L);
+        if (o) gptr(o)[(size_t)t * K + h * AD + d] = b;
+        if (su) lds[lds_slot(h * AD + d)] = bf16_to_f32(b) * (float)gptr(su)[h * AD + d];
+    }
+    if (!su) return;
+    __syncthreads();
+    float amx = 0.f;
+    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; amx = fmaxf(amx, fabsf(v)); });
+    const float sc = token_scale(block_max(amx, red));
+    if (threadIdx.x == 0) scale[t] = sc;
+    quantize_row(lds, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
+}
+
+// =========================================================================================================== C ABI
+extern "C" int tcq_attend_chunks(int P, int M) { return (P + M + KC - 1) / KC; }
+
+extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
+                          int H, int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale,
+                          tcq_stream_t stream) {
+    if (!q || !k_new || !v_new || !part || M <= 0 || H <= 0 || P < 0 || (P > 0 && (!k_cache || !v_cache))) return TCQ_ERR_ARG;
+    if (!o && !su) return TCQ_ERR_ARG;
+    if (su && (!q8 || !scale)) return TCQ_ERR_ARG;
+    if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
+    if ((uintptr_t)k_new % 16 || (uintptr_t)(k_cache) % 16) return TCQ_ERR_ALIGN;
+    const int NC = tcq_attend_chunks(P, M);
+    if (NC > 65535) return TCQ_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    launch_k(k_attn_part, dim3(M, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
+             (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
+    launch_k(k_attn_combine, dim3(M), dim3(256), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
+             (u16*)o, (const i8*)su, (i8*)q8, scale);
+    return launch_status();
+}

@@ -273,102 +273,112 @@ __global__ void k_postg(SEGS segs, const float* s, const u16* gelu_lut, int maxN
     store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec);
 }
 
-// ------------------------------------------------------------------------------------------------------------ MLP middles
-// Rounding points of the fused MLP middles (each stage is the unfused chain's): GELU and the gate / up products round to
-// BF16 exactly where the separate epilogue + prologue kernels would store BF16 tensors.
-__device__ __forceinline__ u16 gelu_of(const u16* lut, u16 b) { return gptr(lut)[b]; }
-
-// Gated MLP (down(gelu(gate(x)) * up(x))): accumulator row = gate columns [0, N) | up columns [N, 2N), scaled like tcq_post
-// (rs and sv are the concatenated 2N vectors). g = GELU(BF16(walsh(gate) * sv)) is kept in LDS as BF16, then
-// x = BF16(g * BF16(walsh(up) * sv)) * su -> walsh -> per-token INT8 of the down projection's input.
-template <int ADT>
-__global__ void k_mid2(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const u16* lut, const i8* su,
-                       i8* q, int* q4, int ldq, float* scale, int N, int vec) {
-    extern __shared__ float lds[];
-    __shared__ float red[16];
-    u16* g = (u16*)(lds + lds_words(N));
-    const int tok = blockIdx.x;
-    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
-    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, st, rs, N, vec);
-    block_walsh(lds, N, [&](int i, float v) { g[i] = gelu_of(lut, f32_to_bf16(v * (float)gptr(sv)[i])); });
-    __syncthreads();
-    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + N, st, rs + (ADT == TCQ_F32 ? 0 : N), N, vec);
-    block_walsh(lds, N, [&](int i, float v) {
-        const u16 u = f32_to_bf16(v * (float)gptr(sv)[N + i]);
-        lds[lds_slot(i)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(g[i]) * bf16_to_f32(u))) * (float)gptr(su)[i];
-    });
-    __syncthreads();
-    float mx = 0.f;
-    block_walsh(lds, N, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
-    const float sc = token_scale(block_max(mx, red));
-    if (threadIdx.x == 0) scale[tok] = sc;
-    quantize_row(lds, sc, q ? q + (size_t)tok * N : nullptr, q4, tok, N, ldq);
+// ------------------------------------------------------------------------------------------------ 16-element chunks
+// The row kernels below keep every global access out of the Walsh passes: the passes read and write LDS only, and the
+// side vectors (signs, bias, residual, norm weight) are read per 16-element chunk with 16-byte loads (vec) or element by
+// element (rows whose base or length breaks the alignment), all loads of a chunk issued before any of them is used.
+__device__ __forceinline__ void c16_bf16(const u16* p, bool vec, float (&v)[16]) {
+    if (vec) {
+        const uint4_t a = gptr((const uint4_t*)p)[0], b = gptr((const uint4_t*)p)[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = bf16_to_f32((u16)(a[k] & 0xffffu)); v[2 * k + 1] = bf16_to_f32((u16)(a[k] >> 16));
+            v[8 + 2 * k] = bf16_to_f32((u16)(b[k] & 0xffffu)); v[9 + 2 * k] = bf16_to_f32((u16)(b[k] >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32(gptr(p)[k]);
+    }
+}
+__device__ __forceinline__ void c16_store_bf16(u16* p, bool vec, const u16 (&h)[16]) {
+    if (vec) {
+        uint4_t a, b;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[k] = (u32)h[2 * k] | ((u32)h[2 * k + 1] << 16);
+            b[k] = (u32)h[8 + 2 * k] | ((u32)h[9 + 2 * k] << 16);
+        }
+        gptr((uint4_t*)p)[0] = a;
+        gptr((uint4_t*)p)[1] = b;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) gptr(p)[k] = h[k];
+    }
+}
+__device__ __forceinline__ void c16_i8(const i8* p, bool vec, float (&v)[16]) {
+    if (vec) {
+        const uint4_t a = gptr((const uint4_t*)p)[0];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a[k >> 2] >> (8 * (k & 3)));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (float)gptr(p)[k];
+    }
+}
+__device__ __forceinline__ void c16_f32(const float* p, bool vec, float (&v)[16]) {
+    if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4_t a = gptr((const uint4_t*)p)[q];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * q + k] = __uint_as_float(a[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = gptr(p)[k];
+    }
 }
 
-// Plain MLP (fc2(gelu(fc1(x)))): x = GELU(BF16(walsh(acc) * sv + bias)) * su -> walsh -> per-token INT8 of fc2's input.
-template <int ADT>
-__global__ void k_mid1(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const float* bias, const u16* lut,
-                       const i8* su, i8* q, int* q4, int ldq, float* scale, int N, int vec) {
-    extern __shared__ float lds[];
-    __shared__ float red[16];
-    const int tok = blockIdx.x;
-    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
-    block_walsh(lds, N, [&](int i, float v) {
-        v = v * (float)gptr(sv)[i];
-        if (bias) v = v + gptr(bias)[i];
-        lds[lds_slot(i)] = bf16_to_f32(gelu_of(lut, f32_to_bf16(v))) * (float)gptr(su)[i];
-    });
+// Sum of squares of a row in an order fixed by K alone: chunk sums of 16 consecutive values (sequential, part[j] for chunk
+// j), then a pairwise tree over the chunks, stage h adding chunk j + h into chunk j for j a multiple of 2h. Stages h < 64 run
+// in registers across the lanes of a wave (chunks past the end count as +0, which leaves every partial sum unchanged), the
+// rest over the per-wave results. part: the K / 16 chunk sums (LDS, complete on entry: the caller synchronises); red: >= 16
+// floats of LDS. Every thread gets the total. Ends with a barrier.
+__device__ __forceinline__ float chunk_sumsq(const float (&v)[16]) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a = a + v[k] * v[k];
+    return a;
+}
+__device__ __forceinline__ float tree_total(const float* part, float* red, int K) {
+    const int C = K >> 4, groups = (C + 63) >> 6;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int g = wid; g < groups; g += nw) {
+        const int j = (g << 6) + lane;
+        float v = j < C ? part[j] : 0.f;
+#pragma unroll
+        for (int h = 1; h < 64; h <<= 1) {
+            const float o = __shfl_down(v, h, 64);
+            if ((lane & (2 * h - 1)) == 0) v = v + o;
+        }
+        if (lane == 0) red[g] = v;
+    }
     __syncthreads();
-    float mx = 0.f;
-    block_walsh(lds, N, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
-    const float sc = token_scale(block_max(mx, red));
-    if (threadIdx.x == 0) scale[tok] = sc;
-    quantize_row(lds, sc, q ? q + (size_t)tok * N : nullptr, q4, tok, N, ldq);
+    float r[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) r[g] = g < groups ? red[g] : 0.f;
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+        for (int g = 0; g + h < 16; g += 2 * h) r[g] = r[g] + r[g + h];
+    __syncthreads();
+    return r[0];
 }
 
-// Second half of a split gated-MLP middle: x = BF16(g * u) * su (g = GELU(gate), u = up, both BF16 (M, K)) -> walsh -> INT8.
-__global__ void k_pre2(const u16* g, const u16* u, const i8* su, i8* q, int* q4, int ldq, float* scale, int K) {
-    extern __shared__ float lds[];
-    __shared__ float red[16];
-    const int tok = blockIdx.x;
-    const size_t base = (size_t)tok * K;
-    for (int i = threadIdx.x; i < K; i += blockDim.x)
-        lds[lds_slot(i)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gptr(g)[base + i]) * bf16_to_f32(gptr(u)[base + i]))) *
-                           (float)gptr(su)[i];
-    __syncthreads();
-    float mx = 0.f;
-    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
-    const float sc = token_scale(block_max(mx, red));
-    if (threadIdx.x == 0) scale[tok] = sc;
-    quantize_row(lds, sc, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
-}
-
-// --------------------------------------------------------------------------------------------- RMSNorm and its fusions
-// RMSNorm of a row held in LDS (BF16 values as FP32): v <- bf16((v * r) * (1 + w[i])) (* su[i]), r = 1 / sqrt(ss / K + eps),
-// the Gemma norm with FP32 arithmetic and a BF16 result. ss is summed in an order that depends only on K (16-element
-// chunk sums, then a pairwise tree over the chunks), so every kernel that normalises a row of width K gets the same bits
-// whatever its block size. part: K / 16 floats of LDS. K % 16 == 0. Ends with a barrier.
-__device__ __forceinline__ void rmsnorm_row(float* lds, float* part, const u16* w, float eps, const i8* su, int K) {
-    const int C = K >> 4;
-    for (int j = threadIdx.x; j < C; j += blockDim.x) {
-        float a = 0.f;
+// RMSNorm of the LDS row (BF16 values as FP32) given its sum of squares: v <- bf16((v * r) * (1 + w[i])) * su[i] (su may be
+// NULL), r = 1 / sqrt(ss / K + eps). Ends with a barrier.
+__device__ __forceinline__ void norm_apply(float* lds, float ss, const u16* w, const i8* su, float eps, int K, bool vec) {
+    const float r = 1.f / __builtin_sqrtf(ss / (float)K + eps);
+    for (int j = threadIdx.x; j < (K >> 4); j += blockDim.x) {
+        float wv[16], sg[16];
+        c16_bf16(w + 16 * j, vec, wv);
+        if (su) c16_i8(su + 16 * j, vec, sg);
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float v = lds[lds_slot(16 * j + k)];
-            a = a + v * v;
+            float v = bf16_to_f32(f32_to_bf16((lds[lds_slot(16 * j + k)] * r) * (1.f + wv[k])));
+            if (su) v = v * sg[k];
+            lds[lds_slot(16 * j + k)] = v;
         }
-        part[j] = a;
-    }
-    __syncthreads();
-    for (int h = 1; h < C; h <<= 1) {
-        for (int j = 2 * h * threadIdx.x; j + h < C; j += 2 * h * blockDim.x) part[j] = part[j] + part[j + h];
-        __syncthreads();
-    }
-    const float r = 1.f / __builtin_sqrtf(part[0] / (float)K + eps);
-    for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        float v = bf16_to_f32(f32_to_bf16((lds[lds_slot(i)] * r) * (1.f + bf16_to_f32(gptr(w)[i]))));
-        if (su) v = v * (float)gptr(su)[i];
-        lds[lds_slot(i)] = v;
     }
     __syncthreads();
 }
@@ -382,12 +392,129 @@ __device__ __forceinline__ void rotate_quantize(float* lds, float* red, i8* q, i
     quantize_row(lds, sc, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
 }
 
+// ------------------------------------------------------------------------------------------------------------ MLP middles
+// Rounding points of the fused MLP middles (each stage is the unfused chain's): GELU and the gate / up products round to
+// BF16 exactly where the separate epilogue + prologue kernels would store BF16 tensors. GELU comes from the 65536-entry
+// table (lut) of PyTorch's own results; its 16 lookups per chunk are issued together.
+__device__ __forceinline__ void gelu16(const u16* lut, const float (&v)[16], u16 (&g)[16]) {
+    u16 b[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) b[k] = f32_to_bf16(v[k]);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) g[k] = gptr(lut)[b[k]];
+}
+
+// Gated MLP (down(gelu(gate(x)) * up(x))): accumulator row = gate columns [0, N) | up columns [N, 2N), scaled like tcq_post
+// (rs and sv are the concatenated 2N vectors). g = GELU(BF16(walsh(gate) * sv)) is kept in LDS as BF16, then
+// x = BF16(g * BF16(walsh(up) * sv)) * su -> walsh -> per-token INT8 of the down projection's input.
+template <int ADT>
+__global__ void k_mid2(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const u16* lut, const i8* su,
+                       i8* q, int* q4, int ldq, float* scale, int N, int vec, int svec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    u16* g = (u16*)(lds + lds_words(N));
+    const int tok = blockIdx.x;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, st, rs, N, vec);
+    walsh_inplace(lds, N);
+    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+        float sg[16], v[16];
+        u16 gv[16];
+        c16_i8(sv + 16 * j, svec, sg);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = lds[lds_slot(16 * j + k)] * sg[k];
+        gelu16(lut, v, gv);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) g[16 * j + k] = gv[k];
+    }
+    __syncthreads();
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + N, st, rs + (ADT == TCQ_F32 ? 0 : N), N, vec);
+    walsh_inplace(lds, N);
+    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+        float sg[16], sn[16];
+        c16_i8(sv + N + 16 * j, svec, sg);
+        c16_i8(su + 16 * j, svec, sn);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float u = bf16_to_f32(f32_to_bf16(lds[lds_slot(16 * j + k)] * sg[k]));
+            lds[lds_slot(16 * j + k)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(g[16 * j + k]) * u)) * sn[k];
+        }
+    }
+    __syncthreads();
+    rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
+}
+
+// Plain MLP (fc2(gelu(fc1(x)))): x = GELU(BF16(walsh(acc) * sv + bias)) * su -> walsh -> per-token INT8 of fc2's input.
+template <int ADT>
+__global__ void k_mid1(const void* acc, int lda, const float* s, const float* rs, const i8* sv, const float* bias, const u16* lut,
+                       const i8* su, i8* q, int* q4, int ldq, float* scale, int N, int vec, int svec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x;
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
+    walsh_inplace(lds, N);
+    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+        float sg[16], sn[16], b[16], v[16];
+        u16 gv[16];
+        c16_i8(sv + 16 * j, svec, sg);
+        c16_i8(su + 16 * j, svec, sn);
+        if (bias) c16_f32(bias + 16 * j, svec, b);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            v[k] = lds[lds_slot(16 * j + k)] * sg[k];
+            if (bias) v[k] = v[k] + b[k];
+        }
+        gelu16(lut, v, gv);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) lds[lds_slot(16 * j + k)] = bf16_to_f32(gv[k]) * sn[k];
+    }
+    __syncthreads();
+    rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
+}
+
+// Second half of a split gated-MLP middle: x = BF16(g * u) * su (g = GELU(gate), u = up, both BF16 (M, K)) -> walsh -> INT8.
+__global__ void k_pre2(const u16* g, const u16* u, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x;
+    const size_t base = (size_t)tok * K;
+    for (int j = threadIdx.x; j < (K >> 4); j += blockDim.x) {
+        float gv[16], uv[16], sn[16];
+        c16_bf16(g + base + 16 * j, vec, gv);
+        c16_bf16(u + base + 16 * j, vec, uv);
+        c16_i8(su + 16 * j, vec, sn);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) lds[lds_slot(16 * j + k)] = bf16_to_f32(f32_to_bf16(gv[k] * uv[k])) * sn[k];
+    }
+    for (int i = (K & ~15) + threadIdx.x; i < K; i += blockDim.x)        // widths that are not a multiple of 16
+        lds[lds_slot(i)] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gptr(g)[base + i]) * bf16_to_f32(gptr(u)[base + i]))) *
+                           (float)gptr(su)[i];
+    __syncthreads();
+    rotate_quantize(lds, red, q, q4, ldq, scale, tok, K);
+}
+
+// --------------------------------------------------------------------------------------------- RMSNorm and its fusions
+// Gemma RMSNorm with FP32 arithmetic and a BF16 result: y = bf16((x * r) * (1 + w)), r = 1 / sqrt(ss / K + eps), ss summed
+// in the order of tree_total, so every kernel that normalises a row of width K gives the same bits. K % 16 == 0.
+// The row is loaded (and its chunk sums taken) in one pass.
+__device__ __forceinline__ void load_row_sumsq(float* lds, float* part, const u16* x, int K, bool vec) {
+    for (int j = threadIdx.x; j < (K >> 4); j += blockDim.x) {
+        float v[16];
+        c16_bf16(x + 16 * j, vec, v);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) lds[lds_slot(16 * j + k)] = v[k];
+        part[j] = chunk_sumsq(v);
+    }
+    __syncthreads();
+}
+
 __global__ void k_rmsnorm(const u16* x, const u16* w, float eps, u16* y, int K, int vec) {
     extern __shared__ float lds[];
+    __shared__ float red[16];
     float* part = lds + lds_words(K);
     const size_t base = (size_t)blockIdx.x * K;
-    load_row<TCQ_BF16>(lds, x, base, nullptr, K, vec);
-    rmsnorm_row(lds, part, w, eps, nullptr, K);
+    load_row_sumsq(lds, part, x + base, K, vec);
+    norm_apply(lds, tree_total(part, red, K), w, nullptr, eps, K, vec);
     store_row<TCQ_BF16>(lds, y, base, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
 }
 
@@ -399,8 +526,8 @@ __global__ void k_norm_pre(const u16* x, const u16* w, float eps, const i8* su, 
     __shared__ float red[16];
     float* part = lds + lds_words(K);
     const int tok = blockIdx.x;
-    load_row<TCQ_BF16>(lds, x, (size_t)tok * K, nullptr, K, vec);
-    rmsnorm_row(lds, part, w, eps, su, K);
+    load_row_sumsq(lds, part, x + (size_t)tok * K, K, vec);
+    norm_apply(lds, tree_total(part, red, K), w, su, eps, K, vec);
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, K);
 }
 
@@ -409,23 +536,34 @@ __global__ void k_norm_pre(const u16* x, const u16* w, float eps, const i8* su, 
 template <int ADT>
 __global__ void k_post_add_norm_pre(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv,
                                     const float* bias, const u16* x, u16* xout, const u16* w, float eps, const i8* su, i8* q,
-                                    int* q4, int ldq, float* scale, int N, int vec) {
+                                    int* q4, int ldq, float* scale, int N, int vec, int svec) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     float* part = lds + lds_words(N);
     const int tok = blockIdx.x;
     const size_t row = (size_t)tok * N;
     load_acc_row<ADT>(lds, acc, (size_t)tok * lda + col0, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
-    block_walsh(lds, N, [&](int i, float v) {
-        v = v * (float)gptr(sv)[i];
-        if (bias) v = v + gptr(bias)[i];
-        const u16 xn = f32_to_bf16(bf16_to_f32(gptr(x)[row + i]) + bf16_to_f32(f32_to_bf16(v)));
-        gptr(xout)[row + i] = xn;
-        lds[lds_slot(i)] = bf16_to_f32(xn);
-    });
+    walsh_inplace(lds, N);
+    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+        float sg[16], b[16], xv[16];
+        u16 xn[16];
+        c16_i8(sv + 16 * j, svec, sg);
+        if (bias) c16_f32(bias + 16 * j, svec, b);
+        c16_bf16(x + row + 16 * j, svec, xv);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            float v = lds[lds_slot(16 * j + k)] * sg[k];
+            if (bias) v = v + b[k];
+            xn[k] = f32_to_bf16(xv[k] + bf16_to_f32(f32_to_bf16(v)));
+            xv[k] = bf16_to_f32(xn[k]);
+            lds[lds_slot(16 * j + k)] = xv[k];
+        }
+        c16_store_bf16(xout + row + 16 * j, svec, xn);
+        part[j] = chunk_sumsq(xv);
+    }
     __syncthreads();
     if (!w) return;
-    rmsnorm_row(lds, part, w, eps, su, N);
+    norm_apply(lds, tree_total(part, red, N), w, su, eps, N, svec);
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
 }
 
@@ -570,18 +708,18 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
     if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < 2 * N || (q4 && ldq < M))
         return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
-    if (N % 4 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N) + (size_t)N * 2;
     const int asz = dsize(acc_dtype);
-    const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)N * asz) % 16 == 0 &&
-                    (!rs || (al16(rs) && (N * 4) % 16 == 0));
+    const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && (!rs || al16(rs));
+    const int svec = al16(sv) && al16(su);
     hipStream_t st = (hipStream_t)stream;
     const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
     switch (acc_dtype) {
-        case TCQ_I32: launch_k(k_mid2<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
-        case TCQ_F32: launch_k(k_mid2<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
-        case TCQ_BF16: launch_k(k_mid2<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_I32: launch_k(k_mid2<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
+        case TCQ_F32: launch_k(k_mid2<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
+        case TCQ_BF16: launch_k(k_mid2<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
         default: return TCQ_ERR_DTYPE;
     }
     return launch_status();
@@ -593,17 +731,18 @@ extern "C" int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s,
     if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < N || (q4 && ldq < M))
         return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
-    if (N % 4 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N);
     const int asz = dsize(acc_dtype);
-    const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && (!rs || al16(rs));
+    const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && (!rs || al16(rs));
+    const int svec = al16(sv) && al16(su) && (!bias || al16(bias));
     hipStream_t st = (hipStream_t)stream;
     const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
     switch (acc_dtype) {
-        case TCQ_I32: launch_k(k_mid1<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
-        case TCQ_F32: launch_k(k_mid1<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
-        case TCQ_BF16: launch_k(k_mid1<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec); break;
+        case TCQ_I32: launch_k(k_mid1<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
+        case TCQ_F32: launch_k(k_mid1<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
+        case TCQ_BF16: launch_k(k_mid1<TCQ_BF16>, grid, block, sh, st, acc, lda, s, rs, svp, bias, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
         default: return TCQ_ERR_DTYPE;
     }
     return launch_status();
@@ -613,8 +752,9 @@ extern "C" int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* 
                         tcq_stream_t stream) {
     if (!g || !u || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const int vec = K % 8 == 0 && al16(g) && al16(u) && al16(su);
     launch_k(k_pre2, dim3(M), dim3(row_threads(M, K)), row_lds(K), (hipStream_t)stream, (const u16*)g, (const u16*)u, (const i8*)su,
-             (i8*)q, (int*)q4, ldq, scale, K);
+             (i8*)q, (int*)q4, ldq, scale, K, vec);
     return launch_status();
 }
 
@@ -660,7 +800,7 @@ static size_t norm_lds(int K) { return row_lds(K) + (size_t)(K / 16) * sizeof(fl
 extern "C" int tcq_rmsnorm(const void* x, const void* w, float eps, void* y, int M, int K, tcq_stream_t stream) {
     if (!x || !w || !y || M <= 0 || K <= 0) return TCQ_ERR_ARG;
     if (K % 16 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const int vec = al16(x) && al16(y) && (K * 2) % 16 == 0;
+    const int vec = al16(x) && al16(y) && al16(w);
     launch_k(k_rmsnorm, dim3(M), dim3(row_threads(M, K)), norm_lds(K), (hipStream_t)stream, (const u16*)x, (const u16*)w, eps,
              (u16*)y, K, vec);
     return launch_status();
@@ -670,7 +810,7 @@ extern "C" int tcq_norm_pre(const void* x, const void* w, float eps, const int8_
                             int M, int K, tcq_stream_t stream) {
     if (!x || !w || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
     if (K % 16 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
-    const int vec = al16(x) && (K * 2) % 16 == 0;
+    const int vec = al16(x) && al16(w) && al16(su);
     launch_k(k_norm_pre, dim3(M), dim3(row_threads(M, K)), norm_lds(K), (hipStream_t)stream, (const u16*)x, (const u16*)w, eps,
              (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec);
     return launch_status();
@@ -686,12 +826,13 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     const int asz = dsize(acc_dtype);
     const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && (!rs || al16(rs));
+    const int svec = al16(sv) && al16(x) && al16(xout) && (!bias || al16(bias)) && (!w || (al16(w) && al16(su)));
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = norm_lds(N);
     hipStream_t st = (hipStream_t)stream;
     const u16 *xp = (const u16*)x, *wp = (const u16*)w;
 #define PANP(AD) launch_k(k_post_add_norm_pre<AD>, grid, block, sh, st, acc, lda, col0, s, rs, (const i8*)sv, bias, xp, (u16*)xout, \
-                          wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N, vec)
+                          wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N, vec, svec)
     switch (acc_dtype) {
         case TCQ_I32: PANP(TCQ_I32); break;
         case TCQ_F32: PANP(TCQ_F32); break;

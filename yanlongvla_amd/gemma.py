@@ -69,11 +69,26 @@ class GemmaAttention(nn.Module):
         self.v_proj = nn.Linear(width, head_dim, bias=False)
         self.o_proj = nn.Linear(heads * head_dim, width, bias=False)
 
+    def _device(self, q):
+        return q.is_cuda and q.dtype == torch.bfloat16 and self.head_dim == 256 and self.heads <= 8
+
     def core(self, q, k, v, cache_k=None, cache_v=None, causal_offset=None):
-        """Attention of the projected q / k / v (the cache rows, if any, before this call's own keys / values)."""
+        """Attention of the projected q / k / v (the cache rows, if any, before this call's own keys / values). Device
+        BF16 tensors go to the HIP attention kernel; host tensors (CPU twins in tests) to the same formula in PyTorch."""
+        if self._device(q):
+            from . import kernels
+            o = torch.empty(q.shape[0], self.heads * self.head_dim, dtype=torch.bfloat16, device=q.device)
+            return kernels.attend(q.contiguous(), cache_k, cache_v, k.contiguous(), v.contiguous(), self.heads, causal_offset, o=o)
         kk = k if cache_k is None else torch.cat([cache_k, k.to(cache_k.dtype)], 0)
         vv = v if cache_v is None else torch.cat([cache_v, v.to(cache_v.dtype)], 0)
         return attend(q, kk, vv, self.heads, causal_offset).to(q.dtype)
+
+    def core_quantized(self, q, k, v, cache_k, cache_v, causal_offset, su, q8, scale):
+        """core followed by the rotate + quantize prologue of o_proj (signs su) in the same launches: q8 / scale of the
+        BF16 attention output, which itself is not stored. Device tensors only."""
+        from . import kernels
+        kernels.attend(q.contiguous(), cache_k, cache_v, k.contiguous(), v.contiguous(), self.heads, causal_offset, su=su,
+                       q8=q8, scale=scale)
 
     def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
         """x (M, width) -> (o_proj output, this call's k, v)."""

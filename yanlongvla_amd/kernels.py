@@ -168,6 +168,24 @@ def post_add_norm_pre(acc, s, rs, sv, bias, x, xout, w=None, eps=0.0, su=None, q
     return xout
 
 
+# ------------------------------------------------------------------------------------------------------------- attention
+def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None, su=None, q8=None, scale=None):
+    """Multi-query attention (H <= 8 heads, head dim 256), BF16: keys / values = cache rows (or None) then the new rows.
+    Writes o (M, H * 256) BF16 and / or, with su, q8 / scale of the rotate + quantize prologue of the next projection."""
+    M = q.shape[0]
+    P = 0 if k_cache is None else k_cache.shape[0]
+    for t in (q, k_cache, v_cache, k_new, v_new, o):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError('attend: BF16 tensors only')
+    _contig(q, k_cache, v_cache, k_new, v_new, o, su, q8, scale)
+    D = k_new.shape[1]
+    nc = int(_lib.lib().tcq_attend_chunks(P, M))
+    part = torch.empty(M * nc * heads * (D + 2), dtype=torch.float32, device=q.device)
+    call('tcq_attend', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, D,
+         -1 if causal_offset is None else int(causal_offset), ptr(part), ptr(o), ptr(su), ptr(q8), ptr(scale), stream())
+    return o
+
+
 # -------------------------------------------------------------------------------------------------------------- products
 def gemv_descriptors(layers):
     """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers each). Keep the tensors alive."""

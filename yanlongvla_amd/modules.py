@@ -243,8 +243,11 @@ class KDecoderLayer(torch.nn.Module):
         b = qkv.buffers(M, dev)
         kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], scale=b['scale'])
         q, k, v = qkv.posts(qkv.product(b), b, x2.shape)
-        o = self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)
-        b2 = og.quantize(og.prep(o))
+        if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
+            b2 = og.buffers(M, dev)
+            self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'])
+        else:
+            b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
         z = og.product(b2)
         x3 = torch.empty_like(x2)
         b3 = gu.buffers(M, dev)
