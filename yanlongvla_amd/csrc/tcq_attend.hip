@@ -2,7 +2,7 @@
 // arithmetic: the attention of the Gemma decoder layers whose projections run on the TCQ kernels. The keys are the cache
 // rows followed by this call's own rows, so no concatenated copy is made.
 //
-// Split over the keys (64 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
+// Split over the keys (256 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
 // head, their chunk maximum m, the exponentials e = exp(s - m), l = sum e and the unnormalised outputs o = sum e v; then
 // k_attn_combine merges the chunks of a token (weights exp(m_c - max_c m_c)) and divides by the merged sum. The result
 // depends on the number of keys only through this fixed chunking, never on launch shapes. The combine can feed its BF16
@@ -14,7 +14,7 @@ namespace {
 
 constexpr int AD = 256;          // head dim
 constexpr int AH = 8;            // most query heads
-constexpr int KC = 64;           // keys per chunk
+constexpr int KC = 256;          // keys per chunk
 constexpr int AT = 256;          // threads of k_attn_part
 
 __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh, int P, int j) {
@@ -32,25 +32,32 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     const int T = P + M, j0 = c * KC;
     const int jend = min(T, causal >= 0 ? causal + t + 1 : T);        // keys j < jend are visible to this query
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
-    for (int i = tid; i < AH * AD; i += AT) {
-        const int h = i / AD, d = i - h * AD;
-        qs[h][d] = h < H ? bf16_to_f32(gptr(q)[(size_t)t * H * AD + h * AD + d]) : 0.f;
+    if (j0 < jend) {
+        for (int i = tid; i < AH * AD; i += AT) {
+            const int h = i / AD, d = i - h * AD;
+            qs[h][d] = h < H ? bf16_to_f32(gptr(q)[(size_t)t * H * AD + h * AD + d]) : 0.f;
+        }
     }
     __syncthreads();
-    // scores: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the 4 quarters
-    {
-        const int kk = tid >> 2, p = tid & 3, j = j0 + kk;
+    // scores, 64 keys per pass: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the quarters
+    for (int pass = 0; pass < KC / 64; ++pass) {
+        const int kk = pass * 64 + (tid >> 2), p = tid & 3, j = j0 + kk;
         float a[AH];
 #pragma unroll
         for (int h = 0; h < AH; ++h) a[h] = 0.f;
         if (j < jend) {
             const u16* kr = key_row(kc, kn, P, j) + 64 * p;
+            uint4_t w[8];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) w[b] = gptr((const uint4_t*)kr)[b];
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const uint4_t w = gptr((const uint4_t*)kr)[b];
                 float kv[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) { kv[2 * e] = bf16_to_f32((u16)(w[e] & 0xffffu)); kv[2 * e + 1] = bf16_to_f32((u16)(w[e] >> 16)); }
+                for (int e = 0; e < 4; ++e) {
+                    kv[2 * e] = bf16_to_f32((u16)(w[b][e] & 0xffffu));
+                    kv[2 * e + 1] = bf16_to_f32((u16)(w[b][e] >> 16));
+                }
 #pragma unroll
                 for (int h = 0; h < AH; ++h)
 #pragma unroll
@@ -68,19 +75,28 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
         }
     }
     __syncthreads();
-    // chunk softmax statistics: wave w takes heads 2w, 2w + 1, lane = key
+    // chunk softmax statistics: wave w takes heads 2w, 2w + 1; lane holds keys lane + 64 i
     {
         const int w = tid >> 6, lane = tid & 63;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * w + hh;
-            const float s = ps[h][lane];
-            const float m = wave_max(s);
-            const float e = m == -__builtin_inff() ? 0.f : expf(s - m);
-            float l = e;
+            float sv[KC / 64], m = -__builtin_inff();
+#pragma unroll
+            for (int i = 0; i < KC / 64; ++i) {
+                sv[i] = ps[h][lane + 64 * i];
+                m = fmaxf(m, sv[i]);
+            }
+            m = wave_max(m);
+            float l = 0.f;
+#pragma unroll
+            for (int i = 0; i < KC / 64; ++i) {
+                const float e = m == -__builtin_inff() ? 0.f : expf(sv[i] - m);
+                ps[h][lane + 64 * i] = e;
+                l = l + e;
+            }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
-            ps[h][lane] = e;
             if (lane == 0 && h < H) {
                 float* base = part + (((size_t)t * NC + c) * H + h) * (AD + 2);
                 base[AD] = m;
@@ -89,14 +105,24 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
         }
     }
     __syncthreads();
-    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order
+    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order (values loaded 8 keys ahead)
     {
         const int d = tid;
         float o[AH];
 #pragma unroll
         for (int h = 0; h < AH; ++h) o[h] = 0.f;
         const int kn_end = min(KC, jend - j0);
-        for (int kk = 0; kk < kn_end; ++kk) {
+        int kk = 0;
+        for (; kk + 8 <= kn_end; kk += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = bf16_to_f32(gptr(key_row(vc, vn, P, j0 + kk + u))[d]);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][kk + u] * v[u];
+        }
+        for (; kk < kn_end; ++kk) {
             const float v = bf16_to_f32(gptr(key_row(vc, vn, P, j0 + kk))[d]);
 #pragma unroll
             for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][kk] * v;
@@ -106,24 +132,50 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 }
 
 // grid M, block 256 (one thread per dim). o (M, H * AD) BF16 (or NULL); with su, the row also goes through the rotate +
-// quantize prologue (q8 row-major (M, H * AD), scale (M,)).
+// quantize prologue (q8 row-major (M, H * AD), scale (M,)). The chunk statistics of the token are staged in LDS first and
+// the weights exp(m_c - max m) computed once per (chunk, head); each thread then sums its dim over the chunks, the loads
+// of all chunks in flight together.
+constexpr int MAXC = 64;         // most chunks a token may have in the combine (16384 keys)
 __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
     extern __shared__ float lds[];
     __shared__ float red[16];
+    __shared__ float wts[AH][MAXC];
+    __shared__ float inv[AH];
     const int t = blockIdx.x, d = threadIdx.x, K = H * AD;
-    for (int h = 0; h < H; ++h) {
-        const float* base = part + ((size_t)t * NC * H + h) * (AD + 2);
-        const size_t cs = (size_t)H * (AD + 2);                      // stride between chunks
+    const size_t cs = (size_t)H * (AD + 2);                          // stride between chunks
+    const float* tb = part + (size_t)t * NC * cs;
+    for (int i = threadIdx.x; i < H * NC; i += blockDim.x) {
+        const int h = i / NC, c = i - h * NC;
+        wts[h][c] = tb[c * cs + h * (AD + 2) + AD];                  // m
+    }
+    __syncthreads();
+    if (threadIdx.x < H) {
+        const int h = threadIdx.x;
         float mx = -__builtin_inff();
-        for (int c = 0; c < NC; ++c) mx = fmaxf(mx, base[c * cs + AD]);
-        float L = 0.f, acc = 0.f;
+        for (int c = 0; c < NC; ++c) mx = fmaxf(mx, wts[h][c]);
+        float L = 0.f;
         for (int c = 0; c < NC; ++c) {
-            const float m = base[c * cs + AD];
-            const float wgt = m == -__builtin_inff() ? 0.f : expf(m - mx);
-            L = L + wgt * base[c * cs + AD + 1];
-            acc = acc + wgt * base[c * cs + d];
+            const float m = wts[h][c];
+            const float w = m == -__builtin_inff() ? 0.f : expf(m - mx);
+            L = L + w * tb[c * cs + h * (AD + 2) + AD + 1];
+            wts[h][c] = w;
         }
-        const u16 b = f32_to_bf16(acc / L);
+        inv[h] = L;
+    }
+    __syncthreads();
+    float acc[AH];
+#pragma unroll
+    for (int h = 0; h < AH; ++h) acc[h] = 0.f;
+    for (int c = 0; c < NC; ++c) {
+        const float* col = tb + c * cs + d;
+        float v[AH];
+#pragma unroll
+        for (int h = 0; h < AH; ++h) v[h] = h < H ? col[h * (AD + 2)] : 0.f;
+#pragma unroll
+        for (int h = 0; h < AH; ++h) acc[h] = acc[h] + wts[h][c] * v[h];
+    }
+    for (int h = 0; h < H; ++h) {
+        const u16 b = f32_to_bf16(acc[h] / inv[h]);
         if (o) gptr(o)[(size_t)t * K + h * AD + d] = b;
         if (su) lds[lds_slot(h * AD + d)] = bf16_to_f32(b) * (float)gptr(su)[h * AD + d];
     }
@@ -148,7 +200,7 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
     if ((uintptr_t)k_new % 16 || (uintptr_t)(k_cache) % 16) return TCQ_ERR_ALIGN;
     const int NC = tcq_attend_chunks(P, M);
-    if (NC > 65535) return TCQ_ERR_UNSUPPORTED;
+    if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     launch_k(k_attn_part, dim3(M, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
              (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
