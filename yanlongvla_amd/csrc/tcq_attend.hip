@@ -24,54 +24,71 @@ __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh
 }  // namespace
 
 // grid (tokens M, chunks NC), AT threads. part: (M, NC, H, AD + 2) FP32: o[AD], m, l per head.
+// Keys: each pass of 64 keys loads its rows with 16-byte loads (the next pass's are in flight while one is used). Values:
+// blocks of 64 rows staged in LDS with 16-byte loads (the next block's loads in flight while one is used), then one thread
+// per dim walks the block's keys in order.
 __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, const u16* vc, int P, const u16* kn, const u16* vn,
                                                   int M, int H, int causal, float* part) {
     __shared__ float qs[AH][AD];
     __shared__ float ps[AH][KC + 1];
+    __shared__ __attribute__((aligned(16))) u16 vs[64][AD];
     const int t = blockIdx.x, c = blockIdx.y, NC = gridDim.y, tid = threadIdx.x;
     const int T = P + M, j0 = c * KC;
     const int jend = min(T, causal >= 0 ? causal + t + 1 : T);        // keys j < jend are visible to this query
+    const int nvis = max(0, min(KC, jend - j0));                        // visible keys of this chunk
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
-    if (j0 < jend) {
+    if (nvis > 0) {
         for (int i = tid; i < AH * AD; i += AT) {
             const int h = i / AD, d = i - h * AD;
             qs[h][d] = h < H ? bf16_to_f32(gptr(q)[(size_t)t * H * AD + h * AD + d]) : 0.f;
         }
     }
     __syncthreads();
-    // scores, 64 keys per pass: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the quarters
-    for (int pass = 0; pass < KC / 64; ++pass) {
-        const int kk = pass * 64 + (tid >> 2), p = tid & 3, j = j0 + kk;
-        float a[AH];
+    const int npass = (nvis + 63) >> 6;
+    // scores: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the quarters
+    {
+        const int p = tid & 3;
+        uint4_t w[2][8];
+        auto fetch = [&](int pass, uint4_t(&dst)[8]) {
+            const int j = j0 + pass * 64 + (tid >> 2);
+            if (pass < npass && j < jend) {
+                const u16* kr = key_row(kc, kn, P, j) + 64 * p;
 #pragma unroll
-        for (int h = 0; h < AH; ++h) a[h] = 0.f;
-        if (j < jend) {
-            const u16* kr = key_row(kc, kn, P, j) + 64 * p;
-            uint4_t w[8];
-#pragma unroll
-            for (int b = 0; b < 8; ++b) w[b] = gptr((const uint4_t*)kr)[b];
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                float kv[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kv[2 * e] = bf16_to_f32((u16)(w[b][e] & 0xffffu));
-                    kv[2 * e + 1] = bf16_to_f32((u16)(w[b][e] >> 16));
-                }
-#pragma unroll
-                for (int h = 0; h < AH; ++h)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][64 * p + 8 * b + e] * kv[e];
+                for (int b = 0; b < 8; ++b) dst[b] = gptr((const uint4_t*)kr)[b];
             }
-        }
+        };
+        fetch(0, w[0]);
 #pragma unroll
-        for (int h = 0; h < AH; ++h) {
-            a[h] = a[h] + __shfl_xor(a[h], 1, 64);
-            a[h] = a[h] + __shfl_xor(a[h], 2, 64);
-        }
-        if (p == 0) {
+        for (int pass = 0; pass < KC / 64; ++pass) {
+            const int kk = pass * 64 + (tid >> 2), j = j0 + kk;
+            if (pass + 1 < KC / 64) fetch(pass + 1, w[(pass + 1) & 1]);
+            float a[AH];
 #pragma unroll
-            for (int h = 0; h < AH; ++h) ps[h][kk] = j < jend ? a[h] * scl : -__builtin_inff();
+            for (int h = 0; h < AH; ++h) a[h] = 0.f;
+            if (pass < npass && j < jend) {
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    float kv[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kv[2 * e] = bf16_to_f32((u16)(w[pass & 1][b][e] & 0xffffu));
+                        kv[2 * e + 1] = bf16_to_f32((u16)(w[pass & 1][b][e] >> 16));
+                    }
+#pragma unroll
+                    for (int h = 0; h < AH; ++h)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][64 * p + 8 * b + e] * kv[e];
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < AH; ++h) {
+                a[h] = a[h] + __shfl_xor(a[h], 1, 64);
+                a[h] = a[h] + __shfl_xor(a[h], 2, 64);
+            }
+            if (p == 0) {
+#pragma unroll
+                for (int h = 0; h < AH; ++h) ps[h][kk] = j < jend ? a[h] * scl : -__builtin_inff();
+            }
         }
     }
     __syncthreads();
@@ -104,28 +121,36 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
             }
         }
     }
-    __syncthreads();
-    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order (values loaded 8 keys ahead)
+    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order, values from the LDS stage
     {
         const int d = tid;
         float o[AH];
 #pragma unroll
         for (int h = 0; h < AH; ++h) o[h] = 0.f;
-        const int kn_end = min(KC, jend - j0);
-        int kk = 0;
-        for (; kk + 8 <= kn_end; kk += 8) {
-            float v[8];
+        uint4_t v[8];                                              // this thread's 8 of the block's 2048 16-byte granules
+        auto vfetch = [&](int blk) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = bf16_to_f32(gptr(key_row(vc, vn, P, j0 + kk + u))[d]);
+            for (int u = 0; u < 8; ++u) {
+                const int gi = u * AT + tid, row = gi >> 5, col = gi & 31, j = j0 + blk * 64 + row;
+                v[u] = j < jend ? gptr((const uint4_t*)(key_row(vc, vn, P, j) + 8 * col))[0] : uint4_t{0, 0, 0, 0};
+            }
+        };
+        if (npass > 0) vfetch(0);
+        for (int blk = 0; blk < npass; ++blk) {
+            __syncthreads();                                       // ps complete (first block) / previous block consumed
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < 8; ++u) {
+                const int gi = u * AT + tid;
+                *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = v[u];
+            }
+            __syncthreads();
+            if (blk + 1 < npass) vfetch(blk + 1);
+            const int kend = min(64, nvis - blk * 64);
+            for (int kk = 0; kk < kend; ++kk) {
+                const float x = bf16_to_f32(vs[kk][d]);
 #pragma unroll
-                for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][kk + u] * v[u];
-        }
-        for (; kk < kn_end; ++kk) {
-            const float v = bf16_to_f32(gptr(key_row(vc, vn, P, j0 + kk))[d]);
-#pragma unroll
-            for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][kk] * v;
+                for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][blk * 64 + kk] * x;
+            }
         }
         for (int h = 0; h < H; ++h) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = o[h];
     }
@@ -140,6 +165,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
     extern __shared__ float lds[];
     __shared__ float red[16];
     __shared__ float wts[AH][MAXC];
+    __shared__ float ls[AH][MAXC];
     __shared__ float inv[AH];
     const int t = blockIdx.x, d = threadIdx.x, K = H * AD;
     const size_t cs = (size_t)H * (AD + 2);                          // stride between chunks
@@ -147,6 +173,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
     for (int i = threadIdx.x; i < H * NC; i += blockDim.x) {
         const int h = i / NC, c = i - h * NC;
         wts[h][c] = tb[c * cs + h * (AD + 2) + AD];                  // m
+        ls[h][c] = tb[c * cs + h * (AD + 2) + AD + 1];               // l
     }
     __syncthreads();
     if (threadIdx.x < H) {
@@ -157,7 +184,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
         for (int c = 0; c < NC; ++c) {
             const float m = wts[h][c];
             const float w = m == -__builtin_inff() ? 0.f : expf(m - mx);
-            L = L + w * tb[c * cs + h * (AD + 2) + AD + 1];
+            L = L + w * ls[h][c];
             wts[h][c] = w;
         }
         inv[h] = L;
@@ -166,6 +193,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
     float acc[AH];
 #pragma unroll
     for (int h = 0; h < AH; ++h) acc[h] = 0.f;
+#pragma unroll 4
     for (int c = 0; c < NC; ++c) {
         const float* col = tb + c * cs + d;
         float v[AH];
@@ -198,7 +226,7 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     if (!o && !su) return TCQ_ERR_ARG;
     if (su && (!q8 || !scale)) return TCQ_ERR_ARG;
     if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
-    if ((uintptr_t)k_new % 16 || (uintptr_t)(k_cache) % 16) return TCQ_ERR_ALIGN;
+    if ((uintptr_t)k_new % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_new % 16 || (uintptr_t)v_cache % 16) return TCQ_ERR_ALIGN;
     const int NC = tcq_attend_chunks(P, M);
     if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
