@@ -2,7 +2,7 @@
 // arithmetic: the attention of the Gemma decoder layers whose projections run on the TCQ kernels. The keys are the cache
 // rows followed by this call's own rows, so no concatenated copy is made.
 //
-// Split over the keys (256 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
+// Split over the keys (64 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
 // head, their chunk maximum m, the exponentials e = exp(s - m), l = sum e and the unnormalised outputs o = sum e v; then
 // k_attn_combine merges the chunks of a token (weights exp(m_c - max_c m_c)) and divides by the merged sum. The result
 // depends on the number of keys only through this fixed chunking, never on launch shapes. The combine can feed its BF16
@@ -14,7 +14,7 @@ namespace {
 
 constexpr int AD = 256;          // head dim
 constexpr int AH = 8;            // most query heads
-constexpr int KC = 256;          // keys per chunk
+constexpr int KC = 64;           // keys per chunk
 constexpr int AT = 256;          // threads of k_attn_part
 
 __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh, int P, int j) {
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 // quantize prologue (q8 row-major (M, H * AD), scale (M,)). The chunk statistics of the token are staged in LDS first and
 // the weights exp(m_c - max m) computed once per (chunk, head); each thread then sums its dim over the chunks, the loads
 // of all chunks in flight together.
-constexpr int MAXC = 64;         // most chunks a token may have in the combine (16384 keys)
+constexpr int MAXC = 256;        // most chunks a token may have in the combine (16384 keys)
 __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
     extern __shared__ float lds[];
     __shared__ float red[16];
