@@ -45,16 +45,17 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     }
     __syncthreads();
     const int npass = (nvis + 63) >> 6;
-    // scores: thread (key kk = tid / 4, quarter p = tid % 4 of the dims), 8 heads, reduced over the quarters
+    // scores: thread (key kk = tid / 4, part p = tid % 4: dims 32 b + 8 p + e), 8 heads, reduced over the 4 parts; the
+    // 4 parts of a key read adjacent 32-byte pieces of the query rows (different LDS banks)
     {
         const int p = tid & 3;
         uint4_t w[2][8];
         auto fetch = [&](int pass, uint4_t(&dst)[8]) {
             const int j = j0 + pass * 64 + (tid >> 2);
             if (pass < npass && j < jend) {
-                const u16* kr = key_row(kc, kn, P, j) + 64 * p;
+                const u16* kr = key_row(kc, kn, P, j) + 8 * p;
 #pragma unroll
-                for (int b = 0; b < 8; ++b) dst[b] = gptr((const uint4_t*)kr)[b];
+                for (int b = 0; b < 8; ++b) dst[b] = gptr((const uint4_t*)(kr + 32 * b))[0];
             }
         };
         fetch(0, w[0]);
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 #pragma unroll
                     for (int h = 0; h < AH; ++h)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][64 * p + 8 * b + e] * kv[e];
+                        for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][32 * b + 8 * p + e] * kv[e];
                 }
             }
 #pragma unroll
