@@ -512,7 +512,7 @@ def main():
                                'FP16 512x2 codebook, L=16 K=2 V=2, input and output block-Walsh rotations',
                    'layers': nl, 'm': M_DIM, 'n': N_DIM, 'tokens': 1, 'packed_bytes_per_step': byts},
         'hbm_frac': round(byts / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1> (layer-stream plan)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
+        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1, 1024> (layer-stream plan)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_from_profile(nl),
                      'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
         'single_layer_ms': {'graph_replay_median': round(lat_med, 5), 'graph_replay_p95': round(lat_p95, 5),

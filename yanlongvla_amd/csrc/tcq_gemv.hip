@@ -22,11 +22,13 @@ namespace {
 
 constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v >> 1); }
 
-template <int C>
+// Codebook in LDS: NE = 1024 entries with the sign of the first coordinate folded in (bit 9), or NE = 512 entries with the
+// sign applied in registers; C copies, entry e copy c at word e C + c.
+template <int C, int NE>
 __device__ __forceinline__ void fill_table(u32* tab, const u16* tl) {
-    for (int e = threadIdx.x; e < 1024; e += blockDim.x) {
+    for (int e = threadIdx.x; e < NE; e += blockDim.x) {
         const int h = e & 511;
-        const u32 v = ((u32)gptr(tl)[2 * h] ^ ((u32)(e >> 9) << 15)) | ((u32)gptr(tl)[2 * h + 1] << 16);
+        const u32 v = ((u32)gptr(tl)[2 * h] ^ (NE == 1024 ? (u32)(e >> 9) << 15 : 0u)) | ((u32)gptr(tl)[2 * h + 1] << 16);
         if constexpr (C % 4 == 0) {
 #pragma unroll
             for (int c = 0; c < C; c += 4) *(uint4_t*)(tab + e * C + c) = uint4_t{v, v, v, v};
@@ -48,10 +50,10 @@ __device__ __forceinline__ void fill_table(u32* tab, const u16* tl) {
 // Dynamic LDS: h16 (M, 256 nch) FP16 with zero columns from n on, the FP32 row scales of the workgroup's rows, then for
 // KS > 1 the partial sums (nw R 64 float4). Two accumulators per tile row (pairs 0..3 and 4..7) halve the MFMA dependency
 // chain.
-template <int C, int R, int D, int AUX, int KS>
+template <int C, int R, int D, int AUX, int KS, int NE = 1024>
 __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers, const u16* h16, const float* hscale, int M,
                                                    int m, int n, int rows_per_wg) {
-    __shared__ __attribute__((aligned(16))) u32 tab[1024 * C];
+    __shared__ __attribute__((aligned(16))) u32 tab[NE * C];
     extern __shared__ __attribute__((aligned(16))) u32 dyn[];
     const tcq_gemv_layer L = layers[blockIdx.y];
     const int tiles_m = m >> 4, nch = (n + 255) >> 8, np = nch << 8;
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
 
     u16* hl = (u16*)dyn;
     float* sl = (float*)(dyn + (M * np >> 1));
-    fill_table<C>(tab, (const u16*)L.tlut);
+    fill_table<C, NE>(tab, (const u16*)L.tlut);
     for (int i = threadIdx.x; i < (M * np) >> 3; i += blockDim.x) {      // 8 FP16 per thread-step, rows padded to np
         const int t = i / (np >> 3), k = (i - t * (np >> 3)) << 3;
         ((uint4_t*)hl)[i] = k < n ? gptr((const uint4_t*)(h16 + (size_t)t * n + k))[0] : uint4_t{0, 0, 0, 0};
@@ -138,8 +140,12 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
-                v[p] = *(const u32*)((const char*)tab + (((x >> 22) << ESH) | cp4));
-                v[4 + p] = *(const u32*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));
+                v[p] = *(const u32*)((const char*)tab + ((((x >> 22) & (NE - 1)) << ESH) | cp4));
+                v[4 + p] = *(const u32*)((const char*)tab + ((((x >> 6) & (NE - 1)) << ESH) | cp4));
+                if (NE == 512) {                       // sign of the first coordinate: bit 15 of each code
+                    v[p] ^= (x >> 16) & 0x8000u;
+                    v[4 + p] ^= x & 0x8000u;
+                }
             }
         };
         auto consume = [&](int q, const u32(&v)[8]) {

@@ -568,12 +568,14 @@ __global__ void k_post_add_norm_pre(const void* acc, int lda, int col0, const fl
 }
 
 // =========================================================================================================== C ABI
-// Threads per row: few rows (latency) -> about one 8-element vector per thread; many rows (throughput) -> four vectors per
-// thread so more rows share a CU.
+// Threads per row: few rows (latency) -> about one 8-element vector per thread (up to 1024 threads when there are fewer
+// rows than CUs); many rows (throughput) -> four vectors per thread so more rows share a CU. Every row kernel's result is
+// independent of the thread count.
 static int row_threads(int M, int K) {
     const int per = M <= 256 ? 8 : 32;
+    const int cap = M <= 64 ? 1024 : 512;        // fewer rows than CUs: wide rows take whole 1024-thread workgroups
     int t = 64;
-    while (t < 512 && t * per < K) t <<= 1;
+    while (t < cap && t * per < K) t <<= 1;
     return t;
 }
 static size_t row_lds(int K) { return (size_t)lds_words(K) * sizeof(float); }
