@@ -65,8 +65,10 @@ int64_t tcq_repack_words(int m, int n);
  * (deploy/tcq_kernels/kernels.py:339-349, 653-656); definition tcq_format.Layer.w8_reference (tcq_format.py:97-98). */
 int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream);
 
-/* Dense decode through the FP16 table: out (m, n) FP16 = sign * tlut[hash(state)] (exact). Counterpart of
- * tcq_format.lookup(states, tlut.float()) (tcq_format.py:66-71, 103, 139) and of kernels.decode_bf16 (kernels.py:320-337). */
+/* Dense decode through a 16-bit table: out (m, n) = sign * tlut[hash(state)], the sign flipping bit 15 of the first
+ * coordinate (exact for FP16 and BF16 tables). With the FP16 table: tcq_format.lookup(states, tlut.float())
+ * (tcq_format.py:66-71, 103, 139); with the BF16 bit patterns of the INT8 table values: kernels.decode_bf16 / k_decode_bf16
+ * (kernels.py:320-337, 683-686). */
 int tcq_decode_f16(const void* bits, const void* tlut, void* out, int m, int n, tcq_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------------------------- rotation */
@@ -237,6 +239,14 @@ int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float
  * rest the tiled GEMM. */
 int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
                 int K, tcq_stream_t stream);
+
+/* BF16 GEMM of the W2 float path: acc = sum_k a[m, k] w[n, k] with FP32 accumulation, a (M, K) BF16 (rotated activations),
+ * w (N, K) BF16 (the INT8 table values as BF16, tcq_decode_f16 with the BF16 table); out = (acc * sa[m]) * sw[n] as FP32 or
+ * BF16 (sa / sw may be NULL: factor 1). K % 16 == 0, N % 4 == 0; a, w, out 16-byte aligned. Replaces the BF16 product of
+ * Group.run_float (`h @ W.t()` on decoded BF16 weights, deploy/tcq_kernels/modules.py:125-130) and the float small-M
+ * products kernels.gemmf_w8 / gemmf_tcq (kernels.py:442-489, 686-696) with sw = rs, FP32 output. */
+int tcq_gemm_bf16(const void* a, const void* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
+                  int K, tcq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ How each function is pinned (tests/test_oracle.py):
          s[t+1] = ((s[t] << 4) | next nibble) & 0xffff with tail-biting, exact int64 products (int_matmul).
   gelu_tanh_bf16 -> PyTorch's own torch.nn.functional.gelu(approximate='tanh') (the library routine the reference tabulates).
   rmsnorm_bf16 -> PyTorch's own RMSNorm formula in FP64 (within one BF16 rounding; the summation order is the kernels').
-  mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference -> compositions of the pinned functions with the rounding points written in
+  mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference, w2_linear -> compositions of the pinned functions with the rounding points written in
          deploy/tcq_kernels/kernels.py:272-277, 303 (checked against the unfused chain in the tests).
 """
 import math
@@ -27,7 +27,7 @@ import math
 import numpy as np
 
 __all__ = ['block_widths', 'fwht', 'states_from_bits', 'lookup', 'snap', 'quantize_tokens', 'int_matmul', 'Layer',
-           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'plain_middle', 'pre2', 'rmsnorm_bf16', 'quantize_channels',
+           'reference_linear', 'bf16_bits', 'bf16_to_f32', 'gelu_tanh_bf16', 'mlp_middle', 'plain_middle', 'pre2', 'rmsnorm_bf16', 'w2_linear', 'quantize_channels',
            'w8a8_reference', 'q4_layout', 'random_layer']
 
 
@@ -237,6 +237,19 @@ def plain_middle(z, sv, bias, su, gelu=gelu_tanh_bf16):
     g = gelu(post_bf16(z, sv, bias))
     q, s = quantize_tokens(fwht(bf16_to_f32(g) * np.asarray(su).astype(np.float32)))
     return q, s, g
+
+
+def w2_linear(x, layer, small):
+    """W2 float path (deploy/tcq_kernels/modules.py:117-144; kernels.py:309-337, 442-489): h = BF16(fwht(x * su)), the
+    INT8 table values as weights, FP32 accumulation. Expert (small): z = acc * rs in FP32. Prefill: acc rounded to BF16 (the
+    BF16 result of the BF16 matmul), z = bf16(acc) * rs. Then fwht(z) * sv (+ bias) -> BF16 bits. The product is summed in
+    FP64 here; a device's FP32 sums differ in the last bits."""
+    x = np.asarray(x, dtype=np.float32)
+    h = bf16_to_f32(bf16_bits(fwht(x.reshape(-1, layer.n) * layer.su.astype(np.float32))))
+    acc = (h.astype(np.float64) @ layer.w8_reference().astype(np.float64).T).astype(np.float32)
+    if not small:
+        acc = bf16_to_f32(bf16_bits(acc))
+    return post_bf16(acc * layer.rs[None, :], layer.sv, layer.bias)
 
 
 def rmsnorm_bf16(x, w_bits, eps):

@@ -223,3 +223,68 @@ def test_chunk_close_to_cpu_oracle():
     v_gpu = model.velocity(x.to(DEV)).float().cpu()
     v_cpu = cpu.velocity(x).float()
     assert (v_gpu - v_cpu).norm() / v_cpu.norm() < 2e-2
+
+
+# ---------------------------------------------------------------------------------------------------- W2 float path
+def test_decode_bf16_bitexact():
+    """BF16 decode == the INT8 decode's values; the sign flips bit 15 as in k_decode_bf16 (kernels.py:320-337), so a zero
+    table value with the sign bit set decodes to -0.0 (bit-exact after mapping -0.0 -> +0.0)."""
+    from yanlongvla_amd import kernels as K
+    L, ol = device_layer(256, 512, 31)
+    tb = L.t8.to(torch.bfloat16).contiguous()
+    out = torch.empty(256, 512, dtype=torch.bfloat16, device=DEV)
+    K.decode_bf16(L.bits, tb, out)
+    got = bits16(out)
+    got = np.where(got == 0x8000, 0, got).astype(np.uint16)
+    assert np.array_equal(got, O.bf16_bits(ol.w8_reference().astype(np.float32)))
+
+
+@pytest.mark.parametrize('M,N,K', [(800, 2048, 1024), (65, 4096, 1024), (1, 1024, 4096), (50, 2560, 1024), (7, 16, 48)])
+def test_gemm_bf16_matches_fp64(M, N, K):
+    from yanlongvla_amd import kernels as Kn
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g, device=DEV).bfloat16()
+    w = torch.randint(-127, 128, (N, K), generator=g, device=DEV).float().bfloat16()
+    sw = torch.rand(N, generator=g, device=DEV) + 0.5
+    ref = (a.double().cpu() @ w.double().cpu().t())
+    z = Kn.gemm_bf16(a, w, torch.empty(M, N, device=DEV), sw=sw)
+    zr = ref * sw.double().cpu()[None, :]
+    assert ((z.double().cpu() - zr).norm() / zr.norm()).item() < 1e-6
+    y = Kn.gemm_bf16(a, w, torch.empty(M, N, dtype=torch.bfloat16, device=DEV))
+    z0 = Kn.gemm_bf16(a, w, torch.empty(M, N, device=DEV))
+    assert np.array_equal(bits16(y), O.bf16_bits(z0.cpu().numpy()))              # BF16 output = RNE of the FP32 sums
+    assert ((z0.double().cpu() - ref).norm() / ref.norm()).item() < 1e-6
+
+
+@pytest.mark.parametrize('M,part', [(50, 'expert'), (1, 'expert'), (200, 'llm'), (16, 'llm')])
+@pytest.mark.parametrize('mode', ['fly', 'resident'])
+def test_group_float_path_matches_oracle(M, part, mode):
+    """W2 float path of a q / k / v group against the oracle's restatement: relative L2 <= 2e-3 (FP32 device sums against
+    FP64; the prefill variant rounds the product to BF16 before the row scale)."""
+    from yanlongvla_amd.modules import Group, KLinear
+    layers, oracles = qkv_layers(300 + M)
+    g = Group(layers, part, mode, a8=False)
+    mods = [KLinear(g, i) for i in range(3)]
+    x = torch.randn(M, 1024, device=DEV).bfloat16()
+    xs = x.float().cpu().numpy()
+    for mod, ol in zip(mods, oracles):
+        y = O.bf16_to_f32(bits16(mod(x)))
+        ref = O.bf16_to_f32(O.w2_linear(xs, ol, part == 'expert'))
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 2e-3
+
+
+def test_install_float_runtime():
+    """install(a8=False): the W2 float path at the fly / resident / hybrid operating points gives the same chunk; MLPs and
+    decoder layers stay unfused (the fused middles are W2A8 kernels)."""
+    from yanlongvla_amd import gemma, modules
+    outs, infos = {}, {}
+    noise = torch.randn(50, 32, generator=torch.Generator(device=DEV).manual_seed(8), device=DEV)
+    for runtime in ('fly', 'resident', 'hybrid'):
+        model = small_expert()
+        infos[runtime] = modules.install(model, runtime=runtime, a8=False, layers=gemma.synthetic_layers(model, 12, DEV))
+        if runtime == 'hybrid':
+            modules.decode_chunk(model)
+        outs[runtime] = model.sample_chunk(noise, steps=2)
+    assert infos['fly']['fused_mlps'] == 0 and infos['fly']['fused_layers'] == 0
+    assert torch.equal(outs['fly'], outs['resident']) and torch.equal(outs['fly'], outs['hybrid'])
+    assert torch.isfinite(outs['fly']).all()

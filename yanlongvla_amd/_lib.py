@@ -36,6 +36,7 @@ SIGNATURES = {
     'tcq_norm_pre': [_P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_post_add_norm_pre': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_attend_chunks': [_I, _I],
+    'tcq_gemm_bf16': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],

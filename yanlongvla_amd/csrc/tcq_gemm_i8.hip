@@ -1,7 +1,12 @@
-// W8A8 INT8 GEMM for many tokens on v_mfma_i32_32x32x32_i8 (measured on MI355X: 4.05 POPS for back-to-back independent
-// 32 x 32 x 32 products against 2.7 for 16 x 16 x 64): acc[m, n] = sum_k a[m, k] w[n, k] (exact int32), written as
-// int32, as FP32 (float(acc) * sa[m]) * sw[n], or as BF16 of that. a (M, K) and w (N, K) are both row-major with K
-// contiguous, so every MFMA operand is 16 consecutive bytes of one row.
+// GEMM for many tokens, acc[m, n] = sum_k a[m, k] w[n, k], a (M, K) and w (N, K) both row-major with K contiguous, so every
+// MFMA operand is 16 consecutive bytes of one row:
+//   INT8 (W8A8) on v_mfma_i32_32x32x32_i8 (measured on MI355X: 4.05 POPS for back-to-back independent 32 x 32 x 32 products
+//   against 2.7 for 16 x 16 x 64): exact int32 acc, written as int32, as FP32 (float(acc) * sa[m]) * sw[n], or as BF16 of
+//   that;
+//   BF16 (the W2 float path: BF16 rotated activations times the INT8 table values as BF16) on v_mfma_f32_32x32x16_bf16 with
+//   FP32 accumulation, written as FP32 (acc * sa[m]) * sw[n] (either scale may be absent) or as BF16 of that.
+// Both take 64-byte K steps: 64 int8 = two 32-element MFMA halves, or 32 bf16 = two 16-element MFMA steps, with the same
+// 16-byte fragment per lane.
 //
 // Workgroup tile TN weights x TM tokens, WN x WM waves, each (TN / WN) x (TM / WM) in 32 x 32 MFMA blocks. MFMA A = 32
 // token rows (lane (h, r): row r, 16 columns of half h of the 32), B = 32 weight rows, D: register 4 q + e of lane (h, c)
@@ -37,9 +42,29 @@ __device__ __forceinline__ void barrier_nofence() {
 
 }  // namespace
 
-template <int TN, int TM, int WN, int WM, int NS, int ODT>
-__global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const i8* a, const i8* w, const float* sa, const float* sw, void* out,
-                                                          int ldo, int M, int N, int K) {
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+template <int ESZ> struct MfmaOf;
+template <> struct MfmaOf<1> {                 // INT8
+    typedef int16v acc_t;
+    static __device__ __forceinline__ acc_t mma(int4v a, int4v b, acc_t c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+};
+template <> struct MfmaOf<2> {                 // BF16
+    typedef float16v acc_t;
+    static __device__ __forceinline__ acc_t mma(int4v a, int4v b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+
+// ESZ: element size (1 INT8, 2 BF16); K in elements.
+template <int ESZ, int TN, int TM, int WN, int WM, int NS, int ODT>
+__global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const void* w_, const float* sa, const float* sw, void* out,
+                                                          int ldo, int M, int N, int K_) {
+    typedef typename MfmaOf<ESZ>::acc_t acc_t;
+    const char* a = (const char*)a_;
+    const char* w = (const char*)w_;
+    const int K = K_ * ESZ;                                              // row length in bytes
     constexpr int NWAVE = WN * WM;
     constexpr int WBLK = TN / 16, ABLK = TM / 16, BLK = WBLK + ABLK;    // 1 KiB blocks (16 rows x 64 bytes) per step
     constexpr int PW = BLK / NWAVE;                                      // direct loads per wave per step
@@ -77,7 +102,7 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const i8* a, const i8*
         return *(const int4v*)(st + (b0 + (l32 >> 4)) * 1024 + swz(l32 & 15, 2 * kk + lh));
     };
 
-    int16v acc[BN][BM];
+    acc_t acc[BN][BM];
 #pragma unroll
     for (int i = 0; i < BN; ++i)
 #pragma unroll
@@ -104,7 +129,7 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const i8* a, const i8*
 #pragma unroll
             for (int j = 0; j < BM; ++j)
 #pragma unroll
-                for (int i = 0; i < BN; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[j], B[i], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < BN; ++i) acc[i][j] = MfmaOf<ESZ>::mma(A[j], B[i], acc[i][j]);
         }
     }
 
@@ -117,21 +142,22 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const i8* a, const i8*
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int m = mb + 8 * (r >> 2) + (r & 3);
-            sam[r] = (ODT != TCQ_I32 && m < M) ? gptr(sa)[m] : 0.f;
+            sam[r] = (ODT != TCQ_I32 && m < M && sa) ? gptr(sa)[m] : 1.f;
         }
 #pragma unroll
         for (int i = 0; i < BN; ++i) {
             const int n = n0 + (wn * BN + i) * 32 + l32;
             if (n >= N) continue;
-            const float swn = ODT != TCQ_I32 ? gptr(sw)[n] : 0.f;
+            const float swn = (ODT != TCQ_I32 && sw) ? gptr(sw)[n] : 1.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mb + 8 * (r >> 2) + (r & 3);
                 if (m >= M) continue;
                 const size_t o = (size_t)m * ldo + n;
-                if (ODT == TCQ_I32) gptr((int*)out)[o] = acc[i][j][r];
+                if (ODT == TCQ_I32) gptr((int*)out)[o] = (int)acc[i][j][r];
                 else {
-                    const float v = ((float)acc[i][j][r] * sam[r]) * swn;
+                    const float v = ESZ == 1 ? ((float)acc[i][j][r] * sam[r]) * swn
+                                             : (sa ? (float)acc[i][j][r] * sam[r] : (float)acc[i][j][r]) * (sw ? swn : 1.f);
                     if (ODT == TCQ_F32) gptr((float*)out)[o] = v;
                     else gptr((u16*)out)[o] = f32_to_bf16(v);
                 }
@@ -141,13 +167,22 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const i8* a, const i8*
 }
 
 // =========================================================================================================== C ABI
-template <int TN, int TM, int WN, int WM, int NS>
-static void launch_gemm(int odt, hipStream_t st, const i8* a, const i8* w, const float* sa, const float* sw, void* out, int ldo,
+template <int ESZ, int TN, int TM, int WN, int WM, int NS>
+static void launch_gemm(int odt, hipStream_t st, const void* a, const void* w, const float* sa, const float* sw, void* out, int ldo,
                         int M, int N, int K) {
     const dim3 grid((N + TN - 1) / TN, (M + TM - 1) / TM), block(64 * WN * WM);
-    if (odt == TCQ_I32) launch_k(k_gemm_i8<TN, TM, WN, WM, NS, TCQ_I32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
-    else if (odt == TCQ_F32) launch_k(k_gemm_i8<TN, TM, WN, WM, NS, TCQ_F32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
-    else launch_k(k_gemm_i8<TN, TM, WN, WM, NS, TCQ_BF16>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+    if (odt == TCQ_I32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_I32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+    else if (odt == TCQ_F32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_F32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+    else launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_BF16>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+}
+
+template <int ESZ>
+static void launch_by_m(int odt, hipStream_t st, const void* a, const void* w, const float* sa, const float* sw, void* out, int ldo,
+                        int M, int N, int K) {
+    // token tile by M (a 256-token tile is mostly padding for tens of tokens); 256 x 256 measured best at M = 800
+    if (M <= 64) launch_gemm<ESZ, 256, 64, 4, 1, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    else if (M <= 128) launch_gemm<ESZ, 256, 128, 4, 2, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    else launch_gemm<ESZ, 256, 256, 2, 4, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
 }
 
 extern "C" int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo,
@@ -163,11 +198,17 @@ extern "C" int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, co
         if (N % 16 == 0) return tcq_gemm_w8(&seg, 1, a, sa, M, K, out_dtype, ldo, stream);
     }
     if (out_dtype != TCQ_I32 && out_dtype != TCQ_F32 && out_dtype != TCQ_BF16) return TCQ_ERR_DTYPE;
-    hipStream_t st = (hipStream_t)stream;
-    const i8 *aa = (const i8*)a, *ww = (const i8*)w;
-    // token tile by M (a 256-token tile is mostly padding for tens of tokens); 256 x 256 measured best at M = 800
-    if (M <= 64) launch_gemm<256, 64, 4, 1, 4>(out_dtype, st, aa, ww, sa, sw, out, ldo, M, N, K);
-    else if (M <= 128) launch_gemm<256, 128, 4, 2, 4>(out_dtype, st, aa, ww, sa, sw, out, ldo, M, N, K);
-    else launch_gemm<256, 256, 2, 4, 4>(out_dtype, st, aa, ww, sa, sw, out, ldo, M, N, K);
+    launch_by_m<1>(out_dtype, (hipStream_t)stream, a, w, sa, sw, out, ldo, M, N, K);
+    return launch_status();
+}
+
+extern "C" int tcq_gemm_bf16(const void* a, const void* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M,
+                             int N, int K, tcq_stream_t stream) {
+    if (!a || !w || !out || M <= 0 || N <= 0 || K <= 0 || ldo < N) return TCQ_ERR_ARG;
+    if (out_dtype != TCQ_F32 && out_dtype != TCQ_BF16) return TCQ_ERR_DTYPE;
+    if (K % 16 || N % 4) return TCQ_ERR_SHAPE;
+    if ((size_t)M * K * 2 >= ((size_t)1 << 31) || (size_t)N * K * 2 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if ((uintptr_t)a % 16 || (uintptr_t)w % 16 || (uintptr_t)out % 16 || (sw && (uintptr_t)sw % 16) || ldo % 4) return TCQ_ERR_ALIGN;
+    launch_by_m<2>(out_dtype, (hipStream_t)stream, a, w, sa, sw, out, ldo, M, N, K);
     return launch_status();
 }

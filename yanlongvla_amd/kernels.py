@@ -60,6 +60,14 @@ def decode_f16(bits, tlut, out):
     call('tcq_decode_f16', ptr(bits), ptr(tlut), ptr(out), m, n, stream())
 
 
+def decode_bf16(bits, tb, out):
+    """Dense decode through the BF16 bit patterns tb (512, 2) of the INT8 table values (the W2 float path), out (m, n)
+    bfloat16 (reference kernels.decode_bf16, kernels.py:683-686)."""
+    m, n = out.shape
+    _contig(bits, tb, out)
+    call('tcq_decode_f16', ptr(bits), ptr(tb), ptr(out), m, n, stream())
+
+
 # -------------------------------------------------------------------------------------------------------------- rotation
 def rht(x, su, y):
     """y = fwht(x * su) row by row (su may be None). x, y (M, n); dtypes float32 / bfloat16 / float16."""
@@ -317,6 +325,21 @@ def gemm_w8(segs, q, s, ldo):
     """One-shot INT8-resident product over segments (see SmallProduct)."""
     _contig(q, s)
     SmallProduct(segs, ldo, resident=True)(q, s)
+
+
+def gemm_bf16(a, w, out, sa=None, sw=None):
+    """acc = a w^T with FP32 accumulation, a (M, K) / w (N, K) BF16; out (M, ldo) FP32 or BF16 of (acc * sa) * sw (either
+    scale may be None). The W2 float path's product (Group.run_float, deploy/tcq_kernels/modules.py:117-144)."""
+    M, K = a.shape
+    N = w.shape[0]
+    if a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError('gemm_bf16: a and w must be bfloat16')
+    _contig(a, w, sa, sw)
+    if w.shape[1] != K or out.shape[0] != M or out.stride(1) != 1:
+        raise ValueError('gemm_bf16: shapes do not match')
+    call('tcq_gemm_bf16', ptr(a), ptr(w), ptr(sa), ptr(sw), ptr(out), _dt(out, (0, 1), 'gemm_bf16 out'), out.stride(0), M, N, K,
+         stream())
+    return out
 
 
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM

@@ -50,12 +50,10 @@ def is_quantizable(name, module):
 class Group:
     """Layers sharing one input rotation + quantization and one product, columns side by side (modules.py:29-155).
     mode: resident (INT8 weights, stream released) | fly (decoded on every call) | chunk (INT8 weights re-decoded by
-    decode_chunk); a8: INT8 activations (the only variant built here)."""
+    decode_chunk); a8: INT8 activations, else the W2 float path (BF16 rotated activations, the INT8 table values as BF16
+    weights, FP32 accumulation; modules.py:117-144)."""
 
     def __init__(self, layers, part, mode, a8=True):
-        if not a8:
-            raise NotImplementedError('FP activations (a8=False) through the INT8 table are not built; the FP16-table float '
-                                      'path is kernels.pre_h16 + kernels.gemv_f16')
         self.layers, self.part, self.mode, self.a8 = layers, part, mode, a8
         self.K = layers[0].n
         if not all(L.n == self.K and torch.equal(L.su, layers[0].su) for L in layers):
@@ -74,10 +72,12 @@ class Group:
         self.rs_parts = [self.rs[c:c + n] for c, n in zip(self.col0, self.N)]
         self.sv_parts = [self.sv[c:c + n] for c, n in zip(self.col0, self.N)]
         self.bias_parts = [None if self.bias is None else self.bias[c:c + n] for c, n in zip(self.col0, self.N)]
+        if not a8:                                          # BF16 bit patterns of the INT8 table values (modules.py:60)
+            self.tb = [L.t8.to(torch.bfloat16).contiguous() for L in layers]
         if mode in ('resident', 'chunk'):
-            self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8, device=self.su.device)
+            self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8 if a8 else torch.bfloat16, device=self.su.device)
             self.decode()
-        else:
+        elif a8:
             for L in layers:
                 L.words()                                   # repack once at load: the fused small-M product reads it
         self.x = self.outs = None
@@ -85,8 +85,11 @@ class Group:
 
     def decode(self, W=None):
         W = self.W if W is None else W
-        for L, c in zip(self.layers, self.col0):
-            kernels.decode(L.bits, L.t8, W[c:c + L.m])
+        for i, (L, c) in enumerate(zip(self.layers, self.col0)):
+            if self.a8:
+                kernels.decode(L.bits, L.t8, W[c:c + L.m])
+            else:
+                kernels.decode_bf16(L.bits, self.tb[i], W[c:c + L.m])
         return W
 
     def prep(self, x):
@@ -124,19 +127,38 @@ class Group:
         return kernels.gemm_i8(q, W, acc)
 
     def posts(self, acc, b, shape, gelu0=False):
+        """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs)."""
         M, dev = acc.shape[0], acc.device
         ys = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in self.N]
         scaled = acc.dtype == torch.float32
         segs = [(acc, c, None if scaled else r, v, bb, y, gelu0 and i == 0)
                 for i, (c, r, v, bb, y) in enumerate(zip(self.col0, self.rs_parts, self.sv_parts, self.bias_parts, ys))]
-        kernels.post_group(segs, acc.dtype, torch.bfloat16, None if scaled else b['scale'], M,
+        kernels.post_group(segs, acc.dtype, torch.bfloat16, b['scale'] if acc.dtype == torch.int32 else None, M,
                            gelu_lut=kernels.gelu_table(dev) if gelu0 else None)
         return [y.reshape(*shape[:-1], n) for y, n in zip(ys, self.N)]
 
     def run(self, x):
         x2 = self.prep(x)
+        if not self.a8:
+            return self.run_float(x2, x.shape)
         b = self.quantize(x2)
         outs = self.posts(self.product(b), b, x.shape)
+        STATS['group_runs'] += 1
+        return outs
+
+    def run_float(self, x2, shape):
+        """W2: BF16 rotated activations (kernels.rht), BF16 weights decoded from the INT8 table values, FP32 accumulation
+        (tcq_gemm_bf16). Expert: z = acc * rs in FP32; prefill: the product rounded to BF16, scaled by rs in the epilogue
+        (modules.py:117-144)."""
+        M, dev = x2.shape[0], x2.device
+        h = torch.empty(M, self.K, dtype=torch.bfloat16, device=dev)
+        kernels.rht(x2, self.su, h)
+        W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.bfloat16, device=dev))
+        if self.small:
+            acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.float32, device=dev), sw=self.rs)
+        else:
+            acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.bfloat16, device=dev))
+        outs = self.posts(acc, None, shape)
         STATS['group_runs'] += 1
         return outs
 
@@ -397,7 +419,7 @@ def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', refere
                 L._words = None
         groups.append(group)
     fused = 0
-    if FUSE['mlp']:
+    if a8 and FUSE['mlp']:
         by_name = {g.layers[0].name: g for g in groups}
         for g in list(groups):
             parent, _, leaf = g.layers[0].name.rpartition('.')
@@ -412,7 +434,7 @@ def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', refere
                 set_submodule(model, parent, KPlainMLP(g, by_name[f'{parent}.fc2']))
                 fused += 1
     layers_fused = 0
-    if FUSE['mlp'] and FUSE['layer']:
+    if a8 and FUSE['mlp'] and FUSE['layer']:
         by_name = {g.layers[0].name: g for g in groups}
         for g in groups:
             attn, _, leaf = g.layers[0].name.rpartition('.')
