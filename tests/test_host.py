@@ -50,3 +50,37 @@ def test_packed_file_schema(tmp_path):
 def test_runtime_names_are_checked():
     with pytest.raises(ValueError):
         modules.install(torch.nn.Linear(2, 2), runtime='fast', layers={})
+
+
+def test_from_qtip_matches_qtip_reconstruction(tmp_path):
+    """The packed tensors converted from a QTIP-official record give, through the oracle's dense weight, QTIP's own inverse
+    transform W = (hadU((hadU(Wscale Q) * SU)^T) * SV)^T with the normalised Sylvester Hadamard (quantize_qtip.py:72-74)."""
+    from safetensors.torch import save_file
+    from oracle import tcq_oracle as O
+    rng = np.random.default_rng(9)
+    m, n = 64, 128
+    bits = rng.integers(-32768, 32768, ((m // 16) * (n // 16), 32)).astype(np.int16)
+    tlut = rng.standard_normal((512, 2)).astype(np.float16)
+    su = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+    sv = np.where(rng.random(m) < 0.5, -1.0, 1.0).astype(np.float16)
+    wscale = np.float32(0.0625)                                              # exact in FP16
+    rec = dict(trellis_int16=torch.from_numpy(bits.reshape(-1)), tlut_fp16=torch.from_numpy(tlut),
+               su_fp16=torch.from_numpy(su), sv_fp16=torch.from_numpy(sv), wscale_fp32=torch.tensor([wscale]))
+    save_file(rec, str(tmp_path / 'q.safetensors'))
+    p = F.convert_qtip({'l.q_proj': tmp_path / 'q.safetensors'}, tmp_path / 'packed.safetensors')
+    from safetensors import safe_open
+    with safe_open(str(p), framework='pt') as f:
+        t = {k: f.get_tensor(f'l.q_proj::{k}').numpy() for k in F.TENSORS}
+    L = O.Layer('l.q_proj', t)
+
+    def H(k):
+        h = np.ones((1, 1))
+        while h.shape[0] < k:
+            h = np.block([[h, h], [h, -h]])
+        return h / np.sqrt(k)
+    Q = O.lookup(L.states(), tlut.astype(np.float32)).astype(np.float64)
+    hadU = lambda X: X @ H(X.shape[-1]).T
+    W = (hadU((hadU(wscale * Q) * su.astype(np.float64)).T) * sv.astype(np.float64)).T
+    assert np.allclose(L.dense('fp16'), W, atol=1e-5 * np.abs(W).max())
+    with pytest.raises(ValueError):
+        F.from_qtip(dict(rec, su_fp16=torch.ones(4480, dtype=torch.float16), trellis_int16=torch.zeros(4, 32, dtype=torch.int16)))

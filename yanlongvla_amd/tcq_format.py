@@ -126,3 +126,33 @@ def save(tensors, path):
     path.parent.mkdir(parents=True, exist_ok=True)
     save_file(flat, str(path))
     return path
+
+
+# ------------------------------------------------------------------------------------------- QTIP-official output
+def from_qtip(rec):
+    """One layer of QTIP-official output (baselines/quantize_qtip.py:66-84: trellis_int16, tlut_fp16, su_fp16, sv_fp16,
+    wscale_fp32) -> the packed tensors {bits, tlut, row_scale, su, sv} (CPU tensors).
+
+    QTIP's incoherence transform Wr = H_m S_V W S_U H_n (utils.matmul_hadUt on both sides, quantize_qtip.py:61) inverts to
+    W = S_V H_m (Wscale Q) H_n S_U, the deploy format's S_v H_m diag(r) Q H_n S_u with the scalar Wscale as a constant row
+    scale, whenever both Hadamards are the Sylvester ones the block Walsh uses: power-of-two m and n. The scale becomes FP16
+    (the format's row-scale type). Layers padded for QTIP's other Hadamard sizes (4304 -> 4480, quantize_qtip.py:31) are
+    refused: their transform is not a block Walsh."""
+    su, sv = rec['su_fp16'].float(), rec['sv_fp16'].float()
+    m, n = sv.numel(), su.numel()
+    if m & (m - 1) or n & (n - 1):
+        raise ValueError(f'QTIP layer {m} x {n}: only power-of-two dims use the Sylvester Hadamard of the block Walsh')
+    bits = rec['trellis_int16'].contiguous().view(torch.int16).reshape(-1, 32)
+    if bits.shape[0] != (m // 16) * (n // 16):
+        raise ValueError(f'trellis holds {bits.shape[0]} tiles, a {m} x {n} layer has {(m // 16) * (n // 16)}')
+    if not (torch.all(su.abs() == 1) and torch.all(sv.abs() == 1)):
+        raise ValueError('sign vectors must hold +-1')
+    wscale = rec['wscale_fp32'].reshape(-1)[0].float()
+    return dict(bits=bits, tlut=rec['tlut_fp16'].to(torch.float16).reshape(512, 2).contiguous(),
+                row_scale=wscale.to(torch.float16).expand(m).contiguous(), su=su.to(torch.int8), sv=sv.to(torch.int8))
+
+
+def convert_qtip(files, path):
+    """{layer name: QTIP-official per-layer .safetensors} -> one packed file at path."""
+    from safetensors.torch import load_file
+    return save({name: from_qtip(load_file(str(f))) for name, f in files.items()}, path)
