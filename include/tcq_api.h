@@ -51,6 +51,12 @@ int tcq_max_width(void);
  * Replaces tcq_format.snap (deploy/tcq_kernels/tcq_format.py:74-77), called by tcq_format.Layer.__init__ (:90). */
 int tcq_snap(const void* tlut, const void* row_scale, int m, int8_t* t8, float* rs, float* gain, tcq_stream_t stream);
 
+/* Row-group tables (the GR00T variants, baselines/groot/simpler/main_row/scripts/groot_tcq.py:154-175): tlut (G, 512, 2), rows
+ * split evenly into G contiguous groups (row i reads table i / (m / G)). Each table snaps on its own: t8 (G, 512, 2), gain
+ * (G,), rs[i] = row_scale[i] / gain[group of i]. m % G == 0. No reference counterpart for the INT8 snap of grouped tables:
+ * it is tcq_format.snap applied per group. */
+int tcq_snap_groups(const void* tlut, int G, const void* row_scale, int m, int8_t* t8, float* rs, float* gain, tcq_stream_t stream);
+
 /* Reference word layout -> device layout for the fused products (tcq_gemv_f16, tcq_gemm_tcq). For tile row I and chunk c of
  * 16 tiles (columns 256 c .. 256 c + 255) the device layout holds 1 KiB: dword 4 l + j of lane l = 16 g + r is the 32-bit
  * window (word[2r] << 16) | word[2r + 1] of tile 16 c + 4 j + g. n is padded to a multiple of 256 with zero words.
@@ -64,12 +70,16 @@ int64_t tcq_repack_words(int m, int n);
 /* Dense INT8 decode: out (m, n) int8 = sign * t8[hash(state)]. Replaces kernels.decode / k_decode
  * (deploy/tcq_kernels/kernels.py:339-349, 653-656); definition tcq_format.Layer.w8_reference (tcq_format.py:97-98). */
 int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream);
+/* The same with G row-group tables t8 (G, 512, 2); (m / G) % 16 == 0. */
+int tcq_decode_i8_groups(const void* bits, const int8_t* t8, int G, int8_t* out, int m, int n, tcq_stream_t stream);
 
 /* Dense decode through a 16-bit table: out (m, n) = sign * tlut[hash(state)], the sign flipping bit 15 of the first
  * coordinate (exact for FP16 and BF16 tables). With the FP16 table: tcq_format.lookup(states, tlut.float())
  * (tcq_format.py:66-71, 103, 139); with the BF16 bit patterns of the INT8 table values: kernels.decode_bf16 / k_decode_bf16
  * (kernels.py:320-337, 683-686). */
 int tcq_decode_f16(const void* bits, const void* tlut, void* out, int m, int n, tcq_stream_t stream);
+/* The same with G row-group tables (G, 512, 2) (groot_tcq.py:165-175 decode_normalized); (m / G) % 16 == 0. */
+int tcq_decode_f16_groups(const void* bits, const void* tlut, int G, void* out, int m, int n, tcq_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------------------------- rotation */
 
@@ -196,9 +206,10 @@ int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, c
  * All layers of a batch share m, n, M, h16 and hscale. */
 typedef struct tcq_gemv_layer {
     const void* wdev;       /* tcq_repack layout */
-    const void* tlut;       /* (512, 2) FP16 */
+    const void* tlut;       /* (512, 2) FP16, or (G, 512, 2) row-group tables */
     const void* row_scale;  /* (m,) FP16 */
     float* z;               /* (M, m) FP32 out */
+    int rows_per_table;     /* row-group tables: rows m / G per table (a multiple of 16); 0 = one table */
 } tcq_gemv_layer;
 
 /* layers: a DEVICE array of nlayers descriptors. The FP16-table product of tcq_format.reference_linear(table='fp16',
@@ -206,15 +217,20 @@ typedef struct tcq_gemv_layer {
  * counterpart is kernels.gemmf_tcq / k_gemmf_tcq (kernels.py:465-489). */
 int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                  tcq_stream_t stream);
+/* The same for layers with row-group tables: every descriptor's rows_per_table must equal rows_per_table (the launch plan
+ * keeps each workgroup inside one group). */
+int tcq_gemv_f16_groups(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
+                        int rows_per_table, tcq_stream_t stream);
 
 /* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
  * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
 typedef struct tcq_gemm_seg {
     const void* w;       /* tcq_gemm_tcq: tcq_repack words of an (m, K) layer; tcq_gemm_w8: (m, K) int8 row-major weights */
-    const int8_t* t8;    /* (512, 2) INT8 table (tcq_gemm_tcq only) */
+    const int8_t* t8;    /* (512, 2) INT8 table, or (G, 512, 2) row-group tables (tcq_gemm_tcq only) */
     const float* rs;     /* (m,) FP32 row scale (unused for I32 output) */
     void* out;           /* output, first column of the segment */
     int m;               /* output rows, a multiple of 16 */
+    int rows_per_table;  /* row-group tables: rows m / G per table (a multiple of 16); 0 = one table */
 } tcq_gemm_seg;
 
 /* W2A8 fused decode + product for M <= 64 tokens: acc[t, i] = sum_k q[t, k] * w8[i, k], exact in int32, with w8 = sign *

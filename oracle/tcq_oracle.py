@@ -87,9 +87,16 @@ def states_from_bits(bits, m, n):
 
 def lookup(states, table):
     """(m, n/2) states + (512, 2) table -> (m, n): x = (s + 1) s, value = table[(x >> 6) & 511], the first coordinate negated
-    when bit 15 of x is set (tcq_format.py:66-71)."""
+    when bit 15 of x is set (tcq_format.py:66-71). A (G, 512, 2) table holds row-group tables: rows split evenly into G
+    contiguous groups, row i reading table i // (m / G) (groot_tcq.py:154-175, decode_normalized)."""
     x = (states + 1) * states
-    v = np.asarray(table)[(x >> 6) & 511]
+    table = np.asarray(table)
+    if table.ndim == 3:
+        G, m = table.shape[0], states.shape[0]
+        grp = (np.arange(m) // (m // G))[:, None]
+        v = table[grp, (x >> 6) & 511]
+    else:
+        v = table[(x >> 6) & 511]
     v0 = np.where(((x >> 15) & 1).astype(bool), -v[..., 0], v[..., 0])
     return np.stack((v0, v[..., 1]), -1).reshape(states.shape[0], -1)
 
@@ -98,6 +105,11 @@ def snap(tlut, row_scale):
     """INT8 table and row scale (tcq_format.py:74-77). `127.0 / tensor` is Tensor.__rdiv__ = reciprocal() * 127, so the gain is
     float32(float32(1 / amax) * 127); t8 = clamp(round_half_even(tlut * g), +-127); rs = float32(row_scale) / g (true division)."""
     t = np.asarray(tlut).astype(np.float32)
+    if t.ndim == 3:                       # row-group tables: each table snaps on its own, each row uses its group's gain
+        G = t.shape[0]
+        parts = [snap(t[i], np.asarray(row_scale).reshape(G, -1)[i]) for i in range(G)]
+        return (np.stack([p[0] for p in parts]), np.concatenate([p[1] for p in parts]),
+                np.array([p[2] for p in parts], dtype=np.float32))
     amax = np.float32(np.abs(t).max())
     g = np.float32(np.float32(1.0) / amax) * np.float32(127.0)
     t8 = np.clip(np.round(t * g), -127, 127).astype(np.int8)
@@ -284,12 +296,15 @@ def w8a8_reference(a, w):
 
 
 # ----------------------------------------------------------------------------------------------------------- synthetic layers
-def random_layer(m, n, seed, name='layer', bias=False, scale_range=(0.5, 1.5), per_layer_scale=True):
-    """Seeded synthetic layer: uniform-random packed words, N(0, 1) FP16 table, +-1 signs, FP16 scale drawn from scale_range
-    (one per layer broadcast to all rows when per_layer_scale, else one per row)."""
+def random_layer(m, n, seed, name='layer', bias=False, scale_range=(0.5, 1.5), per_layer_scale=True, groups=1):
+    """Seeded synthetic layer: uniform-random packed words, N(0, 1) FP16 table (groups > 1: (G, 512, 2) row-group tables,
+    table g scaled by 1 + g / 4), +-1 signs, FP16 scale drawn from scale_range (one per layer broadcast to all rows when
+    per_layer_scale, else one per row)."""
     rng = np.random.default_rng(seed)
     bits = rng.integers(0, 1 << 16, size=((m // 16) * (n // 16), 32), dtype=np.uint32).astype(np.uint16).view(np.int16)
     tlut = rng.standard_normal((512, 2)).astype(np.float16)
+    if groups > 1:
+        tlut = np.stack([(rng.standard_normal((512, 2)) * (1 + g / 4)).astype(np.float16) for g in range(groups)])
     if per_layer_scale:
         row_scale = np.full(m, rng.uniform(*scale_range), dtype=np.float16)
     else:

@@ -25,9 +25,9 @@ def oracle_of(L):
     return O.Layer(L.name, t, bias=None if L.bias is None else L.bias.cpu().numpy())
 
 
-def device_layer(m, n, seed, bias=False, name='layer'):
+def device_layer(m, n, seed, bias=False, name='layer', groups=1):
     from yanlongvla_amd import tcq_format as F
-    ol = O.random_layer(m, n, seed, name=name, bias=bias, per_layer_scale=False)
+    ol = O.random_layer(m, n, seed, name=name, bias=bias, per_layer_scale=False, groups=groups)
     t = dict(bits=torch.from_numpy(ol.bits), tlut=torch.from_numpy(ol.tlut), row_scale=torch.from_numpy(ol.row_scale),
              su=torch.from_numpy(ol.su), sv=torch.from_numpy(ol.sv))
     return F.Layer(name, t, bias=None if ol.bias is None else torch.from_numpy(ol.bias), device=DEV), ol
@@ -288,3 +288,49 @@ def test_install_float_runtime():
     assert infos['fly']['fused_mlps'] == 0 and infos['fly']['fused_layers'] == 0
     assert torch.equal(outs['fly'], outs['resident']) and torch.equal(outs['fly'], outs['hybrid'])
     assert torch.isfinite(outs['fly']).all()
+
+
+# ------------------------------------------------------------------------------- row-group tables and GR00T shapes
+@pytest.mark.parametrize('m,n,G', [(1536, 1536, 16), (3072, 1024, 16), (256, 512, 2), (6144, 1536, 8)])
+def test_row_group_tables_bitexact(m, n, G):
+    """(G, 512, 2) row-group tables: per-group snap, dense INT8 / FP16 decode, the fused small-M product (q / k / v-style
+    Group at 50 tokens), the prefill path (200 tokens) and RefLinear, all bit-exact against the oracle."""
+    from yanlongvla_amd import kernels as K
+    from yanlongvla_amd.modules import Group, KLinear, RefLinear
+    L, ol = device_layer(m, n, m + G, groups=G)
+    assert L.groups == G
+    assert np.array_equal(L.t8.cpu().numpy(), ol.t8) and np.array_equal(L.rs.cpu().numpy().view(np.uint32), ol.rs.view(np.uint32))
+    assert np.array_equal(L.w8_reference().cpu().numpy(), ol.w8_reference())
+    f16 = L.decode_f16()
+    assert np.array_equal(f16.cpu().numpy(), O.lookup(ol.states(), ol.tlut.astype(np.float32)).astype(np.float16))
+    for M, part in ((50, 'expert'), (200, 'llm')):
+        x = torch.randn(M, n, device=DEV).bfloat16()
+        ref = O.reference_linear(x.float().cpu().numpy(), ol)
+        for mode in ('fly', 'resident'):
+            y = KLinear(Group([L], part, mode), 0)(x)
+            assert np.array_equal(bits16(y), ref), (M, mode)
+        assert np.array_equal(bits16(RefLinear(L)(x)), ref)
+
+
+@pytest.mark.parametrize('nl,M', [(1, 1), (3, 4), (300, 1)])
+def test_row_group_tables_gemv(nl, M):
+    """FP16-table decode-GEMV over layers with row-group tables (latency and layer-stream plans) against the oracle."""
+    from yanlongvla_amd import kernels as K
+    m, n, G = 512, 1024, 4
+    layers = [device_layer(m, n, 900 + i, groups=G) for i in range(nl)]
+    su = layers[0][0].su
+    x = torch.randn(M, n, device=DEV).half()
+    h16 = torch.empty(M, n, dtype=torch.float16, device=DEV)
+    hs = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.pre_h16(x, su, h16, hs)
+    zs = [torch.empty(M, m, device=DEV) for _ in layers]
+    words = [L.words() for L, _ in layers]
+    desc = K.gemv_descriptors([(w, L.tlut, L.row_scale, z) for w, (L, _), z in zip(words, layers, zs)])
+    K.gemv_f16(desc, h16, hs, m, n, rows_per_table=m // G)
+    xs = x.float().cpu().numpy()
+    for (L, ol), z in list(zip(layers, zs))[:4] + list(zip(layers, zs))[-2:]:
+        ol.su = su.cpu().numpy()
+        y = torch.empty(M, m, device=DEV)
+        K.post(z, None, None, L.sv, None, y)
+        ref = O.reference_linear(xs, ol, a8=False, table='fp16', out_dtype='f32')
+        assert np.linalg.norm(y.cpu().numpy() - ref) / np.linalg.norm(ref) < 2e-3

@@ -292,3 +292,25 @@ def test_rmsnorm_close_to_the_formula():
     assert np.abs(y - bad).max() > 0.1
     bad_eps = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True)) * (1 + w64)
     assert np.abs(y[5] - bad_eps[5]).max() > 1e-3 * np.abs(bad_eps[5]).max()
+
+
+def test_row_group_tables():
+    """(G, 512, 2) row-group tables: G = 1 is the single table; each group's rows equal the single-table path on that group's
+    rows and table (groot_tcq.py decode_normalized), and each table snaps on its own."""
+    rng = np.random.default_rng(12)
+    m, n, G = 64, 32, 4
+    bits = rng.integers(0, 1 << 16, size=((m // 16) * (n // 16), 32), dtype=np.uint32).astype(np.uint16).view(np.int16)
+    tabs = rng.standard_normal((G, 512, 2)).astype(np.float32) * np.arange(1, G + 1)[:, None, None]
+    st = O.states_from_bits(bits, m, n)
+    assert np.array_equal(O.lookup(st, tabs[:1]), O.lookup(st, tabs[0]))
+    got = O.lookup(st, tabs)
+    rpg = m // G
+    for g in range(G):
+        assert np.array_equal(got[g * rpg:(g + 1) * rpg], O.lookup(st[g * rpg:(g + 1) * rpg], tabs[g]))
+    rsc = rng.uniform(0.5, 1.5, m).astype(np.float16)
+    t8, rs, gain = O.snap(tabs.astype(np.float16), rsc)
+    assert t8.shape == (G, 512, 2) and gain.shape == (G,)
+    for g in range(G):
+        t8g, rsg, gg = O.snap(tabs[g].astype(np.float16), rsc[g * rpg:(g + 1) * rpg])
+        assert np.array_equal(t8[g], t8g) and np.array_equal(rs[g * rpg:(g + 1) * rpg], rsg) and gain[g] == gg
+    assert len(set(gain.tolist())) == G                                   # the tables really differ

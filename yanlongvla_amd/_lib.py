@@ -36,6 +36,10 @@ SIGNATURES = {
     'tcq_norm_pre': [_P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_post_add_norm_pre': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_attend_chunks': [_I, _I],
+    'tcq_snap_groups': [_P, _I, _P, _I, _P, _P, _P, _P],
+    'tcq_decode_i8_groups': [_P, _P, _I, _P, _I, _I, _P],
+    'tcq_decode_f16_groups': [_P, _P, _I, _P, _I, _I, _P],
+    'tcq_gemv_f16_groups': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_bf16': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
@@ -63,7 +67,7 @@ class PostSeg(ctypes.Structure):
 class GemmSeg(ctypes.Structure):
     """tcq_gemm_seg (include/tcq_api.h)."""
     _fields_ = [('w', ctypes.c_void_p), ('t8', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('out', ctypes.c_void_p),
-                ('m', ctypes.c_int)]
+                ('m', ctypes.c_int), ('rows_per_table', ctypes.c_int)]
 
 
 _state = {}

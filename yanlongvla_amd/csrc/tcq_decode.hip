@@ -10,8 +10,12 @@ __device__ __forceinline__ u32 row_state(u32 hi, u32 lo16, int p) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------ snap
-__global__ void k_snap(const u16* tlut, const u16* row_scale, int m, i8* t8, float* rs, float* gain) {
+// Workgroup g snaps table g of G (row-group tables: rows [g rpt, (g + 1) rpt) read table g, rpt = m / G).
+__global__ void k_snap(const u16* tlut_all, const u16* row_scale, int rpt, i8* t8_all, float* rs, float* gain) {
     __shared__ float red[16];
+    const int gi = blockIdx.x;
+    const u16* tlut = tlut_all + 1024 * gi;
+    i8* t8 = t8_all + 1024 * gi;
     float mx = 0.f;
     for (int i = threadIdx.x; i < 1024; i += blockDim.x) mx = fmaxf(mx, fabsf(f16_to_f32(tlut[i])));
     mx = block_max(mx, red);
@@ -22,8 +26,8 @@ __global__ void k_snap(const u16* tlut, const u16* row_scale, int m, i8* t8, flo
         v = fminf(fmaxf(v, -127.f), 127.f);
         t8[i] = (i8)(int)v;
     }
-    for (int i = threadIdx.x; i < m; i += blockDim.x) rs[i] = f16_to_f32(row_scale[i]) / g;
-    if (threadIdx.x == 0 && gain) *gain = g;
+    for (int i = threadIdx.x; i < rpt; i += blockDim.x) rs[gi * rpt + i] = f16_to_f32(row_scale[gi * rpt + i]) / g;
+    if (threadIdx.x == 0 && gain) gain[gi] = g;
 }
 
 // ---------------------------------------------------------------------------------------------------------------- repack
@@ -44,9 +48,11 @@ __global__ void k_repack(const u16* bits, u32* wdev, int m, int n, long long tot
 }
 
 // --------------------------------------------------------------------------------------------------------- dense decode
-// One thread per (row, tile column): the 16 weights of one tile row. Sign-folded tables in LDS.
-__global__ void k_decode_i8(const u16* bits, const i8* t8, i8* out, int m, int n) {
+// One thread per (row, tile column): the 16 weights of one tile row. Sign-folded tables in LDS. grid (blocks per row group,
+// row groups): the workgroups of group g (rows [g rpt, (g + 1) rpt)) load table g.
+__global__ void k_decode_i8(const u16* bits, const i8* t8_all, i8* out, int rpt, int n) {
     __shared__ u16 tab[1024];
+    const i8* t8 = t8_all + 1024 * blockIdx.y;
     for (int e = threadIdx.x; e < 1024; e += blockDim.x) {
         const int h = e & 511;
         int v0 = t8[2 * h];
@@ -57,8 +63,8 @@ __global__ void k_decode_i8(const u16* bits, const i8* t8, i8* out, int m, int n
     __syncthreads();
     const int tiles = n >> 4;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)m * tiles) return;
-    const int row = (int)(idx / tiles), J = (int)(idx % tiles), r = row & 15;
+    if (idx >= (size_t)rpt * tiles) return;
+    const int row = blockIdx.y * rpt + (int)(idx / tiles), J = (int)(idx % tiles), r = row & 15;
     const u16* t = bits + ((size_t)(row >> 4) * tiles + J) * 32;
     const u32 hi = ((u32)t[2 * r] << 16) | t[2 * r + 1], lo = t[(2 * r + 2) & 31];
     uint4_t w;
@@ -70,8 +76,9 @@ __global__ void k_decode_i8(const u16* bits, const i8* t8, i8* out, int m, int n
     *(uint4_t*)(out + (size_t)row * n + 16 * J) = w;
 }
 
-__global__ void k_decode_f16(const u16* bits, const u16* tlut, u16* out, int m, int n) {
+__global__ void k_decode_f16(const u16* bits, const u16* tlut_all, u16* out, int rpt, int n) {
     __shared__ u32 tab[1024];
+    const u16* tlut = tlut_all + 1024 * blockIdx.y;
     for (int e = threadIdx.x; e < 1024; e += blockDim.x) {
         const int h = e & 511;
         tab[e] = ((u32)tlut[2 * h] ^ ((u32)(e >> 9) << 15)) | ((u32)tlut[2 * h + 1] << 16);
@@ -79,8 +86,8 @@ __global__ void k_decode_f16(const u16* bits, const u16* tlut, u16* out, int m, 
     __syncthreads();
     const int tiles = n >> 4;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)m * tiles) return;
-    const int row = (int)(idx / tiles), J = (int)(idx % tiles), r = row & 15;
+    if (idx >= (size_t)rpt * tiles) return;
+    const int row = blockIdx.y * rpt + (int)(idx / tiles), J = (int)(idx % tiles), r = row & 15;
     const u16* t = bits + ((size_t)(row >> 4) * tiles + J) * 32;
     const u32 hi = ((u32)t[2 * r] << 16) | t[2 * r + 1], lo = t[(2 * r + 2) & 31];
     uint4_t w0, w1;
@@ -99,10 +106,19 @@ __global__ void k_decode_f16(const u16* bits, const u16* tlut, u16* out, int m, 
 extern "C" const char* tcq_version(void) { return "tcq-mi355x 0.1 (gfx950)"; }
 extern "C" int tcq_max_width(void) { return TCQ_MAX_WIDTH; }
 
-extern "C" int tcq_snap(const void* tlut, const void* row_scale, int m, int8_t* t8, float* rs, float* gain, tcq_stream_t stream) {
-    if (!tlut || !row_scale || !t8 || !rs || m <= 0) return TCQ_ERR_ARG;
-    launch_k(k_snap, dim3(1), dim3(256), 0, (hipStream_t)stream, (const u16*)tlut, (const u16*)row_scale, m, (i8*)t8, rs, gain);
+// Row groups: m rows split evenly into G contiguous groups of rpt = m / G rows, each a whole number of 16-row tiles.
+static bool groups_ok(int m, int G) { return G >= 1 && G <= 65535 && m % G == 0 && (m / G) % 16 == 0; }
+
+extern "C" int tcq_snap_groups(const void* tlut, int G, const void* row_scale, int m, int8_t* t8, float* rs, float* gain,
+                               tcq_stream_t stream) {
+    if (!tlut || !row_scale || !t8 || !rs || m <= 0 || G <= 0) return TCQ_ERR_ARG;
+    if (m % G) return TCQ_ERR_SHAPE;
+    launch_k(k_snap, dim3(G), dim3(256), 0, (hipStream_t)stream, (const u16*)tlut, (const u16*)row_scale, m / G, (i8*)t8, rs, gain);
     return launch_status();
+}
+
+extern "C" int tcq_snap(const void* tlut, const void* row_scale, int m, int8_t* t8, float* rs, float* gain, tcq_stream_t stream) {
+    return tcq_snap_groups(tlut, 1, row_scale, m, t8, rs, gain, stream);
 }
 
 extern "C" int64_t tcq_repack_words(int m, int n) {
@@ -119,22 +135,30 @@ extern "C" int tcq_repack(const void* bits, void* wdev, int m, int n, tcq_stream
     return launch_status();
 }
 
-extern "C" int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream) {
-    if (!bits || !t8 || !out || m <= 0 || n <= 0) return TCQ_ERR_ARG;
-    if (m % 16 || n % 16) return TCQ_ERR_SHAPE;
+extern "C" int tcq_decode_i8_groups(const void* bits, const int8_t* t8, int G, int8_t* out, int m, int n, tcq_stream_t stream) {
+    if (!bits || !t8 || !out || m <= 0 || n <= 0 || G <= 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16 || !groups_ok(m, G)) return TCQ_ERR_SHAPE;
     if ((uintptr_t)out % 16) return TCQ_ERR_ALIGN;
-    const size_t total = (size_t)m * (n / 16);
-    launch_k(k_decode_i8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
-             (const i8*)t8, (i8*)out, m, n);
+    const size_t per = (size_t)(m / G) * (n / 16);
+    launch_k(k_decode_i8, dim3((unsigned)((per + 255) / 256), G), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
+             (const i8*)t8, (i8*)out, m / G, n);
+    return launch_status();
+}
+
+extern "C" int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream) {
+    return tcq_decode_i8_groups(bits, t8, 1, out, m, n, stream);
+}
+
+extern "C" int tcq_decode_f16_groups(const void* bits, const void* tlut, int G, void* out, int m, int n, tcq_stream_t stream) {
+    if (!bits || !tlut || !out || m <= 0 || n <= 0 || G <= 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16 || !groups_ok(m, G)) return TCQ_ERR_SHAPE;
+    if ((uintptr_t)out % 16) return TCQ_ERR_ALIGN;
+    const size_t per = (size_t)(m / G) * (n / 16);
+    launch_k(k_decode_f16, dim3((unsigned)((per + 255) / 256), G), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
+             (const u16*)tlut, (u16*)out, m / G, n);
     return launch_status();
 }
 
 extern "C" int tcq_decode_f16(const void* bits, const void* tlut, void* out, int m, int n, tcq_stream_t stream) {
-    if (!bits || !tlut || !out || m <= 0 || n <= 0) return TCQ_ERR_ARG;
-    if (m % 16 || n % 16) return TCQ_ERR_SHAPE;
-    if ((uintptr_t)out % 16) return TCQ_ERR_ALIGN;
-    const size_t total = (size_t)m * (n / 16);
-    launch_k(k_decode_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
-             (const u16*)tlut, (u16*)out, m, n);
-    return launch_status();
+    return tcq_decode_f16_groups(bits, tlut, 1, out, m, n, stream);
 }

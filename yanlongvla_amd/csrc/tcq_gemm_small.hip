@@ -99,7 +99,7 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* 
 #pragma unroll
         for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
     }
-    if (MODE == 0) fill_table_i8(tab, S.t8);
+    if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I / S.rows_per_table) * 1024 : 0));
     __syncthreads();
     for (int c = wave; c < nch; c += nw) {
         if (c != wave) load(c);
@@ -185,6 +185,7 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
         const tcq_gemm_seg& g = segs[i];
         if (!g.w || !g.out || (MODE == 0 && !g.t8) || (odt != TCQ_I32 && !g.rs) || g.m <= 0) return TCQ_ERR_ARG;
         if (g.m % 16) return TCQ_ERR_SHAPE;
+        if (g.rows_per_table < 0 || (g.rows_per_table > 0 && (g.rows_per_table % 16 || g.m % g.rows_per_table))) return TCQ_ERR_SHAPE;
         if ((size_t)g.m * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
         const size_t osz = odt == TCQ_BF16 ? 2 : 4;
         if ((uintptr_t)g.out % (4 * osz) || (g.rs && (uintptr_t)g.rs % 16)) return TCQ_ERR_ALIGN;

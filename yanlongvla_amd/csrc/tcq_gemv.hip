@@ -98,7 +98,7 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
 
     u16* hl = (u16*)dyn;
     float* sl = (float*)(dyn + (M * np >> 1));
-    fill_table<C, NE>(tab, (const u16*)L.tlut);
+    fill_table<C, NE>(tab, (const u16*)L.tlut + (L.rows_per_table > 0 ? (size_t)(16 * I0 / L.rows_per_table) * 1024 : 0));
     for (int i = threadIdx.x; i < (M * np) >> 3; i += blockDim.x) {      // 8 FP16 per thread-step, rows padded to np
         const int t = i / (np >> 3), k = (i - t * (np >> 3)) << 3;
         ((uint4_t*)hl)[i] = k < n ? gptr((const uint4_t*)(h16 + (size_t)t * n + k))[0] : uint4_t{0, 0, 0, 0};
@@ -213,7 +213,8 @@ struct GemvPlan {
     size_t dyn;
 };
 
-static GemvPlan gemv_plan(int nlayers, int M, int m, int n) {
+// rpt > 0 (row-group tables of rpt rows): a workgroup of the stream plan covers one group, so it fills one table.
+static GemvPlan gemv_plan(int nlayers, int M, int m, int n, int rpt) {
     const int tiles_m = m / 16, nch = (n + 255) / 256;
     const size_t hbytes = (size_t)M * nch * 256 * 2;
     GemvPlan p;
@@ -236,6 +237,7 @@ static GemvPlan gemv_plan(int nlayers, int M, int m, int n) {
     }
     rows = (rows + GEMV_R - 1) / GEMV_R * GEMV_R;
     while (hbytes + (size_t)rows * 64 + 4096 * GEMV_C > 160 * 1024 && rows > GEMV_R) rows = (rows / 2 + GEMV_R - 1) / GEMV_R * GEMV_R;
+    if (rpt > 0) rows = rpt / 16;                       // rows past a group's end are computed by its last wave but not stored
     p.ks = 1;
     p.rows_per_wg = rows;
     p.wgs = (tiles_m + rows - 1) / rows;
@@ -244,14 +246,14 @@ static GemvPlan gemv_plan(int nlayers, int M, int m, int n) {
     return p;
 }
 
-extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
-                            tcq_stream_t stream) {
-    if (!layers || !h16 || !hscale || nlayers <= 0 || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
-    if (m % 16 || n % 16) return TCQ_ERR_SHAPE;
+extern "C" int tcq_gemv_f16_groups(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m,
+                                   int n, int rows_per_table, tcq_stream_t stream) {
+    if (!layers || !h16 || !hscale || nlayers <= 0 || M <= 0 || m <= 0 || n <= 0 || rows_per_table < 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16 || (rows_per_table > 0 && (rows_per_table % 16 || m % rows_per_table))) return TCQ_ERR_SHAPE;
     if (M > 16 || nlayers > 65535) return TCQ_ERR_UNSUPPORTED;
     if ((uintptr_t)h16 % 16) return TCQ_ERR_ALIGN;
     if ((size_t)(m / 16) * ((n + 255) / 256) * 1024 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;   // one layer's words < 2 GiB
-    const GemvPlan p = gemv_plan(nlayers, M, m, n);
+    const GemvPlan p = gemv_plan(nlayers, M, m, n, rows_per_table);
     const int C = p.ks == 1 ? GEMV_C : LAT_C;
     if (p.dyn + 4096 * C > 160 * 1024) return TCQ_ERR_UNSUPPORTED;                                // activations do not fit LDS
     constexpr int NT = 2;   // non-temporal loads: every packed word is read once
@@ -265,4 +267,9 @@ extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const voi
         default: launch_k(k_gemv_f16<LAT_C, 1, 1, NT, 16>, grid, block, p.dyn, st, layers, h, hscale, M, m, n, p.rows_per_wg); break;
     }
     return launch_status();
+}
+
+extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
+                            tcq_stream_t stream) {
+    return tcq_gemv_f16_groups(layers, nlayers, h16, hscale, M, m, n, 0, stream);
 }

@@ -22,14 +22,25 @@ def _contig(*ts):
 
 
 # ------------------------------------------------------------------------------------------------------------- load time
+def _groups(table):
+    """Number of (512, 2) tables in a table tensor: (512, 2) -> 1, (G, 512, 2) -> G (row-group tables)."""
+    n = table.numel()
+    if n % 1024:
+        raise ValueError(f'a table tensor holds whole (512, 2) tables, got {tuple(table.shape)}')
+    return n // 1024
+
+
 def snap(tlut, row_scale, t8=None, rs=None, gain=None):
-    """INT8 table / row scale / gain of tcq_format.snap (reference tcq_format.py:74-77), computed on the device."""
+    """INT8 table / row scale / gain of tcq_format.snap (reference tcq_format.py:74-77), computed on the device. A
+    (G, 512, 2) row-group table snaps per group: t8 (G, 512, 2), gain (G,), rs of each row from its group's gain."""
     dev = tlut.device
-    t8 = torch.empty(512, 2, dtype=torch.int8, device=dev) if t8 is None else t8
+    G = _groups(tlut)
+    shape = (512, 2) if tlut.dim() == 2 else (G, 512, 2)
+    t8 = torch.empty(*shape, dtype=torch.int8, device=dev) if t8 is None else t8
     rs = torch.empty(row_scale.numel(), dtype=torch.float32, device=dev) if rs is None else rs
-    gain = torch.empty(1, dtype=torch.float32, device=dev) if gain is None else gain
+    gain = torch.empty(G, dtype=torch.float32, device=dev) if gain is None else gain
     _contig(tlut, row_scale, t8, rs)
-    call('tcq_snap', ptr(tlut), ptr(row_scale), row_scale.numel(), ptr(t8), ptr(rs), ptr(gain), stream())
+    call('tcq_snap_groups', ptr(tlut), G, ptr(row_scale), row_scale.numel(), ptr(t8), ptr(rs), ptr(gain), stream())
     return t8, rs, gain
 
 
@@ -47,17 +58,17 @@ def repack(bits, m, n, out=None):
 
 # ---------------------------------------------------------------------------------------------------------------- decode
 def decode(bits, t8, out):
-    """Dense INT8 decode, out (m, n) int8 (reference kernels.py:653-656)."""
+    """Dense INT8 decode, out (m, n) int8 (reference kernels.py:653-656); t8 (512, 2) or (G, 512, 2) row-group tables."""
     m, n = out.shape
     _contig(bits, t8, out)
-    call('tcq_decode_i8', ptr(bits), ptr(t8), ptr(out), m, n, stream())
+    call('tcq_decode_i8_groups', ptr(bits), ptr(t8), _groups(t8), ptr(out), m, n, stream())
 
 
 def decode_f16(bits, tlut, out):
     """Dense decode through the FP16 table, out (m, n) float16 (exact lookup(states, tlut))."""
     m, n = out.shape
     _contig(bits, tlut, out)
-    call('tcq_decode_f16', ptr(bits), ptr(tlut), ptr(out), m, n, stream())
+    call('tcq_decode_f16_groups', ptr(bits), ptr(tlut), _groups(tlut), ptr(out), m, n, stream())
 
 
 def decode_bf16(bits, tb, out):
@@ -65,7 +76,7 @@ def decode_bf16(bits, tb, out):
     bfloat16 (reference kernels.decode_bf16, kernels.py:683-686)."""
     m, n = out.shape
     _contig(bits, tb, out)
-    call('tcq_decode_f16', ptr(bits), ptr(tb), ptr(out), m, n, stream())
+    call('tcq_decode_f16_groups', ptr(bits), ptr(tb), _groups(tb), ptr(out), m, n, stream())
 
 
 # -------------------------------------------------------------------------------------------------------------- rotation
@@ -196,24 +207,25 @@ def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None,
 
 # -------------------------------------------------------------------------------------------------------------- products
 def gemv_descriptors(layers):
-    """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers each). Keep the tensors alive."""
+    """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers + rows_per_table each; z (M, m) gives
+    m, a (G, 512, 2) tlut gives m / G rows per table). Keep the tensors alive."""
     flat = []
     for wdev, tlut, row_scale, z in layers:
         _contig(wdev, tlut, row_scale, z)
-        flat += [ptr(wdev), ptr(tlut), ptr(row_scale), ptr(z)]
+        G = _groups(tlut)
+        flat += [ptr(wdev), ptr(tlut), ptr(row_scale), ptr(z), 0 if G == 1 else z.shape[-1] // G]
     dev = layers[0][0].device
     return torch.tensor(flat, dtype=torch.int64).to(dev)
 
 
-def gemv_f16(desc, h16, hscale, m, n):
-    """Batched FP16-table decode-GEMV: for every layer in desc, z (M, m) = (h16 Q^T) * hscale * row_scale (M <= 16)."""
+def gemv_f16(desc, h16, hscale, m, n, rows_per_table=0):
+    """Batched FP16-table decode-GEMV: for every layer in desc, z (M, m) = (h16 Q^T) * hscale * row_scale (M <= 16). Layers
+    with row-group tables pass their common rows_per_table."""
     M = h16.shape[0]
     _contig(h16, hscale)
-    call('tcq_gemv_f16', ptr(desc), desc.shape[0] // 4 if desc.dim() == 1 else desc.shape[0], ptr(h16), ptr(hscale), M, m, n,
-         stream())
+    call('tcq_gemv_f16_groups', ptr(desc), desc.numel() // 5, ptr(h16), ptr(hscale), M, m, n, rows_per_table, stream())
 
 
-# ------------------------------------------------------------------------------------------------------ batched epilogue
 _SEG = None
 
 
@@ -304,7 +316,8 @@ class SmallProduct:
             if self.odt is not None and d != self.odt:
                 raise TypeError('all segments need one output dtype')
             self.odt = d
-            self.arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(out), rs.numel())
+            G = 1 if t8 is None else _groups(t8)
+            self.arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(out), rs.numel(), 0 if G == 1 else rs.numel() // G)
         self.n, self.ldo = len(segs), ldo
         self.fn = getattr(_lib.lib(), self.name)
 

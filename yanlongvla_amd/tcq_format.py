@@ -5,7 +5,8 @@ the HIP library instead of PyTorch ops:
 
 packed.safetensors: per quantized Linear `name`
   <name>::bits       int16 view of the uint16 words (m/16 * n/16, 32): 512 bits per 16 x 16 tile
-  <name>::tlut       FP16 (512, 2) table
+  <name>::tlut       FP16 (512, 2) table, or (G, 512, 2) row-group tables (rows split evenly into G contiguous groups, the
+                     GR00T variants of baselines/groot/simpler/main_row/scripts/groot_tcq.py:154-175)
   <name>::row_scale  FP16 (m,)
   <name>::su, ::sv   int8 (n,), (m,) input / output signs of the two-sided block-Walsh rotation
 Derived at load (tcq_snap on the device): t8 = clamp(round(tlut * g)), g = float(1 / max|tlut|) * 127; rs = row_scale / g.
@@ -47,8 +48,13 @@ class Layer:
         self.m, self.n = self.sv.numel(), self.su.numel()
         if not (self.bits.shape == ((self.m // 16) * (self.n // 16), 32) and self.m % 16 == 0 and self.n % 16 == 0):
             raise ValueError(f'{name}: bits {tuple(self.bits.shape)} do not fit a ({self.m}, {self.n}) layer of 16 x 16 tiles')
-        if self.tlut.shape != (512, 2):
+        if self.tlut.dim() == 3:                      # row-group tables (G, 512, 2): rows split evenly into G groups
+            G = self.tlut.shape[0]
+            if self.tlut.shape[1:] != (512, 2) or self.m % G or (self.m // G) % 16:
+                raise ValueError(f'{name}: {G} row-group tables need (G, 512, 2) and m / G a multiple of 16 (m = {self.m})')
+        elif self.tlut.shape != (512, 2):
             raise ValueError(f'{name}: table shape {tuple(self.tlut.shape)} != (512, 2)')
+        self.groups = 1 if self.tlut.dim() == 2 else self.tlut.shape[0]
         self.t8, self.rs, self.gain = K.snap(self.tlut, self.row_scale)
         self.bias = None if bias is None else bias.float().to(device).contiguous()
         self._words = None
