@@ -7,10 +7,10 @@ activations and the FP16 512 x 2 codebook (bitshift trellis L = 16, K = 2, V = 2
 (1 MiB of packed words each; 1024 layers = 1 GiB, four times the 256 MB Infinity Cache, so the words come from HBM). One
 step = the complete layer forward of every layer on the same input token:
     input rotation h = fwht(x * su) -> FP16 (tcq_pre_h16, once: the layers share the input signs, as a q/k/v group does)
-    fused decode-GEMV z_l = (h Q_l^T) * r_l for all layers (tcq_gemv_f16, one launch)
-    output rotation y_l = fwht(z_l) * sv_l (tcq_postg, one launch over all layers).
-value = packed-weight bytes per step / step time (GB/s). roofline = the decode-GEMV kernel alone, timed with HIP events on
-the stream it runs on. cpu_baseline = the oracle's restatement of the reference layer (reference_linear, FP16 table,
+    fused decode-GEMV and output rotation y_l = fwht((h Q_l^T) * r_l) * sv_l for all layers (tcq_gemv_f16_post, one launch,
+    one workgroup per layer).
+value = packed-weight bytes per step / step time (GB/s). roofline = the fused decode-GEMV kernel alone, timed with HIP events
+on the stream it runs on. cpu_baseline = the oracle's restatement of the reference layer (reference_linear, FP16 table,
 unquantized activations) timed on the host over a bounded sample of the same layers.
 """
 import argparse
@@ -95,7 +95,7 @@ def make_stream(nl, seed, dev):
 class Stream:
     """Buffers and launch descriptors of one pass over the layer stream (allocated once; the pass allocates nothing)."""
 
-    def __init__(self, L, x, M=1):
+    def __init__(self, L, x, M=1, fused=True):
         import torch
         from yanlongvla_amd import kernels as K
         dev = x.device
@@ -106,14 +106,21 @@ class Stream:
         self.z = torch.empty(nl, M, M_DIM, dtype=torch.float32, device=dev)
         self.y = torch.empty(nl, M, M_DIM, dtype=torch.float16, device=dev)
         w = L['wdev'].view(nl, L['per'])
+        self.fused = fused
         self.gdesc = K.gemv_descriptors([(w[i], L['tlut'][i], L['row_scale'][i], self.z[i]) for i in range(nl)])
         self.pdesc = K.post_segments([(self.z[i], 0, None, L['sv'][i], None, self.y[i], False) for i in range(nl)], dev)
+        self.fdesc = K.gemv_post_descriptors([(w[i], L['tlut'][i], L['row_scale'][i], L['sv'][i], None, self.y[i])
+                                              for i in range(nl)])
 
     def rotate_in(self):
         self.K.pre_h16(self.x, self.L['su'], self.h16, self.hs)
 
     def gemv(self):
-        self.K.gemv_f16(self.gdesc, self.h16, self.hs, M_DIM, N_DIM)
+        if self.fused:
+            import torch
+            self.K.gemv_f16_post(self.fdesc, self.h16, self.hs, M_DIM, N_DIM, torch.float16)
+        else:
+            self.K.gemv_f16(self.gdesc, self.h16, self.hs, M_DIM, N_DIM)
 
     def rotate_out(self):
         import torch
@@ -122,7 +129,8 @@ class Stream:
     def step(self):
         self.rotate_in()
         self.gemv()
-        self.rotate_out()
+        if not self.fused:
+            self.rotate_out()
 
 
 def timed(fn, steps, warmup):
@@ -485,7 +493,7 @@ def main():
     achieved = byts / (ms_gemv * 1e-3) / 1e9
     # single-layer latency (one layer, one token: rotation, decode-GEMV, rotation), HIP graph replays
     L1 = dict(L, tlut=L['tlut'][:1], row_scale=L['row_scale'][:1], sv=L['sv'][:1], wdev=L['wdev'][:L['per']])
-    S1 = Stream(L1, x)
+    S1 = Stream(L1, x, fused=False)            # a single layer runs the latency plan (128 workgroups) and a separate rotation
     lat_med, lat_p95 = graph_latency(S1.step)
     am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
@@ -512,7 +520,7 @@ def main():
                                'FP16 512x2 codebook, L=16 K=2 V=2, input and output block-Walsh rotations',
                    'layers': nl, 'm': M_DIM, 'n': N_DIM, 'tokens': 1, 'packed_bytes_per_step': byts},
         'hbm_frac': round(byts / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1, 1024> (layer-stream plan)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
+        'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1, 1024, true, tcq_gemv_post_layer, 2> (layer stream, output rotation fused)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_from_profile(nl),
                      'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
         'single_layer_ms': {'graph_replay_median': round(lat_med, 5), 'graph_replay_p95': round(lat_p95, 5),

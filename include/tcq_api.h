@@ -222,6 +222,26 @@ int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, con
 int tcq_gemv_f16_groups(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                         int rows_per_table, tcq_stream_t stream);
 
+/* One layer of a decode-GEMV stream with the output rotation fused: y (M, m) = walsh(z) * sv (+ bias) as tcq_post on the FP32
+ * z of tcq_gemv_f16, stored as y_dtype (F16 / BF16 / F32). sv (m,) int8 and bias (m,) FP32 (or NULL) 16-byte aligned. */
+typedef struct tcq_gemv_post_layer {
+    const void* wdev;       /* tcq_repack layout */
+    const void* tlut;       /* (512, 2) FP16 (one table) */
+    const void* row_scale;  /* (m,) FP16 */
+    int rows_per_table;     /* must be 0 */
+    const int8_t* sv;       /* (m,) output signs */
+    const float* bias;      /* (m,) FP32 or NULL */
+    void* y;                /* (M, m) output */
+} tcq_gemv_post_layer;
+
+/* tcq_gemv_f16 + tcq_postg in one launch for layer streams: one workgroup per layer computes its whole z (M <= 16 rows of m
+ * outputs kept in LDS) and rotates it, so z never goes to memory. Bit for bit the two launches when tcq_gemv_f16 runs its
+ * layer-stream plan (from 256 layers on); its latency plan for small batches sums the K chunks in another order.
+ * No reference counterpart (the reference's float path runs the product and the epilogue as separate kernels,
+ * kernels.py:465-489, 612-615). */
+int tcq_gemv_f16_post(const tcq_gemv_post_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
+                      int y_dtype, tcq_stream_t stream);
+
 /* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
  * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
 typedef struct tcq_gemm_seg {

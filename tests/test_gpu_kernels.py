@@ -260,6 +260,33 @@ def test_gemv_f16_deterministic():
     assert torch.equal(z1, z2)
 
 
+@pytest.mark.parametrize('nl,M,m,n', [(300, 1, 512, 1024), (260, 3, 256, 512), (3, 4, 2048, 2048), (2, 1, 8192, 1024),
+                                      (5, 16, 256, 512)])
+@pytest.mark.parametrize('ydt', [torch.float16, torch.bfloat16, torch.float32])
+def test_gemv_post_fused_equals_unfused(nl, M, m, n, ydt):
+    """tcq_gemv_f16_post == tcq_gemv_f16 then tcq_post (FP32 z), with and without bias: bit for bit when the unfused launch
+    also runs the layer-stream plan (>= 256 layers), else within the summation-order difference of its latency plan."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(nl + M + m)
+    layers = [dev_layer(O.random_layer(m, n, 50 + i, bias=i % 2 == 1)) for i in range(nl)]
+    h16 = T(rng.standard_normal((M, n)).astype(np.float16))
+    hs = T(np.full(M, 0.5, np.float32))
+    ws = [K.repack(d['bits'], m, n) for d in layers]
+    zs = [torch.empty(M, m, device=DEV) for _ in layers]
+    K.gemv_f16(K.gemv_descriptors([(w, d['tlut'], d['row_scale'], z) for w, d, z in zip(ws, layers, zs)]), h16, hs, m, n)
+    ys = [torch.empty(M, m, dtype=ydt, device=DEV) for _ in layers]
+    biases = [T(rng.standard_normal(m).astype(np.float32)) if i % 2 else None for i in range(nl)]
+    desc = K.gemv_post_descriptors([(w, d['tlut'], d['row_scale'], d['sv'], b, y) for w, d, b, y in zip(ws, layers, biases, ys)])
+    K.gemv_f16_post(desc, h16, hs, m, n, ydt)
+    for z, d, b, y in zip(zs, layers, biases, ys):
+        ref = torch.empty(M, m, dtype=ydt, device=DEV)
+        K.post(z, None, None, d['sv'], b, ref)
+        if nl >= 256:
+            assert torch.equal(y.view(torch.int16) if ydt != torch.float32 else y, ref.view(torch.int16) if ydt != torch.float32 else ref)
+        else:
+            assert ((y.double() - ref.double()).norm() / ref.double().norm()).item() < (2e-3 if ydt != torch.float32 else 1e-6)
+
+
 # ------------------------------------------------------------------------------------------------------ batched epilogue
 @pytest.mark.parametrize('M', [1, 10, 50])
 def test_postg_matches_post_and_oracle(M):

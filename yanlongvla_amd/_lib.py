@@ -40,6 +40,7 @@ SIGNATURES = {
     'tcq_decode_i8_groups': [_P, _P, _I, _P, _I, _I, _P],
     'tcq_decode_f16_groups': [_P, _P, _I, _P, _I, _I, _P],
     'tcq_gemv_f16_groups': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
+    'tcq_gemv_f16_post': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_bf16': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],

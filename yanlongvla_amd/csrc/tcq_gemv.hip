@@ -50,12 +50,18 @@ __device__ __forceinline__ void fill_table(u32* tab, const u16* tl) {
 // Dynamic LDS: h16 (M, 256 nch) FP16 with zero columns from n on, the FP32 row scales of the workgroup's rows, then for
 // KS > 1 the partial sums (nw R 64 float4). Two accumulators per tile row (pairs 0..3 and 4..7) halve the MFMA dependency
 // chain.
-template <int C, int R, int D, int AUX, int KS, int NE = 1024>
-__global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers, const u16* h16, const float* hscale, int M,
+// POST (layer streams, one workgroup per layer, one table): the output rotation of tcq_post runs in the same workgroup, on the
+// z rows staged in LDS (dynamic LDS then also holds M rows of lds_words(m) floats), and y = walsh(z) * sv (+ bias) is stored
+// as YDT; DESC is then tcq_gemv_post_layer.
+template <class DESC> __device__ __forceinline__ float* zout(const DESC& L) { return nullptr; }
+template <> __device__ __forceinline__ float* zout<tcq_gemv_layer>(const tcq_gemv_layer& L) { return L.z; }
+
+template <int C, int R, int D, int AUX, int KS, int NE = 1024, bool POST = false, class DESC = tcq_gemv_layer, int YDT = TCQ_F16>
+__global__ __launch_bounds__(1024) void k_gemv_f16(const DESC* layers, const u16* h16, const float* hscale, int M,
                                                    int m, int n, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) u32 tab[NE * C];
     extern __shared__ __attribute__((aligned(16))) u32 dyn[];
-    const tcq_gemv_layer L = layers[blockIdx.y];
+    const DESC L = layers[blockIdx.y];
     const int tiles_m = m >> 4, nch = (n + 255) >> 8, np = nch << 8;
     const int I0 = blockIdx.x * rows_per_wg, I1 = min(I0 + rows_per_wg, tiles_m);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
@@ -104,20 +110,28 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
         ((uint4_t*)hl)[i] = k < n ? gptr((const uint4_t*)(h16 + (size_t)t * n + k))[0] : uint4_t{0, 0, 0, 0};
     }
     const u16* rsc = (const u16*)L.row_scale;
-    for (int i = threadIdx.x; i < (I1 - I0) * 16; i += blockDim.x) sl[i] = f16_to_f32(gptr(rsc)[I0 * 16 + i]);
+    if (!POST)                               // POST applies the row scales to the staged z rows instead (keeps two workgroups per CU)
+        for (int i = threadIdx.x; i < (I1 - I0) * 16; i += blockDim.x) sl[i] = f16_to_f32(gptr(rsc)[I0 * 16 + i]);
     __syncthreads();
-    if (KS == 1 && iters == 0) return;
+    if (KS == 1 && !POST && iters == 0) return;
     const float hs = gptr(hscale)[tok ? lr : 0];
     const char* hb = (const char*)hl + (size_t)(lr * np + 16 * lg) * 2;
+    float* zr = sl;                                        // POST: z rows of the layer (before the row scale), stride lds_words(m)
+    const int zw = lds_words(m);
 
     auto epilogue = [&](int r, int Ig, const float4_t& a) {
         const int I = Ig + r;
         if (I < I1 && tok) {
-            const float* s = sl + (I - I0) * 16 + 4 * lg;
-            float4_t o;
+            if constexpr (POST) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (a[e] * hs) * s[e];
-            *gptr((float4_t*)(L.z + (size_t)lr * m + 16 * I + 4 * lg)) = o;
+                for (int e = 0; e < 4; ++e) zr[lr * zw + lds_slot(16 * I + 4 * lg + e)] = a[e] * hs;
+            } else {
+                const float* s = sl + (I - I0) * 16 + 4 * lg;
+                float4_t o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (a[e] * hs) * s[e];
+                *gptr((float4_t*)(zout(L) + (size_t)lr * m + 16 * I + 4 * lg)) = o;
+            }
         }
     };
 
@@ -191,6 +205,49 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(const tcq_gemv_layer* layers,
                 float4_t a = part[(wave * R + r) * 64 + lane];
                 for (int k = 1; k < KS; ++k) a += part[((wave + k) * R + r) * 64 + lane];
                 epilogue(r, Ig, a);
+            }
+        }
+    }
+    if constexpr (POST) {                    // output rotation of every token row: walsh(z) * sv (+ bias) -> y, as tcq_post
+        __syncthreads();
+        for (int i = 8 * threadIdx.x; i < m; i += 8 * blockDim.x) {       // z = (acc * hs) * row scale, as the unfused epilogue
+            const uint4_t rsv = *gptr((const uint4_t*)(rsc + i));
+            float r8[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { r8[2 * k] = f16_to_f32((u16)(rsv[k] & 0xffffu)); r8[2 * k + 1] = f16_to_f32((u16)(rsv[k] >> 16)); }
+            for (int t = 0; t < M; ++t)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) zr[t * zw + lds_slot(i + k)] = zr[t * zw + lds_slot(i + k)] * r8[k];
+        }
+        __syncthreads();
+        for (int t = 0; t < M; ++t) {
+            float* row = zr + t * zw;
+            block_walsh(row, m, [&](int i, float v) { row[lds_slot(i)] = v; });
+            __syncthreads();
+            for (int i = 8 * threadIdx.x; i < m; i += 8 * blockDim.x) {
+                const u64 sg = *gptr((const u64*)((const i8*)L.sv + i));
+                float v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = row[lds_slot(i + k)] * (float)(i8)(sg >> (8 * k));
+                if (L.bias) {
+                    const float4_t b0 = gptr((const float4_t*)(L.bias + i))[0], b1 = gptr((const float4_t*)(L.bias + i))[1];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) { v[k] = v[k] + b0[k]; v[4 + k] = v[4 + k] + b1[k]; }
+                }
+                if constexpr (YDT == TCQ_F32) {
+                    float* y = (float*)L.y + (size_t)t * m + i;
+                    gptr((float4_t*)y)[0] = float4_t{v[0], v[1], v[2], v[3]};
+                    gptr((float4_t*)y)[1] = float4_t{v[4], v[5], v[6], v[7]};
+                } else {
+                    uint4_t w;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const u32 a = YDT == TCQ_BF16 ? f32_to_bf16(v[2 * k]) : f32_to_f16(v[2 * k]);
+                        const u32 b = YDT == TCQ_BF16 ? f32_to_bf16(v[2 * k + 1]) : f32_to_f16(v[2 * k + 1]);
+                        w[k] = a | (b << 16);
+                    }
+                    *gptr((uint4_t*)((u16*)L.y + (size_t)t * m + i)) = w;
+                }
             }
         }
     }
@@ -272,4 +329,30 @@ extern "C" int tcq_gemv_f16_groups(const tcq_gemv_layer* layers, int nlayers, co
 extern "C" int tcq_gemv_f16(const tcq_gemv_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                             tcq_stream_t stream) {
     return tcq_gemv_f16_groups(layers, nlayers, h16, hscale, M, m, n, 0, stream);
+}
+
+// Layer streams with the output rotation fused (POST): one workgroup per layer, single-table layers, M rows of z in LDS.
+extern "C" int tcq_gemv_f16_post(const tcq_gemv_post_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m,
+                                 int n, int y_dtype, tcq_stream_t stream) {
+    if (!layers || !h16 || !hscale || nlayers <= 0 || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16 || m > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (M > 16 || nlayers > 65535) return TCQ_ERR_UNSUPPORTED;
+    if ((uintptr_t)h16 % 16) return TCQ_ERR_ALIGN;
+    if ((size_t)(m / 16) * ((n + 255) / 256) * 1024 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    const int tiles_m = m / 16, nch = (n + 255) / 256;
+    const size_t dyn = (size_t)M * nch * 256 * 2 + (size_t)M * lds_words(m) * 4;
+    if (dyn + 4096 * GEMV_C > 160 * 1024) return TCQ_ERR_UNSUPPORTED;                 // z rows / activations do not fit LDS
+    constexpr int NT = 2;
+    const dim3 grid(1, nlayers), block(GEMV_THREADS);
+    const hipStream_t st = (hipStream_t)stream;
+    const u16* h = (const u16*)h16;
+#define GEMV_POST(YD) launch_k(k_gemv_f16<GEMV_C, GEMV_R, GEMV_D, NT, 1, 1024, true, tcq_gemv_post_layer, YD>, grid, block, dyn, st, \
+                               layers, h, hscale, M, m, n, tiles_m)
+    switch (y_dtype) {
+        case TCQ_F16: GEMV_POST(TCQ_F16); break;
+        case TCQ_BF16: GEMV_POST(TCQ_BF16); break;
+        case TCQ_F32: GEMV_POST(TCQ_F32); break;
+        default: return TCQ_ERR_DTYPE;
+    }
+    return launch_status();
 }

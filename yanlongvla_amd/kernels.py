@@ -226,6 +226,26 @@ def gemv_f16(desc, h16, hscale, m, n, rows_per_table=0):
     call('tcq_gemv_f16_groups', ptr(desc), desc.numel() // 5, ptr(h16), ptr(hscale), M, m, n, rows_per_table, stream())
 
 
+def gemv_post_descriptors(layers):
+    """[(wdev, tlut, row_scale, sv, bias, y), ...] -> device array of tcq_gemv_post_layer (single-table layers; bias may be
+    None). Keep the tensors alive."""
+    flat = []
+    for wdev, tlut, row_scale, sv, bias, y in layers:
+        _contig(wdev, tlut, row_scale, sv, bias, y)
+        if _groups(tlut) != 1:
+            raise ValueError('the fused output rotation takes single-table layers')
+        flat += [ptr(wdev), ptr(tlut), ptr(row_scale), 0, ptr(sv), ptr(bias) or 0, ptr(y)]
+    return torch.tensor(flat, dtype=torch.int64).to(layers[0][0].device)
+
+
+def gemv_f16_post(desc, h16, hscale, m, n, y_dtype):
+    """Layer stream with the output rotation fused: y = walsh((h16 Q^T) * hscale * row_scale) * sv (+ bias) per layer, one
+    launch (bit-identical to gemv_f16 followed by post / postg)."""
+    M = h16.shape[0]
+    _contig(h16, hscale)
+    call('tcq_gemv_f16_post', ptr(desc), desc.numel() // 7, ptr(h16), ptr(hscale), M, m, n, DTYPE[y_dtype], stream())
+
+
 _SEG = None
 
 
