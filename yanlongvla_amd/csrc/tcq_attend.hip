@@ -6,7 +6,8 @@
 // head, their chunk maximum m, the exponentials e = exp(s - m), l = sum e and the unnormalised outputs o = sum e v; then
 // k_attn_combine merges the chunks of a token (weights exp(m_c - max_c m_c)) and divides by the merged sum. The result
 // depends on the number of keys only through this fixed chunking, never on launch shapes. The combine can feed its BF16
-// output row straight into the rotate + quantize prologue of the output projection.
+// output row straight into the rotate + quantize prologue of the output projection. The dot products and weighted sums
+// use fused multiply-adds (this attention is the decoder layers' own definition, not a reference rounding chain).
 #include "tcq_device.h"
 #include "tcq_launch.h"
 
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 #pragma unroll
                     for (int h = 0; h < AH; ++h)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) a[h] = a[h] + qs[h][32 * b + 8 * p + e] * kv[e];
+                        for (int e = 0; e < 8; ++e) a[h] = __builtin_fmaf(qs[h][32 * b + 8 * p + e], kv[e], a[h]);
                 }
             }
 #pragma unroll
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
             for (int kk = 0; kk < kend; ++kk) {
                 const float x = bf16_to_f32(vs[kk][d]);
 #pragma unroll
-                for (int h = 0; h < AH; ++h) o[h] = o[h] + ps[h][blk * 64 + kk] * x;
+                for (int h = 0; h < AH; ++h) o[h] = __builtin_fmaf(ps[h][blk * 64 + kk], x, o[h]);
             }
         }
         for (int h = 0; h < H; ++h) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = o[h];
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
 #pragma unroll
         for (int h = 0; h < AH; ++h) v[h] = h < H ? col[h * (AD + 2)] : 0.f;
 #pragma unroll
-        for (int h = 0; h < AH; ++h) acc[h] = acc[h] + wts[h][c] * v[h];
+        for (int h = 0; h < AH; ++h) acc[h] = __builtin_fmaf(wts[h][c], v[h], acc[h]);
     }
     for (int h = 0; h < H; ++h) {
         const u16 b = f32_to_bf16(acc[h] / inv[h]);
