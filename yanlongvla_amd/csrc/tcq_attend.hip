@@ -3,7 +3,8 @@
 // rows followed by this call's own rows, so no concatenated copy is made.
 //
 // Split over the keys (64 per chunk): k_attn_part computes, for one query token and one key chunk, the scores of every
-// head, their chunk maximum m, the exponentials e = exp(s - m), l = sum e and the unnormalised outputs o = sum e v; then
+// head (BF16 MFMA, FP32 sums), their chunk maximum m, the exponentials e = exp(s - m), l = sum e (FP32) and the unnormalised
+// outputs o = sum bf16(e) v (BF16 MFMA, FP32 sums); then
 // k_attn_combine merges the chunks of a token (weights exp(m_c - max_c m_c)) and divides by the merged sum. The result
 // depends on the number of keys only through this fixed chunking, never on launch shapes. The combine can feed its BF16
 // output row straight into the rotate + quantize prologue of the output projection. The dot products and weighted sums
@@ -24,137 +25,117 @@ __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh
 
 }  // namespace
 
-// grid (tokens M, chunks NC), AT threads. part: (M, NC, H, AD + 2) FP32: o[AD], m, l per head.
-// Keys: each pass of 64 keys loads its rows with 16-byte loads (the next pass's are in flight while one is used). Values:
-// blocks of 64 rows staged in LDS with 16-byte loads (the next block's loads in flight while one is used), then one thread
-// per dim walks the block's keys in order.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+constexpr int VST = 272;          // u16 stride of the staged value rows: 136 words, so keys lg + 4i of lane groups lg = 0..3 fall
+                                  // 8 banks apart and a 16-lane x 2-byte fragment read is free of conflicts
+
+__device__ __forceinline__ float4_t mma_bf16(uint4_t a, uint4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// grid (tokens M, chunks NC), AT = 256 threads (4 waves). part: (M, NC, H, AD + 2) FP32: o[AD], m, l per head.
+// Scores on v_mfma_f32_16x16x32_bf16: A = the query rows of the token (heads 0..7, rows 8..15 zero), B = 16 keys per wave, 8
+// K steps of 32 dims; lane (g, c) of D holds heads 4g..4g+3 of key c. Softmax statistics per head over the chunk's 64 keys.
+// Outputs on the same MFMA: A = the exponentials e (BF16, heads x keys), B = 16 value columns x 32 keys gathered from the LDS
+// stage; each wave owns 4 of the 16 column tiles, 2 K steps. Element i of lane group lg in K step ks is key 32 ks + lg + 4 i
+// in both operands (any common order of the K index gives the same product).
 __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, const u16* vc, int P, const u16* kn, const u16* vn,
                                                   int M, int H, int causal, float* part) {
-    __shared__ float qs[AH][AD];
     __shared__ float ps[AH][KC + 1];
-    __shared__ __attribute__((aligned(16))) u16 vs[64][AD];
+    __shared__ __attribute__((aligned(16))) u16 vs[KC][VST];
     const int t = blockIdx.x, c = blockIdx.y, NC = gridDim.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int T = P + M, j0 = c * KC;
     const int jend = min(T, causal >= 0 ? causal + t + 1 : T);        // keys j < jend are visible to this query
     const int nvis = max(0, min(KC, jend - j0));                        // visible keys of this chunk
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
-    if (nvis > 0) {
-        for (int i = tid; i < AH * AD; i += AT) {
-            const int h = i / AD, d = i - h * AD;
-            qs[h][d] = h < H ? bf16_to_f32(gptr(q)[(size_t)t * H * AD + h * AD + d]) : 0.f;
+    // value stage: 64 rows x 256 dims, 8 granules of 16 bytes per thread, issued first
+    uint4_t vg[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int gi = u * AT + tid, row = gi >> 5, col = gi & 31, j = j0 + row;
+        vg[u] = j < jend ? gptr((const uint4_t*)(key_row(vc, vn, P, j) + 8 * col))[0] : uint4_t{0, 0, 0, 0};
+    }
+    // scores
+    {
+        const int j = j0 + 16 * wave + lr;                               // this lane's key (B column)
+        const bool kv = j < jend;
+        const u16* kr = kv ? key_row(kc, kn, P, j) : nullptr;
+        const u16* qr = q + (size_t)t * H * AD + (size_t)lr * AD;        // query row of head lr (A row)
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        uint4_t A[8], B[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            A[ks] = lr < H ? gptr((const uint4_t*)(qr + 32 * ks + 8 * lg))[0] : uint4_t{0, 0, 0, 0};
+            B[ks] = kv ? gptr((const uint4_t*)(kr + 32 * ks + 8 * lg))[0] : uint4_t{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) acc = mma_bf16(A[ks], B[ks], acc);
+        if (lg < 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ps[4 * lg + e][16 * wave + lr] = kv ? acc[e] * scl : -__builtin_inff();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int gi = u * AT + tid;
+        *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = vg[u];
+    }
+    __syncthreads();
+    // chunk softmax statistics: wave w takes heads 2w, 2w + 1, lane = key
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const int h = 2 * wave + hh;
+        const float sv = ps[h][lane];
+        const float m = wave_max(sv);
+        const float e = m == -__builtin_inff() ? 0.f : expf(sv - m);
+        float l = e;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
+        ps[h][lane] = e;
+        if (lane == 0 && h < H) {
+            float* base = part + (((size_t)t * NC + c) * H + h) * (AD + 2);
+            base[AD] = m;
+            base[AD + 1] = l;
         }
     }
     __syncthreads();
-    const int npass = (nvis + 63) >> 6;
-    // scores: thread (key kk = tid / 4, part p = tid % 4: dims 32 b + 8 p + e), 8 heads, reduced over the 4 parts; the
-    // 4 parts of a key read adjacent 32-byte pieces of the query rows (different LDS banks)
+    // unnormalised outputs o[h][d] = sum_k e[h][k] v[k][d]
     {
-        const int p = tid & 3;
-        uint4_t w[2][8];
-        auto fetch = [&](int pass, uint4_t(&dst)[8]) {
-            const int j = j0 + pass * 64 + (tid >> 2);
-            if (pass < npass && j < jend) {
-                const u16* kr = key_row(kc, kn, P, j) + 8 * p;
+        uint4_t A[2];                                                   // e of heads lr (< 8), BF16
 #pragma unroll
-                for (int b = 0; b < 8; ++b) dst[b] = gptr((const uint4_t*)(kr + 32 * b))[0];
+        for (int ks = 0; ks < 2; ++ks) {
+            u32 w[4];
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const int k0 = 32 * ks + lg + 8 * k2;                   // elements 2 k2, 2 k2 + 1: keys k0, k0 + 4
+                const float e0 = lr < AH ? ps[lr][k0] : 0.f, e1 = lr < AH ? ps[lr][k0 + 4] : 0.f;
+                w[k2] = (u32)f32_to_bf16(e0) | ((u32)f32_to_bf16(e1) << 16);
             }
-        };
-        fetch(0, w[0]);
+            A[ks] = uint4_t{w[0], w[1], w[2], w[3]};
+        }
 #pragma unroll
-        for (int pass = 0; pass < KC / 64; ++pass) {
-            const int kk = pass * 64 + (tid >> 2), j = j0 + kk;
-            if (pass + 1 < KC / 64) fetch(pass + 1, w[(pass + 1) & 1]);
-            float a[AH];
+        for (int tl = 0; tl < 4; ++tl) {
+            const int d = 16 * (4 * wave + tl) + lr;                     // this lane's value column
+            float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int h = 0; h < AH; ++h) a[h] = 0.f;
-            if (pass < npass && j < jend) {
+            for (int ks = 0; ks < 2; ++ks) {
+                u32 w[4];
 #pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    float kv[8];
+                for (int k2 = 0; k2 < 4; ++k2) {
+                    const int k0 = 32 * ks + lg + 8 * k2;
+                    w[k2] = (u32)vs[k0][d] | ((u32)vs[k0 + 4][d] << 16);
+                }
+                acc = mma_bf16(A[ks], uint4_t{w[0], w[1], w[2], w[3]}, acc);
+            }
+            if (lg < 2) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kv[2 * e] = bf16_to_f32((u16)(w[pass & 1][b][e] & 0xffffu));
-                        kv[2 * e + 1] = bf16_to_f32((u16)(w[pass & 1][b][e] >> 16));
-                    }
-#pragma unroll
-                    for (int h = 0; h < AH; ++h)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) a[h] = __builtin_fmaf(qs[h][32 * b + 8 * p + e], kv[e], a[h]);
+                for (int e = 0; e < 4; ++e) {
+                    const int h = 4 * lg + e;
+                    if (h < H) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = acc[e];
                 }
             }
-#pragma unroll
-            for (int h = 0; h < AH; ++h) {
-                a[h] = a[h] + __shfl_xor(a[h], 1, 64);
-                a[h] = a[h] + __shfl_xor(a[h], 2, 64);
-            }
-            if (p == 0) {
-#pragma unroll
-                for (int h = 0; h < AH; ++h) ps[h][kk] = j < jend ? a[h] * scl : -__builtin_inff();
-            }
         }
-    }
-    __syncthreads();
-    // chunk softmax statistics: wave w takes heads 2w, 2w + 1; lane holds keys lane + 64 i
-    {
-        const int w = tid >> 6, lane = tid & 63;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const int h = 2 * w + hh;
-            float sv[KC / 64], m = -__builtin_inff();
-#pragma unroll
-            for (int i = 0; i < KC / 64; ++i) {
-                sv[i] = ps[h][lane + 64 * i];
-                m = fmaxf(m, sv[i]);
-            }
-            m = wave_max(m);
-            float l = 0.f;
-#pragma unroll
-            for (int i = 0; i < KC / 64; ++i) {
-                const float e = m == -__builtin_inff() ? 0.f : expf(sv[i] - m);
-                ps[h][lane + 64 * i] = e;
-                l = l + e;
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
-            if (lane == 0 && h < H) {
-                float* base = part + (((size_t)t * NC + c) * H + h) * (AD + 2);
-                base[AD] = m;
-                base[AD + 1] = l;
-            }
-        }
-    }
-    // unnormalised outputs: thread = dim d, 8 heads, keys of the chunk in order, values from the LDS stage
-    {
-        const int d = tid;
-        float o[AH];
-#pragma unroll
-        for (int h = 0; h < AH; ++h) o[h] = 0.f;
-        uint4_t v[8];                                              // this thread's 8 of the block's 2048 16-byte granules
-        auto vfetch = [&](int blk) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int gi = u * AT + tid, row = gi >> 5, col = gi & 31, j = j0 + blk * 64 + row;
-                v[u] = j < jend ? gptr((const uint4_t*)(key_row(vc, vn, P, j) + 8 * col))[0] : uint4_t{0, 0, 0, 0};
-            }
-        };
-        if (npass > 0) vfetch(0);
-        for (int blk = 0; blk < npass; ++blk) {
-            __syncthreads();                                       // ps complete (first block) / previous block consumed
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int gi = u * AT + tid;
-                *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = v[u];
-            }
-            __syncthreads();
-            if (blk + 1 < npass) vfetch(blk + 1);
-            const int kend = min(64, nvis - blk * 64);
-            for (int kk = 0; kk < kend; ++kk) {
-                const float x = bf16_to_f32(vs[kk][d]);
-#pragma unroll
-                for (int h = 0; h < AH; ++h) o[h] = __builtin_fmaf(ps[h][blk * 64 + kk], x, o[h]);
-            }
-        }
-        for (int h = 0; h < H; ++h) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = o[h];
     }
 }
 
