@@ -462,6 +462,11 @@ def backbone(args, dev):
                 decode_effective_int8_GBs_resident=round(BACKBONE_WEIGHTS / (res['resident']['decode_ms_per_token'] * 1e-3) / 1e9, 1))
 
 
+def note(msg):
+    """Progress line of a finished stage, on stderr (the JSON result line stays alone on stdout)."""
+    print(f'[bench] {msg}', file=sys.stderr, flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -486,27 +491,36 @@ def main():
     err = check_against_oracle(L, S)
     if not err < 2e-3:
         raise SystemExit(f'decode-GEMV output differs from the oracle: relative L2 {err}')
+    note(f'layer stream checked against the oracle (relative L2 {err:.2e})')
 
     ms_step = timed(S.step, args.steps, args.warmup)
     ms_gemv = timed(S.gemv, args.steps, args.warmup)
     byts = nl * PACKED_BYTES
     achieved = byts / (ms_gemv * 1e-3) / 1e9
+    note(f'layer stream timed: {ms_step:.4f} ms per step, {ms_gemv:.4f} ms per decode-GEMV launch')
     # single-layer latency (one layer, one token: rotation, decode-GEMV, rotation), HIP graph replays
     L1 = dict(L, tlut=L['tlut'][:1], row_scale=L['row_scale'][:1], sv=L['sv'][:1], wdev=L['wdev'][:L['per']])
     S1 = Stream(L1, x, fused=False)            # a single layer runs the latency plan (128 workgroups) and a separate rotation
     lat_med, lat_p95 = graph_latency(S1.step)
     am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
+    note(f'single-layer latency timed: {lat_med:.4f} ms per graph replay')
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
+    if cpu:
+        note(f'CPU baseline timed: {cpu["value"]} {cpu["unit"]}')
     ops = None
     if not args.no_ops:
         ops = {'rht_bf16': rht_figures(dev, args.seed), 'w8a8_gemm_K2048_N16384': gemm_figures(dev, args.seed)}
+        note('RHT and W8A8 GEMM shapes timed')
     chunk = None
     if not args.no_chunk:
         del S1, L1
         chunk, keep, setup = action_chunk(args, dev)
         if not all(chunk['bitexact_vs_reference_runtime'].values()):
             raise SystemExit(f'action chunk differs from the reference runtime: {chunk["bitexact_vs_reference_runtime"]}')
+        note(f'action chunk timed: {chunk["ms_per_chunk"]} ms (fly)')
         chunk['cpu_baseline'] = None if args.no_cpu else chunk_cpu_baseline(keep, setup, args.cpu_seconds)
+        if chunk['cpu_baseline']:
+            note('action chunk CPU baseline timed')
     out = {
         'metric': 'TCQ-2bit decode-GEMV GB/s (% HBM peak) + ms per action chunk, 1 GPU',
         'value': round(byts / (ms_step * 1e-3) / 1e9, 2),
@@ -533,6 +547,7 @@ def main():
     }
     if not args.no_backbone:
         out['backbone'] = backbone(args, dev)
+        note('backbone timed')
         if not all(out['backbone']['bitexact_vs_reference_runtime'].values()):
             raise SystemExit(f'backbone differs from the reference runtime: {out["backbone"]["bitexact_vs_reference_runtime"]}')
     print(json.dumps(out), flush=True)
