@@ -139,56 +139,88 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     }
 }
 
-// grid M, block 256 (one thread per dim). o (M, H * AD) BF16 (or NULL); with su, the row also goes through the rotate +
-// quantize prologue (q8 row-major (M, H * AD), scale (M,)). The chunk statistics of the token are staged in LDS first and
-// the weights exp(m_c - max m) computed once per (chunk, head); each thread then sums its dim over the chunks, the loads
-// of all chunks in flight together.
+// grid M, CT = 1024 threads: thread (d, g) = (tid % 256, tid / 256) sums dim d of every head over the chunks c = g (mod 4);
+// wave h < H first merges head h's chunk statistics (lane = chunk). The four partial sums of a head add in the fixed order
+// ((g0 + g1) + g2) + g3, so the result depends only on NC. With su set, the BF16 row (H x 256) is rotated and quantized
+// in place as the output projection's prologue.
 constexpr int MAXC = 256;        // most chunks a token may have in the combine (16384 keys)
-__global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
+constexpr int CT = 1024, CG = CT / AD, CB = 4;   // threads, chunk groups, chunks per group held in registers per batch
+
+__global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
     extern __shared__ float lds[];
-    __shared__ float red[16];
+    __shared__ float red[CT / 64];
     __shared__ float wts[AH][MAXC];
-    __shared__ float ls[AH][MAXC];
     __shared__ float inv[AH];
-    const int t = blockIdx.x, d = threadIdx.x, K = H * AD;
+    __shared__ float sums[CG][AH][AD];
+    const int t = blockIdx.x, tid = threadIdx.x, d = tid & (AD - 1), g = tid / AD, lane = tid & 63, wave = tid >> 6, K = H * AD;
     const size_t cs = (size_t)H * (AD + 2);                          // stride between chunks
     const float* tb = part + (size_t)t * NC * cs;
-    for (int i = threadIdx.x; i < H * NC; i += blockDim.x) {
-        const int h = i / NC, c = i - h * NC;
-        wts[h][c] = tb[c * cs + h * (AD + 2) + AD];                  // m
-        ls[h][c] = tb[c * cs + h * (AD + 2) + AD + 1];               // l
-    }
-    __syncthreads();
-    if (threadIdx.x < H) {
-        const int h = threadIdx.x;
-        float mx = -__builtin_inff();
-        for (int c = 0; c < NC; ++c) mx = fmaxf(mx, wts[h][c]);
-        float L = 0.f;
-        for (int c = 0; c < NC; ++c) {
-            const float m = wts[h][c];
-            const float w = m == -__builtin_inff() ? 0.f : expf(m - mx);
-            L = L + w * ls[h][c];
-            wts[h][c] = w;
+    constexpr int SR = MAXC / 64;
+    float mv[SR], lv[SR];
+    if (wave < H) {
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int c = 64 * r + lane;
+            mv[r] = c < NC ? tb[c * cs + wave * (AD + 2) + AD] : -__builtin_inff();
+            lv[r] = c < NC ? tb[c * cs + wave * (AD + 2) + AD + 1] : 0.f;
         }
-        inv[h] = L;
+    }
+    float v[CB][AH];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            const int c = c0 + g + CG * i;
+#pragma unroll
+            for (int h = 0; h < AH; ++h) v[i][h] = c < NC && h < H ? tb[c * cs + h * (AD + 2) + d] : 0.f;
+        }
+    };
+    load(0);
+    if (wave < H) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < SR; ++r) mx = fmaxf(mx, mv[r]);
+        mx = wave_max(mx);
+        float L = 0.f;
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int c = 64 * r + lane;
+            const float w = mv[r] == -__builtin_inff() ? 0.f : expf(mv[r] - mx);
+            if (c < NC) wts[wave][c] = w;
+            L = __builtin_fmaf(w, lv[r], L);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) L = L + __shfl_xor(L, off, 64);
+        if (lane == 0) inv[wave] = L;
     }
     __syncthreads();
     float acc[AH];
 #pragma unroll
     for (int h = 0; h < AH; ++h) acc[h] = 0.f;
-#pragma unroll 4
-    for (int c = 0; c < NC; ++c) {
-        const float* col = tb + c * cs + d;
-        float v[AH];
+    for (int c0 = 0; c0 < NC; c0 += CG * CB) {
+        if (c0) load(c0);
 #pragma unroll
-        for (int h = 0; h < AH; ++h) v[h] = h < H ? col[h * (AD + 2)] : 0.f;
+        for (int i = 0; i < CB; ++i) {
+            const int c = c0 + g + CG * i;
+            if (c < NC) {
 #pragma unroll
-        for (int h = 0; h < AH; ++h) acc[h] = __builtin_fmaf(wts[h][c], v[h], acc[h]);
+                for (int h = 0; h < AH; ++h)
+                    if (h < H) acc[h] = __builtin_fmaf(wts[h][c], v[i][h], acc[h]);
+            }
+        }
     }
-    for (int h = 0; h < H; ++h) {
-        const u16 b = f32_to_bf16(acc[h] / inv[h]);
-        if (o) gptr(o)[(size_t)t * K + h * AD + d] = b;
-        if (su) lds[lds_slot(h * AD + d)] = bf16_to_f32(b) * (float)gptr(su)[h * AD + d];
+#pragma unroll
+    for (int h = 0; h < AH; ++h)
+        if (h < H) sums[g][h][d] = acc[h];
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < AH / CG; ++hh) {
+        const int h = (AH / CG) * g + hh;
+        if (h < H) {
+            const float tot = ((sums[0][h][d] + sums[1][h][d]) + sums[2][h][d]) + sums[3][h][d];
+            const u16 b = f32_to_bf16(tot / inv[h]);
+            if (o) gptr(o)[(size_t)t * K + h * AD + d] = b;
+            if (su) lds[lds_slot(h * AD + d)] = bf16_to_f32(b) * (float)gptr(su)[h * AD + d];
+        }
     }
     if (!su) return;
     __syncthreads();
@@ -199,7 +231,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, int NC,
     quantize_row(lds, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
 }
 
-// =========================================================================================================== C ABI
 extern "C" int tcq_attend_chunks(int P, int M) { return (P + M + KC - 1) / KC; }
 
 extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
@@ -215,7 +246,7 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     hipStream_t st = (hipStream_t)stream;
     launch_k(k_attn_part, dim3(M, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
              (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
-    launch_k(k_attn_combine, dim3(M), dim3(256), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
+    launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
              (u16*)o, (const i8*)su, (i8*)q8, scale);
     return launch_status();
 }
