@@ -134,32 +134,78 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const 
     }
 
     // epilogue: block (i, j), register 4 q + e of lane (lh, l32) = token m0 + (wm BM + j) 32 + 8 q + 4 lh + e, weight
-    // n0 + (wn BN + i) 32 + l32: the 32 lanes of a half store 32 consecutive output columns (coalesced)
+    // n0 + (wn BN + i) 32 + l32.
+    if constexpr (ODT == TCQ_I32) {
+        // the 32 lanes of a half store 32 consecutive int32 columns: whole 128-byte lines
 #pragma unroll
-    for (int j = 0; j < BM; ++j) {
-        const int mb = m0 + (wm * BM + j) * 32 + 4 * lh;
-        float sam[16];
+        for (int j = 0; j < BM; ++j) {
+            const int mb = m0 + (wm * BM + j) * 32 + 4 * lh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = mb + 8 * (r >> 2) + (r & 3);
-            sam[r] = (ODT != TCQ_I32 && m < M && sa) ? gptr(sa)[m] : 1.f;
+            for (int i = 0; i < BN; ++i) {
+                const int n = n0 + (wn * BN + i) * 32 + l32;
+                if (n >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mb + 8 * (r >> 2) + (r & 3);
+                    if (m < M) gptr((int*)out)[(size_t)m * ldo + n] = (int)acc[i][j][r];
+                }
+            }
         }
+    } else {
+        // FP32 / BF16: each wave stages one 32-token block row of its tile at a time in its own slice of the (now idle) LDS
+        // ring, row-major, and stores it back as 16-byte pieces of whole row segments (2-byte scattered stores of BF16
+        // leave half lines and run at a fraction of the bandwidth).
+        constexpr int OSZ = ODT == TCQ_BF16 ? 2 : 4;
+        constexpr int WTN = TN / WN, RB = WTN * OSZ, GPR = RB / 16, EPG = 16 / OSZ;
+        constexpr int SLICE = NS * BLK * 1024 / NWAVE;
+        static_assert(32 * RB <= SLICE, "epilogue staging slice");
+        __syncthreads();                                                 // every wave is done with the ring
+        char* slice = &lds[0][0] + wave * SLICE;
+        const int nw0 = n0 + wn * WTN;
+        const bool vec = ((size_t)ldo * OSZ) % 16 == 0 && ((uintptr_t)out % 16) == 0;
+        float swv[BN];
 #pragma unroll
         for (int i = 0; i < BN; ++i) {
-            const int n = n0 + (wn * BN + i) * 32 + l32;
-            if (n >= N) continue;
-            const float swn = (ODT != TCQ_I32 && sw) ? gptr(sw)[n] : 1.f;
+            const int n = nw0 + i * 32 + l32;
+            swv[i] = (sw && n < N) ? gptr(sw)[n] : 1.f;
+        }
+#pragma unroll
+        for (int j = 0; j < BM; ++j) {
+            const int mb = m0 + (wm * BM + j) * 32;
+            float sam[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = mb + 8 * (r >> 2) + (r & 3);
-                if (m >= M) continue;
-                const size_t o = (size_t)m * ldo + n;
-                if (ODT == TCQ_I32) gptr((int*)out)[o] = (int)acc[i][j][r];
-                else {
-                    const float v = ESZ == 1 ? ((float)acc[i][j][r] * sam[r]) * swn
-                                             : (sa ? (float)acc[i][j][r] * sam[r] : (float)acc[i][j][r]) * (sw ? swn : 1.f);
-                    if (ODT == TCQ_F32) gptr((float*)out)[o] = v;
-                    else gptr((u16*)out)[o] = f32_to_bf16(v);
+                const int m = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+                sam[r] = (sa && m < M) ? gptr(sa)[m] : 1.f;
+            }
+#pragma unroll
+            for (int i = 0; i < BN; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int tr = 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const float v = ESZ == 1 ? ((float)acc[i][j][r] * sam[r]) * swv[i]
+                                             : (sa ? (float)acc[i][j][r] * sam[r] : (float)acc[i][j][r]) * (sw ? swv[i] : 1.f);
+                    char* dst = slice + tr * RB + (i * 32 + l32) * OSZ;
+                    if (ODT == TCQ_F32) *(float*)dst = v;
+                    else *(u16*)dst = f32_to_bf16(v);
+                }
+#pragma unroll
+            for (int g = lane; g < 32 * GPR; g += 64) {
+                const int tr = g / GPR, cg = g - tr * GPR;
+                const int m = mb + tr, n = nw0 + cg * EPG;
+                if (m >= M || n >= N) continue;
+                const uint4_t v = *(const uint4_t*)(slice + tr * RB + cg * 16);
+                char* o = (char*)out + ((size_t)m * ldo + n) * OSZ;
+                if (vec && n + EPG <= N) {
+                    *gptr((uint4_t*)o) = v;
+                } else {                                                 // row end or unaligned rows: element stores
+#pragma unroll
+                    for (int e = 0; e < EPG; ++e) {
+                        if (n + e >= N) break;
+                        const u32 word = v[e * OSZ / 4];
+                        if (OSZ == 2) gptr((u16*)o)[e] = (u16)(word >> (16 * (e & 1)));
+                        else gptr((u32*)o)[e] = word;
+                    }
                 }
             }
         }
