@@ -156,6 +156,44 @@ def test_install_operating_points_agree():
     assert torch.isfinite(outs['fly']).all()
 
 
+@pytest.mark.parametrize('part', ['expert', 'backbone'])
+def test_chained_prologues_bitexact(part):
+    """A decoder layer's last epilogue computing the next layer's norm + rotate + quantize prologue (FUSE['chain']) gives
+    the same outputs as each layer running its own tcq_norm_pre, and the hand-off is taken at every layer boundary: a
+    3-layer expert over a 2-step chunk (inside inference mode), and a 3-layer backbone over a 120-token prefill plus 2
+    decode steps (version counters)."""
+    from yanlongvla_amd import gemma, modules
+    outs, taken = {}, {}
+    for chain in (False, True):
+        modules.FUSE['chain'] = chain
+        try:
+            if part == 'expert':
+                model = small_expert(layers=3, seed=4)
+                modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 13, DEV))
+                noise = torch.randn(50, 32, generator=torch.Generator(device=DEV).manual_seed(6), device=DEV)
+                before = modules.STATS['chained_prologues']
+                with torch.inference_mode():                 # inference tensors: the identity check
+                    outs[chain] = [model.sample_chunk(noise, steps=2)]
+                expect = 2 * 2
+            else:
+                model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
+                modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 14, DEV))
+                x = torch.randn(120, 2048, generator=torch.Generator(device=DEV).manual_seed(7), device=DEV).bfloat16()
+                before = modules.STATS['chained_prologues']
+                h, ks, vs = model.prefill(x)
+                outs[chain] = [h]
+                for t in range(2):
+                    h, ks, vs = model.decode_step(x[t:t + 1], ks, vs)
+                    outs[chain].append(h)
+                expect = 2 * 3
+            taken[chain] = modules.STATS['chained_prologues'] - before
+        finally:
+            modules.FUSE['chain'] = True
+    assert taken == {False: 0, True: expect}
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+
+
 def test_load_from_packed_file(tmp_path):
     from yanlongvla_amd import gemma, modules
     from yanlongvla_amd import tcq_format as F

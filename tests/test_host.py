@@ -84,3 +84,43 @@ def test_from_qtip_matches_qtip_reconstruction(tmp_path):
     assert np.allclose(L.dense('fp16'), W, atol=1e-5 * np.abs(W).max())
     with pytest.raises(ValueError):
         F.from_qtip(dict(rec, su_fp16=torch.ones(4480, dtype=torch.float16), trellis_int16=torch.zeros(4, 32, dtype=torch.int16)))
+
+
+def test_decoder_layer_handoff_rules():
+    """The chained prologue is taken only for the very tensor it was computed from (a view of it is fine), unmodified,
+    and only once; for inference tensors (no version counter) only for the very object the previous layer returned."""
+    import torch
+    from yanlongvla_amd.modules import KDecoderLayer
+    layer = KDecoderLayer.__new__(KDecoderLayer)
+    torch.nn.Module.__init__(layer)
+    b = dict(q=torch.zeros(4, 8, dtype=torch.int8), scale=torch.zeros(4))
+
+    def hand(x4):
+        out = x4.reshape(2, 2, 8)
+        layer._handoff = (x4, None if x4.is_inference() else x4._version, out, b)
+        return out
+
+    def take(x):
+        return layer._prologue(x, x.reshape(-1, 8).contiguous())
+
+    x4 = torch.zeros(4, 8, dtype=torch.bfloat16)
+    out = hand(x4)
+    assert take(out) is b
+    assert take(out) is None                                     # taken once
+    out = hand(x4)
+    assert take(x4) is b                                         # another view of the same storage, unmodified
+    out = hand(x4)
+    out.add_(1)
+    assert take(out) is None                                     # modified in place since
+    out = hand(x4)
+    assert take(out.clone()) is None                             # another tensor with equal values
+    out = hand(x4)
+    assert layer._prologue(out, x4[:2]) is None                  # another shape
+    with torch.inference_mode():
+        y4 = torch.zeros(4, 8, dtype=torch.bfloat16)
+        out = hand(y4)
+        assert take(out) is b                                    # the returned object itself
+        out = hand(y4)
+        assert take(out + 0) is None                             # a new tensor
+        out = hand(y4)
+        assert take(y4.reshape(2, 2, 8)) is None                 # another object over the same storage

@@ -25,10 +25,11 @@ from . import tcq_format as F
 
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
-STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0)
+STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
-# and residual adds fused into the prologues / epilogues)
-FUSE = dict(post3=True, mlp=True, split=False, layer=True)
+# and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
+# layer's norm + rotate + quantize prologue
+FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -247,13 +248,36 @@ class KDecoderLayer(torch.nn.Module):
     model's own), o rotate + quantize, o product, o epilogue + residual + norm2 + rotate + quantize (tcq_post_add_norm_pre),
     gate/up product, gated middle (tcq_mid2), down product, down epilogue + residual. Every rounding point is the unfused
     layer's, so the output equals the module-by-module forward bit for bit. No reference counterpart: it extends the
-    reference's MLP fusion (modules.py:170-189) to the whole layer."""
+    reference's MLP fusion (modules.py:170-189) to the whole layer.
+
+    Chained layers (install links the consecutive decoder layers of a stack): the down epilogue + residual also runs the
+    next layer's norm1 + rotate + quantize on the residual output it writes, and leaves the result with the next layer.
+    That layer takes it instead of launching tcq_norm_pre only when its input is that very output (same storage and shape;
+    the hand-off keeps the output alive, so its memory cannot be reused meanwhile) and unmodified: same version counter,
+    or, for inference tensors (torch.inference_mode keeps no version counters), the very object this layer returned. An
+    in-place change of that returned object between two layers inside inference mode is the one case the check cannot
+    see; FUSE['chain'] = False turns the hand-off off."""
 
     def __init__(self, layer, qkv, o, mlp):
         super().__init__()
         self.input_layernorm, self.post_attention_layernorm = layer.input_layernorm, layer.post_attention_layernorm
         self.self_attn, self.mlp = layer.self_attn, mlp
         self.groups = [qkv, o]
+        self._next = []          # the following decoder layer of the stack (kept out of the module tree)
+        self._handoff = None     # (residual output, its version, q / scale buffers) left by the previous layer
+
+    def _prologue(self, x, x2):
+        """The q/k/v input buffers the previous layer computed for exactly this input (x as passed, x2 its 2-D view), or
+        None."""
+        h, self._handoff = self._handoff, None
+        if h is None:
+            return None
+        xo, ver, ret, b = h
+        if x2.data_ptr() != xo.data_ptr() or x2.shape != xo.shape or x2.dtype != xo.dtype:
+            return None
+        if ver is None:
+            return b if x is ret else None
+        return b if (not x2.is_inference() and x2._version == ver) else None
 
     def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
         qkv, og = self.groups
@@ -262,8 +286,12 @@ class KDecoderLayer(torch.nn.Module):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1]).contiguous()
         M, dev = x2.shape[0], x2.device
-        b = qkv.buffers(M, dev)
-        kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], scale=b['scale'])
+        b = self._prologue(x, x2)
+        if b is None:
+            b = qkv.buffers(M, dev)
+            kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], scale=b['scale'])
+        else:
+            STATS['chained_prologues'] += 1
         q, k, v = qkv.posts(qkv.product(b), b, x2.shape)
         if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
             b2 = og.buffers(M, dev)
@@ -283,9 +311,19 @@ class KDecoderLayer(torch.nn.Module):
         z4 = dn.product(b4)
         x4 = torch.empty_like(x2)
         sc = z4.dtype == torch.float32
-        kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4)
+        nxt = self._next[0] if (self._next and FUSE['chain']) else None
+        if nxt is None:
+            kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4)
+        else:
+            nq, nn1 = nxt.groups[0], nxt.input_layernorm
+            bn = nq.buffers(M, dev)
+            kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4,
+                                      nn1.weight, nn1.eps, nq.su, q=bn['q'], scale=bn['scale'])
+        out = x4.reshape(shape)
+        if nxt is not None:
+            nxt._handoff = (x4, None if x4.is_inference() else x4._version, out, bn)
         STATS['fused_layers'] += 1
-        return x4.reshape(shape), k, v
+        return out, k, v
 
 
 class RefLinear(torch.nn.Module):
@@ -447,6 +485,11 @@ def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', refere
                 continue
             set_submodule(model, lname, KDecoderLayer(layer, g, by_name[f'{attn}.o_proj'], mlp))
             layers_fused += 1
+        for ml in model.modules():                     # link consecutive decoder layers of each stack
+            if isinstance(ml, torch.nn.ModuleList):
+                for a, b in zip(ml[:-1], ml[1:]):
+                    if isinstance(a, KDecoderLayer) and isinstance(b, KDecoderLayer):
+                        a._next = [b]
     torch.cuda.synchronize()
     policy._tcq_groups = groups
     info['fused_layers'] = layers_fused
