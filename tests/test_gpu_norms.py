@@ -61,13 +61,16 @@ def test_norm_pre_bitexact(M, K):
 
 
 @pytest.mark.parametrize('kind', ['f32', 'i32'])
-@pytest.mark.parametrize('M,N', [(1, 1024), (50, 1024), (300, 2048)])
+@pytest.mark.parametrize('M,N,col0', [(1, 1024, 16), (50, 1024, 16), (300, 2048, 16), (5, 4096, 16), (2, 16384, 16),
+                                      (50, 1024, 2), (3, 4096, 2)])
 @pytest.mark.parametrize('with_norm', [True, False])
-def test_post_add_norm_pre_bitexact(kind, M, N, with_norm):
-    """== post (BF16) -> BF16 residual add -> rmsnorm -> pre, the unfused chain of launches, and the oracle."""
+def test_post_add_norm_pre_bitexact(kind, M, N, col0, with_norm):
+    """== post (BF16) -> BF16 residual add -> rmsnorm -> pre, the unfused chain of launches. Aligned power-of-two rows
+    run the register path (rows of 4096 and 16384 exchange between waves), col0 = 2 (rows not 16-byte aligned) the LDS
+    path."""
     from yanlongvla_amd import kernels as Kn
     rng = np.random.default_rng(M * 5 + N)
-    lda, col0 = N + 32, 16
+    lda = N + 32
     if kind == 'i32':
         acc = T(rng.integers(-2 ** 18, 2 ** 18, size=(M, lda)).astype(np.int32))
         s = T((rng.random(M) * 1e-3 + 1e-4).astype(np.float32))

@@ -165,6 +165,37 @@ __device__ __forceinline__ void block_walsh(float* lds, int K, Out&& out) {
     }
 }
 
+// Register-resident Walsh transform of a power-of-two row held by the whole workgroup: thread t owns elements
+// [16 t, 16 t + 16) (K = 16 * blockDim.x, 16 <= K <= 16384). Stages h = 1, 2, 4, 8 run inside the thread, h = 16 .. 512
+// between the lanes of a wave (partner lane t ^ (h / 16)), larger h between waves through xs (LDS, >= K floats, k-major
+// so every exchange is conflict-free). Every stage is the (a + b, a - b) butterfly of tcq_format.fwht in stage order, the
+// lower index keeping a + b, so the result equals walsh_segment's bit for bit. Unnormalised; ends with a barrier when
+// K > 1024 (xs may then be reused), otherwise touches no LDS at all.
+__device__ __forceinline__ void reg_walsh16(float (&v)[16], int K, float* xs) {
+    butterflies<4>(v);
+    const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
+    for (int m = 1; m < nt && m < 64; m <<= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float p = __shfl_xor(v[k], m, 64);
+            v[k] = upper ? p - v[k] : v[k] + p;
+        }
+    }
+    for (int m = 64; m < nt; m <<= 1) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) xs[k * nt + t] = v[k];
+        __syncthreads();
+        const bool upper = t & m;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float p = xs[k * nt + (t ^ m)];
+            v[k] = upper ? p - v[k] : v[k] + p;
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------- activation quantizer
 // Per-token symmetric INT8 of tcq_format.quantize_tokens (reference tcq_format.py:119-122): IEEE division, half-even, clamp.
 __device__ __forceinline__ int q8(float v, float s) {

@@ -176,12 +176,46 @@ __global__ void k_quantize_rows(const void* x, int ldx, i8* q, float* scale, int
 
 // ------------------------------------------------------------------------------------------------- scale + rotate epilogue
 // Accumulator column i of a row -> FP32: I32 (float(a) * s) * rs[i]; BF16 bf16(a) * rs[i]; F32 a (already scaled).
+// This thread's first 8-element vector of an accumulator row (raw words: 32 bytes of FP32 / INT32, 16 of BF16) and of its
+// row scales, loaded ahead of the rest of the row (vec rows only).
+struct AccVec {
+    uint4_t a[2], r[2];
+};
 template <int ADT>
-__device__ __forceinline__ void load_acc_row(float* lds, const void* acc, size_t base, float s, const float* rs, int N, bool vec) {
+__device__ __forceinline__ void load_acc_vec(AccVec& p, const void* acc, size_t base, const float* rs, int i) {
+    if (ADT == TCQ_BF16) {
+        p.a[0] = gptr((const uint4_t*)((const u16*)acc + base + i))[0];
+    } else {
+        p.a[0] = gptr((const uint4_t*)((const u32*)acc + base + i))[0];
+        p.a[1] = gptr((const uint4_t*)((const u32*)acc + base + i))[1];
+    }
+    if (ADT != TCQ_F32) {
+        p.r[0] = gptr((const uint4_t*)(rs + i))[0];
+        p.r[1] = gptr((const uint4_t*)(rs + i))[1];
+    }
+}
+
+template <int ADT>
+__device__ __forceinline__ void load_acc_row(float* lds, const void* acc, size_t base, float s, const float* rs, int N, bool vec,
+                                             bool pre = false, const AccVec& p0 = AccVec{}) {
     if (vec) {
         for (int i = 8 * threadIdx.x; i < N; i += 8 * blockDim.x) {
             float v[8];
-            if (ADT == TCQ_I32) {
+            if (pre && i == 8 * (int)threadIdx.x) {
+                float r[8];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { r[k] = __uint_as_float(p0.r[0][k]); r[4 + k] = __uint_as_float(p0.r[1][k]); }
+                if (ADT == TCQ_I32) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = ((float)(int)p0.a[k >> 2][k & 3] * s) * r[k];
+                } else if (ADT == TCQ_BF16) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = bf16_to_f32((u16)(p0.a[0][k >> 1] >> (16 * (k & 1)))) * r[k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = __uint_as_float(p0.a[k >> 2][k & 3]);
+                }
+            } else if (ADT == TCQ_I32) {
                 int a[8];
                 float r[8];
                 Elem<TCQ_I32>::ld8i(acc, base + i, a);
@@ -213,17 +247,41 @@ __device__ __forceinline__ void load_acc_row(float* lds, const void* acc, size_t
 }
 
 // y = walsh(row) * sv (+ bias) [-> GELU table for BF16 outputs]
+// (sv0, b0: the signs and bias of this thread's first 8-element vector, loaded ahead with the accumulator row; vec only)
+struct PostSide {
+    u64 sv;
+    uint4_t b[2];
+};
+__device__ __forceinline__ void load_post_side(PostSide& p, const i8* sv, const float* bias, int i) {
+    p.sv = *gptr((const u64*)(sv + i));
+    if (bias) {
+        p.b[0] = gptr((const uint4_t*)(bias + i))[0];
+        p.b[1] = gptr((const uint4_t*)(bias + i))[1];
+    }
+}
 template <int YDT>
 __device__ __forceinline__ void store_post_row(const float* lds, void* y, size_t base, const i8* sv, const float* bias,
-                                               const u16* gelu, int N, bool vec) {
+                                               const u16* gelu, int N, bool vec, bool pre = false,
+                                               const PostSide& p0 = PostSide{}) {
     store_row<YDT>(lds, y, base, N, vec, [&](int i, float(&v)[8]) {
+        const bool first = pre && i == 8 * (int)threadIdx.x;
         float s[8];
-        ld8_i8(sv, i, s);
+        if (first) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s[k] = (float)(i8)(p0.sv >> (8 * k));
+        } else {
+            ld8_i8(sv, i, s);
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = v[k] * s[k];
         if (bias) {
             float b[8];
-            ld8_f32(bias, i, b);
+            if (first) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { b[k] = __uint_as_float(p0.b[0][k]); b[4 + k] = __uint_as_float(p0.b[1][k]); }
+            } else {
+                ld8_f32(bias, i, b);
+            }
 #pragma unroll
             for (int k = 0; k < 8; ++k) v[k] = v[k] + b[k];
         }
@@ -244,9 +302,12 @@ __global__ void k_post(const void* acc, int lda, int col0, const float* s, const
                        void* y, int N, int vec) {
     extern __shared__ float lds[];
     const int tok = blockIdx.x;
+    PostSide p0{};
+    const bool has0 = vec && 8 * (int)threadIdx.x < N;
+    if (has0) load_post_side(p0, sv, bias, 8 * threadIdx.x);
     load_acc_row<ADT>(lds, acc, (size_t)tok * lda + col0, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
     walsh_inplace(lds, N);
-    store_post_row<YDT>(lds, y, (size_t)tok * N, sv, bias, nullptr, N, vec);
+    store_post_row<YDT>(lds, y, (size_t)tok * N, sv, bias, nullptr, N, vec, has0, p0);
 }
 
 // Batched epilogue: workgroup (token, segment). Segments with N outside (0, maxN], or without the row scale their
@@ -268,9 +329,12 @@ __global__ void k_postg(SEGS segs, const float* s, const u16* gelu_lut, int maxN
     const bool vec = N % 8 == 0 && aligned16(S.acc) && ((size_t)S.lda * esz) % 16 == 0 && ((size_t)S.col0 * esz) % 16 == 0 &&
                      aligned16(S.y) && ((size_t)N * ysz) % 16 == 0 && ((uintptr_t)S.sv & 7) == 0 && (!S.rs || aligned16(S.rs)) &&
                      (!S.bias || aligned16(S.bias));
+    PostSide p0{};
+    const bool has0 = vec && 8 * (int)threadIdx.x < N;
+    if (has0) load_post_side(p0, S.sv, S.bias, 8 * threadIdx.x);
     load_acc_row<ADT>(lds, S.acc, (size_t)tok * S.lda + S.col0, ADT == TCQ_I32 ? s[tok] : 1.f, S.rs, N, vec);
     walsh_inplace(lds, N);
-    store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec);
+    store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec, has0, p0);
 }
 
 // ------------------------------------------------------------------------------------------------ 16-element chunks
@@ -329,6 +393,43 @@ __device__ __forceinline__ void c16_f32(const float* p, bool vec, float (&v)[16]
     }
 }
 
+// Raw 16-element chunks of the side vectors, loaded at kernel entry together with the accumulator row (they do not depend
+// on it) and converted where they are used, so no global round trip waits behind a Walsh pass. ESZ: element bytes (1 INT8,
+// 2 BF16, 4 FP32); the raw words hold the elements little-endian, as in memory. Unaligned rows load element by element.
+template <int ESZ> struct Raw16 {
+    uint4_t r[ESZ];
+};
+template <int ESZ>
+__device__ __forceinline__ Raw16<ESZ> raw16(const void* p, bool vec) {
+    Raw16<ESZ> o;
+    if (vec) {
+#pragma unroll
+        for (int q = 0; q < ESZ; ++q) o.r[q] = gptr((const uint4_t*)p)[q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < ESZ; ++q) o.r[q] = uint4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const u32 e = ESZ == 1 ? (u32)(uint8_t)gptr((const i8*)p)[k] : ESZ == 2 ? (u32)gptr((const u16*)p)[k] : gptr((const u32*)p)[k];
+            const int bit = 8 * ESZ * k;                                 // bit offset of element k in the 16 * ESZ bytes
+            o.r[bit >> 7][(bit >> 5) & 3] |= e << (bit & 31);
+        }
+    }
+    return o;
+}
+__device__ __forceinline__ void cv16(const Raw16<1>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a.r[0][k >> 2] >> (8 * (k & 3)));
+}
+__device__ __forceinline__ void cv16(const Raw16<2>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32((u16)(a.r[k >> 3][(k >> 1) & 3] >> (16 * (k & 1))));
+}
+__device__ __forceinline__ void cv16(const Raw16<4>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = __uint_as_float(a.r[k >> 2][k & 3]);
+}
+
 // Sum of squares of a row in an order fixed by K alone: chunk sums of 16 consecutive values (sequential, part[j] for chunk
 // j), then a pairwise tree over the chunks, stage h adding chunk j + h into chunk j for j a multiple of 2h. Stages h < 64 run
 // in registers across the lanes of a wave (chunks past the end count as +0, which leaves every partial sum unchanged), the
@@ -367,12 +468,19 @@ __device__ __forceinline__ float tree_total(const float* part, float* red, int K
 
 // RMSNorm of the LDS row (BF16 values as FP32) given its sum of squares: v <- bf16((v * r) * (1 + w[i])) * su[i] (su may be
 // NULL), r = 1 / sqrt(ss / K + eps). Ends with a barrier.
-__device__ __forceinline__ void norm_apply(float* lds, float ss, const u16* w, const i8* su, float eps, int K, bool vec) {
+// pre: w0 / su0 hold this thread's first chunk of w / su, loaded ahead.
+__device__ __forceinline__ void norm_apply(float* lds, float ss, const u16* w, const i8* su, float eps, int K, bool vec,
+                                           bool pre = false, const Raw16<2>& w0 = Raw16<2>{}, const Raw16<1>& su0 = Raw16<1>{}) {
     const float r = 1.f / __builtin_sqrtf(ss / (float)K + eps);
     for (int j = threadIdx.x; j < (K >> 4); j += blockDim.x) {
         float wv[16], sg[16];
-        c16_bf16(w + 16 * j, vec, wv);
-        if (su) c16_i8(su + 16 * j, vec, sg);
+        const bool first = pre && j == (int)threadIdx.x;
+        if (first) cv16(w0, wv);
+        else c16_bf16(w + 16 * j, vec, wv);
+        if (su) {
+            if (first) cv16(su0, sg);
+            else c16_i8(su + 16 * j, vec, sg);
+        }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             float v = bf16_to_f32(f32_to_bf16((lds[lds_slot(16 * j + k)] * r) * (1.f + wv[k])));
@@ -413,14 +521,25 @@ __global__ void k_mid2(const void* acc, int lda, const float* s, const float* rs
     extern __shared__ float lds[];
     __shared__ float red[16];
     u16* g = (u16*)(lds + lds_words(N));
-    const int tok = blockIdx.x;
+    const int tok = blockIdx.x, j0 = threadIdx.x;
     const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    const bool has0 = j0 < (N >> 4);
+    Raw16<1> svg0{}, svu0{}, sn0{};                                     // this thread's first chunk of sv (gate, up) and su
+    if (has0) {
+        svg0 = raw16<1>(sv + 16 * j0, svec);
+        svu0 = raw16<1>(sv + N + 16 * j0, svec);
+        sn0 = raw16<1>(su + 16 * j0, svec);
+    }
+    AccVec up0{};                                                       // first vector of the up half, loaded ahead
+    const bool hasv = vec && 8 * (int)threadIdx.x < N;
+    if (hasv) load_acc_vec<ADT>(up0, acc, (size_t)tok * lda + N, rs + (ADT == TCQ_F32 ? 0 : N), 8 * threadIdx.x);
     load_acc_row<ADT>(lds, acc, (size_t)tok * lda, st, rs, N, vec);
     walsh_inplace(lds, N);
-    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+    for (int j = j0; j < (N >> 4); j += blockDim.x) {
         float sg[16], v[16];
         u16 gv[16];
-        c16_i8(sv + 16 * j, svec, sg);
+        if (j == j0) cv16(svg0, sg);
+        else c16_i8(sv + 16 * j, svec, sg);
 #pragma unroll
         for (int k = 0; k < 16; ++k) v[k] = lds[lds_slot(16 * j + k)] * sg[k];
         gelu16(lut, v, gv);
@@ -428,12 +547,17 @@ __global__ void k_mid2(const void* acc, int lda, const float* s, const float* rs
         for (int k = 0; k < 16; ++k) g[16 * j + k] = gv[k];
     }
     __syncthreads();
-    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + N, st, rs + (ADT == TCQ_F32 ? 0 : N), N, vec);
+    load_acc_row<ADT>(lds, acc, (size_t)tok * lda + N, st, rs + (ADT == TCQ_F32 ? 0 : N), N, vec, hasv, up0);
     walsh_inplace(lds, N);
-    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+    for (int j = j0; j < (N >> 4); j += blockDim.x) {
         float sg[16], sn[16];
-        c16_i8(sv + N + 16 * j, svec, sg);
-        c16_i8(su + 16 * j, svec, sn);
+        if (j == j0) {
+            cv16(svu0, sg);
+            cv16(sn0, sn);
+        } else {
+            c16_i8(sv + N + 16 * j, svec, sg);
+            c16_i8(su + 16 * j, svec, sn);
+        }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const float u = bf16_to_f32(f32_to_bf16(lds[lds_slot(16 * j + k)] * sg[k]));
@@ -525,31 +649,55 @@ __global__ void k_norm_pre(const u16* x, const u16* w, float eps, const i8* su, 
     extern __shared__ float lds[];
     __shared__ float red[16];
     float* part = lds + lds_words(K);
-    const int tok = blockIdx.x;
+    const int tok = blockIdx.x, j0 = threadIdx.x;
+    const bool has0 = j0 < (K >> 4);
+    Raw16<2> w0{};
+    Raw16<1> su0{};
+    if (has0) {
+        w0 = raw16<2>(w + 16 * j0, vec);
+        if (su) su0 = raw16<1>(su + 16 * j0, vec);
+    }
     load_row_sumsq(lds, part, x + (size_t)tok * K, K, vec);
-    norm_apply(lds, tree_total(part, red, K), w, su, eps, K, vec);
+    norm_apply(lds, tree_total(part, red, K), w, su, eps, K, vec, has0, w0, su0);
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, K);
 }
 
 // Epilogue of a projection fused with the residual add and (w != NULL) the next norm + rotate + quantize:
 // a = BF16(walsh(SCALE(acc)) * sv + bias); x_out = BF16(x + a); then, as k_norm_pre, q / scale of RMSNorm(x_out).
 template <int ADT>
-__global__ void k_post_add_norm_pre(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv,
+__global__ __launch_bounds__(512) void k_post_add_norm_pre(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv,
                                     const float* bias, const u16* x, u16* xout, const u16* w, float eps, const i8* su, i8* q,
                                     int* q4, int ldq, float* scale, int N, int vec, int svec) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     float* part = lds + lds_words(N);
-    const int tok = blockIdx.x;
+    const int tok = blockIdx.x, j0 = threadIdx.x;
     const size_t row = (size_t)tok * N;
+    const bool has0 = j0 < (N >> 4);
+    Raw16<1> sv0{}, su0{};                                              // this thread's first chunk of every side vector
+    Raw16<4> b0{};
+    Raw16<2> x0{}, w0{};
+    if (has0) {
+        sv0 = raw16<1>(sv + 16 * j0, svec);
+        if (bias) b0 = raw16<4>(bias + 16 * j0, svec);
+        x0 = raw16<2>(x + row + 16 * j0, svec);
+        if (w) w0 = raw16<2>(w + 16 * j0, svec);
+        if (w && su) su0 = raw16<1>(su + 16 * j0, svec);
+    }
     load_acc_row<ADT>(lds, acc, (size_t)tok * lda + col0, ADT == TCQ_I32 ? s[tok] : 1.f, rs, N, vec);
     walsh_inplace(lds, N);
-    for (int j = threadIdx.x; j < (N >> 4); j += blockDim.x) {
+    for (int j = j0; j < (N >> 4); j += blockDim.x) {
         float sg[16], b[16], xv[16];
         u16 xn[16];
-        c16_i8(sv + 16 * j, svec, sg);
-        if (bias) c16_f32(bias + 16 * j, svec, b);
-        c16_bf16(x + row + 16 * j, svec, xv);
+        if (j == j0) {
+            cv16(sv0, sg);
+            if (bias) cv16(b0, b);
+            cv16(x0, xv);
+        } else {
+            c16_i8(sv + 16 * j, svec, sg);
+            if (bias) c16_f32(bias + 16 * j, svec, b);
+            c16_bf16(x + row + 16 * j, svec, xv);
+        }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             float v = lds[lds_slot(16 * j + k)] * sg[k];
@@ -563,8 +711,98 @@ __global__ void k_post_add_norm_pre(const void* acc, int lda, int col0, const fl
     }
     __syncthreads();
     if (!w) return;
-    norm_apply(lds, tree_total(part, red, N), w, su, eps, N, svec);
+    norm_apply(lds, tree_total(part, red, N), w, su, eps, N, svec, has0, w0, su0);
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
+}
+
+// Register path of k_post_add_norm_pre for power-of-two rows of 256 .. 16384 (K / 16 threads, thread t owns chunk t, every
+// pointer 16-byte aligned): the same operations in the same order, with the row in registers instead of LDS, the Walsh
+// transforms on reg_walsh16 and every global load issued at entry.
+template <int ADT>
+__global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc, int lda, int col0, const float* s, const float* rs,
+                                                                const i8* sv, const float* bias, const u16* x, u16* xout, const u16* w,
+                                                                float eps, const i8* su, i8* q, int* q4, int ldq, float* scale, int N) {
+    extern __shared__ float xs[];                                      // N floats: cross-wave exchange and chunk sums
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = 16 * t;
+    const size_t row = (size_t)tok * N, base = (size_t)tok * lda + col0 + i0;
+    // every global read of the thread, issued together
+    const Raw16<1> sv0 = raw16<1>(sv + i0, true);
+    const Raw16<2> x0 = raw16<2>(x + row + i0, true);
+    Raw16<4> b0{}, rs0{};
+    Raw16<2> w0{};
+    Raw16<1> su0{};
+    if (bias) b0 = raw16<4>(bias + i0, true);
+    if (w) {
+        w0 = raw16<2>(w + i0, true);
+        su0 = raw16<1>(su + i0, true);
+    }
+    float v[16];
+    if (ADT == TCQ_BF16) {
+        const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
+        rs0 = raw16<4>(rs + i0, true);
+        float r[16];
+        cv16(a, v);
+        cv16(rs0, r);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
+    } else {
+        const Raw16<4> a = raw16<4>((const u32*)acc + base, true);
+        if (ADT == TCQ_I32) {
+            rs0 = raw16<4>(rs + i0, true);
+            const float st = s[tok];
+            float r[16];
+            cv16(rs0, r);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = ((float)(int)a.r[k >> 2][k & 3] * st) * r[k];
+        } else {
+            cv16(a, v);
+        }
+    }
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    reg_walsh16(v, N, xs);
+    float sg[16], b[16], xv[16];
+    u16 xn[16];
+    cv16(sv0, sg);
+    if (bias) cv16(b0, b);
+    cv16(x0, xv);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        float a = (v[k] * c) * sg[k];
+        if (bias) a = a + b[k];
+        xn[k] = f32_to_bf16(xv[k] + bf16_to_f32(f32_to_bf16(a)));
+        xv[k] = bf16_to_f32(xn[k]);
+    }
+    c16_store_bf16(xout + row + i0, true, xn);
+    if (!w) return;
+    xs[t] = chunk_sumsq(xv);
+    __syncthreads();
+    const float ss = tree_total(xs, red, N);
+    const float r = 1.f / __builtin_sqrtf(ss / (float)N + eps);
+    float wv[16], sn[16];
+    cv16(w0, wv);
+    cv16(su0, sn);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32(f32_to_bf16((xv[k] * r) * (1.f + wv[k]))) * sn[k];
+    reg_walsh16(v, N, xs);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    const float sc = token_scale(block_max(mx, red));
+    if (t == 0) scale[tok] = sc;
+    u32 words[4];
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+    if (q) *gptr((uint4_t*)(q + row + i0)) = uint4_t{words[0], words[1], words[2], words[3]};
+    if (q4) {
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
+    }
 }
 
 // =========================================================================================================== C ABI
@@ -829,10 +1067,24 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     const int asz = dsize(acc_dtype);
     const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && (!rs || al16(rs));
     const int svec = al16(sv) && al16(x) && al16(xout) && (!bias || al16(bias)) && (!w || (al16(w) && al16(su)));
-    const dim3 grid(M), block(row_threads(M, N));
-    const size_t sh = norm_lds(N);
     hipStream_t st = (hipStream_t)stream;
     const u16 *xp = (const u16*)x, *wp = (const u16*)w;
+    // register path: power-of-two rows of 1024 .. 16384 (one 16-element chunk per thread, at least one full wave), aligned
+    if ((N & (N - 1)) == 0 && N >= 1024 && vec && svec && (!q || al16(q))) {
+#define PANR(AD) launch_k(k_post_add_norm_pre_reg<AD>, dim3(M), dim3(N / 16), (size_t)N * sizeof(float), st, acc, lda, col0, s, rs, \
+                          (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N)
+        switch (acc_dtype) {
+            case TCQ_I32: PANR(TCQ_I32); break;
+            case TCQ_F32: PANR(TCQ_F32); break;
+            case TCQ_BF16: PANR(TCQ_BF16); break;
+            default: return TCQ_ERR_DTYPE;
+        }
+#undef PANR
+        return launch_status();
+    }
+    // 512 threads at most: the side vectors the kernel loads ahead need more than the 128 registers of 1024-thread groups
+    const dim3 grid(M), block(row_threads(M, N) < 512 ? row_threads(M, N) : 512);
+    const size_t sh = norm_lds(N);
 #define PANP(AD) launch_k(k_post_add_norm_pre<AD>, grid, block, sh, st, acc, lda, col0, s, rs, (const i8*)sv, bias, xp, (u16*)xout, \
                           wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N, vec, svec)
     switch (acc_dtype) {
