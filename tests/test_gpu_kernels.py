@@ -364,7 +364,8 @@ def _small_product_case(shapes, M, seed):
 
 @pytest.mark.parametrize('shapes,M', [([(2048, 1024)], 1), ([(2048, 1024), (256, 1024), (256, 1024)], 50),
                                       ([(1024, 2048)], 16), ([(4096, 1024), (4096, 1024)], 17), ([(1024, 4096)], 64),
-                                      ([(64, 1152)], 33), ([(48, 80), (32, 80)], 5), ([(256, 16384)], 10)])
+                                      ([(64, 1152)], 33), ([(48, 80), (32, 80)], 5), ([(256, 16384)], 10),
+                                      ([(4112, 1024), (2048, 1024)], 50)])
 def test_gemm_tcq_and_w8_bitexact(shapes, M):
     """Fused decode + INT8 product and the INT8-resident product against the oracle, FP32 bits equal (exact int32 sums)."""
     from yanlongvla_amd import kernels as K

@@ -51,7 +51,7 @@ def accumulators(rng, M, width, kind):
 
 
 @pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
-@pytest.mark.parametrize("M,N", [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 48)])
+@pytest.mark.parametrize("M,N", [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 48), (4, 1024), (2, 2048), (3, 8192)])
 def test_mid2_bitexact(kind, M, N):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * 7 + N)

@@ -42,16 +42,17 @@ struct SegPack {
     tcq_gemm_seg s[TCQ_MAX_SEGS];
 };
 
-// grid (tile rows of the largest segment, segments), NW = blockDim.x / 64 waves. MODE 0: decode from tcq_repack words;
-// MODE 1: resident INT8 weights. ODT: output dtype (F32 scaled, BF16 scaled, I32 accumulators).
-template <int MODE, int NB, int ODT>
-__global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
+// grid (tile-row groups of the largest segment, segments), NW = blockDim.x / 64 waves; a workgroup takes TR consecutive tile
+// rows (the activation fragments of its chunks, the bulk of the loads, then serve TR rows). MODE 0: decode from tcq_repack
+// words; MODE 1: resident INT8 weights. ODT: output dtype (F32 scaled, BF16 scaled, I32 accumulators).
+template <int MODE, int NB, int ODT, int TR>
+__global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
-    __shared__ __attribute__((aligned(16))) int4v red[(SM_MAXW - 1) * NB * 64];
+    __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
     const tcq_gemm_seg S = P.s[blockIdx.y];
     const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
-    const int I = blockIdx.x;
-    if (I >= tiles_m) return;                                             // uniform
+    const int I0 = blockIdx.x * TR;
+    if (I0 >= tiles_m) return;                                            // uniform
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int lr = lane & 15, lg = lane >> 4;
@@ -62,17 +63,21 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* 
     else Wr = make_rsrc(S.w, (u32)S.m * (u32)K);
     const rsrc_t Q = make_rsrc(q, (u32)M * (u32)K);
 
-    uint4_t wa[MODE == 0 ? 1 : 4];
+    uint4_t wa[TR][MODE == 0 ? 1 : 4];
     int4v B[4][NB];
     auto load = [&](int c) {                                              // words / weights and activations of chunk c
-        if (MODE == 0) {
-            wa[0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
-        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k0 = 256 * c + 64 * j + 16 * lg;
-                const u32 off = k0 < K ? (u32)(16 * I + lr) * (u32)K + (u32)k0 : RSRC_OOB;
-                wa[j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, off, 0, 2));
+        for (int r = 0; r < TR; ++r) {
+            const int I = min(I0 + r, tiles_m - 1);                       // a row past the end reloads the last (never stored)
+            if (MODE == 0) {
+                wa[r][0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k0 = 256 * c + 64 * j + 16 * lg;
+                    const u32 off = k0 < K ? (u32)(16 * I + lr) * (u32)K + (u32)k0 : RSRC_OOB;
+                    wa[r][j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, off, 0, 2));
+                }
             }
         }
 #pragma unroll
@@ -85,74 +90,91 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* 
             }
     };
 
-    int4v acc[NB];
+    int4v acc[TR][NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = int4v{0, 0, 0, 0};
+    for (int r = 0; r < TR; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
     if (wave < nch) load(wave);
     // epilogue scales, loaded with the operands (wave 0 stores)
-    float4_t rsv = {0.f, 0.f, 0.f, 0.f};
+    float4_t rsv[TR];
     float sv[NB];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) rsv[r] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NB; ++b) sv[b] = 0.f;
     if (ODT != TCQ_I32 && wave == 0) {
-        rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
+#pragma unroll
+        for (int r = 0; r < TR; ++r) rsv[r] = gptr((const float4_t*)(S.rs + 16 * min(I0 + r, tiles_m - 1) + 4 * lg))[0];
 #pragma unroll
         for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
     }
-    if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I / S.rows_per_table) * 1024 : 0));
+    if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
     __syncthreads();
     for (int c = wave; c < nch; c += nw) {
         if (c != wave) load(c);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            int4v A;
-            if (MODE == 0) {
-                const u32 hi = wa[0][j];
-                const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
-                u32 e0[4], e1[4];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
-                    e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << ESH) | cp4));             // pair p
-                    e1[p] = *(const u16*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));    // pair p + 4
+            for (int r = 0; r < TR; ++r) {
+                int4v A;
+                if (MODE == 0) {
+                    const u32 hi = wa[r][0][j];
+                    const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+                    u32 e0[4], e1[4];
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                        e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << ESH) | cp4));             // pair p
+                        e1[p] = *(const u16*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));    // pair p + 4
+                    }
+                    A = int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
+                              (int)(e1[2] | (e1[3] << 16))};
+                } else {
+                    A = __builtin_bit_cast(int4v, wa[r][j]);
                 }
-                A = int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
-                          (int)(e1[2] | (e1[3] << 16))};
-            } else {
-                A = __builtin_bit_cast(int4v, wa[j]);
-            }
 #pragma unroll
-            for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[b], 0, 0, 0);
+                for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[r][b], 0, 0, 0);
+            }
         }
     }
     // sum the waves' partial accumulators (exact int32) through LDS, then scale and store
     if (wave > 0) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) red[((wave - 1) * NB + b) * 64 + lane] = acc[b];
+        for (int r = 0; r < TR; ++r)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) red[(((wave - 1) * TR + r) * NB + b) * 64 + lane] = acc[r][b];
     }
     __syncthreads();
     if (wave != 0) return;
     for (int w = 0; w < nw - 1; ++w)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b] += red[(w * NB + b) * 64 + lane];
+        for (int r = 0; r < TR; ++r)
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int t = 16 * b + lr;
-        if (t < M) {
-            const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
-            if (ODT == TCQ_I32) {
-                *gptr((int4v*)((int*)S.out + o)) = acc[b];
-            } else {
-                const float st = sv[b];
-                float v[4];
+            for (int b = 0; b < NB; ++b) acc[r][b] += red[((w * TR + r) * NB + b) * 64 + lane];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = ((float)acc[b][e] * st) * rsv[e];
-                if (ODT == TCQ_F32) {
-                    *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
+    for (int r = 0; r < TR; ++r) {
+        const int I = I0 + r;
+        if (I >= tiles_m) break;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int t = 16 * b + lr;
+            if (t < M) {
+                const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
+                if (ODT == TCQ_I32) {
+                    *gptr((int4v*)((int*)S.out + o)) = acc[r][b];
                 } else {
-                    const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
-                    const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
-                    *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
+                    const float st = sv[b];
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = ((float)acc[r][b][e] * st) * rsv[r][e];
+                    if (ODT == TCQ_F32) {
+                        *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
+                    } else {
+                        const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
+                        const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
+                        *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
+                    }
                 }
             }
         }
@@ -160,14 +182,21 @@ __global__ __launch_bounds__(1024) void k_gemm_small(const SegPack P, const i8* 
 }
 
 // =========================================================================================================== C ABI
-template <int MODE, int NB>
+template <int MODE, int NB, int TR>
 static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                             int ldo, int odt) {
     switch (odt) {
-        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
     }
+}
+template <int MODE, int TR>
+static void launch_small_tr(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                            int ldo, int odt) {
+    if (M <= 16) launch_small_nb<MODE, 1, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
+    else if (M <= 32) launch_small_nb<MODE, 2, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
+    else launch_small_nb<MODE, 4, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
 }
 
 template <int MODE>
@@ -194,12 +223,20 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     }
     if ((size_t)M * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
-    const dim3 grid(max_m / 16, nseg), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
     const i8* qq = (const i8*)q;
-    if (M <= 16) launch_small_nb<MODE, 1>(grid, block, st, P, qq, s, M, K, ldo, odt);
-    else if (M <= 32) launch_small_nb<MODE, 2>(grid, block, st, P, qq, s, M, K, ldo, odt);
-    else launch_small_nb<MODE, 4>(grid, block, st, P, qq, s, M, K, ldo, odt);
+    // two tile rows per workgroup when there are many (their activation fragments are then loaded once for both), at most 8
+    // waves (the partial sums of both rows fit the LDS) and row-group tables that never split a pair
+    int tiles = 0;
+    bool pairs = nw <= 8;
+    for (int i = 0; i < nseg; ++i) {
+        tiles += segs[i].m / 16;
+        if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
+    }
+    pairs = pairs && tiles >= 384;
+    const dim3 block(64 * nw);
+    if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt);
+    else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt);
     return launch_status();
 }
 

@@ -715,6 +715,91 @@ __global__ __launch_bounds__(512) void k_post_add_norm_pre(const void* acc, int 
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
 }
 
+// Accumulator chunk 16 t .. 16 t + 15 of a row (scaled like load_acc_row), loaded at kernel entry.
+template <int ADT>
+__device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st, const float* rs, float (&v)[16]) {
+    if (ADT == TCQ_BF16) {
+        const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
+        const Raw16<4> r4 = raw16<4>(rs, true);
+        float r[16];
+        cv16(a, v);
+        cv16(r4, r);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
+    } else {
+        const Raw16<4> a = raw16<4>((const u32*)acc + base, true);
+        if (ADT == TCQ_I32) {
+            const Raw16<4> r4 = raw16<4>(rs, true);
+            float r[16];
+            cv16(r4, r);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = ((float)(int)a.r[k >> 2][k & 3] * st) * r[k];
+        } else {
+            cv16(a, v);
+        }
+    }
+}
+
+// Rotate + quantize of a register row (values already signed): walsh, * c, per-token absmax, INT8 words (as k_pre).
+__device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float* xs, float* red, i8* q, int* q4, int ldq,
+                                                    float* scale, int tok) {
+    const int t = threadIdx.x;
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    reg_walsh16(v, N, xs);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    const float sc = token_scale(block_max(mx, red));
+    if (t == 0) scale[tok] = sc;
+    u32 words[4];
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+    if (q) *gptr((uint4_t*)(q + (size_t)tok * N + 16 * t)) = uint4_t{words[0], words[1], words[2], words[3]};
+    if (q4) {
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
+    }
+}
+
+// Register path of k_mid2 (power-of-two N of 1024 .. 8192, N / 16 threads, aligned): thread t owns chunk t of the gate half
+// and of the up half; the same operations and rounding points as k_mid2.
+template <int ADT>
+__global__ __launch_bounds__(512) void k_mid2_reg(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
+                                                  const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale, int N) {
+    extern __shared__ float xs[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = 16 * t;
+    const size_t base = (size_t)tok * lda + i0;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    const Raw16<1> svg = raw16<1>(sv + i0, true), svu = raw16<1>(sv + N + i0, true), sn0 = raw16<1>(su + i0, true);
+    float g[16], u[16];
+    acc_chunk<ADT>(acc, base, st, rs ? rs + i0 : nullptr, g);
+    acc_chunk<ADT>(acc, base + N, st, rs ? rs + N + i0 : nullptr, u);
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    reg_walsh16(g, N, xs);
+    float sg[16];
+    cv16(svg, sg);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) g[k] = g[k] * c * sg[k];
+    u16 gv[16];
+    gelu16(lut, g, gv);
+    reg_walsh16(u, N, xs);
+    float sgu[16], sn[16];
+    cv16(svu, sgu);
+    cv16(sn0, sn);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float uu = bf16_to_f32(f32_to_bf16((u[k] * c) * sgu[k]));
+        u[k] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gv[k]) * uu)) * sn[k];
+    }
+    reg_rotate_quantize(u, N, xs, red, q, q4, ldq, scale, tok);
+}
+
 // Register path of k_post_add_norm_pre for power-of-two rows of 256 .. 16384 (K / 16 threads, thread t owns chunk t, every
 // pointer 16-byte aligned): the same operations in the same order, with the row in registers instead of LDS, the Walsh
 // transforms on reg_walsh16 and every global load issued at entry.
@@ -729,7 +814,7 @@ __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc,
     // every global read of the thread, issued together
     const Raw16<1> sv0 = raw16<1>(sv + i0, true);
     const Raw16<2> x0 = raw16<2>(x + row + i0, true);
-    Raw16<4> b0{}, rs0{};
+    Raw16<4> b0{};
     Raw16<2> w0{};
     Raw16<1> su0{};
     if (bias) b0 = raw16<4>(bias + i0, true);
@@ -738,27 +823,7 @@ __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc,
         su0 = raw16<1>(su + i0, true);
     }
     float v[16];
-    if (ADT == TCQ_BF16) {
-        const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
-        rs0 = raw16<4>(rs + i0, true);
-        float r[16];
-        cv16(a, v);
-        cv16(rs0, r);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
-    } else {
-        const Raw16<4> a = raw16<4>((const u32*)acc + base, true);
-        if (ADT == TCQ_I32) {
-            rs0 = raw16<4>(rs + i0, true);
-            const float st = s[tok];
-            float r[16];
-            cv16(rs0, r);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = ((float)(int)a.r[k >> 2][k & 3] * st) * r[k];
-        } else {
-            cv16(a, v);
-        }
-    }
+    acc_chunk<ADT>(acc, base, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 : nullptr, v);
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
     reg_walsh16(v, N, xs);
     float sg[16], b[16], xv[16];
@@ -784,25 +849,7 @@ __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc,
     cv16(su0, sn);
 #pragma unroll
     for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32(f32_to_bf16((xv[k] * r) * (1.f + wv[k]))) * sn[k];
-    reg_walsh16(v, N, xs);
-    float mx = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        v[k] = v[k] * c;
-        mx = fmaxf(mx, fabsf(v[k]));
-    }
-    const float sc = token_scale(block_max(mx, red));
-    if (t == 0) scale[tok] = sc;
-    u32 words[4];
-#pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4)
-        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
-                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
-    if (q) *gptr((uint4_t*)(q + row + i0)) = uint4_t{words[0], words[1], words[2], words[3]};
-    if (q4) {
-#pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
-    }
+    reg_rotate_quantize(v, N, xs, red, q, q4, ldq, scale, tok);
 }
 
 // =========================================================================================================== C ABI
@@ -956,6 +1003,18 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
     const int svec = al16(sv) && al16(su);
     hipStream_t st = (hipStream_t)stream;
     const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
+    // register path: power-of-two widths of 1024 .. 8192 (one 16-element chunk of each half per thread), aligned
+    if ((N & (N - 1)) == 0 && N >= 1024 && N <= 8192 && vec && svec && (!q || al16(q))) {
+        const dim3 rb(N / 16);
+        const size_t rsh = (size_t)N * sizeof(float);
+        switch (acc_dtype) {
+            case TCQ_I32: launch_k(k_mid2_reg<TCQ_I32>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
+            case TCQ_F32: launch_k(k_mid2_reg<TCQ_F32>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
+            case TCQ_BF16: launch_k(k_mid2_reg<TCQ_BF16>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
+            default: return TCQ_ERR_DTYPE;
+        }
+        return launch_status();
+    }
     switch (acc_dtype) {
         case TCQ_I32: launch_k(k_mid2<TCQ_I32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
         case TCQ_F32: launch_k(k_mid2<TCQ_F32>, grid, block, sh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N, vec, svec); break;
