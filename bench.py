@@ -149,10 +149,8 @@ def timed(fn, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
-def graph_latency(fn, replays=200, warmup=20, per_graph=1):
-    """Median / p95 ms per call of fn from HIP-graph replays (the reference's timing protocol: 20 warm-up + 200 timed
-    replays, each bracketed by events). With per_graph > 1 the graph holds that many calls back to back and the replay time
-    is divided by it: the device time per call without the graph's own submission latency."""
+def capture(fn, per_graph=1):
+    """A HIP graph of per_graph back-to-back calls of fn (one eager call on a side stream first, as graph capture wants)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -164,6 +162,15 @@ def graph_latency(fn, replays=200, warmup=20, per_graph=1):
     with torch.cuda.graph(g):
         for _ in range(per_graph):
             fn()
+    return g
+
+
+def graph_latency(fn, replays=200, warmup=20, per_graph=1):
+    """Median / p95 ms per call of fn from HIP-graph replays (the reference's timing protocol: 20 warm-up + 200 timed
+    replays, each bracketed by events, so each includes the graph's submission). With per_graph > 1 the graph holds that
+    many calls back to back and the replay time is divided by it."""
+    import torch
+    g = capture(fn, per_graph)
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -231,9 +238,22 @@ MFMA_I8_PEAK_TOPS = 5000.0     # MI355X dense INT8 MFMA, published peak
 
 
 def graph_per_call(fn, calls=20, replays=20):
-    """Device ms per call of fn: a HIP graph of `calls` back-to-back calls, replayed, median replay / calls."""
-    med, _ = graph_latency(fn, replays=replays, warmup=3, per_graph=calls)
-    return med
+    """Device ms per call of fn: a HIP graph of `calls` back-to-back calls replayed `replays` times back to back between two
+    events. One untimed replay runs first, so the GPU is busy while the host queues the timed ones and no submission gap
+    falls inside the timed region; the total is divided by replays x calls."""
+    import torch
+    g = capture(fn, calls)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g.replay()
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / (replays * calls)
 
 
 def rht_figures(dev, seed):
