@@ -191,7 +191,7 @@ int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, con
  * call's M rows (k_new, v_new (M, D)); query t sees key j iff causal_offset < 0 or j <= causal_offset + t. Scores
  * (q . k) / 16, softmax over the visible keys, computed in chunks of 64 keys (chunk maximum, exponentials, sums) merged
  * per token: the result depends on the number of keys only through that fixed chunking. part: workspace of
- * M * tcq_attend_chunks(P, M) * H * (D + 2) floats. Outputs: o (M, H * D) BF16 (may be NULL when su is given) and, when su
+ * M * tcq_attend_chunks(P, M) * H * (D + 4) floats, 16-byte aligned. Outputs: o (M, H * D) BF16 (may be NULL when su is given) and, when su
  * is given, the rotate + quantize prologue of the next projection applied to the BF16 o row (q8 (M, H * D) int8, scale (M,)).
  * No reference counterpart: the reference policy's attention is PyTorch; this is the decoder layers' attention between
  * the TCQ projections, with the o-projection prologue (kernels.pre, deploy/tcq_kernels/kernels.py:208-219) fused in. */

@@ -18,6 +18,7 @@ constexpr int AD = 256;          // head dim
 constexpr int AH = 8;            // most query heads
 constexpr int KC = 64;           // keys per chunk
 constexpr int AT = 256;          // threads of k_attn_part
+constexpr int PS = AD + 4;       // floats per (token, chunk, head) partial: o[AD], m, l and 2 pad words (16-byte rows)
 
 __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh, int P, int j) {
     return j < P ? cache + (size_t)j * AD : fresh + (size_t)(j - P) * AD;
@@ -33,7 +34,7 @@ __device__ __forceinline__ float4_t mma_bf16(uint4_t a, uint4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// grid (token groups ceil(M / TPB), chunks NC), AT = 256 threads (4 waves). part: (M, NC, H, AD + 2) FP32: o[AD], m, l per
+// grid (token groups ceil(M / TPB), chunks NC), AT = 256 threads (4 waves). part: (M, NC, H, PS) FP32: o[AD], m, l per
 // head. The query rows of the group (row r = token TPB x + r / 8, head r % 8; zero rows for heads >= H and tokens >= M) form
 // RB = TPB / 2 blocks of 16 MFMA rows, staged once in LDS, so one staged chunk of keys / values serves TPB tokens (the keys
 // and values are the bulk of the traffic: every group reads every chunk).
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
         for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
         ps[r][lane] = e;
         if (lane == 0 && h < H && t < M) {
-            float* base = part + (((size_t)t * NC + c) * H + h) * (AD + 2);
+            float* base = part + (((size_t)t * NC + c) * H + h) * PS;
             base[AD] = m;
             base[AD + 1] = l;
         }
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int h = 4 * (lg & 1) + e;
-                    if (h < H) part[(((size_t)t * NC + c) * H + h) * (AD + 2) + d] = acc[e];
+                    if (h < H) part[(((size_t)t * NC + c) * H + h) * PS + d] = acc[e];
                 }
             }
         }
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     __shared__ float inv[AH];
     __shared__ float sums[CG][AH][AD];
     const int t = blockIdx.x, tid = threadIdx.x, d = tid & (AD - 1), g = tid / AD, lane = tid & 63, wave = tid >> 6, K = H * AD;
-    const size_t cs = (size_t)H * (AD + 2);                          // stride between chunks
+    const size_t cs = (size_t)H * PS;                          // stride between chunks
     const float* tb = part + (size_t)t * NC * cs;
     constexpr int SR = MAXC / 64;
     float mv[SR], lv[SR];
@@ -183,8 +184,8 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
 #pragma unroll
         for (int r = 0; r < SR; ++r) {
             const int c = 64 * r + lane;
-            mv[r] = c < NC ? tb[c * cs + wave * (AD + 2) + AD] : -__builtin_inff();
-            lv[r] = c < NC ? tb[c * cs + wave * (AD + 2) + AD + 1] : 0.f;
+            mv[r] = c < NC ? tb[c * cs + wave * PS + AD] : -__builtin_inff();
+            lv[r] = c < NC ? tb[c * cs + wave * PS + AD + 1] : 0.f;
         }
     }
     float v[CB][AH];
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
         for (int i = 0; i < CB; ++i) {
             const int c = c0 + g + CG * i;
 #pragma unroll
-            for (int h = 0; h < AH; ++h) v[i][h] = c < NC && h < H ? tb[c * cs + h * (AD + 2) + d] : 0.f;
+            for (int h = 0; h < AH; ++h) v[i][h] = c < NC && h < H ? tb[c * cs + h * PS + d] : 0.f;
         }
     };
     load(0);
@@ -253,6 +254,96 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     quantize_row(lds, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
 }
 
+// grid M, H * 16 threads (H * AD = 1024 or 2048): thread 16 h + g owns dims 16 g .. 16 g + 15 of head h, summed over the
+// chunks straight from the partials; the 16 lanes of head h first merge its chunk statistics (lane = chunk mod 16, a
+// butterfly over the 16 lanes, so every lane holds the same total). With su, the BF16 row goes through the register Walsh
+// engine and the quantizer of the output projection's prologue.
+__global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int NC, int H, u16* o, const i8* su, i8* q8,
+                                                          float* scale) {
+    extern __shared__ float xs[];                                        // H * AD floats: cross-wave exchange
+    __shared__ float wts[AH][MAXC];
+    __shared__ float red[16];
+    const int t = blockIdx.x, tid = threadIdx.x, h = tid >> 4, g = tid & 15, d0 = 16 * g, K = H * AD;
+    const size_t cs = (size_t)H * PS;
+    const float* hb = part + (size_t)t * NC * cs + (size_t)h * PS;      // head h of chunk 0
+    // every load issued at entry: this lane's chunk statistics (chunks g, g + 16, ...) and the first 8 chunks' values
+    constexpr int SC = MAXC / 16, VB = 8;
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    f2_t ml[SC];
+#pragma unroll
+    for (int r = 0; r < SC; ++r) {
+        const int c = g + 16 * r;
+        ml[r] = c < NC ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
+    }
+    float4_t v0[VB][4];
+#pragma unroll
+    for (int i = 0; i < VB; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v0[i][q] = i < NC ? gptr((const float4_t*)(hb + i * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float L = 0.f;
+#pragma unroll
+    for (int r = 0; r < SC; ++r) {
+        const int c = g + 16 * r;
+        if (c < NC) {
+            const float w = ml[r].x == -__builtin_inff() ? 0.f : expf(ml[r].x - mx);
+            wts[h][c] = w;                                               // read back by this wave only: LDS keeps its order
+            L = __builtin_fmaf(w, ml[r].y, L);
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) L = L + __shfl_xor(L, m, 64);
+    float acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+        if (i >= NC) break;
+        const float w = wts[h][i];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(w, v0[i][k >> 2][k & 3], acc[k]);
+    }
+    for (int c0 = VB; c0 < NC; c0 += 4) {
+        float4_t v[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[i][q] = c0 + i < NC ? gptr((const float4_t*)(hb + (c0 + i) * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (c0 + i >= NC) break;
+            const float w = wts[h][c0 + i];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(w, v[i][k >> 2][k & 3], acc[k]);
+        }
+    }
+    u16 b[16];
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        b[k] = f32_to_bf16(acc[k] / L);
+        v[k] = bf16_to_f32(b[k]);
+    }
+    if (o) {
+        uint4_t w2[2];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w2[k >> 2][k & 3] = (u32)b[2 * k] | ((u32)b[2 * k + 1] << 16);
+        u16* op = o + (size_t)t * K + h * AD + d0;
+        gptr((uint4_t*)op)[0] = w2[0];
+        gptr((uint4_t*)op)[1] = w2[1];
+    }
+    if (!su) return;
+    const uint4_t sg = gptr((const uint4_t*)(su + h * AD + d0))[0];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = v[k] * (float)(i8)(sg[k >> 2] >> (8 * (k & 3)));
+    reg_rotate_quantize(v, K, xs, red, q8, nullptr, 0, scale, t);
+}
+
 extern "C" int tcq_attend_chunks(int P, int M) { return (P + M + KC - 1) / KC; }
 
 extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
@@ -262,7 +353,8 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     if (!o && !su) return TCQ_ERR_ARG;
     if (su && (!q8 || !scale)) return TCQ_ERR_ARG;
     if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
-    if ((uintptr_t)k_new % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_new % 16 || (uintptr_t)v_cache % 16) return TCQ_ERR_ALIGN;
+    if ((uintptr_t)k_new % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_new % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)part % 16)
+        return TCQ_ERR_ALIGN;
     const int NC = tcq_attend_chunks(P, M);
     if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
@@ -270,7 +362,13 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     // and 8 run 20 us (fewer, longer groups); single tokens (8 rows, half the MFMA rows empty) match pairs
     launch_k(k_attn_part<2>, dim3((M + 1) / 2, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
              (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
-    launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
-             (u16*)o, (const i8*)su, (i8*)q8, scale);
+    // combine: the register path for H * AD of 1024 / 2048 (with 16-byte aligned outputs), else 1024 threads over LDS
+    const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
+    if ((H == 4 || H == 8) && oal)
+        launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC, H,
+                 (u16*)o, (const i8*)su, (i8*)q8, scale);
+    else
+        launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
+                 (u16*)o, (const i8*)su, (i8*)q8, scale);
     return launch_status();
 }

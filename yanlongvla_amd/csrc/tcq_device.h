@@ -216,6 +216,7 @@ __device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, i
     }
 }
 
+
 // ------------------------------------------------------------------------------------------------------------- trellis code
 // One 16 x 16 tile = 32 uint16 words, 512 bits, most significant bit first; state t = bits [4t, 4t + 16) (tail-biting).
 // Tile row r, weight pair p (columns 2p, 2p + 1) has state t = 8 r + p (reference tcq_format.py:58-63).
@@ -252,4 +253,30 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* gptr(T* p) {
 template <class T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const T* p) {
     return (const __attribute__((address_space(1))) T*)p;
+}
+
+// Rotate + quantize of a register row (values already signed): walsh, * c, per-token absmax, INT8 words (as k_pre).
+__device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float* xs, float* red, i8* q, int* q4, int ldq,
+                                                    float* scale, int tok) {
+    const int t = threadIdx.x;
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    reg_walsh16(v, N, xs);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    const float sc = token_scale(block_max(mx, red));
+    if (t == 0) scale[tok] = sc;
+    u32 words[4];
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+    if (q) *gptr((uint4_t*)(q + (size_t)tok * N + 16 * t)) = uint4_t{words[0], words[1], words[2], words[3]};
+    if (q4) {
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
+    }
 }

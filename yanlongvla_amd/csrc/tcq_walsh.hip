@@ -740,32 +740,6 @@ __device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st
     }
 }
 
-// Rotate + quantize of a register row (values already signed): walsh, * c, per-token absmax, INT8 words (as k_pre).
-__device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float* xs, float* red, i8* q, int* q4, int ldq,
-                                                    float* scale, int tok) {
-    const int t = threadIdx.x;
-    const float c = (float)(1.0 / __builtin_sqrt((double)N));
-    reg_walsh16(v, N, xs);
-    float mx = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        v[k] = v[k] * c;
-        mx = fmaxf(mx, fabsf(v[k]));
-    }
-    const float sc = token_scale(block_max(mx, red));
-    if (t == 0) scale[tok] = sc;
-    u32 words[4];
-#pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4)
-        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
-                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
-    if (q) *gptr((uint4_t*)(q + (size_t)tok * N + 16 * t)) = uint4_t{words[0], words[1], words[2], words[3]};
-    if (q4) {
-#pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
-    }
-}
-
 // Register path of k_mid2 (power-of-two N of 1024 .. 8192, N / 16 threads, aligned): thread t owns chunk t of the gate half
 // and of the up half; the same operations and rounding points as k_mid2.
 template <int ADT>

@@ -199,7 +199,7 @@ def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None,
     _contig(q, k_cache, v_cache, k_new, v_new, o, su, q8, scale)
     D = k_new.shape[1]
     nc = int(_lib.lib().tcq_attend_chunks(P, M))
-    part = torch.empty(M * nc * heads * (D + 2), dtype=torch.float32, device=q.device)
+    part = torch.empty(M * nc * heads * (D + 4), dtype=torch.float32, device=q.device)
     call('tcq_attend', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, D,
          -1 if causal_offset is None else int(causal_offset), ptr(part), ptr(o), ptr(su), ptr(q8), ptr(scale), stream())
     return o
