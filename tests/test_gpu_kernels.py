@@ -80,7 +80,7 @@ def test_decode_golden(golden, tag):
 
 
 # -------------------------------------------------------------------------------------------------------------------- RHT
-RHT_CASES = [(1, 1), (3, 16), (2, 48), (5, 80), (2, 20), (1, 1024), (16, 2048), (50, 4096), (16, 16384), (4, 1152), (3, 4304),
+RHT_CASES = [(1, 1), (3, 16), (2, 48), (5, 80), (2, 20), (1, 1024), (16, 2048), (50, 4096), (3, 8192), (16, 16384), (4, 1152), (3, 4304),
              (800, 1024), (800, 16384)]
 
 

@@ -255,6 +255,43 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const
     return (const __attribute__((address_space(1))) T*)p;
 }
 
+// Raw 16-element chunks of the side vectors, loaded at kernel entry together with the accumulator row (they do not depend
+// on it) and converted where they are used, so no global round trip waits behind a Walsh pass. ESZ: element bytes (1 INT8,
+// 2 BF16, 4 FP32); the raw words hold the elements little-endian, as in memory. Unaligned rows load element by element.
+template <int ESZ> struct Raw16 {
+    uint4_t r[ESZ];
+};
+template <int ESZ>
+__device__ __forceinline__ Raw16<ESZ> raw16(const void* p, bool vec) {
+    Raw16<ESZ> o;
+    if (vec) {
+#pragma unroll
+        for (int q = 0; q < ESZ; ++q) o.r[q] = gptr((const uint4_t*)p)[q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < ESZ; ++q) o.r[q] = uint4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const u32 e = ESZ == 1 ? (u32)(uint8_t)gptr((const i8*)p)[k] : ESZ == 2 ? (u32)gptr((const u16*)p)[k] : gptr((const u32*)p)[k];
+            const int bit = 8 * ESZ * k;                                 // bit offset of element k in the 16 * ESZ bytes
+            o.r[bit >> 7][(bit >> 5) & 3] |= e << (bit & 31);
+        }
+    }
+    return o;
+}
+__device__ __forceinline__ void cv16(const Raw16<1>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a.r[0][k >> 2] >> (8 * (k & 3)));
+}
+__device__ __forceinline__ void cv16(const Raw16<2>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32((u16)(a.r[k >> 3][(k >> 1) & 3] >> (16 * (k & 1))));
+}
+__device__ __forceinline__ void cv16(const Raw16<4>& a, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = __uint_as_float(a.r[k >> 2][k & 3]);
+}
+
 // Rotate + quantize of a register row (values already signed): walsh, * c, per-token absmax, INT8 words (as k_pre).
 __device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float* xs, float* red, i8* q, int* q4, int ldq,
                                                     float* scale, int tok) {

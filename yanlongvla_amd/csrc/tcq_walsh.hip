@@ -124,6 +124,34 @@ __global__ void k_rht(const void* x, int ldx, const i8* su, void* y, int ldy, in
     store_row<YDT>(lds, y, tok * ldy, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
 }
 
+// Register path of k_rht for power-of-two rows (K / 16 threads, thread t owns elements 16 t .. 16 t + 15;
+// rows and signs 16-byte aligned): x * su -> reg_walsh16 -> * c, the same operations in the same order as k_rht.
+template <int XDT, int YDT>
+__global__ __launch_bounds__(1024) void k_rht_reg(const void* x, int ldx, const i8* su, void* y, int ldy, int K) {
+    extern __shared__ float xs[];
+    const size_t tok = blockIdx.x;
+    const int i0 = 16 * threadIdx.x;
+    float v[16], a[8], b[8];
+    Elem<XDT>::ld8(x, tok * ldx + i0, a);
+    Elem<XDT>::ld8(x, tok * ldx + i0 + 8, b);
+    Raw16<1> s0{};
+    if (su) s0 = raw16<1>(su + i0, true);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { v[k] = a[k]; v[8 + k] = b[k]; }
+    if (su) {
+        float sg[16];
+        cv16(s0, sg);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = v[k] * sg[k];
+    }
+    reg_walsh16(v, K, xs);
+    const float c = (float)(1.0 / __builtin_sqrt((double)K));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { a[k] = v[k] * c; b[k] = v[8 + k] * c; }
+    Elem<YDT>::st8(y, tok * ldy + i0, a);
+    Elem<YDT>::st8(y, tok * ldy + i0 + 8, b);
+}
+
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
 template <int XDT>
 __global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec) {
@@ -391,43 +419,6 @@ __device__ __forceinline__ void c16_f32(const float* p, bool vec, float (&v)[16]
 #pragma unroll
         for (int k = 0; k < 16; ++k) v[k] = gptr(p)[k];
     }
-}
-
-// Raw 16-element chunks of the side vectors, loaded at kernel entry together with the accumulator row (they do not depend
-// on it) and converted where they are used, so no global round trip waits behind a Walsh pass. ESZ: element bytes (1 INT8,
-// 2 BF16, 4 FP32); the raw words hold the elements little-endian, as in memory. Unaligned rows load element by element.
-template <int ESZ> struct Raw16 {
-    uint4_t r[ESZ];
-};
-template <int ESZ>
-__device__ __forceinline__ Raw16<ESZ> raw16(const void* p, bool vec) {
-    Raw16<ESZ> o;
-    if (vec) {
-#pragma unroll
-        for (int q = 0; q < ESZ; ++q) o.r[q] = gptr((const uint4_t*)p)[q];
-    } else {
-#pragma unroll
-        for (int q = 0; q < ESZ; ++q) o.r[q] = uint4_t{0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const u32 e = ESZ == 1 ? (u32)(uint8_t)gptr((const i8*)p)[k] : ESZ == 2 ? (u32)gptr((const u16*)p)[k] : gptr((const u32*)p)[k];
-            const int bit = 8 * ESZ * k;                                 // bit offset of element k in the 16 * ESZ bytes
-            o.r[bit >> 7][(bit >> 5) & 3] |= e << (bit & 31);
-        }
-    }
-    return o;
-}
-__device__ __forceinline__ void cv16(const Raw16<1>& a, float (&v)[16]) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a.r[0][k >> 2] >> (8 * (k & 3)));
-}
-__device__ __forceinline__ void cv16(const Raw16<2>& a, float (&v)[16]) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32((u16)(a.r[k >> 3][(k >> 1) & 3] >> (16 * (k & 1))));
-}
-__device__ __forceinline__ void cv16(const Raw16<4>& a, float (&v)[16]) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = __uint_as_float(a.r[k >> 2][k & 3]);
 }
 
 // Sum of squares of a row in an order fixed by K alone: chunk sums of 16 consecutive values (sequential, part[j] for chunk
@@ -859,6 +850,22 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
     const int vec = n % 8 == 0 && al16(x) && al16(y) && ((size_t)ldx * dsize(x_dtype)) % 16 == 0 &&
                     ((size_t)ldy * dsize(y_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
+    // register path for power-of-two rows of 1024 / 2048 (measured on MI355X: 800 x 2048 in 5.8 us against 7.8 on the LDS
+    // engine; from 4096 on, the exchanges between waves make it slower: 800 x 16384 in 35 us against 28)
+    if ((n & (n - 1)) == 0 && n >= 1024 && n <= 2048 && vec && (!su || al16(su))) {
+#define RHT_Y(XD, YD) launch_k(k_rht_reg<XD, YD>, grid, dim3(n / 16), (size_t)n * sizeof(float), st, x, ldx, (const i8*)su, y, ldy, n)
+#define RHT_X(XD, _)                                          \
+    switch (y_dtype) {                                        \
+        case TCQ_F32: RHT_Y(XD, TCQ_F32); break;              \
+        case TCQ_BF16: RHT_Y(XD, TCQ_BF16); break;            \
+        case TCQ_F16: RHT_Y(XD, TCQ_F16); break;              \
+        default: return TCQ_ERR_DTYPE;                        \
+    }
+        DISPATCH_X(x_dtype, RHT_X, 0)
+#undef RHT_Y
+#undef RHT_X
+        return launch_status();
+    }
 #define RHT_Y(XD, YD) launch_k(k_rht<XD, YD>, grid, block, sh, st, x, ldx, (const i8*)su, y, ldy, n, vec)
 #define RHT_X(XD, _)                                          \
     switch (y_dtype) {                                        \
