@@ -51,7 +51,8 @@ def accumulators(rng, M, width, kind):
 
 
 @pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
-@pytest.mark.parametrize("M,N", [(1, 4096), (50, 4096), (3, 16384), (7, 1152), (2, 48), (4, 1024), (2, 2048), (3, 8192)])
+@pytest.mark.parametrize("M,N", [(1, 4096), (50, 4096), (3, 16384), (1, 16384), (7, 1152), (2, 48), (4, 1024), (2, 2048),
+                                 (3, 8192), (70, 8192)])
 def test_mid2_bitexact(kind, M, N):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * 7 + N)
@@ -68,11 +69,12 @@ def test_mid2_bitexact(kind, M, N):
     assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
 
 
-def test_mid2_strided_accumulator():
+@pytest.mark.parametrize('N', [1024, 4096])
+def test_mid2_strided_accumulator(N):
     """Gate | up columns inside a wider accumulator row (lda > 2N), as when more layers share the product."""
     from yanlongvla_amd import kernels as K
-    rng = np.random.default_rng(11)
-    M, N, lda = 5, 1024, 2 * 1024 + 256
+    rng = np.random.default_rng(11 + N)
+    M, lda = 5, 2 * N + 256
     full = rng.integers(-2 ** 18, 2 ** 18, size=(M, lda)).astype(np.int32)
     s = (rng.random(M) * 1e-3 + 1e-4).astype(np.float32)
     rs = (rng.random(2 * N) * 1e-2).astype(np.float32)

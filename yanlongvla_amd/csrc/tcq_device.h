@@ -19,6 +19,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef int int4_t __attribute__((ext_vector_type(4)));
 typedef u32 uint4_t __attribute__((ext_vector_type(4)));
+typedef u16 u16x2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------------------------------------------------ conversions
 __device__ __forceinline__ float bf16_to_f32(u16 b) { return __uint_as_float(((u32)b) << 16); }
@@ -196,6 +197,75 @@ __device__ __forceinline__ void reg_walsh16(float (&v)[16], int K, float* xs) {
     }
 }
 
+// Register + transpose Walsh engine: a power-of-two row of 2^L values held 2^LE per thread by 2^(L - LE) threads
+// (2 LE <= L <= 3 LE). Three layouts give the row index of register k in thread t:
+//   A (natural):  (t << LE) | k                                              -- register bits = index bits [0, LE)
+//   B (middle):   t bits [0, LE) -> [0, LE), t bits [LE, ..) -> [L - LE, ..),
+//                 k bits [0, MB) -> [LE, L - LE), k bits [MB, LE) -> [L - LE + MB, L)   (MB = L - 2 LE)
+//   C (top):      t | (k << (L - LE))                                        -- register bits = index bits [L - LE, L)
+// A pass runs the butterflies of its layout's register bits inside the thread; between passes the row goes once through
+// LDS (lds_slot padding: every access of a half-wave hits 32 distinct banks). Since the passes cover index bits in
+// ascending order, every stage is walsh_segment's butterfly in the same stage order and the sums are equal bit for bit.
+// The index parts of t and k use disjoint bits, so lds_slot(t part | k part) = lds_slot(t part) + lds_slot(k part) and
+// the k parts are compile-time offsets.
+template <int L, int LE>
+struct Tw {
+    static constexpr int E = 1 << LE, T = 1 << (L - LE), H = L - LE, MB = L - 2 * LE;
+    static_assert(MB >= 0 && MB <= LE, "register + transpose Walsh needs 2 LE <= L <= 3 LE");
+    template <int X>
+    __device__ static int tpart(int t) {
+        return X == 0 ? t << LE : X == 1 ? (t & (E - 1)) | ((t >> LE) << H) : t;
+    }
+    template <int X>
+    __host__ __device__ static constexpr int kpart(int k) {
+        return X == 0 ? k : X == 1 ? ((k & ((1 << MB) - 1)) << LE) | ((k >> MB) << (H + MB)) : k << H;
+    }
+};
+
+// Stores the thread's values of layout X to their row slots in xs / loads them from there.
+template <int L, int LE, int X>
+__device__ __forceinline__ void tw_put(const float (&v)[1 << LE], float* xs) {
+    using W = Tw<L, LE>;
+    const int b = lds_slot(W::template tpart<X>(threadIdx.x));
+#pragma unroll
+    for (int k = 0; k < W::E; ++k) xs[b + lds_slot(W::template kpart<X>(k))] = v[k];
+}
+template <int L, int LE, int X>
+__device__ __forceinline__ void tw_get(float (&v)[1 << LE], const float* xs) {
+    using W = Tw<L, LE>;
+    const int b = lds_slot(W::template tpart<X>(threadIdx.x));
+#pragma unroll
+    for (int k = 0; k < W::E; ++k) v[k] = xs[b + lds_slot(W::template kpart<X>(k))];
+}
+
+// Unnormalised Walsh of the row held in layout A (v: the thread's 2^LE values); leaves it in layout C. xs: lds_words(2^L)
+// floats. On entry no other thread may still read the thread's layout-A slots (a barrier, or only the thread itself read
+// them last); on exit the thread may rewrite its own layout-C slots at once, any other slot only after a barrier.
+template <int L, int LE>
+__device__ __forceinline__ void tw_walsh(float (&v)[1 << LE], float* xs) {
+    using W = Tw<L, LE>;
+    butterflies<LE>(v);
+    tw_put<L, LE, 0>(v, xs);
+    __syncthreads();
+    if constexpr (W::MB > 0) {
+        tw_get<L, LE, 1>(v, xs);
+#pragma unroll
+        for (int g = 0; g < (W::E >> W::MB); ++g) butterflies<W::MB>(v + (g << W::MB));
+        tw_put<L, LE, 1>(v, xs);
+        __syncthreads();
+    }
+    tw_get<L, LE, 2>(v, xs);
+    butterflies<LE>(v);
+}
+
+// Layout C -> layout A through xs (own slots first, one barrier).
+template <int L, int LE>
+__device__ __forceinline__ void tw_to_natural(float (&v)[1 << LE], float* xs) {
+    tw_put<L, LE, 2>(v, xs);
+    __syncthreads();
+    tw_get<L, LE, 0>(v, xs);
+}
+
 // ---------------------------------------------------------------------------------------------------- activation quantizer
 // Per-token symmetric INT8 of tcq_format.quantize_tokens (reference tcq_format.py:119-122): IEEE division, half-even, clamp.
 __device__ __forceinline__ int q8(float v, float s) {
@@ -315,5 +385,75 @@ __device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float
     if (q4) {
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
+    }
+}
+
+// 16-element view of part h of a register array (for the 16-wide loaders and converters).
+template <int E>
+__device__ __forceinline__ float (&part16(float (&v)[E], int h))[16] { return *reinterpret_cast<float(*)[16]>(&v[16 * h]); }
+
+// reg_rotate_quantize on the register + transpose engine: v holds the natural-layout values 2^LE t .. 2^LE t + 2^LE - 1 of
+// the row (N = 2^L); the same operations in the same order (Walsh, * c, row max, per-token INT8, q and / or q4 words).
+template <int L, int LE>
+__device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* xs, float* red, i8* q, int* q4, int ldq,
+                                                   float* scale, int tok) {
+    constexpr int N = 1 << L, E = 1 << LE;
+    const int t = threadIdx.x;
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh<L, LE>(v, xs);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    const float sc = token_scale(block_max(mx, red));
+    if (t == 0) scale[tok] = sc;
+    tw_to_natural<L, LE>(v, xs);
+    u32 words[E / 4];
+#pragma unroll
+    for (int k4 = 0; k4 < E / 4; ++k4)
+        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+    if (q) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h)
+            *gptr((uint4_t*)(q + (size_t)tok * N + E * t + 16 * h)) =
+                uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+    }
+    if (q4) {
+#pragma unroll
+        for (int k4 = 0; k4 < E / 4; ++k4) q4[(size_t)((E / 4) * t + k4) * ldq + tok] = (int)words[k4];
+    }
+}
+
+// Coalesced loading of a wave's span of a row of 4-byte values: the wave's threads hold the 64 * 2^LE values
+// [64 w 2^LE, 64 (w + 1) 2^LE) in layout A, and reading them thread by thread (2^LE values = 2^(LE+2) bytes per lane)
+// makes every load instruction touch 64 cache lines. Instead lane l loads the 16-byte pieces 64 j + l (j < 2^LE / 4) of the
+// span, so each instruction covers one contiguous KiB, and tw_span_put places the values at their row slots in xs.
+template <int LE>
+struct Span4 {
+    uint4_t p[(1 << LE) / 4];
+};
+template <int LE>
+__device__ __forceinline__ Span4<LE> tw_span_load(const u32* row) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint4_t* s = (const uint4_t*)(row + ((size_t)w << (LE + 6)));
+    Span4<LE> r;
+#pragma unroll
+    for (int j = 0; j < (1 << LE) / 4; ++j) r.p[j] = *gptr(s + 64 * j + lane);
+    return r;
+}
+// f(j, m, bits) converts value m of piece j; the piece's 4 slots are consecutive (pieces never straddle a padding word) and
+// the lanes of a half-wave hit 32 distinct banks.
+template <int LE, class F>
+__device__ __forceinline__ void tw_span_put(const Span4<LE>& r, float* xs, F&& f) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < (1 << LE) / 4; ++j) {
+        const int i = (w << (LE + 6)) + 4 * (64 * j + lane);
+        float* d = xs + lds_slot(i);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) d[m] = f(j, m, r.p[j][m]);
     }
 }

@@ -765,6 +765,100 @@ __global__ __launch_bounds__(512) void k_mid2_reg(const void* acc, int lda, cons
     reg_rotate_quantize(u, N, xs, red, q, q4, ldq, scale, tok);
 }
 
+// k_mid2 on the register + transpose engine for N = 2^L (2^LE values per thread, 2^(L - LE) threads, aligned): both halves
+// are loaded at entry, each transform returns to the natural layout through LDS, so signs, GELU and rounding points are
+// applied exactly as in k_mid2.
+template <int ADT, int L, int LE>
+__global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
+                                                           const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale) {
+    constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
+    extern __shared__ float xs[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = E * t;
+    const size_t base = (size_t)tok * lda + i0;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    Raw16<1> svg[NP], svu[NP], sn0[NP];
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        svg[h] = raw16<1>(sv + i0 + 16 * h, true);
+        svu[h] = raw16<1>(sv + N + i0 + 16 * h, true);
+        sn0[h] = raw16<1>(su + i0 + 16 * h, true);
+    }
+    float g[E], u[E];
+    // 4-byte accumulators: coalesced span loads staged through xs (the up half is loaded during the gate's transform and
+    // staged after it); BF16: per-thread loads
+    const u32* arow = (const u32*)acc + (size_t)tok * lda;
+    Span4<LE> ga{}, ua{};
+    auto stage = [&](const Span4<LE>& a, const float* r) {
+        if (ADT == TCQ_I32) {
+            // the scales' span in two halves, so that only half of it is live at a time
+            const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+            const uint4_t* rp = (const uint4_t*)((const u32*)r + ((size_t)w << (LE + 6)));
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                uint4_t rv[E / 8];
+#pragma unroll
+                for (int j = 0; j < E / 8; ++j) rv[j] = *gptr(rp + 64 * (j + hh * E / 8) + lane);
+#pragma unroll
+                for (int j = 0; j < E / 8; ++j) {
+                    const int jj = j + hh * E / 8;
+                    float* d = xs + lds_slot((w << (LE + 6)) + 4 * (64 * jj + lane));
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) d[m] = ((float)(int)a.p[jj][m] * st) * __uint_as_float(rv[j][m]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            tw_span_put<LE>(a, xs, [&](int, int, u32 b) { return __uint_as_float(b); });
+        }
+        __syncthreads();
+    };
+    if constexpr (ADT == TCQ_BF16) {
+#pragma unroll
+        for (int h = 0; h < NP; ++h) {
+            acc_chunk<ADT>(acc, base + 16 * h, st, rs + i0 + 16 * h, part16(g, h));
+            acc_chunk<ADT>(acc, base + N + 16 * h, st, rs + N + i0 + 16 * h, part16(u, h));
+        }
+    } else {
+        ga = tw_span_load<LE>(arow);
+        stage(ga, rs);
+        ua = tw_span_load<LE>(arow + N);      // after the barrier: in flight during the gate's transform
+        tw_get<L, LE, 0>(g, xs);
+    }
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh<L, LE>(g, xs);
+    tw_to_natural<L, LE>(g, xs);
+    u16x2_t gv[E / 2];                      // GELU values two per register (half-register gathers)
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        float sg[16];
+        cv16(svg[h], sg);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) g[16 * h + k] = g[16 * h + k] * c * sg[k];
+#pragma unroll
+        for (int k = 0; k < 16; k += 2)
+            gv[8 * h + k / 2] = u16x2_t{gptr(lut)[f32_to_bf16(g[16 * h + k])], gptr(lut)[f32_to_bf16(g[16 * h + k + 1])]};
+    }
+    if constexpr (ADT != TCQ_BF16) {
+        stage(ua, rs ? rs + N : nullptr);     // writes only the wave's own span: its threads have finished reading it
+        tw_get<L, LE, 0>(u, xs);
+    }
+    tw_walsh<L, LE>(u, xs);
+    tw_to_natural<L, LE>(u, xs);
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        float sgu[16], sn[16];
+        cv16(svu[h], sgu);
+        cv16(sn0[h], sn);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float uu = bf16_to_f32(f32_to_bf16((u[16 * h + k] * c) * sgu[k]));
+            u[16 * h + k] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gv[8 * h + k / 2][k & 1]) * uu)) * sn[k];
+        }
+    }
+    tw_rotate_quantize<L, LE>(u, xs, red, q, q4, ldq, scale, tok);
+}
+
 // Register path of k_post_add_norm_pre for power-of-two rows of 256 .. 16384 (K / 16 threads, thread t owns chunk t, every
 // pointer 16-byte aligned): the same operations in the same order, with the row in registers instead of LDS, the Walsh
 // transforms on reg_walsh16 and every global load issued at entry.
@@ -984,6 +1078,25 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
     const int svec = al16(sv) && al16(su);
     hipStream_t st = (hipStream_t)stream;
     const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
+    // register + transpose engine: widths 2^12 .. 2^14 (32 values of each half per thread), aligned
+    if (N >= 4096 && (N & (N - 1)) == 0 && vec && svec && (!q || al16(q))) {
+        const size_t tsh = (size_t)lds_words(N) * sizeof(float);
+#define MID2_TW(L)                                                                                                            \
+    switch (acc_dtype) {                                                                                                      \
+        case TCQ_I32: launch_k(k_mid2_tw<TCQ_I32, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+                               (i8*)q, (int*)q4, ldq, scale); break;                                                          \
+        case TCQ_F32: launch_k(k_mid2_tw<TCQ_F32, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+                               (i8*)q, (int*)q4, ldq, scale); break;                                                          \
+        case TCQ_BF16: launch_k(k_mid2_tw<TCQ_BF16, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut,    \
+                                sup, (i8*)q, (int*)q4, ldq, scale); break;                                                    \
+        default: return TCQ_ERR_DTYPE;                                                                                        \
+    }
+        if (N == 4096) MID2_TW(12)
+        else if (N == 8192) MID2_TW(13)
+        else MID2_TW(14)
+#undef MID2_TW
+        return launch_status();
+    }
     // register path: power-of-two widths of 1024 .. 8192 (one 16-element chunk of each half per thread), aligned
     if ((N & (N - 1)) == 0 && N >= 1024 && N <= 8192 && vec && svec && (!q || al16(q))) {
         const dim3 rb(N / 16);

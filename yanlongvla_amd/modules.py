@@ -111,7 +111,8 @@ class Group:
         return b
 
     def product(self, b):
-        """INT8 activations -> few tokens: FP32 z = (acc * s) * rs (M, Ntot) | many tokens: exact INT32 acc (M, Ntot)."""
+        """INT8 activations -> FP32 z = (float(acc) * s) * rs (M, Ntot) of the exact int32 product acc: few tokens on the
+        fused decode products, many tokens on the INT8 MFMA GEMM with the scaling in its epilogue (the order of tcq_post)."""
         q, dev = b['q'], b['q'].device
         M = q.shape[0]
         if M <= SMALL_M:
@@ -124,8 +125,8 @@ class Group:
                 kernels.gemm_tcq(segs, q, b['scale'], self.Ntot)
             return z
         W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.int8, device=dev))
-        acc = torch.empty(M, self.Ntot, dtype=torch.int32, device=dev)
-        return kernels.gemm_i8(q, W, acc)
+        z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
+        return kernels.gemm_i8(q, W, z, sa=b['scale'], sw=self.rs)
 
     def posts(self, acc, b, shape, gelu0=False):
         """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs)."""
