@@ -100,6 +100,52 @@ def test_rht_bitexact(M, n, xdt):
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
 
 
+@pytest.mark.parametrize('M,n,off', [(3, 4096, 32), (5, 16384, 32), (4, 2048, 32), (3, 8192, 1)])
+def test_rht_strided_rows_f16_out(M, n, off):
+    """Rows inside wider buffers (ldx = n + 64, ldy = n + 32) and FP16 output; off = 1 starts the rows off 16-byte
+    alignment, which the aligned register paths must leave to the LDS engine."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(n + off)
+    xf = rng.standard_normal((M, n + 64)).astype(np.float32)
+    xb = torch.from_numpy(xf).bfloat16()
+    su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.int8)
+    x = xb.to(DEV)[:, off:off + n]
+    yfull = torch.zeros(M, n + 32, dtype=torch.float16, device=DEV)
+    K.rht(x, T(su), yfull[:, :n])
+    ref = O.fwht(xb[:, off:off + n].float().numpy() * su.astype(np.float32))
+    assert np.array_equal(yfull[:, :n].cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    assert not yfull[:, n:].any()
+
+
+def fp16_tie_weight(n):
+    """A value w whose product with c = float32(1/sqrt(n)), rounded to FP32, is an exact FP16 tie while the exact product is
+    not: FP32-then-FP16 rounding (the definition) and a single rounding of the exact product to FP16 then differ."""
+    c = np.float32(1.0 / np.sqrt(n))
+    w = (1.0 + np.arange(1, 1 << 20) * 2.0 ** -20).astype(np.float32)
+    p = w * c
+    h = p.astype(np.float16)
+    half_ulp = np.spacing(np.abs(h)).astype(np.float64) / 2
+    tie = np.abs(p.astype(np.float64) - h.astype(np.float64)) == half_ulp
+    single = (w.astype(np.float64) * np.float64(c)).astype(np.float16)
+    cand = w[tie & (single != h)]
+    assert cand.size, n
+    return cand[0]
+
+
+@pytest.mark.parametrize('n', [2048, 8192])
+def test_rht_fp16_output_rounds_through_fp32(n):
+    """Every output of a one-hot row is w * c: at an FP16 tie of the FP32 product the FP16 output must round that FP32 value
+    (half-even), not the exact product (a fused multiply-convert would)."""
+    from yanlongvla_amd import kernels as K
+    w = fp16_tie_weight(n)
+    x = np.zeros((2, n), dtype=np.float32)
+    x[:, 0] = w
+    y = torch.empty(2, n, dtype=torch.float16, device=DEV)
+    K.rht(T(x), None, y)
+    ref = O.fwht(x).astype(np.float16)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
 @pytest.mark.parametrize('M,n', [(1, 1024), (16, 2048), (50, 4096)])
 def test_rht_vs_dense_hadamard(M, n):
     """C1 contract: FP32 result within 1e-3 relative of a dense-Hadamard FP64 reference (closed form, not the oracle)."""

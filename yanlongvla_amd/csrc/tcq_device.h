@@ -30,7 +30,13 @@ __device__ __forceinline__ u16 f32_to_bf16(float f) {
     return (u16)(u >> 16);
 }
 __device__ __forceinline__ float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
+// FP32 -> FP16 of an FP32 value. The value is pinned in a register first: otherwise the compiler may fuse a preceding multiply
+// and this conversion into one mixed-precision FMA (v_fma_mixlo_f16), a single rounding of the exact product, where the
+// defined result rounds to FP32 and then to FP16 (the two differ when the FP32 product is an exact FP16 tie).
+__device__ __forceinline__ u16 f32_to_f16(float f) {
+    asm("" : "+v"(f));
+    return __builtin_bit_cast(u16, (_Float16)f);
+}
 
 // load element i of a row of dtype `dt` as FP32 (exact for every supported input type)
 __device__ __forceinline__ float load_as_f32(const void* p, size_t i, int dt) {
@@ -427,33 +433,52 @@ __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* x
     }
 }
 
-// Coalesced loading of a wave's span of a row of 4-byte values: the wave's threads hold the 64 * 2^LE values
-// [64 w 2^LE, 64 (w + 1) 2^LE) in layout A, and reading them thread by thread (2^LE values = 2^(LE+2) bytes per lane)
-// makes every load instruction touch 64 cache lines. Instead lane l loads the 16-byte pieces 64 j + l (j < 2^LE / 4) of the
-// span, so each instruction covers one contiguous KiB, and tw_span_put places the values at their row slots in xs.
-template <int LE>
-struct Span4 {
-    uint4_t p[(1 << LE) / 4];
+// Coalesced loading / storing of a wave's span of a row (elements of ESZ = 2 or 4 bytes): the wave's threads hold the
+// 64 * 2^LE values [64 w 2^LE, 64 (w + 1) 2^LE) in layout A, and moving them thread by thread (2^LE * ESZ bytes per lane)
+// makes every memory instruction touch up to 64 cache lines. Instead lane l moves the 16-byte pieces 64 j + l of the span,
+// so each instruction covers one contiguous KiB, and the values pass through their row slots in xs. A piece holds
+// 16 / ESZ consecutive values, which never straddle a padding word; the lanes of a half-wave hit 32 distinct banks.
+template <int LE, int ESZ>
+struct Span {
+    uint4_t p[(1 << LE) * ESZ / 16];
 };
-template <int LE>
-__device__ __forceinline__ Span4<LE> tw_span_load(const u32* row) {
+template <int LE, int ESZ>
+__device__ __forceinline__ Span<LE, ESZ> tw_span_load(const void* row) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint4_t* s = (const uint4_t*)(row + ((size_t)w << (LE + 6)));
-    Span4<LE> r;
+    const uint4_t* s = (const uint4_t*)((const char*)row + ((size_t)w << (LE + 6)) * ESZ);
+    Span<LE, ESZ> r;
 #pragma unroll
-    for (int j = 0; j < (1 << LE) / 4; ++j) r.p[j] = *gptr(s + 64 * j + lane);
+    for (int j = 0; j < (1 << LE) * ESZ / 16; ++j) r.p[j] = *gptr(s + 64 * j + lane);
     return r;
 }
-// f(j, m, bits) converts value m of piece j; the piece's 4 slots are consecutive (pieces never straddle a padding word) and
-// the lanes of a half-wave hit 32 distinct banks.
-template <int LE, class F>
-__device__ __forceinline__ void tw_span_put(const Span4<LE>& r, float* xs, F&& f) {
+// xs slot of value m of piece j; f(j, m, bits) converts the raw bits of a value (ESZ = 2: the low 16 bits)
+template <int LE, int ESZ>
+__device__ __forceinline__ float* tw_piece_slot(float* xs, int j) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    return xs + lds_slot((w << (LE + 6)) + (16 / ESZ) * (64 * j + lane));
+}
+template <int LE, int ESZ, class F>
+__device__ __forceinline__ void tw_span_put(const Span<LE, ESZ>& r, float* xs, F&& f) {
 #pragma unroll
-    for (int j = 0; j < (1 << LE) / 4; ++j) {
-        const int i = (w << (LE + 6)) + 4 * (64 * j + lane);
-        float* d = xs + lds_slot(i);
+    for (int j = 0; j < (1 << LE) * ESZ / 16; ++j) {
+        float* d = tw_piece_slot<LE, ESZ>(xs, j);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) d[m] = f(j, m, r.p[j][m]);
+        for (int m = 0; m < 16 / ESZ; ++m)
+            d[m] = f(j, m, ESZ == 4 ? r.p[j][m] : (r.p[j][m >> 1] >> (16 * (m & 1))) & 0xffffu);
+    }
+}
+// the span from its row slots to memory; g(v) gives the raw bits of value v (ESZ = 2: in the low 16 bits)
+template <int LE, int ESZ, class G>
+__device__ __forceinline__ void tw_span_store(void* row, float* xs, G&& g) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint4_t* o = (uint4_t*)((char*)row + ((size_t)w << (LE + 6)) * ESZ);
+#pragma unroll
+    for (int j = 0; j < (1 << LE) * ESZ / 16; ++j) {
+        const float* d = tw_piece_slot<LE, ESZ>(xs, j);
+        uint4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = ESZ == 4 ? g(d[e]) : (g(d[2 * e]) & 0xffffu) | (g(d[2 * e + 1]) << 16);
+        *gptr(o + 64 * j + lane) = v;
     }
 }

@@ -152,6 +152,54 @@ __global__ __launch_bounds__(1024) void k_rht_reg(const void* x, int ldx, const 
     Elem<YDT>::st8(y, tok * ldy + i0 + 8, b);
 }
 
+// raw element bits <-> FP32 for FP32 / BF16 / FP16 rows (2-byte types in the low 16 bits)
+template <int DT>
+__device__ __forceinline__ float bits_to_f32(u32 b) {
+    if constexpr (DT == TCQ_F32) return __uint_as_float(b);
+    else return Elem16<DT>::cv((u16)b);
+}
+template <int DT>
+__device__ __forceinline__ u32 f32_to_bits(float f) {
+    if constexpr (DT == TCQ_F32) return __float_as_uint(f);
+    else return (u32)Elem16<DT>::cv(f);
+}
+
+// k_rht on the register + transpose engine for rows of 2^L (2^LE values per thread, rows and signs 16-byte aligned): the
+// row comes in and goes out as coalesced spans through LDS; x * su -> Walsh -> * c, the same operations as k_rht.
+template <int XDT, int YDT, int L, int LE>
+__global__ __launch_bounds__(1 << (L - LE)) void k_rht_tw(const void* x, int ldx, const i8* su, void* y, int ldy) {
+    constexpr int E = 1 << LE, XS = XDT == TCQ_F32 ? 4 : 2, YS = YDT == TCQ_F32 ? 4 : 2;
+    extern __shared__ float xs[];
+    const size_t tok = blockIdx.x;
+    const int i0 = E * threadIdx.x;
+    Raw16<1> s0[E / 16];
+    if (su) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) s0[h] = raw16<1>(su + i0 + 16 * h, true);
+    }
+    const Span<LE, XS> xa = tw_span_load<LE, XS>((const char*)x + tok * ldx * XS);
+    tw_span_put<LE, XS>(xa, xs, [](int, int, u32 b) { return bits_to_f32<XDT>(b); });
+    __syncthreads();
+    float v[E];
+    tw_get<L, LE, 0>(v, xs);
+    if (su) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) {
+            float sg[16];
+            cv16(s0[h], sg);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[16 * h + k] = v[16 * h + k] * sg[k];
+        }
+    }
+    tw_walsh<L, LE>(v, xs);
+    const float c = (float)(1.0 / __builtin_sqrt((double)(1 << L)));
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = v[k] * c;
+    tw_put<L, LE, 2>(v, xs);
+    __syncthreads();
+    tw_span_store<LE, YS>((char*)y + tok * ldy * YS, xs, [](float f) { return f32_to_bits<YDT>(f); });
+}
+
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
 template <int XDT>
 __global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec) {
@@ -788,8 +836,8 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int 
     // 4-byte accumulators: coalesced span loads staged through xs (the up half is loaded during the gate's transform and
     // staged after it); BF16: per-thread loads
     const u32* arow = (const u32*)acc + (size_t)tok * lda;
-    Span4<LE> ga{}, ua{};
-    auto stage = [&](const Span4<LE>& a, const float* r) {
+    Span<LE, 4> ga{}, ua{};
+    auto stage = [&](const Span<LE, 4>& a, const float* r) {
         if (ADT == TCQ_I32) {
             // the scales' span in two halves, so that only half of it is live at a time
             const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -809,7 +857,7 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int 
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            tw_span_put<LE>(a, xs, [&](int, int, u32 b) { return __uint_as_float(b); });
+            tw_span_put<LE, 4>(a, xs, [&](int, int, u32 b) { return __uint_as_float(b); });
         }
         __syncthreads();
     };
@@ -820,9 +868,9 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int 
             acc_chunk<ADT>(acc, base + N + 16 * h, st, rs + N + i0 + 16 * h, part16(u, h));
         }
     } else {
-        ga = tw_span_load<LE>(arow);
+        ga = tw_span_load<LE, 4>(arow);
         stage(ga, rs);
-        ua = tw_span_load<LE>(arow + N);      // after the barrier: in flight during the gate's transform
+        ua = tw_span_load<LE, 4>(arow + N);      // after the barrier: in flight during the gate's transform
         tw_get<L, LE, 0>(g, xs);
     }
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
@@ -935,6 +983,14 @@ static int dsize(int dt) { return dt == TCQ_F32 || dt == TCQ_I32 ? 4 : dt == TCQ
         default: return TCQ_ERR_DTYPE;                                                          \
     }
 
+template <int XD, int YD>
+static void launch_rht_tw(int n, int M, hipStream_t st, const void* x, int ldx, const i8* su, void* y, int ldy) {
+    const size_t sh = (size_t)lds_words(n) * sizeof(float);
+    if (n == 4096) launch_k(k_rht_tw<XD, YD, 12, 5>, dim3(M), dim3(128), sh, st, x, ldx, su, y, ldy);
+    else if (n == 8192) launch_k(k_rht_tw<XD, YD, 13, 5>, dim3(M), dim3(256), sh, st, x, ldx, su, y, ldy);
+    else launch_k(k_rht_tw<XD, YD, 14, 5>, dim3(M), dim3(512), sh, st, x, ldx, su, y, ldy);
+}
+
 extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, void* y, int y_dtype, int ldy, int M, int n,
                        tcq_stream_t stream) {
     if (!x || !y || M <= 0 || n <= 0 || ldx < n || ldy < n) return TCQ_ERR_ARG;
@@ -944,8 +1000,23 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
     const int vec = n % 8 == 0 && al16(x) && al16(y) && ((size_t)ldx * dsize(x_dtype)) % 16 == 0 &&
                     ((size_t)ldy * dsize(y_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
+    // register + transpose engine for power-of-two rows of 4096 .. 16384
+    if ((n & (n - 1)) == 0 && n >= 4096 && vec && (!su || al16(su))) {
+#define RHT_Y(XD, YD) launch_rht_tw<XD, YD>(n, M, st, x, ldx, (const i8*)su, y, ldy)
+#define RHT_X(XD, _)                                          \
+    switch (y_dtype) {                                        \
+        case TCQ_F32: RHT_Y(XD, TCQ_F32); break;              \
+        case TCQ_BF16: RHT_Y(XD, TCQ_BF16); break;            \
+        case TCQ_F16: RHT_Y(XD, TCQ_F16); break;              \
+        default: return TCQ_ERR_DTYPE;                        \
+    }
+        DISPATCH_X(x_dtype, RHT_X, 0)
+#undef RHT_X
+#undef RHT_Y
+        return launch_status();
+    }
     // register path for power-of-two rows of 1024 / 2048 (measured on MI355X: 800 x 2048 in 5.8 us against 7.8 on the LDS
-    // engine; from 4096 on, the exchanges between waves make it slower: 800 x 16384 in 35 us against 28)
+    // engine)
     if ((n & (n - 1)) == 0 && n >= 1024 && n <= 2048 && vec && (!su || al16(su))) {
 #define RHT_Y(XD, YD) launch_k(k_rht_reg<XD, YD>, grid, dim3(n / 16), (size_t)n * sizeof(float), st, x, ldx, (const i8*)su, y, ldy, n)
 #define RHT_X(XD, _)                                          \
