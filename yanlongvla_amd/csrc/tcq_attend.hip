@@ -99,21 +99,30 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
         for (int e = 0; e < 4; ++e) ps[16 * rb + 4 * lg + e][16 * wave + lr] = vis ? acc[e] * scl : -__builtin_inff();
     }
     __syncthreads();
-    // chunk softmax statistics: wave w takes rows w, w + 4, ..., lane = key
+    // chunk softmax statistics: wave w takes rows w, w + 4, ..., lane = key; the rows' reductions run side by side (each
+    // row's own order unchanged), so their cross-lane exchanges overlap instead of forming one long dependent chain
+    constexpr int RW = AR / 4;
+    float sv[RW], m[RW], e[RW], l[RW];
 #pragma unroll
-    for (int rr = 0; rr < AR / 4; ++rr) {
+    for (int rr = 0; rr < RW; ++rr) m[rr] = sv[rr] = ps[4 * rr + wave][lane];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) m[rr] = fmaxf(m[rr], __shfl_xor(m[rr], o, 64));
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) l[rr] = e[rr] = m[rr] == -__builtin_inff() ? 0.f : expf(sv[rr] - m[rr]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) l[rr] = l[rr] + __shfl_xor(l[rr], o, 64);
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
         const int r = 4 * rr + wave, t = t0 + (r >> 3), h = r & 7;
-        const float sv = ps[r][lane];
-        const float m = wave_max(sv);
-        const float e = m == -__builtin_inff() ? 0.f : expf(sv - m);
-        float l = e;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
-        ps[r][lane] = e;
+        ps[r][lane] = e[rr];
         if (lane == 0 && h < H && t < M) {
             float* base = part + (((size_t)t * NC + c) * H + h) * PS;
-            base[AD] = m;
-            base[AD + 1] = l;
+            base[AD] = m[rr];
+            base[AD + 1] = l[rr];
         }
     }
     __syncthreads();
@@ -254,6 +263,80 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     quantize_row(lds, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
 }
 
+// grid M, H * 64 threads (one wave per head, H <= 8): lane l of wave h owns dims 4 l .. 4 l + 3 of head h and loads them for
+// the first CW chunks together with the chunk statistics at entry, so a token of up to CW chunks costs one memory round trip
+// (k_attn_combine_reg holds 8 chunks and goes back to memory for the rest). Every 16-lane group repeats the statistics merge
+// of k_attn_combine_reg in its order (lane g: chunks g, g + 16, ...; butterfly over the 16 lanes), and the chunks add in
+// chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
+// register engine) and quantized.
+constexpr int CW = 16;
+__global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int H, u16* o, const i8* su, i8* q8,
+                                                        float* scale) {
+    extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
+    __shared__ float wts[AH][MAXC];
+    __shared__ float red[16];
+    const int t = blockIdx.x, tid = threadIdx.x, h = tid >> 6, lane = tid & 63, g = lane & 15, d0 = 4 * lane, K = H * AD;
+    const size_t cs = (size_t)H * PS;
+    const float* hb = part + (size_t)t * NC * cs + (size_t)h * PS;      // head h of chunk 0
+    constexpr int SC = MAXC / 16;
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    f2_t ml[SC];
+#pragma unroll
+    for (int r = 0; r < SC; ++r) {
+        const int c = g + 16 * r;
+        ml[r] = c < NC ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
+    }
+    float4_t v[CW];
+#pragma unroll
+    for (int i = 0; i < CW; ++i) v[i] = i < NC ? gptr((const float4_t*)(hb + i * cs + d0))[0] : float4_t{0.f, 0.f, 0.f, 0.f};
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float L = 0.f;
+#pragma unroll
+    for (int r = 0; r < SC; ++r) {
+        const int c = g + 16 * r;
+        if (c < NC) {
+            const float w = ml[r].x == -__builtin_inff() ? 0.f : expf(ml[r].x - mx);
+            if (lane < 16) wts[h][c] = w;                                // read back by this wave only: LDS keeps its order
+            L = __builtin_fmaf(w, ml[r].y, L);
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) L = L + __shfl_xor(L, m, 64);
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+        if (i < NC) {
+            const float w = wts[h][i];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, v[i][k], acc[k]);
+        }
+    }
+    for (int c = CW; c < NC; ++c) {
+        const float4_t vc = gptr((const float4_t*)(hb + c * cs + d0))[0];
+        const float w = wts[h][c];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, vc[k], acc[k]);
+    }
+    u16 b[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) b[k] = f32_to_bf16(acc[k] / L);
+    if (o) *gptr((u64*)(o + (size_t)t * K + h * AD + d0)) = (u64)b[0] | ((u64)b[1] << 16) | ((u64)b[2] << 32) | ((u64)b[3] << 48);
+    if (!su) return;                                                     // uniform
+    const u32 sg = *gptr((const u32*)(su + h * AD + d0));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xs[lds_slot(h * AD + d0 + k)] = bf16_to_f32(b[k]) * (float)(i8)(sg >> (8 * k));
+    __syncthreads();
+    float amx = 0.f;
+    block_walsh(xs, K, [&](int i, float x) { xs[lds_slot(i)] = x; amx = fmaxf(amx, fabsf(x)); });
+    const float sc = token_scale(block_max(amx, red));
+    if (tid == 0) scale[t] = sc;
+    quantize_row(xs, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
+}
+
 // grid M, H * 16 threads (H * AD = 1024 or 2048): thread 16 h + g owns dims 16 g .. 16 g + 15 of head h, summed over the
 // chunks straight from the partials; the 16 lanes of head h first merge its chunk statistics (lane = chunk mod 16, a
 // butterfly over the 16 lanes, so every lane holds the same total). With su, the BF16 row goes through the register Walsh
@@ -362,9 +445,13 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     // and 8 run 20 us (fewer, longer groups); single tokens (8 rows, half the MFMA rows empty) match pairs
     launch_k(k_attn_part<2>, dim3((M + 1) / 2, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
              (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
-    // combine: the register path for H * AD of 1024 / 2048 (with 16-byte aligned outputs), else 1024 threads over LDS
+    // combine: one wave per head with every load at entry (8-byte aligned o, 4-byte aligned su), else the register path for
+    // H * AD of 1024 / 2048 (16-byte aligned outputs), else 1024 threads over LDS
     const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
-    if ((H == 4 || H == 8) && oal)
+    if ((!o || (uintptr_t)o % 8 == 0) && (!su || (uintptr_t)su % 4 == 0))
+        launch_k(k_attn_combine_w, dim3(M), dim3(H * 64), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part,
+                 NC, H, (u16*)o, (const i8*)su, (i8*)q8, scale);
+    else if ((H == 4 || H == 8) && oal)
         launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC, H,
                  (u16*)o, (const i8*)su, (i8*)q8, scale);
     else
