@@ -124,34 +124,6 @@ __global__ void k_rht(const void* x, int ldx, const i8* su, void* y, int ldy, in
     store_row<YDT>(lds, y, tok * ldy, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
 }
 
-// Register path of k_rht for power-of-two rows (K / 16 threads, thread t owns elements 16 t .. 16 t + 15;
-// rows and signs 16-byte aligned): x * su -> reg_walsh16 -> * c, the same operations in the same order as k_rht.
-template <int XDT, int YDT>
-__global__ __launch_bounds__(1024) void k_rht_reg(const void* x, int ldx, const i8* su, void* y, int ldy, int K) {
-    extern __shared__ float xs[];
-    const size_t tok = blockIdx.x;
-    const int i0 = 16 * threadIdx.x;
-    float v[16], a[8], b[8];
-    Elem<XDT>::ld8(x, tok * ldx + i0, a);
-    Elem<XDT>::ld8(x, tok * ldx + i0 + 8, b);
-    Raw16<1> s0{};
-    if (su) s0 = raw16<1>(su + i0, true);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) { v[k] = a[k]; v[8 + k] = b[k]; }
-    if (su) {
-        float sg[16];
-        cv16(s0, sg);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = v[k] * sg[k];
-    }
-    reg_walsh16(v, K, xs);
-    const float c = (float)(1.0 / __builtin_sqrt((double)K));
-#pragma unroll
-    for (int k = 0; k < 8; ++k) { a[k] = v[k] * c; b[k] = v[8 + k] * c; }
-    Elem<YDT>::st8(y, tok * ldy + i0, a);
-    Elem<YDT>::st8(y, tok * ldy + i0 + 8, b);
-}
-
 // raw element bits <-> FP32 for FP32 / BF16 / FP16 rows (2-byte types in the low 16 bits)
 template <int DT>
 __device__ __forceinline__ float bits_to_f32(u32 b) {
@@ -779,43 +751,9 @@ __device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st
     }
 }
 
-// Register path of k_mid2 (power-of-two N of 1024 .. 8192, N / 16 threads, aligned): thread t owns chunk t of the gate half
-// and of the up half; the same operations and rounding points as k_mid2.
-template <int ADT>
-__global__ __launch_bounds__(512) void k_mid2_reg(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
-                                                  const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale, int N) {
-    extern __shared__ float xs[];
-    __shared__ float red[16];
-    const int tok = blockIdx.x, t = threadIdx.x, i0 = 16 * t;
-    const size_t base = (size_t)tok * lda + i0;
-    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
-    const Raw16<1> svg = raw16<1>(sv + i0, true), svu = raw16<1>(sv + N + i0, true), sn0 = raw16<1>(su + i0, true);
-    float g[16], u[16];
-    acc_chunk<ADT>(acc, base, st, rs ? rs + i0 : nullptr, g);
-    acc_chunk<ADT>(acc, base + N, st, rs ? rs + N + i0 : nullptr, u);
-    const float c = (float)(1.0 / __builtin_sqrt((double)N));
-    reg_walsh16(g, N, xs);
-    float sg[16];
-    cv16(svg, sg);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) g[k] = g[k] * c * sg[k];
-    u16 gv[16];
-    gelu16(lut, g, gv);
-    reg_walsh16(u, N, xs);
-    float sgu[16], sn[16];
-    cv16(svu, sgu);
-    cv16(sn0, sn);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const float uu = bf16_to_f32(f32_to_bf16((u[k] * c) * sgu[k]));
-        u[k] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gv[k]) * uu)) * sn[k];
-    }
-    reg_rotate_quantize(u, N, xs, red, q, q4, ldq, scale, tok);
-}
-
-// k_mid2 on the register + transpose engine for N = 2^L (2^LE values per thread, 2^(L - LE) threads, aligned): both halves
-// are loaded at entry, each transform returns to the natural layout through LDS, so signs, GELU and rounding points are
-// applied exactly as in k_mid2.
+// k_mid2 on the register + transpose engine for N = 2^L (2^LE values per thread, 2^(L - LE) threads, aligned): the gate half
+// is loaded at entry and the up half during the gate's transform, each transform returns to the natural layout through LDS,
+// so signs, GELU and rounding points are applied exactly as in k_mid2.
 template <int ADT, int L, int LE>
 __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
                                                            const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale) {
@@ -959,6 +897,71 @@ __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc,
     reg_rotate_quantize(v, N, xs, red, q, q4, ldq, scale, tok);
 }
 
+// k_post_add_norm_pre on the register + transpose engine for N = 2^L (2^LE values per thread, 2^(L - LE) >= 64 threads,
+// every pointer 16-byte aligned): the same operations in the same order as k_post_add_norm_pre_reg; the row is in the
+// natural layout for the epilogue, residual and norm (chunk sums of squares at chunk indices, summed by tree_total).
+template <int ADT, int L, int LE>
+__global__ __launch_bounds__(1 << (L - LE)) void k_post_add_norm_pre_tw(const void* acc, int lda, int col0, const float* s,
+                                                                       const float* rs, const i8* sv, const float* bias, const u16* x,
+                                                                       u16* xout, const u16* w, float eps, const i8* su, i8* q,
+                                                                       int* q4, int ldq, float* scale) {
+    constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
+    extern __shared__ float xs[];                                      // lds_words(N) floats for the transposes, then N / 16 sums
+    float* part = xs + lds_words(N);
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = E * t;
+    const size_t row = (size_t)tok * N, base = (size_t)tok * lda + col0 + i0;
+    Raw16<1> sv0[NP], su0[NP];
+    Raw16<2> x0[NP], w0[NP];
+    Raw16<4> b0[NP];
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        sv0[h] = raw16<1>(sv + i0 + 16 * h, true);
+        x0[h] = raw16<2>(x + row + i0 + 16 * h, true);
+        if (bias) b0[h] = raw16<4>(bias + i0 + 16 * h, true);
+        if (w) {
+            w0[h] = raw16<2>(w + i0 + 16 * h, true);
+            su0[h] = raw16<1>(su + i0 + 16 * h, true);
+        }
+    }
+    float v[E];
+#pragma unroll
+    for (int h = 0; h < NP; ++h) acc_chunk<ADT>(acc, base + 16 * h, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 + 16 * h : nullptr, part16(v, h));
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh<L, LE>(v, xs);
+    tw_to_natural<L, LE>(v, xs);
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        float sg[16], b[16], xv[16];
+        u16 xn[16];
+        cv16(sv0[h], sg);
+        if (bias) cv16(b0[h], b);
+        cv16(x0[h], xv);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            float a = (v[16 * h + k] * c) * sg[k];
+            if (bias) a = a + b[k];
+            xn[k] = f32_to_bf16(xv[k] + bf16_to_f32(f32_to_bf16(a)));
+            v[16 * h + k] = bf16_to_f32(xn[k]);
+        }
+        c16_store_bf16(xout + row + i0 + 16 * h, true, xn);
+        if (w) part[NP * t + h] = chunk_sumsq(part16(v, h));
+    }
+    if (!w) return;                                                    // uniform
+    __syncthreads();
+    const float ss = tree_total(part, red, N);
+    const float r = 1.f / __builtin_sqrtf(ss / (float)N + eps);
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        float wv[16], sn[16];
+        cv16(w0[h], wv);
+        cv16(su0[h], sn);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[16 * h + k] = bf16_to_f32(f32_to_bf16((v[16 * h + k] * r) * (1.f + wv[k]))) * sn[k];
+    }
+    tw_rotate_quantize<L, LE>(v, xs, red, q, q4, ldq, scale, tok);
+}
+
 // =========================================================================================================== C ABI
 // Threads per row: few rows (latency) -> about one 8-element vector per thread (up to 1024 threads when there are fewer
 // rows than CUs); many rows (throughput) -> four vectors per thread so more rows share a CU. Every row kernel's result is
@@ -986,7 +989,9 @@ static int dsize(int dt) { return dt == TCQ_F32 || dt == TCQ_I32 ? 4 : dt == TCQ
 template <int XD, int YD>
 static void launch_rht_tw(int n, int M, hipStream_t st, const void* x, int ldx, const i8* su, void* y, int ldy) {
     const size_t sh = (size_t)lds_words(n) * sizeof(float);
-    if (n == 4096) launch_k(k_rht_tw<XD, YD, 12, 5>, dim3(M), dim3(128), sh, st, x, ldx, su, y, ldy);
+    if (n == 1024) launch_k(k_rht_tw<XD, YD, 10, 4>, dim3(M), dim3(64), sh, st, x, ldx, su, y, ldy);
+    else if (n == 2048) launch_k(k_rht_tw<XD, YD, 11, 4>, dim3(M), dim3(128), sh, st, x, ldx, su, y, ldy);
+    else if (n == 4096) launch_k(k_rht_tw<XD, YD, 12, 4>, dim3(M), dim3(256), sh, st, x, ldx, su, y, ldy);
     else if (n == 8192) launch_k(k_rht_tw<XD, YD, 13, 5>, dim3(M), dim3(256), sh, st, x, ldx, su, y, ldy);
     else launch_k(k_rht_tw<XD, YD, 14, 5>, dim3(M), dim3(512), sh, st, x, ldx, su, y, ldy);
 }
@@ -1000,8 +1005,8 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
     const int vec = n % 8 == 0 && al16(x) && al16(y) && ((size_t)ldx * dsize(x_dtype)) % 16 == 0 &&
                     ((size_t)ldy * dsize(y_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
-    // register + transpose engine for power-of-two rows of 4096 .. 16384
-    if ((n & (n - 1)) == 0 && n >= 4096 && vec && (!su || al16(su))) {
+    // register + transpose engine for power-of-two rows of 1024 .. 16384
+    if ((n & (n - 1)) == 0 && n >= 1024 && vec && (!su || al16(su))) {
 #define RHT_Y(XD, YD) launch_rht_tw<XD, YD>(n, M, st, x, ldx, (const i8*)su, y, ldy)
 #define RHT_X(XD, _)                                          \
     switch (y_dtype) {                                        \
@@ -1013,22 +1018,6 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
         DISPATCH_X(x_dtype, RHT_X, 0)
 #undef RHT_X
 #undef RHT_Y
-        return launch_status();
-    }
-    // register path for power-of-two rows of 1024 / 2048 (measured on MI355X: 800 x 2048 in 5.8 us against 7.8 on the LDS
-    // engine)
-    if ((n & (n - 1)) == 0 && n >= 1024 && n <= 2048 && vec && (!su || al16(su))) {
-#define RHT_Y(XD, YD) launch_k(k_rht_reg<XD, YD>, grid, dim3(n / 16), (size_t)n * sizeof(float), st, x, ldx, (const i8*)su, y, ldy, n)
-#define RHT_X(XD, _)                                          \
-    switch (y_dtype) {                                        \
-        case TCQ_F32: RHT_Y(XD, TCQ_F32); break;              \
-        case TCQ_BF16: RHT_Y(XD, TCQ_BF16); break;            \
-        case TCQ_F16: RHT_Y(XD, TCQ_F16); break;              \
-        default: return TCQ_ERR_DTYPE;                        \
-    }
-        DISPATCH_X(x_dtype, RHT_X, 0)
-#undef RHT_Y
-#undef RHT_X
         return launch_status();
     }
 #define RHT_Y(XD, YD) launch_k(k_rht<XD, YD>, grid, block, sh, st, x, ldx, (const i8*)su, y, ldy, n, vec)
@@ -1149,35 +1138,26 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
     const int svec = al16(sv) && al16(su);
     hipStream_t st = (hipStream_t)stream;
     const i8 *svp = (const i8*)sv, *sup = (const i8*)su;
-    // register + transpose engine: widths 2^12 .. 2^14 (32 values of each half per thread), aligned
-    if (N >= 4096 && (N & (N - 1)) == 0 && vec && svec && (!q || al16(q))) {
+    // register + transpose engine: power-of-two widths 2^10 .. 2^14 (16 values of each half per thread up to 4096, 32 beyond;
+    // measured on MI355X: 50 x 4096 in 7.5 us against 9.8 with 32 and 11.3 on the register engine), aligned
+    if (N >= 1024 && (N & (N - 1)) == 0 && vec && svec && (!q || al16(q))) {
         const size_t tsh = (size_t)lds_words(N) * sizeof(float);
-#define MID2_TW(L)                                                                                                            \
+#define MID2_TW(L, LE)                                                                                                        \
     switch (acc_dtype) {                                                                                                      \
-        case TCQ_I32: launch_k(k_mid2_tw<TCQ_I32, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+        case TCQ_I32: launch_k(k_mid2_tw<TCQ_I32, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
                                (i8*)q, (int*)q4, ldq, scale); break;                                                          \
-        case TCQ_F32: launch_k(k_mid2_tw<TCQ_F32, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+        case TCQ_F32: launch_k(k_mid2_tw<TCQ_F32, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
                                (i8*)q, (int*)q4, ldq, scale); break;                                                          \
-        case TCQ_BF16: launch_k(k_mid2_tw<TCQ_BF16, L, 5>, grid, dim3(1 << (L - 5)), tsh, st, acc, lda, s, rs, svp, gelu_lut,    \
+        case TCQ_BF16: launch_k(k_mid2_tw<TCQ_BF16, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut,  \
                                 sup, (i8*)q, (int*)q4, ldq, scale); break;                                                    \
         default: return TCQ_ERR_DTYPE;                                                                                        \
     }
-        if (N == 4096) MID2_TW(12)
-        else if (N == 8192) MID2_TW(13)
-        else MID2_TW(14)
+        if (N == 1024) MID2_TW(10, 4)
+        else if (N == 2048) MID2_TW(11, 4)
+        else if (N == 4096) MID2_TW(12, 4)
+        else if (N == 8192) MID2_TW(13, 5)
+        else MID2_TW(14, 5)
 #undef MID2_TW
-        return launch_status();
-    }
-    // register path: power-of-two widths of 1024 .. 8192 (one 16-element chunk of each half per thread), aligned
-    if ((N & (N - 1)) == 0 && N >= 1024 && N <= 8192 && vec && svec && (!q || al16(q))) {
-        const dim3 rb(N / 16);
-        const size_t rsh = (size_t)N * sizeof(float);
-        switch (acc_dtype) {
-            case TCQ_I32: launch_k(k_mid2_reg<TCQ_I32>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
-            case TCQ_F32: launch_k(k_mid2_reg<TCQ_F32>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
-            case TCQ_BF16: launch_k(k_mid2_reg<TCQ_BF16>, grid, rb, rsh, st, acc, lda, s, rs, svp, gelu_lut, sup, (i8*)q, (int*)q4, ldq, scale, N); break;
-            default: return TCQ_ERR_DTYPE;
-        }
         return launch_status();
     }
     switch (acc_dtype) {
@@ -1293,6 +1273,29 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     const int svec = al16(sv) && al16(x) && al16(xout) && (!bias || al16(bias)) && (!w || (al16(w) && al16(su)));
     hipStream_t st = (hipStream_t)stream;
     const u16 *xp = (const u16*)x, *wp = (const u16*)w;
+    // register + transpose engine, 16 values per thread: power-of-two rows of 1024 .. 4096, aligned (measured on MI355X
+    // against the register path: 50 x 1024 5.4 us against 6.9, 1 x 2048 5.7 against 7.5, 800 x 4096 13.7 against 19.5; with
+    // 32 values per thread 2048-wide rows of few tokens run slower than the register path)
+    if ((N == 1024 || N == 2048 || N == 4096) && vec && svec && (!q || al16(q))) {
+        const size_t tsh = (size_t)(lds_words(N) + N / 16) * sizeof(float);
+#define PANT(AD, L, LE) launch_k(k_post_add_norm_pre_tw<AD, L, LE>, dim3(M), dim3(1 << (L - LE)), tsh, st, acc, lda, col0, s, rs, \
+                                 (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale)
+#define PANW(L, LE)                                      \
+    switch (acc_dtype) {                                 \
+        case TCQ_I32: PANT(TCQ_I32, L, LE); break;       \
+        case TCQ_F32: PANT(TCQ_F32, L, LE); break;       \
+        case TCQ_BF16: PANT(TCQ_BF16, L, LE); break;     \
+        default: return TCQ_ERR_DTYPE;                   \
+    }
+        switch (N) {
+            case 1024: PANW(10, 4); break;
+            case 2048: PANW(11, 4); break;
+            default: PANW(12, 4); break;
+        }
+#undef PANW
+#undef PANT
+        return launch_status();
+    }
     // register path: power-of-two rows of 1024 .. 16384 (one 16-element chunk per thread, at least one full wave), aligned
     if ((N & (N - 1)) == 0 && N >= 1024 && vec && svec && (!q || al16(q))) {
 #define PANR(AD) launch_k(k_post_add_norm_pre_reg<AD>, dim3(M), dim3(N / 16), (size_t)N * sizeof(float), st, acc, lda, col0, s, rs, \
