@@ -228,10 +228,12 @@ struct Tw {
     }
 };
 
-// Stores the thread's values of layout X to their row slots in xs / loads them from there.
+// Stores the thread's values of layout X to their row slots in xs / loads them from there. Threads from 2^(L - LE) on (a
+// workgroup wider than the row) hold no values: they skip every access but still meet every barrier of the engine.
 template <int L, int LE, int X>
 __device__ __forceinline__ void tw_put(const float (&v)[1 << LE], float* xs) {
     using W = Tw<L, LE>;
+    if ((int)threadIdx.x >= W::T) return;
     const int b = lds_slot(W::template tpart<X>(threadIdx.x));
 #pragma unroll
     for (int k = 0; k < W::E; ++k) xs[b + lds_slot(W::template kpart<X>(k))] = v[k];
@@ -239,6 +241,7 @@ __device__ __forceinline__ void tw_put(const float (&v)[1 << LE], float* xs) {
 template <int L, int LE, int X>
 __device__ __forceinline__ void tw_get(float (&v)[1 << LE], const float* xs) {
     using W = Tw<L, LE>;
+    if ((int)threadIdx.x >= W::T) return;
     const int b = lds_slot(W::template tpart<X>(threadIdx.x));
 #pragma unroll
     for (int k = 0; k < W::E; ++k) v[k] = xs[b + lds_slot(W::template kpart<X>(k))];
