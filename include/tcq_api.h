@@ -16,7 +16,8 @@
  *   wdev       device layout of the same words made by tcq_repack (see there); required by the fused products
  *   tlut       (512, 2) FP16 table; t8: (512, 2) INT8 table (tcq_format.py:74-77)
  *   row_scale  (m,) FP16; rs: (m,) FP32; su: (n,) int8 +-1; sv: (m,) int8 +-1
- *   q          (M, K) int8 row-major; q4: (K/4, ldq) int32, 4 consecutive inputs per word, token = column
+ *   q          (M, K) int8 row-major; q4: (K/4, ldq) int32, 4 consecutive inputs per word, token = column, or with
+ *              ldq == TCQ_LDQ_TOKEN_BLOCKS the token-block layout (16-byte aligned, K % 16 == 0; defined below)
  */
 #ifndef TCQ_API_H
 #define TCQ_API_H
@@ -39,6 +40,16 @@ enum tcq_status {
 };
 
 enum tcq_dtype { TCQ_F32 = 0, TCQ_BF16 = 1, TCQ_F16 = 2, TCQ_I32 = 3, TCQ_I8 = 4 };
+
+/* Token-block layout of INT8 activations (M tokens, K columns, K % 16 == 0): token t, column k at byte
+ * ((t / 16 * K / 16 + k / 16) * 16 + t % 16) * 16 + k % 16, in a buffer of ceil(M / 16) * 16 * K bytes. 16 columns of 16
+ * tokens form a contiguous 256-byte group, so the small-M products read every activation fragment of 16 tokens x 64
+ * columns as one contiguous KiB (row-major rows make it 16 separate 64-byte pieces). No reference counterpart: it plays the
+ * part of the reference's q4 layout (kernels.py:170-184), the layout the reference's small-M kernels read.
+ * The quantizing entry points write it through their q4 output when ldq == TCQ_LDQ_TOKEN_BLOCKS; tcq_gemm_tcq and
+ * tcq_gemm_w8 read q in it when out_dtype carries TCQ_Q_TOKEN_BLOCKS. */
+#define TCQ_LDQ_TOKEN_BLOCKS (-16)
+#define TCQ_Q_TOKEN_BLOCKS 0x100
 
 /* Library version string and the widest row the block-Walsh kernels take (16384). */
 const char* tcq_version(void);
@@ -198,6 +209,11 @@ int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, con
 int tcq_attend_chunks(int P, int M);
 int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
                int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale, tcq_stream_t stream);
+/* tcq_attend whose prologue also writes the q4 output of the quantizing entry points (q4, ldq as tcq_pre; q8 may then be
+ * NULL), e.g. the token-block layout the small-M product of the output projection reads. No reference counterpart. */
+int tcq_attend_q4(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
+                  int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, int32_t* q4, int ldq, float* scale,
+                  tcq_stream_t stream);
 
 /* -------------------------------------------------------------------------------------------------------- products */
 
@@ -255,7 +271,8 @@ typedef struct tcq_gemm_seg {
 
 /* W2A8 fused decode + product for M <= 64 tokens: acc[t, i] = sum_k q[t, k] * w8[i, k], exact in int32, with w8 = sign *
  * t8[hash(state)] decoded from the words on the fly. out_dtype F32: z = (float(acc) * s[t]) * rs[i]; BF16: its rounding;
- * I32: acc. q (M, K) int8 row-major, s (M,) FP32, K a multiple of 16. segs: HOST array of nseg <= TCQ_MAX_SEGS descriptors
+ * I32: acc. q (M, K) int8 row-major (or in the token-block layout when out_dtype carries TCQ_Q_TOKEN_BLOCKS), s (M,) FP32,
+ * K a multiple of 16. segs: HOST array of nseg <= TCQ_MAX_SEGS descriptors
  * (copied into the launch). Replaces kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673),
  * which takes at most three concatenated layers (q/k/v or gate/up, table chosen by tile-row bounds) and MT <= 10 tokens. */
 int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,

@@ -43,6 +43,7 @@ SIGNATURES = {
     'tcq_gemv_f16_post': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_bf16': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    'tcq_attend_q4': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P, _P],
     'tcq_post_group': [_P, _I, _I, _P, _P, _I, _I, _P],
     'tcq_mid2': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],
     'tcq_mid1': [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P],

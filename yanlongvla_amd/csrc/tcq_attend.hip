@@ -178,7 +178,8 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 constexpr int MAXC = 256;        // most chunks a token may have in the combine (16384 keys)
 constexpr int CT = 1024, CG = CT / AD, CB = 4;   // threads, chunk groups, chunks per group held in registers per batch
 
-__global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, float* scale) {
+__global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4, int ldq,
+                                                     float* scale) {
     extern __shared__ float lds[];
     __shared__ float red[CT / 64];
     __shared__ float wts[AH][MAXC];
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; amx = fmaxf(amx, fabsf(v)); });
     const float sc = token_scale(block_max(amx, red));
     if (threadIdx.x == 0) scale[t] = sc;
-    quantize_row(lds, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
+    quantize_row(lds, sc, q8 ? q8 + (size_t)t * K : nullptr, q4, t, K, ldq);
 }
 
 // grid M, H * 64 threads (one wave per head, H <= 8): lane l of wave h owns dims 4 l .. 4 l + 3 of head h and loads them for
@@ -270,8 +271,8 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
 // chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
 // register engine) and quantized.
 constexpr int CW = 16;
-__global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int H, u16* o, const i8* su, i8* q8,
-                                                        float* scale) {
+__global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4,
+                                                        int ldq, float* scale) {
     extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
@@ -334,15 +335,15 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
     block_walsh(xs, K, [&](int i, float x) { xs[lds_slot(i)] = x; amx = fmaxf(amx, fabsf(x)); });
     const float sc = token_scale(block_max(amx, red));
     if (tid == 0) scale[t] = sc;
-    quantize_row(xs, sc, q8 + (size_t)t * K, nullptr, t, K, 0);
+    quantize_row(xs, sc, q8 ? q8 + (size_t)t * K : nullptr, q4, t, K, ldq);
 }
 
 // grid M, H * 16 threads (H * AD = 1024 or 2048): thread 16 h + g owns dims 16 g .. 16 g + 15 of head h, summed over the
 // chunks straight from the partials; the 16 lanes of head h first merge its chunk statistics (lane = chunk mod 16, a
 // butterfly over the 16 lanes, so every lane holds the same total). With su, the BF16 row goes through the register Walsh
 // engine and the quantizer of the output projection's prologue.
-__global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int NC, int H, u16* o, const i8* su, i8* q8,
-                                                          float* scale) {
+__global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4,
+                                                          int ldq, float* scale) {
     extern __shared__ float xs[];                                        // H * AD floats: cross-wave exchange
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
@@ -424,17 +425,19 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
     const uint4_t sg = gptr((const uint4_t*)(su + h * AD + d0))[0];
 #pragma unroll
     for (int k = 0; k < 16; ++k) v[k] = v[k] * (float)(i8)(sg[k >> 2] >> (8 * (k & 3)));
-    reg_rotate_quantize(v, K, xs, red, q8, nullptr, 0, scale, t);
+    reg_rotate_quantize(v, K, xs, red, q8, q4, ldq, scale, t);
 }
 
 extern "C" int tcq_attend_chunks(int P, int M) { return (P + M + KC - 1) / KC; }
 
-extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
-                          int H, int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale,
-                          tcq_stream_t stream) {
+extern "C" int tcq_attend_q4(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new,
+                             int M, int H, int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, int32_t* q4,
+                             int ldq, float* scale, tcq_stream_t stream) {
     if (!q || !k_new || !v_new || !part || M <= 0 || H <= 0 || P < 0 || (P > 0 && (!k_cache || !v_cache))) return TCQ_ERR_ARG;
     if (!o && !su) return TCQ_ERR_ARG;
-    if (su && (!q8 || !scale)) return TCQ_ERR_ARG;
+    if (su && ((!q8 && !q4) || !scale)) return TCQ_ERR_ARG;
+    if (q4 && ldq != TCQ_LDQ_TOKEN_BLOCKS && ldq < M) return TCQ_ERR_ARG;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && (uintptr_t)q4 % 16) return TCQ_ERR_ALIGN;
     if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
     if ((uintptr_t)k_new % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_new % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)part % 16)
         return TCQ_ERR_ALIGN;
@@ -450,12 +453,18 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
     const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
     if ((!o || (uintptr_t)o % 8 == 0) && (!su || (uintptr_t)su % 4 == 0))
         launch_k(k_attn_combine_w, dim3(M), dim3(H * 64), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part,
-                 NC, H, (u16*)o, (const i8*)su, (i8*)q8, scale);
+                 NC, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     else if ((H == 4 || H == 8) && oal)
         launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC, H,
-                 (u16*)o, (const i8*)su, (i8*)q8, scale);
+                 (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     else
         launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
-                 (u16*)o, (const i8*)su, (i8*)q8, scale);
+                 (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     return launch_status();
+}
+
+extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
+                          int H, int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale,
+                          tcq_stream_t stream) {
+    return tcq_attend_q4(q, k_cache, v_cache, P, k_new, v_new, M, H, D, causal_offset, part, o, su, q8, nullptr, 0, scale, stream);
 }

@@ -284,6 +284,11 @@ __device__ __forceinline__ int q8(float v, float s) {
 }
 __device__ __forceinline__ float token_scale(float amax) { return amax > 0.f ? amax / 127.f : 1.f; }
 
+// Byte offset of token t, column k in the token-block layout of a K-column activation matrix (K % 16 == 0).
+__device__ __forceinline__ size_t tb_offset(int t, int k, int K) {
+    return ((size_t)((t >> 4) * (K >> 4) + (k >> 4)) * 16 + (t & 15)) * 16 + (k & 15);
+}
+
 // Quantize an LDS row (logical indices 0..K-1, K % 4 == 0) with scale s: q (K bytes, row-major) and / or the q4 layout
 // (K/4, ldq) int32 words (4 consecutive inputs per word, token = column), as reference kernels.py:170-184.
 __device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, int* q4, int tok, int K, int ldq) {
@@ -291,7 +296,10 @@ __device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, i
         const u32 word = (u32)(q8(lds[lds_slot(4 * j)], s) & 0xff) | ((u32)(q8(lds[lds_slot(4 * j + 1)], s) & 0xff) << 8) |
                          ((u32)(q8(lds[lds_slot(4 * j + 2)], s) & 0xff) << 16) | ((u32)(q8(lds[lds_slot(4 * j + 3)], s) & 0xff) << 24);
         if (q) ((u32*)q)[j] = word;
-        if (q4) q4[(size_t)j * ldq + tok] = (int)word;
+        if (q4) {
+            if (ldq == TCQ_LDQ_TOKEN_BLOCKS) *(u32*)((i8*)q4 + tb_offset(tok, 4 * j, K)) = word;
+            else q4[(size_t)j * ldq + tok] = (int)word;
+        }
     }
 }
 
@@ -391,7 +399,9 @@ __device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float
         words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
                     ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
     if (q) *gptr((uint4_t*)(q + (size_t)tok * N + 16 * t)) = uint4_t{words[0], words[1], words[2], words[3]};
-    if (q4) {
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) {
+        *gptr((uint4_t*)((i8*)q4 + tb_offset(tok, 16 * t, N))) = uint4_t{words[0], words[1], words[2], words[3]};
+    } else if (q4) {
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) q4[(size_t)(4 * t + k4) * ldq + tok] = (int)words[k4];
     }
@@ -430,7 +440,12 @@ __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* x
             *gptr((uint4_t*)(q + (size_t)tok * N + E * t + 16 * h)) =
                 uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
     }
-    if (q4) {
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h)
+            *gptr((uint4_t*)((i8*)q4 + tb_offset(tok, E * t + 16 * h, N))) =
+                uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+    } else if (q4) {
 #pragma unroll
         for (int k4 = 0; k4 < E / 4; ++k4) q4[(size_t)((E / 4) * t + k4) * ldq + tok] = (int)words[k4];
     }

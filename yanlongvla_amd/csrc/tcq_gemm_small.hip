@@ -45,7 +45,7 @@ struct SegPack {
 // grid (tile-row groups of the largest segment, segments), NW = blockDim.x / 64 waves; a workgroup takes TR consecutive tile
 // rows (the activation fragments of its chunks, the bulk of the loads, then serve TR rows). MODE 0: decode from tcq_repack
 // words; MODE 1: resident INT8 weights. ODT: output dtype (F32 scaled, BF16 scaled, I32 accumulators).
-template <int MODE, int NB, int ODT, int TR>
+template <int MODE, int NB, int ODT, int TR, bool QB>
 __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     rsrc_t Wr;
     if (MODE == 0) Wr = make_rsrc(S.w, (u32)(tiles_m * nch) << 10);
     else Wr = make_rsrc(S.w, (u32)S.m * (u32)K);
-    const rsrc_t Q = make_rsrc(q, (u32)M * (u32)K);
+    const rsrc_t Q = make_rsrc(q, QB ? (u32)((M + 15) >> 4) * 16u * (u32)K : (u32)M * (u32)K);   // QB: token-block layout
 
     uint4_t wa[TR][MODE == 0 ? 1 : 4];
     int4v B[4][NB];
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const int t = 16 * b + lr, k = 256 * c + 64 * j + 16 * lg;
-                const u32 off = (t < M && k < K) ? (u32)t * (u32)K + (u32)k : RSRC_OOB;
+                const u32 off = (t < M && k < K) ? (QB ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
                 B[j][b] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
             }
     };
@@ -182,27 +182,35 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 }
 
 // =========================================================================================================== C ABI
-template <int MODE, int NB, int TR>
+template <int MODE, int NB, int TR, bool QB>
 static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                             int ldo, int odt) {
     switch (odt) {
-        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
     }
+}
+template <int MODE, int TR, bool QB>
+static void launch_small_qb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                            int ldo, int odt) {
+    if (M <= 16) launch_small_nb<MODE, 1, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
+    else if (M <= 32) launch_small_nb<MODE, 2, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
+    else launch_small_nb<MODE, 4, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
 }
 template <int MODE, int TR>
 static void launch_small_tr(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
-                            int ldo, int odt) {
-    if (M <= 16) launch_small_nb<MODE, 1, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
-    else if (M <= 32) launch_small_nb<MODE, 2, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
-    else launch_small_nb<MODE, 4, TR>(grid, block, st, P, q, s, M, K, ldo, odt);
+                            int ldo, int odt, bool qb) {
+    if (qb) launch_small_qb<MODE, TR, true>(grid, block, st, P, q, s, M, K, ldo, odt);
+    else launch_small_qb<MODE, TR, false>(grid, block, st, P, q, s, M, K, ldo, odt);
 }
 
 template <int MODE>
 static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int odt, int ldo,
                       tcq_stream_t stream) {
     if (!segs || !q || nseg <= 0 || M <= 0 || K <= 0 || ldo <= 0) return TCQ_ERR_ARG;
+    const bool qb = odt & TCQ_Q_TOKEN_BLOCKS;                          // q in the token-block layout
+    odt &= ~TCQ_Q_TOKEN_BLOCKS;
     if (odt != TCQ_F32 && odt != TCQ_BF16 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (odt != TCQ_I32 && !s) return TCQ_ERR_ARG;
     if (nseg > TCQ_MAX_SEGS || M > 64) return TCQ_ERR_UNSUPPORTED;
@@ -235,8 +243,8 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     }
     pairs = pairs && tiles >= 384;
     const dim3 block(64 * nw);
-    if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt);
-    else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt);
+    if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
+    else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
     return launch_status();
 }
 

@@ -1044,6 +1044,9 @@ static int row_threads(int M, int K) {
 static size_t row_lds(int K) { return (size_t)lds_words(K) * sizeof(float); }
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
+// q4 output: the (K / 4, ldq >= M) word layout, or the token-block layout (ldq == TCQ_LDQ_TOKEN_BLOCKS)
+static bool q4_bad(const void* q4, int ldq, int M) { return q4 && ldq != TCQ_LDQ_TOKEN_BLOCKS && ldq < M; }
+static bool q4_tb_shape_bad(const void* q4, int ldq, int K) { return q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && K % 16; }
 static int dsize(int dt) { return dt == TCQ_F32 || dt == TCQ_I32 ? 4 : dt == TCQ_I8 ? 1 : 2; }
 
 #define DISPATCH_X(dt, KERNEL, ...)                                                             \
@@ -1102,8 +1105,10 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
 
 extern "C" int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
                        tcq_stream_t stream) {
-    if (!x || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
+    if (!x || !scale || (!q && !q4) || M <= 0 || K <= 0 || q4_bad(q4, ldq, M)) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, K)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const dim3 grid(M), block(row_threads(M, K));
     const size_t sh = row_lds(K);
     const int vec = K % 8 == 0 && al16(x) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
@@ -1198,10 +1203,12 @@ extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, cons
 extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv,
                         const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
                         tcq_stream_t stream) {
-    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < 2 * N || (q4 && ldq < M))
+    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < 2 * N || q4_bad(q4, ldq, M))
         return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
     if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, N)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N) + (size_t)N * 2;
     const int asz = dsize(acc_dtype);
@@ -1243,10 +1250,12 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
 extern "C" int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s, const float* rs, const int8_t* sv, const float* bias,
                         const uint16_t* gelu_lut, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
                         tcq_stream_t stream) {
-    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < N || (q4 && ldq < M))
+    if (!acc || !sv || !gelu_lut || !su || !scale || (!q && !q4) || M <= 0 || N <= 0 || lda < N || q4_bad(q4, ldq, M))
         return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
     if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, N)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N);
     const int asz = dsize(acc_dtype);
@@ -1265,8 +1274,10 @@ extern "C" int tcq_mid1(const void* acc, int acc_dtype, int lda, const float* s,
 
 extern "C" int tcq_pre2(const void* g, const void* u, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
                         tcq_stream_t stream) {
-    if (!g || !u || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
+    if (!g || !u || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || q4_bad(q4, ldq, M)) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, K)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const int vec = K % 8 == 0 && al16(g) && al16(u) && al16(su);
     launch_k(k_pre2, dim3(M), dim3(row_threads(M, K)), row_lds(K), (hipStream_t)stream, (const u16*)g, (const u16*)u, (const i8*)su,
              (i8*)q, (int*)q4, ldq, scale, K, vec);
@@ -1328,8 +1339,10 @@ extern "C" int tcq_rmsnorm(const void* x, const void* w, float eps, void* y, int
 
 extern "C" int tcq_norm_pre(const void* x, const void* w, float eps, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale,
                             int M, int K, tcq_stream_t stream) {
-    if (!x || !w || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || (q4 && ldq < M)) return TCQ_ERR_ARG;
+    if (!x || !w || !su || !scale || (!q && !q4) || M <= 0 || K <= 0 || q4_bad(q4, ldq, M)) return TCQ_ERR_ARG;
     if (K % 16 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, K)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const int vec = al16(x) && al16(w) && al16(su);
     launch_k(k_norm_pre, dim3(M), dim3(row_threads(M, K)), norm_lds(K), (hipStream_t)stream, (const u16*)x, (const u16*)w, eps,
              (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec);
@@ -1342,8 +1355,10 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
                                      tcq_stream_t stream) {
     if (!acc || !sv || !x || !xout || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
-    if (w && (!su || !scale || (!q && !q4) || (q4 && ldq < M))) return TCQ_ERR_ARG;
+    if (w && (!su || !scale || (!q && !q4) || q4_bad(q4, ldq, M))) return TCQ_ERR_ARG;
     if (N % 16 || N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (q4_tb_shape_bad(q4, ldq, N)) return TCQ_ERR_SHAPE;
+    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS && !al16(q4)) return TCQ_ERR_ALIGN;
     const int asz = dsize(acc_dtype);
     const int vec = al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && (!rs || al16(rs));
     const int svec = al16(sv) && al16(x) && al16(xout) && (!bias || al16(bias)) && (!w || (al16(w) && al16(su)));

@@ -83,12 +83,12 @@ class GemmaAttention(nn.Module):
         vv = v if cache_v is None else torch.cat([cache_v, v.to(cache_v.dtype)], 0)
         return attend(q, kk, vv, self.heads, causal_offset).to(q.dtype)
 
-    def core_quantized(self, q, k, v, cache_k, cache_v, causal_offset, su, q8, scale):
-        """core followed by the rotate + quantize prologue of o_proj (signs su) in the same launches: q8 / scale of the
-        BF16 attention output, which itself is not stored. Device tensors only."""
+    def core_quantized(self, q, k, v, cache_k, cache_v, causal_offset, su, q8, scale, q4=None):
+        """core followed by the rotate + quantize prologue of o_proj (signs su) in the same launches: q8 (row-major) and / or
+        q4 (token blocks) and scale of the BF16 attention output, which itself is not stored. Device tensors only."""
         from . import kernels
         kernels.attend(q.contiguous(), cache_k, cache_v, k.contiguous(), v.contiguous(), self.heads, causal_offset, su=su,
-                       q8=q8, scale=scale)
+                       q8=q8, scale=scale, q4=q4)
 
     def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
         """x (M, width) -> (o_proj output, this call's k, v)."""

@@ -21,6 +21,23 @@ def _contig(*ts):
             raise ValueError('tensors passed to the TCQ kernels must be contiguous')
 
 
+# Token-block layout of INT8 activations (include/tcq_api.h): a (ceil(M / 16), K / 16, 16, 16) int8 tensor, element
+# [b, g, r, c] = token 16 b + r, column 16 g + c. The quantizers write it through q4 (ldq = LDQ_TOKEN_BLOCKS) and the
+# small-M products read it (out_dtype | Q_TOKEN_BLOCKS): every 16-token x 64-column activation fragment is one contiguous KiB.
+LDQ_TOKEN_BLOCKS = -16
+Q_TOKEN_BLOCKS = 0x100
+
+
+def token_blocks(M, K, device):
+    """An uninitialised token-block activation buffer for M tokens of K columns (K % 16 == 0)."""
+    return torch.empty((M + 15) // 16, K // 16, 16, 16, dtype=torch.int8, device=device)
+
+
+def rows_of_token_blocks(tb, M):
+    """The (M, K) row-major view of a token-block tensor (a copy)."""
+    return tb.permute(0, 2, 1, 3).reshape(tb.shape[0] * 16, tb.shape[1] * 16)[:M]
+
+
 # ------------------------------------------------------------------------------------------------------------- load time
 def _groups(table):
     """Number of (512, 2) tables in a table tensor: (512, 2) -> 1, (G, 512, 2) -> G (row-group tables)."""
@@ -89,11 +106,11 @@ def rht(x, su, y):
 
 
 def pre(x, su, q=None, q4=None, scale=None):
-    """x (M, K) BF16 / FP32 / FP16 contiguous -> q (M, K) int8 and / or q4 (K/4, ld) int32, scale (M,) FP32
+    """x (M, K) BF16 / FP32 / FP16 contiguous -> q (M, K) int8 and / or q4 (K/4, ld) int32 or token blocks, scale (M,) FP32
     (reference kernels.py:602-606)."""
     M, K = x.shape
     _contig(x, su, q, q4, scale)
-    call('tcq_pre', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(q), ptr(q4), 0 if q4 is None else q4.shape[1], ptr(scale),
+    call('tcq_pre', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale),
          M, K, stream())
 
 
@@ -122,7 +139,8 @@ def post(acc, s, rs, sv, bias, y, col0=0):
 
 # ----------------------------------------------------------------------------------------------------------- MLP middles
 def _ldq(q4):
-    return 0 if q4 is None else q4.shape[1]
+    """ldq of a q4 output: the column count of a (K / 4, ldq) word tensor, LDQ_TOKEN_BLOCKS for a token-block tensor."""
+    return 0 if q4 is None else LDQ_TOKEN_BLOCKS if q4.dim() == 4 else q4.shape[1]
 
 
 def mid2(acc, s, rs, sv, su, q=None, q4=None, scale=None, gelu_lut=None):
@@ -188,20 +206,22 @@ def post_add_norm_pre(acc, s, rs, sv, bias, x, xout, w=None, eps=0.0, su=None, q
 
 
 # ------------------------------------------------------------------------------------------------------------- attention
-def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None, su=None, q8=None, scale=None):
+def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None, su=None, q8=None, scale=None, q4=None):
     """Multi-query attention (H <= 8 heads, head dim 256), BF16: keys / values = cache rows (or None) then the new rows.
-    Writes o (M, H * 256) BF16 and / or, with su, q8 / scale of the rotate + quantize prologue of the next projection."""
+    Writes o (M, H * 256) BF16 and / or, with su, q8 / q4 / scale of the rotate + quantize prologue of the next projection
+    (q4 as in pre: word layout or token blocks)."""
     M = q.shape[0]
     P = 0 if k_cache is None else k_cache.shape[0]
     for t in (q, k_cache, v_cache, k_new, v_new, o):
         if t is not None and t.dtype != torch.bfloat16:
             raise TypeError('attend: BF16 tensors only')
-    _contig(q, k_cache, v_cache, k_new, v_new, o, su, q8, scale)
+    _contig(q, k_cache, v_cache, k_new, v_new, o, su, q8, q4, scale)
     D = k_new.shape[1]
     nc = int(_lib.lib().tcq_attend_chunks(P, M))
     part = torch.empty(M * nc * heads * (D + 4), dtype=torch.float32, device=q.device)
-    call('tcq_attend', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, D,
-         -1 if causal_offset is None else int(causal_offset), ptr(part), ptr(o), ptr(su), ptr(q8), ptr(scale), stream())
+    call('tcq_attend_q4', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, D,
+         -1 if causal_offset is None else int(causal_offset), ptr(part), ptr(o), ptr(su), ptr(q8), ptr(q4), _ldq(q4), ptr(scale),
+         stream())
     return o
 
 
@@ -342,8 +362,12 @@ class SmallProduct:
         self.fn = getattr(_lib.lib(), self.name)
 
     def __call__(self, q, s):
-        M, K = q.shape
-        rc = self.fn(self.arr, self.n, q.data_ptr(), None if s is None else s.data_ptr(), M, K, self.odt, self.ldo, stream())
+        """q (M, K) row-major, or a token-block tensor (M = s.numel() tokens; s is then required)."""
+        if q.dim() == 4:
+            M, K, odt = s.numel(), q.shape[1] * 16, self.odt | Q_TOKEN_BLOCKS
+        else:
+            (M, K), odt = q.shape, self.odt
+        rc = self.fn(self.arr, self.n, q.data_ptr(), None if s is None else s.data_ptr(), M, K, odt, self.ldo, stream())
         if rc:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 

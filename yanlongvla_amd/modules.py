@@ -102,19 +102,23 @@ class Group:
         return x2
 
     def buffers(self, M, dev):
-        """Quantized activations (M, K) row-major and the per-token scales."""
-        return dict(q=torch.empty(M, self.K, dtype=torch.int8, device=dev), scale=torch.empty(M, dtype=torch.float32, device=dev))
+        """Quantized activations and the per-token scales: up to SMALL_M tokens in the token-block layout the small-M products
+        read fastest (q4), else (M, K) row-major (q)."""
+        scale = torch.empty(M, dtype=torch.float32, device=dev)
+        if M <= SMALL_M and self.K % 16 == 0:
+            return dict(q=None, q4=kernels.token_blocks(M, self.K, dev), scale=scale)
+        return dict(q=torch.empty(M, self.K, dtype=torch.int8, device=dev), q4=None, scale=scale)
 
     def quantize(self, x2):
         b = self.buffers(x2.shape[0], x2.device)
-        kernels.pre(x2, self.su, q=b['q'], scale=b['scale'])
+        kernels.pre(x2, self.su, q=b['q'], q4=b['q4'], scale=b['scale'])
         return b
 
     def product(self, b):
         """INT8 activations -> FP32 z = (float(acc) * s) * rs (M, Ntot) of the exact int32 product acc: few tokens on the
         fused decode products, many tokens on the INT8 MFMA GEMM with the scaling in its epilogue (the order of tcq_post)."""
-        q, dev = b['q'], b['q'].device
-        M = q.shape[0]
+        q = b['q'] if b['q'] is not None else b['q4']
+        M, dev = b['scale'].numel(), q.device
         if M <= SMALL_M:
             z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
             if self.W is not None:
@@ -215,10 +219,10 @@ class KGatedMLP(torch.nn.Module):
                     (acc, gu.col0[1], None if scaled else gu.rs_parts[1], gu.sv_parts[1], None, u, False)]
             kernels.post_group(segs, acc.dtype, torch.bfloat16, None if scaled else b['scale'], M,
                                gelu_lut=kernels.gelu_table(dev))
-            kernels.pre2(g, u, down.su, q=b2['q'], scale=b2['scale'])
+            kernels.pre2(g, u, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
         else:
             kernels.mid2(acc, None if scaled else b['scale'], None if scaled else gu.rs, gu.sv, down.su, q=b2['q'],
-                         scale=b2['scale'])
+                         q4=b2['q4'], scale=b2['scale'])
         STATS['fused_mlps'] += 1
         return down.posts(down.product(b2), b2, x.shape)[0]
 
@@ -238,7 +242,7 @@ class KPlainMLP(torch.nn.Module):
         b2 = g2.buffers(acc.shape[0], acc.device)
         scaled = acc.dtype == torch.float32
         kernels.mid1(acc, None if scaled else b['scale'], None if scaled else g1.rs, g1.sv, g1.bias, g2.su, q=b2['q'],
-                     scale=b2['scale'])
+                     q4=b2['q4'], scale=b2['scale'])
         STATS['fused_mlps'] += 1
         return g2.posts(g2.product(b2), b2, x.shape)[0]
 
@@ -290,13 +294,13 @@ class KDecoderLayer(torch.nn.Module):
         b = self._prologue(x, x2)
         if b is None:
             b = qkv.buffers(M, dev)
-            kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], scale=b['scale'])
+            kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], q4=b['q4'], scale=b['scale'])
         else:
             STATS['chained_prologues'] += 1
         q, k, v = qkv.posts(qkv.product(b), b, x2.shape)
         if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
             b2 = og.buffers(M, dev)
-            self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'])
+            self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
         else:
             b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
         z = og.product(b2)
@@ -304,11 +308,11 @@ class KDecoderLayer(torch.nn.Module):
         b3 = gu.buffers(M, dev)
         sc = z.dtype == torch.float32
         kernels.post_add_norm_pre(z, None if sc else b2['scale'], None if sc else og.rs, og.sv, og.bias, x2, x3, n2.weight, n2.eps,
-                                  gu.su, q=b3['q'], scale=b3['scale'])
+                                  gu.su, q=b3['q'], q4=b3['q4'], scale=b3['scale'])
         acc = gu.product(b3)
         b4 = dn.buffers(M, dev)
         sc = acc.dtype == torch.float32
-        kernels.mid2(acc, None if sc else b3['scale'], None if sc else gu.rs, gu.sv, dn.su, q=b4['q'], scale=b4['scale'])
+        kernels.mid2(acc, None if sc else b3['scale'], None if sc else gu.rs, gu.sv, dn.su, q=b4['q'], q4=b4['q4'], scale=b4['scale'])
         z4 = dn.product(b4)
         x4 = torch.empty_like(x2)
         sc = z4.dtype == torch.float32
@@ -319,7 +323,7 @@ class KDecoderLayer(torch.nn.Module):
             nq, nn1 = nxt.groups[0], nxt.input_layernorm
             bn = nq.buffers(M, dev)
             kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4,
-                                      nn1.weight, nn1.eps, nq.su, q=bn['q'], scale=bn['scale'])
+                                      nn1.weight, nn1.eps, nq.su, q=bn['q'], q4=bn['q4'], scale=bn['scale'])
         out = x4.reshape(shape)
         if nxt is not None:
             nxt._handoff = (x4, None if x4.is_inference() else x4._version, out, bn)
