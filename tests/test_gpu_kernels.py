@@ -411,7 +411,11 @@ def _small_product_case(shapes, M, seed):
 @pytest.mark.parametrize('shapes,M', [([(2048, 1024)], 1), ([(2048, 1024), (256, 1024), (256, 1024)], 50),
                                       ([(1024, 2048)], 16), ([(4096, 1024), (4096, 1024)], 17), ([(1024, 4096)], 64),
                                       ([(64, 1152)], 33), ([(48, 80), (32, 80)], 5), ([(256, 16384)], 10),
-                                      ([(4112, 1024), (2048, 1024)], 50)])
+                                      ([(4112, 1024), (2048, 1024)], 50),
+                                      # streaming plan of the fused product (one token block, >= 4096 chunks): 16, 4, 2 and 1
+                                      # waves per tile row
+                                      ([(2048, 16384)], 1), ([(16384, 2048)], 16), ([(8192, 2048)] * 4, 1),
+                                      ([(65536, 1024)], 1)])
 def test_gemm_tcq_and_w8_bitexact(shapes, M):
     """Fused decode + INT8 product and the INT8-resident product against the oracle, FP32 bits equal (exact int32 sums)."""
     from yanlongvla_amd import kernels as K
@@ -442,6 +446,24 @@ def test_gemm_tcq_and_w8_bitexact(shapes, M):
     yb = torch.empty(M, ldz, dtype=torch.bfloat16, device=DEV)
     K.gemm_w8([(w, None, rs, yb[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
+
+
+@pytest.mark.parametrize('G,M', [(8, 1), (4, 9)])
+def test_gemm_tcq_streaming_row_group_tables(G, M):
+    """The streaming plan of the fused product (one token block, 2048 x 16384: 8192 chunks) with (G, 512, 2) row-group
+    tables: every workgroup's rows read their group's table; FP32 bits equal the oracle's."""
+    from yanlongvla_amd import kernels as K
+    m, n = 2048, 16384
+    L = O.random_layer(m, n, 70 + G, groups=G)
+    d = dev_layer(L)
+    t8, rs, _ = K.snap(d['tlut'], d['row_scale'])
+    rng = np.random.default_rng(G + M)
+    q = rng.integers(-127, 128, size=(M, n)).astype(np.int8)
+    s = (rng.random(M) * 0.02 + 1e-3).astype(np.float32)
+    ref = (O.int_matmul(q, L.w8_reference()).astype(np.float32) * s[:, None]) * L.rs[None, :]
+    z = torch.full((M, m), float('nan'), device=DEV)
+    K.gemm_tcq([(K.repack(d['bits'], m, n), t8, rs, z)], T(q), T(s), m)
+    assert np.array_equal(bits_of(z), ref.view(np.uint32))
 
 
 def test_gemm_small_rejects_bad_sizes():

@@ -6,8 +6,8 @@
 // columns of tile 16 c + 4 j + g (exactly one decoded tile row per lane); B = activations, lane (g, t) = token t of the
 // token block, the same 16 columns; D: lane (g, t) holds rows 4 g .. 4 g + 3 of token t.
 // A from the trellis words: the window layout of tcq_repack (one dwordx4 per lane per tile row and chunk), 8 lookups of
-// INT8 pairs in a sign-folded LDS table (1024 entries x 16 copies, one 4-byte slot each, lane l reads copy l mod 16), packed
-// into the 16 A bytes. A from resident INT8 weights: one 16-byte load per lane per (tile row, j).
+// INT8 pairs in a sign-folded LDS table (1024 entries x SM_C copies, one 4-byte slot each, lane l reads copy l mod SM_C),
+// packed into the 16 A bytes. A from resident INT8 weights: one 16-byte load per lane per (tile row, j).
 // Work split (few tokens = little work per layer, so the launch is latency-bound): a workgroup takes one tile row (16 output
 // rows) of one segment and its waves split K, one 256-column chunk each (up to 16 waves; wave w takes chunks w, w + NW, ...
 // beyond 16 chunks). Every wave issues the loads of its words / weights and of its activation fragments (16 bytes of each
@@ -181,6 +181,118 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     }
 }
 
+// Streaming plan of the fused decode for one token block (M <= 16) and large layers (the backbone's gate/up and down
+// products at one token: 8.5 and 8.3 us on MI355X against 10.0 and 10.4 on the workgroup plan): a workgroup takes
+// RPW = NW / WPR tile rows, WPR waves per tile row, and wave p of a row takes its chunks p, p + WPR, ... (at most CMAX).
+// Every chunk's words are loaded at entry (they come from HBM); the activation fragments (L2-resident) one chunk ahead.
+// The table has 16 copies (lane l reads copy l mod 16: two lanes per copy in a half-wave), filled once per workgroup. The
+// WPR partial sums of a row are added through LDS, over the table, once every wave has finished its lookups (exact int32).
+constexpr int GV_C = 16;
+constexpr int GV_CMAX = 8;
+constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table fill per 16 waves)
+
+template <int ODT, bool QB, int WPR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
+    constexpr int RPW = NW / WPR;
+    __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
+    const tcq_gemm_seg S = P.s[blockIdx.y];
+    const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
+    const int I0 = blockIdx.x * RPW;
+    if (I0 >= tiles_m) return;                                            // uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int slot = wave / WPR, part = wave % WPR;
+    const int I = min(I0 + slot, tiles_m - 1);                            // a row past the end decodes the last (never stored)
+    const int lr = lane & 15, lg = lane >> 4;
+    const u32 cp4 = (u32)(lane & (GV_C - 1)) << 2;
+    const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch) << 10);
+    const rsrc_t Q = make_rsrc(q, QB ? 16u * (u32)K : (u32)M * (u32)K);
+    uint4_t wa[GV_CMAX];
+#pragma unroll
+    for (int i = 0; i < GV_CMAX; ++i) {
+        const int c = part + WPR * i;
+        if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
+    }
+    auto loadB = [&](int c, int4v* B) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 256 * c + 64 * j + 16 * lg;
+            const u32 off = (lr < M && k < K) ? (QB ? (u32)tb_offset(lr, k, K) : (u32)lr * (u32)K + (u32)k) : RSRC_OOB;
+            B[j] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
+        }
+    };
+    int4v Bf[2][4];                                                        // activation fragments, two chunks in turn
+    loadB(part, Bf[0]);
+    float4_t rsv = float4_t{0.f, 0.f, 0.f, 0.f};
+    float sv = 0.f;
+    if (ODT != TCQ_I32 && part == 0) {
+        rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
+        sv = gptr(s)[min(lr, M - 1)];
+    }
+    {
+        const i8* t8 = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
+        for (int e = threadIdx.x; e < 1024; e += 64 * NW) {
+            const int h = e & 511;
+            int v0 = gptr(t8)[2 * h];
+            const int v1 = gptr(t8)[2 * h + 1];
+            if (e >> 9) v0 = -v0;
+            const u32 v = (u32)(v0 & 0xff) | ((u32)(v1 & 0xff) << 8);
+            const u32 vv = v | (v << 16);
+#pragma unroll
+            for (int c = 0; c < GV_C; c += 4) *(uint4_t*)(tab + e * GV_C + c) = uint4_t{vv, vv, vv, vv};
+        }
+    }
+    __syncthreads();
+    int4v acc = int4v{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < GV_CMAX; ++i) {
+        const int c = part + WPR * i;
+        if (c >= nch) continue;                                            // uniform
+        if (i + 1 < GV_CMAX && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32 hi = wa[i][j];
+            const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+            u16x2_t a[4];                                                  // pairs p (a[0], a[1]) and p + 4 (a[2], a[3])
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                a[p >> 1][p & 1] = *(const u16*)((const char*)tab + (((x >> 22) << 6) | cp4));
+                a[2 + (p >> 1)][p & 1] = *(const u16*)((const char*)tab + ((x & 0xFFC0u) | cp4));
+            }
+            const int4v A = int4v{__builtin_bit_cast(int, a[0]), __builtin_bit_cast(int, a[1]), __builtin_bit_cast(int, a[2]),
+                                  __builtin_bit_cast(int, a[3])};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bf[i & 1][j], acc, 0, 0, 0);
+        }
+    }
+    if constexpr (WPR > 1) {
+        int4v* red = (int4v*)tab;                                          // the table is dead once every wave is past here
+        __syncthreads();
+        if (part > 0) red[((slot * (WPR - 1)) + part - 1) * 64 + lane] = acc;
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int w = 0; w < WPR - 1; ++w) acc += red[(slot * (WPR - 1) + w) * 64 + lane];
+    }
+    if (I0 + slot >= tiles_m) return;
+    const int t = lr;
+    if (t >= M) return;
+    const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
+    if (ODT == TCQ_I32) {
+        *gptr((int4v*)((int*)S.out + o)) = acc;
+    } else {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = ((float)acc[e] * sv) * rsv[e];
+        if (ODT == TCQ_F32) {
+            *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
+        } else {
+            const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
+            const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
+            *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
+        }
+    }
+}
+
 // =========================================================================================================== C ABI
 template <int MODE, int NB, int TR, bool QB>
 static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
@@ -203,6 +315,44 @@ static void launch_small_tr(dim3 grid, dim3 block, hipStream_t st, const SegPack
                             int ldo, int odt, bool qb) {
     if (qb) launch_small_qb<MODE, TR, true>(grid, block, st, P, q, s, M, K, ldo, odt);
     else launch_small_qb<MODE, TR, false>(grid, block, st, P, q, s, M, K, ldo, odt);
+}
+
+template <int ODT, bool QB>
+static void launch_gv(int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                      int ldo) {
+    const int rpw = GV_NW / wpr;
+    const dim3 grid((rows + rpw - 1) / rpw, nseg), block(64 * GV_NW);
+    switch (wpr) {
+        case 1: launch_k(k_gemv_tcq<ODT, QB, 1, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 2: launch_k(k_gemv_tcq<ODT, QB, 2, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 4: launch_k(k_gemv_tcq<ODT, QB, 4, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 8: launch_k(k_gemv_tcq<ODT, QB, 8, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemv_tcq<ODT, QB, 16, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+    }
+}
+
+template <bool QB>
+static void launch_gv_odt(int odt, int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s,
+                          int M, int K, int ldo) {
+    switch (odt) {
+        case TCQ_F32: launch_gv<TCQ_F32, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+        case TCQ_BF16: launch_gv<TCQ_BF16, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+        default: launch_gv<TCQ_I32, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+    }
+}
+
+// Waves per tile row of the streaming plan for a fused decode of `tiles` tile rows (all segments) of nch chunks, or 0 when
+// the workgroup plan serves it: at most GV_CMAX chunks per wave, and enough waves to cover the chip (4096) where the rows
+// allow; row-group tables must hold whole workgroups.
+static int gv_waves_per_row(const tcq_gemm_seg* segs, int nseg, int M, int nch, int tiles) {
+    if (M > 16 || (size_t)tiles * nch < 4096 || nch > 16 * GV_CMAX) return 0;
+    int wpr = 1;
+    while (wpr < 16 && (wpr * GV_CMAX < nch || tiles * wpr < 4096)) wpr *= 2;
+    while (wpr > 1 && (wpr / 2) >= nch) wpr /= 2;
+    const int rpw = GV_NW / wpr;
+    for (int i = 0; i < nseg; ++i)
+        if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % rpw) return 0;
+    return wpr;
 }
 
 template <int MODE>
@@ -242,6 +392,14 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
         if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
     }
     pairs = pairs && tiles >= 384;
+    if (MODE == 0) {
+        const int wpr = gv_waves_per_row(segs, nseg, M, nch, tiles);
+        if (wpr > 0) {
+            if (qb) launch_gv_odt<true>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            else launch_gv_odt<false>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            return launch_status();
+        }
+    }
     const dim3 block(64 * nw);
     if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
     else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
