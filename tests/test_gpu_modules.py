@@ -194,6 +194,33 @@ def test_chained_prologues_bitexact(part):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize('runtime', ['reference', 'fly', 'resident'])
+def test_kv_cache_decode_matches_concatenation(runtime):
+    """Decode steps on a KVCache (the new rows written in place: by the q/k/v epilogue on the fused layers, by a copy on
+    the reference runtime's) give the hidden states and key / value rows of decode_step's concatenated caches bit for bit;
+    a rewound cache replays the same steps, and a full cache refuses another row."""
+    from yanlongvla_amd import gemma, modules
+    model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=2, vocab=512)
+    modules.install(model, runtime=runtime, layers=gemma.synthetic_layers(model, 14, DEV))
+    x = torch.randn(70, 2048, generator=torch.Generator(device=DEV).manual_seed(8), device=DEV).bfloat16()
+    with torch.inference_mode():
+        _, ks, vs = model.prefill(x)
+        cache = gemma.KVCache(ks, vs, 3)
+        ref = []
+        for t in range(3):
+            h, ks, vs = model.decode_step(x[t:t + 1], ks, vs)
+            ref.append(h)
+        for _ in range(2):
+            cache.rewind()
+            got = [model.decode_step_cached(x[t:t + 1], cache) for t in range(3)]
+            assert all(torch.equal(a, b) for a, b in zip(got, ref))
+            assert cache.length == 73
+            for i in range(2):
+                assert torch.equal(cache.k[i], ks[i]) and torch.equal(cache.v[i], vs[i])
+        with pytest.raises(RuntimeError):
+            model.decode_step_cached(x[:1], cache)
+
+
 def test_load_from_packed_file(tmp_path):
     from yanlongvla_amd import gemma, modules
     from yanlongvla_amd import tcq_format as F

@@ -104,9 +104,14 @@ class GemmaDecoderLayer(nn.Module):
         self.post_attention_layernorm = GemmaRMSNorm(width)
         self.mlp = GemmaMLP(width, hidden)
 
-    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
+    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None, kv_out=None):
+        """kv_out: None, or (k, v) tensors this call's keys / values are copied into (then returned in their place)."""
         a, k, v = self.self_attn(self.input_layernorm(x), cache_k, cache_v, causal_offset)
         x = x + a
+        if kv_out is not None:
+            kv_out[0].copy_(k)
+            kv_out[1].copy_(v)
+            k, v = kv_out
         return x + self.mlp(self.post_attention_layernorm(x)), k, v
 
 
@@ -119,6 +124,30 @@ class GemmaStack(nn.Module):
 
 class _Node(nn.Module):
     pass
+
+
+class KVCache:
+    """Per-layer key / value rows of a decoder stack in buffers with room for `room` more rows: a decode step writes its
+    row in place (the layers' kv_out) instead of concatenating the whole cache, so the rows already there are never
+    copied again. rewind() returns to the rows given at construction (the prefill's)."""
+
+    def __init__(self, ks, vs, room):
+        self.base = self.length = ks[0].shape[0]
+        cap = self.base + room
+        self.k = [torch.empty(cap, k.shape[1], dtype=k.dtype, device=k.device) for k in ks]
+        self.v = [torch.empty(cap, v.shape[1], dtype=v.dtype, device=v.device) for v in vs]
+        for dst, src in zip(self.k + self.v, list(ks) + list(vs)):
+            dst[:self.base].copy_(src)
+
+    def rewind(self):
+        self.length = self.base
+
+    def rows(self, i):
+        """Layer i's cache rows so far and the destination views of the next row: (k, v, (k_next, v_next))."""
+        P = self.length
+        if P >= self.k[i].shape[0]:
+            raise RuntimeError(f'KV cache full ({P} rows)')
+        return self.k[i][:P], self.v[i][:P], (self.k[i][P:P + 1], self.v[i][P:P + 1])
 
 
 EXPERT = dict(layers=18, width=1024, hidden=4096, heads=8, head_dim=256, action_dim=32)
@@ -187,6 +216,15 @@ class BackbonePolicy(nn.Module):
             ks.append(k)
             vs.append(v)
         return self.stack.norm(h), ks, vs
+
+    def decode_step_cached(self, x, cache):
+        """decode_step on a KVCache: the same hidden state, with this token's keys / values written into the cache."""
+        h = x
+        for i, layer in enumerate(self.stack.layers):
+            ck, cv, out = cache.rows(i)
+            h, _, _ = layer(h, ck, cv, kv_out=out)
+        cache.length += 1
+        return self.stack.norm(h)
 
     def decode_step(self, x, ks, vs):
         """One token x (1, width) against the caches; returns the hidden state and the caches grown by one row."""

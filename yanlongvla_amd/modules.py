@@ -132,10 +132,16 @@ class Group:
         z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
         return kernels.gemm_i8(q, W, z, sa=b['scale'], sw=self.rs)
 
-    def posts(self, acc, b, shape, gelu0=False):
-        """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs)."""
+    def posts(self, acc, b, shape, gelu0=False, outs=None):
+        """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs).
+        outs: per segment, None or a contiguous (M, n) BF16 tensor the segment's output is written to (e.g. a row of a
+        preallocated key / value cache)."""
         M, dev = acc.shape[0], acc.device
-        ys = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in self.N]
+        ys = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) if outs is None or outs[i] is None else outs[i]
+              for i, n in enumerate(self.N)]
+        for y, n in zip(ys, self.N):
+            if y.shape != (M, n) or y.dtype != torch.bfloat16 or not y.is_contiguous():
+                raise ValueError(f'segment output {tuple(y.shape)} {y.dtype}: expected a contiguous ({M}, {n}) BF16 tensor')
         scaled = acc.dtype == torch.float32
         segs = [(acc, c, None if scaled else r, v, bb, y, gelu0 and i == 0)
                 for i, (c, r, v, bb, y) in enumerate(zip(self.col0, self.rs_parts, self.sv_parts, self.bias_parts, ys))]
@@ -284,7 +290,9 @@ class KDecoderLayer(torch.nn.Module):
             return b if x is ret else None
         return b if (not x2.is_inference() and x2._version == ver) else None
 
-    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
+    def forward(self, x, cache_k=None, cache_v=None, causal_offset=None, kv_out=None):
+        """kv_out: None, or (k, v) contiguous (M, head_dim) BF16 tensors that this call's keys / values are written to by
+        the q/k/v epilogue itself (the rows of a preallocated cache); they are then the returned k, v."""
         qkv, og = self.groups
         gu, dn = self.mlp.groups
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
@@ -297,7 +305,7 @@ class KDecoderLayer(torch.nn.Module):
             kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], q4=b['q4'], scale=b['scale'])
         else:
             STATS['chained_prologues'] += 1
-        q, k, v = qkv.posts(qkv.product(b), b, x2.shape)
+        q, k, v = qkv.posts(qkv.product(b), b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
         if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
             b2 = og.buffers(M, dev)
             self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
