@@ -69,6 +69,26 @@ def test_mid2_bitexact(kind, M, N):
     assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
 
 
+@pytest.mark.parametrize('N', [4096, 16384])
+def test_mid2_gelu_inputs_of_every_magnitude(N):
+    """Rows scaled from 2^-40 to 2^20 (and a zero row): gate values below, inside and above the exponent window whose GELU
+    results the kernel keeps in LDS, so both the LDS copy and the global table are read; bit-exact against the oracle."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(N + 5)
+    M = 25
+    z = rng.standard_normal((M, 2 * N)).astype(np.float32)
+    z *= np.exp2(np.linspace(-40, 20, M)).astype(np.float32)[:, None]
+    z[M // 2] = 0
+    sv, su = signs(rng, 2 * N), signs(rng, N)
+    q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(T(z), None, None, T(sv), T(su), q=q, scale=sc)
+    lut = lut_np()
+    qr, sr, _, _ = O.mlp_middle(z[:, :N], z[:, N:], sv[:N], sv[N:], su, gelu=lambda b: lut[b])
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0])
+
+
 @pytest.mark.parametrize('N', [1024, 4096])
 def test_mid2_strided_accumulator(N):
     """Gate | up columns inside a wider accumulator row (lda > 2N), as when more layers share the product."""
