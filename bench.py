@@ -305,6 +305,14 @@ def gemm_figures(dev, seed):
         if M == 800:
             r['mfma_frac_bf16'] = round(r['TOPS_bf16'] / MFMA_I8_PEAK_TOPS, 4)
             r['mfma_frac_int32'] = round(ops / (t_i32 * 1e-3) / 1e12 / MFMA_I8_PEAK_TOPS, 4)
+            # the reference's own prefill product (torch._int_mm, hipBLASLt on ROCm) on the same operands and box
+            try:
+                wt = qw.t()
+                same = bool(torch.equal(torch._int_mm(qa, wt), acc))
+                r['torch_int_mm_us_int32'] = round(graph_per_call(lambda: torch._int_mm(qa, wt)) * 1e3, 2)
+                r['torch_int_mm_equal'] = same
+            except RuntimeError as e:
+                r['torch_int_mm_us_int32'] = f'unavailable: {e}'[:120]
         else:
             r['hbm_frac_bf16'] = round(r['GBs_bf16'] / HBM_PEAK_GBS, 4)
         if M == 50:
