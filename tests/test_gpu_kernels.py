@@ -446,6 +446,9 @@ def test_gemm_tcq_and_w8_bitexact(shapes, M):
     yb = torch.empty(M, ldz, dtype=torch.bfloat16, device=DEV)
     K.gemm_w8([(w, None, rs, yb[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
+    yb.fill_(float('nan'))
+    K.gemm_tcq([(w, t8, rs, yb[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
 
 
 @pytest.mark.parametrize('G,M', [(8, 1), (4, 9)])
