@@ -225,10 +225,15 @@ static void launch_gemm(int odt, hipStream_t st, const void* a, const void* w, c
 template <int ESZ>
 static void launch_by_m(int odt, hipStream_t st, const void* a, const void* w, const float* sa, const float* sw, void* out, int ldo,
                         int M, int N, int K) {
-    // token tile by M (a 256-token tile is mostly padding for tens of tokens); 256 x 256 measured best at M = 800
-    if (M <= 64) launch_gemm<ESZ, 256, 64, 4, 1, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
-    else if (M <= 128) launch_gemm<ESZ, 256, 128, 4, 2, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
-    else launch_gemm<ESZ, 256, 256, 2, 4, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    // The largest tile (weights x tokens) that still gives one workgroup per CU (256), else the smallest: a narrow product
+    // on 256 x 256 tiles leaves most CUs idle. Measured on MI355X at M = 800 (FP32 out, bit-identical across tiles):
+    // N = 2048, K = 16384: 206.5 us on 256 x 256 (32 workgroups), 84.3 on 128 x 64 (208); N = 2048, K = 2048: 32.3 -> 15.4;
+    // N = 2560: 37.9 -> 16.8; N = 32768 (512 workgroups of 256 x 256): 118.5 against 143-274 on the smaller tiles.
+    auto wgs = [&](int tn, int tm) { return (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm); };
+    if (M > 128 && wgs(256, 256) >= 256) launch_gemm<ESZ, 256, 256, 2, 4, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    else if (M > 64 && wgs(256, 128) >= 256) launch_gemm<ESZ, 256, 128, 4, 2, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    else if (wgs(256, 64) >= 256) launch_gemm<ESZ, 256, 64, 4, 1, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
+    else launch_gemm<ESZ, 128, 64, 4, 1, 4>(odt, st, a, w, sa, sw, out, ldo, M, N, K);
 }
 
 extern "C" int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo,
