@@ -81,6 +81,10 @@ int64_t tcq_repack_words(int m, int n);
 /* Dense INT8 decode: out (m, n) int8 = sign * t8[hash(state)]. Replaces kernels.decode / k_decode
  * (deploy/tcq_kernels/kernels.py:339-349, 653-656); definition tcq_format.Layer.w8_reference (tcq_format.py:97-98). */
 int tcq_decode_i8(const void* bits, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream);
+/* The same from the tcq_repack words of the layer (one table, t8 (512, 2)): the bytes of tcq_decode_i8, read through the
+ * coalesced layout of the fused products (the prefill of a runtime that keeps the repacked words). words and out 16-byte
+ * aligned. No reference counterpart beyond kernels.decode. */
+int tcq_decode_i8_words(const void* words, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream);
 /* The same with G row-group tables t8 (G, 512, 2); (m / G) % 16 == 0. */
 int tcq_decode_i8_groups(const void* bits, const int8_t* t8, int G, int8_t* out, int m, int n, tcq_stream_t stream);
 

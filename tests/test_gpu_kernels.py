@@ -61,7 +61,11 @@ def test_decode_i8_and_f16_bitexact(m, n, seed):
     out = torch.empty(m, n, dtype=torch.int8, device=DEV)
     K.decode(d['bits'], t8, out)
     st = L.states()
-    assert np.array_equal(out.cpu().numpy(), O.lookup(st, L.t8.astype(np.int16)).astype(np.int8))
+    ref8 = O.lookup(st, L.t8.astype(np.int16)).astype(np.int8)
+    assert np.array_equal(out.cpu().numpy(), ref8)
+    out.fill_(77)
+    K.decode_words(K.repack(d['bits'], m, n), t8, out)                   # the same bytes from the repacked words
+    assert np.array_equal(out.cpu().numpy(), ref8)
     out16 = torch.empty(m, n, dtype=torch.int16, device=DEV)
     K.decode_f16(d['bits'], d['tlut'], out16)
     ref16 = O.lookup(st, L.tlut.astype(np.float32)).astype(np.float16)
@@ -76,6 +80,9 @@ def test_decode_golden(golden, tag):
     t8 = T(golden[f'{tag}_t8'])
     out = torch.empty(L.m, L.n, dtype=torch.int8, device=DEV)
     K.decode(d['bits'], t8, out)
+    assert np.array_equal(out.cpu().numpy(), golden[f'{tag}_w8'])
+    out.fill_(77)
+    K.decode_words(K.repack(d['bits'], L.m, L.n), t8, out)
     assert np.array_equal(out.cpu().numpy(), golden[f'{tag}_w8'])
 
 

@@ -26,6 +26,7 @@ SIGNATURES = {
     'tcq_repack': [_P, _P, _I, _I, _P],
     'tcq_repack_words': [_I, _I],
     'tcq_decode_i8': [_P, _P, _P, _I, _I, _P],
+    'tcq_decode_i8_words': [_P, _P, _P, _I, _I, _P],
     'tcq_decode_f16': [_P, _P, _P, _I, _I, _P],
     'tcq_rht': [_P, _I, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_pre': [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P],

@@ -76,6 +76,53 @@ __global__ void k_decode_i8(const u16* bits, const i8* t8_all, i8* out, int rpt,
     *(uint4_t*)(out + (size_t)row * n + 16 * J) = w;
 }
 
+// Dense INT8 decode from the tcq_repack words: a wave takes one 1 KiB chunk (one tile row, 256 columns); lane (g, r)
+// holds the windows of row r for tiles 16 c + 4 j + g (j = 0..3) in one dwordx4 and writes their 16 weights, so a store
+// writes 64 contiguous bytes of each of the 16 rows. The lookups are those of the fused products (pk_code states, a
+// sign-folded table with 16 copies, lane l reading copy l mod 16), whose 16 bytes per lane and j are the row's weights in
+// column order, so the output equals k_decode_i8's byte for byte.
+constexpr int DW_C = 16, DW_NW = 16;
+
+__global__ __launch_bounds__(64 * DW_NW) void k_decode_i8_words(const u32* words, const i8* t8, i8* out, int m, int n) {
+    __shared__ __attribute__((aligned(16))) u32 tab[1024 * DW_C];
+    const int nch = (n + 255) >> 8, tiles = n >> 4;
+    const long long chunk = (long long)blockIdx.x * DW_NW + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const bool live = chunk < (long long)(m >> 4) * nch;                 // uniform per wave
+    uint4_t wa = uint4_t{0u, 0u, 0u, 0u};
+    if (live) wa = gptr((const uint4_t*)(words + chunk * 256))[lane];
+    for (int e = threadIdx.x; e < 1024; e += blockDim.x) {
+        const int h = e & 511;
+        int v0 = t8[2 * h];
+        const int v1 = t8[2 * h + 1];
+        if (e >> 9) v0 = -v0;
+        const u32 v = (u32)(v0 & 0xff) | ((u32)(v1 & 0xff) << 8);
+        const u32 vv = v | (v << 16);
+#pragma unroll
+        for (int c = 0; c < DW_C; c += 4) *(uint4_t*)(tab + e * DW_C + c) = uint4_t{vv, vv, vv, vv};
+    }
+    __syncthreads();
+    if (!live) return;
+    const int I = (int)(chunk / nch), c = (int)(chunk % nch);
+    const u32 cp4 = (u32)(lane & (DW_C - 1)) << 2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const u32 hi = wa[j];
+        const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+        u32 e0[4], e1[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+            e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << 6) | cp4));            // pair p
+            e1[p] = *(const u16*)((const char*)tab + ((x & 0xFFC0u) | cp4));                // pair p + 4
+        }
+        const int tile = 16 * c + 4 * j + g;
+        if (tile < tiles)
+            *gptr((uint4_t*)(out + (size_t)(16 * I + r) * n + 16 * tile)) =
+                uint4_t{e0[0] | (e0[1] << 16), e0[2] | (e0[3] << 16), e1[0] | (e1[1] << 16), e1[2] | (e1[3] << 16)};
+    }
+}
+
 __global__ void k_decode_f16(const u16* bits, const u16* tlut_all, u16* out, int rpt, int n) {
     __shared__ u32 tab[1024];
     const u16* tlut = tlut_all + 1024 * blockIdx.y;
@@ -142,6 +189,16 @@ extern "C" int tcq_decode_i8_groups(const void* bits, const int8_t* t8, int G, i
     const size_t per = (size_t)(m / G) * (n / 16);
     launch_k(k_decode_i8, dim3((unsigned)((per + 255) / 256), G), dim3(256), 0, (hipStream_t)stream, (const u16*)bits,
              (const i8*)t8, (i8*)out, m / G, n);
+    return launch_status();
+}
+
+extern "C" int tcq_decode_i8_words(const void* words, const int8_t* t8, int8_t* out, int m, int n, tcq_stream_t stream) {
+    if (!words || !t8 || !out || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16) return TCQ_ERR_SHAPE;
+    if ((uintptr_t)out % 16 || (uintptr_t)words % 16) return TCQ_ERR_ALIGN;
+    const long long chunks = (long long)(m / 16) * ((n + 255) / 256);
+    launch_k(k_decode_i8_words, dim3((unsigned)((chunks + DW_NW - 1) / DW_NW)), dim3(64 * DW_NW), 0, (hipStream_t)stream,
+             (const u32*)words, (const i8*)t8, (i8*)out, m, n);
     return launch_status();
 }
 

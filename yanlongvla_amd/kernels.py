@@ -81,6 +81,13 @@ def decode(bits, t8, out):
     call('tcq_decode_i8_groups', ptr(bits), ptr(t8), _groups(t8), ptr(out), m, n, stream())
 
 
+def decode_words(words, t8, out):
+    """decode from the tcq_repack words (one (512, 2) table): the same bytes, through the fused products' layout."""
+    m, n = out.shape
+    _contig(words, t8, out)
+    call('tcq_decode_i8_words', ptr(words), ptr(t8), ptr(out), m, n, stream())
+
+
 def decode_f16(bits, tlut, out):
     """Dense decode through the FP16 table, out (m, n) float16 (exact lookup(states, tlut))."""
     m, n = out.shape

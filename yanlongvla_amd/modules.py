@@ -75,6 +75,10 @@ class Group:
         self.bias_parts = [None if self.bias is None else self.bias[c:c + n] for c, n in zip(self.col0, self.N)]
         if not a8:                                          # BF16 bit patterns of the INT8 table values (modules.py:60)
             self.tb = [L.t8.to(torch.bfloat16).contiguous() for L in layers]
+        if mode == 'chunk' and a8:
+            for L in layers:
+                if L.t8.dim() == 2:
+                    L.words()                               # the per-chunk decode reads the repacked words
         if mode in ('resident', 'chunk'):
             self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8 if a8 else torch.bfloat16, device=self.su.device)
             self.decode()
@@ -87,7 +91,9 @@ class Group:
     def decode(self, W=None):
         W = self.W if W is None else W
         for i, (L, c) in enumerate(zip(self.layers, self.col0)):
-            if self.a8:
+            if self.a8 and L.t8.dim() == 2 and L._words is not None:
+                kernels.decode_words(L._words, L.t8, W[c:c + L.m])      # the repacked words the fused products keep
+            elif self.a8:
                 kernels.decode(L.bits, L.t8, W[c:c + L.m])
             else:
                 kernels.decode_bf16(L.bits, self.tb[i], W[c:c + L.m])
