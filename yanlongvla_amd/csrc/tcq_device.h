@@ -267,12 +267,49 @@ __device__ __forceinline__ void tw_walsh(float (&v)[1 << LE], float* xs) {
     butterflies<LE>(v);
 }
 
+// Two independent rows at once (a in xa, b in xb: two lds_words(2^L) regions), as tw_walsh on each: one barrier per pass
+// for both, and twice the independent work between barriers.
+template <int L, int LE>
+__device__ __forceinline__ void tw_walsh2(float (&a)[1 << LE], float (&b)[1 << LE], float* xa, float* xb) {
+    using W = Tw<L, LE>;
+    butterflies<LE>(a);
+    butterflies<LE>(b);
+    tw_put<L, LE, 0>(a, xa);
+    tw_put<L, LE, 0>(b, xb);
+    __syncthreads();
+    if constexpr (W::MB > 0) {
+        tw_get<L, LE, 1>(a, xa);
+        tw_get<L, LE, 1>(b, xb);
+#pragma unroll
+        for (int g = 0; g < (W::E >> W::MB); ++g) {
+            butterflies<W::MB>(a + (g << W::MB));
+            butterflies<W::MB>(b + (g << W::MB));
+        }
+        tw_put<L, LE, 1>(a, xa);
+        tw_put<L, LE, 1>(b, xb);
+        __syncthreads();
+    }
+    tw_get<L, LE, 2>(a, xa);
+    tw_get<L, LE, 2>(b, xb);
+    butterflies<LE>(a);
+    butterflies<LE>(b);
+}
+
 // Layout C -> layout A through xs (own slots first, one barrier).
 template <int L, int LE>
 __device__ __forceinline__ void tw_to_natural(float (&v)[1 << LE], float* xs) {
     tw_put<L, LE, 2>(v, xs);
     __syncthreads();
     tw_get<L, LE, 0>(v, xs);
+}
+
+template <int L, int LE>
+__device__ __forceinline__ void tw_to_natural2(float (&a)[1 << LE], float (&b)[1 << LE], float* xa, float* xb) {
+    tw_put<L, LE, 2>(a, xa);
+    tw_put<L, LE, 2>(b, xb);
+    __syncthreads();
+    tw_get<L, LE, 0>(a, xa);
+    tw_get<L, LE, 0>(b, xb);
 }
 
 // ---------------------------------------------------------------------------------------------------- activation quantizer

@@ -913,6 +913,84 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int 
     tw_rotate_quantize<L, LE>(u, xs, red, q, q4, ldq, scale, tok);
 }
 
+// k_mid2_tw with the gate and up transforms side by side (tw_walsh2: one barrier per pass for both rows; LDS for two rows,
+// so it serves as many rows as fit one wave of workgroups): the same operations on each row in the same order.
+template <int ADT, int L, int LE>
+__global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw2(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
+                                                            const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale) {
+    constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
+    extern __shared__ float xs[];                                       // two lds_words(N) regions: gate, then up
+    float* xu = xs + lds_words(N);
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = E * t;
+    const size_t base = (size_t)tok * lda + i0;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    Raw16<1> svg[NP], svu[NP], sn0[NP];
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        svg[h] = raw16<1>(sv + i0 + 16 * h, true);
+        svu[h] = raw16<1>(sv + N + i0 + 16 * h, true);
+        sn0[h] = raw16<1>(su + i0 + 16 * h, true);
+    }
+    float g[E], u[E];
+    if constexpr (ADT == TCQ_BF16) {
+#pragma unroll
+        for (int h = 0; h < NP; ++h) {
+            acc_chunk<ADT>(acc, base + 16 * h, st, rs + i0 + 16 * h, part16(g, h));
+            acc_chunk<ADT>(acc, base + N + 16 * h, st, rs + N + i0 + 16 * h, part16(u, h));
+        }
+    } else {
+        const u32* arow = (const u32*)acc + (size_t)tok * lda;
+        const Span<LE, 4> ga = tw_span_load<LE, 4>(arow), ua = tw_span_load<LE, 4>(arow + N);
+        // 4-byte accumulators staged through LDS in natural order (int32: scaled as acc_chunk does, the scales' span in two
+        // halves so that only half of it is live at a time)
+        auto stage = [&](const Span<LE, 4>& a, const float* r, float* dst) {
+            if (ADT == TCQ_I32) {
+                const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                const uint4_t* rp = (const uint4_t*)((const u32*)r + ((size_t)w << (LE + 6)));
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    uint4_t rv[E / 8];
+#pragma unroll
+                    for (int j = 0; j < E / 8; ++j) rv[j] = *gptr(rp + 64 * (j + hh * E / 8) + lane);
+#pragma unroll
+                    for (int j = 0; j < E / 8; ++j) {
+                        const int jj = j + hh * E / 8;
+                        float* d = dst + lds_slot((w << (LE + 6)) + 4 * (64 * jj + lane));
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) d[m] = ((float)(int)a.p[jj][m] * st) * __uint_as_float(rv[j][m]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                tw_span_put<LE, 4>(a, dst, [&](int, int, u32 b) { return __uint_as_float(b); });
+            }
+        };
+        stage(ga, rs, xs);
+        stage(ua, rs ? rs + N : nullptr, xu);
+        __syncthreads();
+        tw_get<L, LE, 0>(g, xs);
+        tw_get<L, LE, 0>(u, xu);
+    }
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh2<L, LE>(g, u, xs, xu);
+    tw_to_natural2<L, LE>(g, u, xs, xu);
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+        float sg[16], sgu[16], sn[16];
+        cv16(svg[h], sg);
+        cv16(svu[h], sgu);
+        cv16(sn0[h], sn);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const u16 gv = gptr(lut)[f32_to_bf16(g[16 * h + k] * c * sg[k])];
+            const float uu = bf16_to_f32(f32_to_bf16((u[16 * h + k] * c) * sgu[k]));
+            u[16 * h + k] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gv) * uu)) * sn[k];
+        }
+    }
+    tw_rotate_quantize<L, LE>(u, xs, red, q, q4, ldq, scale, tok);
+}
+
 // Register path of k_post_add_norm_pre for power-of-two rows of 256 .. 16384 (K / 16 threads, thread t owns chunk t, every
 // pointer 16-byte aligned): the same operations in the same order, with the row in registers instead of LDS, the Walsh
 // transforms on reg_walsh16 and every global load issued at entry.
@@ -1220,22 +1298,35 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
     // measured on MI355X: 50 x 4096 in 7.5 us against 9.8 with 32 and 11.3 on the register engine), aligned
     if (N >= 1024 && (N & (N - 1)) == 0 && vec && svec && (!q || al16(q))) {
         const size_t tsh = (size_t)lds_words(N) * sizeof(float);
-#define MID2_TW(L, LE)                                                                                                        \
+#define MID2_TWK(KER, L, LE, SH)                                                                                             \
     switch (acc_dtype) {                                                                                                      \
-        case TCQ_I32: launch_k(k_mid2_tw<TCQ_I32, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+        case TCQ_I32: launch_k(KER<TCQ_I32, L, LE>, grid, dim3(1 << (L - LE)), SH, st, acc, lda, s, rs, svp, gelu_lut, sup,      \
                                (i8*)q, (int*)q4, ldq, scale); break;                                                          \
-        case TCQ_F32: launch_k(k_mid2_tw<TCQ_F32, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut, sup, \
+        case TCQ_F32: launch_k(KER<TCQ_F32, L, LE>, grid, dim3(1 << (L - LE)), SH, st, acc, lda, s, rs, svp, gelu_lut, sup,      \
                                (i8*)q, (int*)q4, ldq, scale); break;                                                          \
-        case TCQ_BF16: launch_k(k_mid2_tw<TCQ_BF16, L, LE>, grid, dim3(1 << (L - LE)), tsh, st, acc, lda, s, rs, svp, gelu_lut,  \
-                                sup, (i8*)q, (int*)q4, ldq, scale); break;                                                    \
+        case TCQ_BF16: launch_k(KER<TCQ_BF16, L, LE>, grid, dim3(1 << (L - LE)), SH, st, acc, lda, s, rs, svp, gelu_lut, sup,    \
+                                (i8*)q, (int*)q4, ldq, scale); break;                                                         \
         default: return TCQ_ERR_DTYPE;                                                                                        \
     }
+        if (M <= 256) {                                   // gate and up side by side (two LDS rows per workgroup)
+#undef MID2_TW
+#define MID2_TW(L, LE) MID2_TWK(k_mid2_tw2, L, LE, 2 * tsh)
+            if (N == 1024) MID2_TW(10, 4)
+            else if (N == 2048) MID2_TW(11, 4)
+            else if (N == 4096) MID2_TW(12, 4)
+            else if (N == 8192) MID2_TW(13, 5)
+            else MID2_TW(14, 5)
+            return launch_status();
+        }
+#undef MID2_TW
+#define MID2_TW(L, LE) MID2_TWK(k_mid2_tw, L, LE, tsh)
         if (N == 1024) MID2_TW(10, 4)
         else if (N == 2048) MID2_TW(11, 4)
         else if (N == 4096) MID2_TW(12, 4)
         else if (N == 8192) MID2_TW(13, 5)
         else MID2_TW(14, 5)
 #undef MID2_TW
+#undef MID2_TWK
         return launch_status();
     }
     switch (acc_dtype) {
