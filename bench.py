@@ -124,7 +124,7 @@ class Stream:
 
     def rotate_out(self):
         import torch
-        self.K.postg(self.pdesc, self.nl, torch.float32, torch.float16, None, self.M, M_DIM)
+        self.K.post_batched(self.pdesc, self.nl, torch.float32, torch.float16, None, self.M, M_DIM)
 
     def step(self):
         self.rotate_in()

@@ -158,6 +158,19 @@ int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s,
 int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype, const float* s, const uint16_t* gelu_lut, int y_dtype,
                    int M, tcq_stream_t stream);
 
+/* kernels.post3 / k_post3_{i32,f32,bf16} (deploy/tcq_kernels/kernels.py:232-247, 618-621), argument for argument: the three
+ * layers of a q / k / v group read accumulator columns side by side (layer i from column n0 + ... + n(i-1) of each row of
+ * stride lda); rs, sv and bias are the (n0 + n1 + n2,) concatenations (rs NULL for an F32 accumulator, bias may be NULL);
+ * y0, y1, y2 (M, n_i) BF16. Same arithmetic as tcq_post per layer. */
+int tcq_post3(const void* acc, int acc_dtype, const float* s, const float* rs, const int8_t* sv, const float* bias, void* y0,
+              void* y1, void* y2, int M, int n0, int n1, int n2, int lda, tcq_stream_t stream);
+/* kernels.postg / k_postg_* (deploy/tcq_kernels/kernels.py:249-261, 624-628), argument for argument: two or three layers
+ * (n2 <= 0 and y2 NULL for two) as tcq_post3, one workgroup per (token, layer); gelu0 nonzero sends the first layer's BF16
+ * output through gelu_lut (65536 BF16 values, required then). */
+int tcq_postg3(const void* acc, int acc_dtype, const float* s, const float* rs, const int8_t* sv, const float* bias,
+               const uint16_t* gelu_lut, void* y0, void* y1, void* y2, int M, int n0, int n1, int n2, int lda, int gelu0,
+               tcq_stream_t stream);
+
 /* ----------------------------------------------------------------------------------------------------- MLP middles */
 
 /* Gated-MLP middle (down(gelu(gate(x)) * up(x))): acc (M, lda >= 2N) holds gate columns [0, N) and up columns [N, 2N),
@@ -286,6 +299,19 @@ int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const floa
  * k_gemm_w8 / k_gemm_w8d (deploy/tcq_kernels/kernels.py:365-399, 662-668). */
 int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                 tcq_stream_t stream);
+
+/* kernels.gemm_w8 / k_gemm_w8 (deploy/tcq_kernels/kernels.py:365-382, 662-668), argument for argument: W (N, K) int8 resident
+ * weights, q4 (K/4, ldq) int32 activation words (the reference passes q4 (K/4, M), ldq = M), s (M,) FP32 token scales, rs (N,)
+ * FP32 row scales, z (M, N) FP32 = (float(acc) * s[t]) * rs[i], acc exact in int32. M <= 64, N and K multiples of 16; z and
+ * rs 16-byte aligned. */
+int tcq_gemm_w8_q4(const int8_t* W, const int32_t* q4, int ldq, const float* s, const float* rs, float* z, int M, int N, int K,
+                   tcq_stream_t stream);
+/* kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673), argument for argument: the fused decode +
+ * product over the packed words as stored (bits (N/16 * K/16, 32) uint16, up to three layers concatenated along the rows,
+ * no tcq_repack), t8 up to three concatenated (512, 2) INT8 tables, tile row I (16 output rows) decoded with table
+ * (I >= nb0) + (I >= nb1) (the reference's bounds; 0 <= nb0 <= nb1); q4, s, rs, z as tcq_gemm_w8_q4. */
+int tcq_gemm_tcq_q4(const void* bits, const int8_t* t8, const int32_t* q4, int ldq, const float* s, const float* rs, float* z, int M,
+                    int N, int K, int nb0, int nb1, tcq_stream_t stream);
 
 /* W8A8 INT8 GEMM: acc[m, n] = sum_k a[m, k] w[n, k], exact int32. a (M, K) int8 per-token quantized activations, w (N, K)
  * int8 per-output-channel quantized weights (both row-major, K a multiple of 16), out (M, ldo) of out_dtype: I32 the

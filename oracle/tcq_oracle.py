@@ -19,8 +19,13 @@ How each function is pinned (tests/test_oracle.py):
          s[t+1] = ((s[t] << 4) | next nibble) & 0xffff with tail-biting, exact int64 products (int_matmul).
   gelu_tanh_bf16 -> PyTorch's own torch.nn.functional.gelu(approximate='tanh') (the library routine the reference tabulates).
   rmsnorm_bf16 -> PyTorch's own RMSNorm formula in FP64 (within one BF16 rounding; the summation order is the kernels').
-  mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference, w2_linear -> compositions of the pinned functions with the rounding points written in
-         deploy/tcq_kernels/kernels.py:272-277, 303 (checked against the unfused chain in the tests).
+  w2_linear -> golden vectors of the reference's reference_linear(a8=False, table='int8') on inputs whose rotated activations
+         are BF16-exact integers (n = 256): the expert variant equals them bit for bit, also for inputs offset by less than
+         half a BF16 ulp (its rounding of h); the prefill variant equals the exact integer product rounded by PyTorch's BF16
+         cast and scaled (modules.py:120-130); planted slips (no rounding of h, accumulator rounded or rounded after the
+         scale) fail (tests/test_oracle.py).
+  mlp_middle, plain_middle, pre2, quantize_channels, w8a8_reference -> compositions of the pinned functions with the rounding
+         points written in deploy/tcq_kernels/kernels.py:272-277, 303 (checked against the unfused chain in the tests).
 """
 import math
 

@@ -105,8 +105,33 @@ def main():
     allb = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     out['gelu_bf16_all'] = torch.nn.functional.gelu(allb, approximate='tanh').view(torch.int16).numpy()
     out['torch_version'] = np.array(torch.__version__)
+    w2_integer_case(out)
     np.savez_compressed(OUT, **out)
     print(f'wrote {OUT} ({OUT.stat().st_size} bytes, {len(out)} arrays)')
+
+
+def w2_integer_case(out):
+    """reference_linear(a8=False, table='int8') on inputs whose rotated activations fwht(x * su) are exact integers (n = 256,
+    where 1 / sqrt(256) is exact): x = su * fwht(v) for integer rows v with 64 <= |v| < 200. Also x_b, whose rotated
+    activations are v + 1/32 (below half a BF16 ulp of v). Own generator, so the cases above keep their bytes."""
+    g = torch.Generator().manual_seed(20261202)
+    m, n = 64, 256
+    t = layer_tensors(g, m, n, True)
+    bias = torch.randn(m, generator=g) * 0.1
+    L = F.Layer('w2i', t, bias=bias, device='cpu')
+    mag = torch.randint(64, 200, (3, n), generator=g).float()
+    v = torch.where(torch.rand(3, n, generator=g) < 0.5, -mag, mag)
+    su = t['su'].float()
+    x = F.fwht(v) * su
+    xb = x.clone()
+    xb[:, 0] += 0.5 * su[0]
+    assert torch.equal(F.fwht(x * su), v), 'rotated activations are not the exact integers'
+    assert torch.equal(F.fwht(xb * su), v + 1.0 / 32), 'offset rotated activations are not exact'
+    for k, val in t.items():
+        out[f'w2i_{k}'] = val.numpy()
+    out.update(w2i_bias=bias.numpy(), w2i_v=v.numpy(), w2i_x=x.numpy(), w2i_xb=xb.numpy(), w2i_w8=L.w8_reference().numpy())
+    out['w2i_y_bf16'] = F.reference_linear(x, L, a8=False, table='int8').view(torch.int16).numpy()
+    out['w2i_y_f32'] = F.reference_linear(x, L, a8=False, table='int8', out_dtype=torch.float32).numpy()
 
 
 if __name__ == '__main__':

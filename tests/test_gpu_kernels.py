@@ -362,7 +362,7 @@ def test_postg_matches_post_and_oracle(M):
         c0 += w
     lut = K.gelu_table(DEV)
     desc = K.post_segments(segs, DEV)
-    K.postg(desc, len(segs), torch.int32, torch.bfloat16, sd, M, max(widths), gelu_lut=lut)
+    K.post_batched(desc, len(segs), torch.int32, torch.bfloat16, sd, M, max(widths), gelu_lut=lut)
     lut_np = lut.view(torch.int16).cpu().numpy().view(np.uint16)
     c0 = 0
     for i, (w, y) in enumerate(zip(widths, ys)):
@@ -377,7 +377,7 @@ def test_postg_matches_post_and_oracle(M):
     svs = [np.where(rng.integers(0, 2, 512) > 0, 1, -1).astype(np.int8) for _ in range(5)]
     outs = [torch.empty(M, 512, dtype=torch.float32, device=DEV) for _ in range(5)]
     desc = K.post_segments([(z, 0, None, T(v), None, y, False) for z, v, y in zip(zs, svs, outs)], DEV)
-    K.postg(desc, 5, torch.float32, torch.float32, None, M, 512)
+    K.post_batched(desc, 5, torch.float32, torch.float32, None, M, 512)
     for z, v, y in zip(zs, svs, outs):
         ref = O.fwht(z.cpu().numpy()) * v.astype(np.float32)
         assert np.array_equal(bits_of(y), ref.view(np.uint32))
@@ -441,20 +441,20 @@ def test_gemm_tcq_and_w8_bitexact(shapes, M):
     for L in layers:
         cols.append(c0)
         c0 += L.m
-    K.gemm_tcq([(w, t8, rs, z[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
-    K.gemm_w8([(w, None, rs, z2[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
+    K.gemm_tcq_segments([(w, t8, rs, z[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
+    K.gemm_w8_segments([(w, None, rs, z2[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(bits_of(z), ref.view(np.uint32))
     assert np.array_equal(bits_of(z2), ref.view(np.uint32))
     # the int32 accumulators and the BF16 output of the same products
     exact = np.concatenate([O.int_matmul(q, L.w8_reference()) for L in layers], 1)
     acc = torch.empty(M, ldz, dtype=torch.int32, device=DEV)
-    K.gemm_tcq([(w, t8, rs, acc[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, None, ldz)
+    K.gemm_tcq_segments([(w, t8, rs, acc[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, None, ldz)
     assert np.array_equal(acc.cpu().numpy(), exact)
     yb = torch.empty(M, ldz, dtype=torch.bfloat16, device=DEV)
-    K.gemm_w8([(w, None, rs, yb[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
+    K.gemm_w8_segments([(w, None, rs, yb[:, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
     yb.fill_(float('nan'))
-    K.gemm_tcq([(w, t8, rs, yb[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
+    K.gemm_tcq_segments([(w, t8, rs, yb[:, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(ref))
 
 
@@ -472,7 +472,7 @@ def test_gemm_tcq_streaming_row_group_tables(G, M):
     s = (rng.random(M) * 0.02 + 1e-3).astype(np.float32)
     ref = (O.int_matmul(q, L.w8_reference()).astype(np.float32) * s[:, None]) * L.rs[None, :]
     z = torch.full((M, m), float('nan'), device=DEV)
-    K.gemm_tcq([(K.repack(d['bits'], m, n), t8, rs, z)], T(q), T(s), m)
+    K.gemm_tcq_segments([(K.repack(d['bits'], m, n), t8, rs, z)], T(q), T(s), m)
     assert np.array_equal(bits_of(z), ref.view(np.uint32))
 
 
@@ -485,9 +485,9 @@ def test_gemm_small_rejects_bad_sizes():
     s = torch.ones(65, device=DEV)
     z = torch.empty(65, 32, device=DEV)
     with pytest.raises(_lib.TcqError):
-        K.gemm_tcq([(K.repack(d['bits'], 32, 64), t8, rs, z)], q, s, 32)      # 65 tokens: more than the small-M product takes
+        K.gemm_tcq_segments([(K.repack(d['bits'], 32, 64), t8, rs, z)], q, s, 32)      # 65 tokens: more than the small-M product takes
     with pytest.raises(ValueError):
-        K.gemm_tcq([(K.repack(d['bits'], 32, 64), t8, rs, z)] * 5, q[:4], s[:4], 32)   # more segments than a launch takes
+        K.gemm_tcq_segments([(K.repack(d['bits'], 32, 64), t8, rs, z)] * 5, q[:4], s[:4], 32)   # more segments than a launch takes
 
 
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM

@@ -155,8 +155,32 @@ def test_mid2_equals_split_middle():
     g = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     u = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     desc = K.post_segments([(acc, 0, rs[:N], sv[:N], None, g, True), (acc, N, rs[N:], sv[N:], None, u, False)], DEV)
-    K.postg(desc, 2, torch.int32, torch.bfloat16, s, M, N, gelu_lut=K.gelu_table(DEV))
+    K.post_batched(desc, 2, torch.int32, torch.bfloat16, s, M, N, gelu_lut=K.gelu_table(DEV))
     q2 = torch.empty(M, N, dtype=torch.int8, device=DEV)
     s2 = torch.empty(M, dtype=torch.float32, device=DEV)
     K.pre2(g, u, su, q=q2, scale=s2)
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize('kind', ['i32', 'f32', 'bf16'])
+@pytest.mark.parametrize('M,N', [(300, 4096), (800, 16384), (257, 1024), (400, 8192), (260, 2048)])
+def test_mid2_many_rows_bitexact(kind, M, N):
+    """More than 256 token rows: the one-row-per-transform branch of tcq_mid2 (the 800-token backbone prefill middle),
+    bit-exact against the oracle for q, the (N/4, M) word layout and the token-block layout of q4."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(M * 3 + N + len(kind))
+    acc, s, rs, z = accumulators(rng, M, 2 * N, kind)
+    sv, su = signs(rng, 2 * N), signs(rng, N)
+    q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+    q4 = torch.empty(N // 4, M, dtype=torch.int32, device=DEV)
+    sc = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(acc, s, rs, T(sv), T(su), q=q, q4=q4, scale=sc)
+    qb = K.token_blocks(M, N, DEV)
+    sc2 = torch.empty(M, dtype=torch.float32, device=DEV)
+    K.mid2(acc, s, rs, T(sv), T(su), q4=qb, scale=sc2)
+    lut = lut_np()
+    qr, sr, _, _ = O.mlp_middle(z[:, :N], z[:, N:], sv[:N], sv[N:], su, gelu=lambda b: lut[b])
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0]) and np.array_equal(sc2.cpu().numpy(), sr[:, 0])
+    assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
+    assert np.array_equal(K.rows_of_token_blocks(qb, M).cpu().numpy(), qr)

@@ -63,9 +63,9 @@ def stage_layers(model, run):
         rec['scales'] = np.array_equal(s.cpu().numpy(), s_ref[:, 0])
         if M <= SMALL_M:
             z1 = torch.empty(M, L.m, device=DEV)
-            K.gemm_tcq([(L.words(), L.t8, L.rs, z1)], q, s, L.m)
+            K.gemm_tcq_segments([(L.words(), L.t8, L.rs, z1)], q, s, L.m)
             z2 = torch.empty(M, L.m, device=DEV)
-            K.gemm_w8([(L.w8_reference(), None, L.rs, z2)], q, s, L.m)
+            K.gemm_w8_segments([(L.w8_reference(), None, L.rs, z2)], q, s, L.m)
             rec['accumulator'] = np.array_equal(z1.cpu().numpy().view(np.uint32), z_ref.view(np.uint32))
             rec['accumulator_resident'] = np.array_equal(z2.cpu().numpy().view(np.uint32), z_ref.view(np.uint32))
             acc, sa, rs = z1, None, None

@@ -143,7 +143,7 @@ def test_small_products_from_token_blocks(M):
         K_.decode(T(L.bits), t8, w8)
         segs_t.append((K_.repack(T(L.bits), L.m, Kd), t8, rs))
         segs_w.append((w8, None, rs))
-    for segs, fn in ((segs_t, K_.gemm_tcq), (segs_w, K_.gemm_w8)):
+    for segs, fn in ((segs_t, K_.gemm_tcq_segments), (segs_w, K_.gemm_w8_segments)):
         for dt in (torch.float32, torch.int32):
             z1 = torch.empty(M, ldz, dtype=dt, device=DEV)
             z2 = torch.empty_like(z1)

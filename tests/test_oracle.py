@@ -314,3 +314,64 @@ def test_row_group_tables():
         t8g, rsg, gg = O.snap(tabs[g].astype(np.float16), rsc[g * rpg:(g + 1) * rpg])
         assert np.array_equal(t8[g], t8g) and np.array_equal(rs[g * rpg:(g + 1) * rpg], rsg) and gain[g] == gg
     assert len(set(gain.tolist())) == G                                   # the tables really differ
+
+
+# ------------------------------------------------------------------------------- W2 float path (Group.run_float)
+def _w2i(golden):
+    t = {k: golden[f'w2i_{k}'] for k in ('bits', 'tlut', 'row_scale', 'su', 'sv')}
+    return O.Layer('w2i', t, bias=golden['w2i_bias'])
+
+
+def _bf16_torch(a):
+    """BF16 rounding by PyTorch's own cast (the library routine), back to float32."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def test_w2_inputs_rotate_to_exact_integers(golden):
+    L = _w2i(golden)
+    v = golden['w2i_v']
+    assert np.array_equal(O.fwht(golden['w2i_x'] * L.su.astype(np.float32)), v)
+    assert np.array_equal(O.fwht(golden['w2i_xb'] * L.su.astype(np.float32)), v + np.float32(1 / 32))
+    assert np.array_equal(L.w8_reference(), golden['w2i_w8'])
+
+
+def test_w2_linear_expert_equals_reference_on_bf16_exact_activations(golden):
+    """Expert variant (deploy/tcq_kernels/modules.py:131-142): with rotated activations that BF16 holds exactly, the W2 float
+    path is the reference's a8=False layer (tcq_format.py:137-138) bit for bit; with activations v + 1/32 its BF16 rounding
+    of h brings them back to v. Leaving the rounding out, or rounding the accumulator, fails."""
+    L = _w2i(golden)
+    ref = golden['w2i_y_bf16'].view(np.uint16)
+    assert np.array_equal(O.w2_linear(golden['w2i_x'], L, small=True), ref)
+    assert np.array_equal(O.w2_linear(golden['w2i_xb'], L, small=True), ref)
+    # planted slips: h not rounded (the reference's own a8=False layer on x_b), accumulator rounded as well
+    assert not np.array_equal(O.reference_linear(golden['w2i_xb'], L, a8=False, table='int8'), ref)
+    assert not np.array_equal(O.w2_linear(golden['w2i_x'], L, small=False), ref)
+
+
+def test_w2_linear_prefill_rounds_the_accumulator(golden):
+    """Prefill variant (modules.py:120-130): h @ W.t() in BF16 -> the FP32 sum rounded to BF16, then k_post_bf16 scales it by
+    rs (SCALE = bf2f(a) * rs, kernels.py:545). Expected value from the exact integer product, PyTorch's BF16 cast, and the
+    golden-pinned output rotation; slips (no rounding, rounding after the row scale) fail."""
+    L = _w2i(golden)
+    v = golden['w2i_v'].astype(np.int64)
+    acc = (v @ golden['w2i_w8'].astype(np.int64).T).astype(np.float32)     # exact: |acc| < 2^24
+    assert np.abs(acc).max() < 2 ** 24
+
+    def post(z):
+        y = O.fwht(z) * L.sv.astype(np.float32) + golden['w2i_bias']
+        return _bf16_torch_bits(y)
+
+    want = post(_bf16_torch(acc) * L.rs[None, :])
+    got = O.w2_linear(golden['w2i_x'], L, small=False)
+    assert np.array_equal(got, want)
+    assert np.array_equal(O.w2_linear(golden['w2i_xb'], L, small=False), want)
+    assert not np.array_equal(post(acc * L.rs[None, :]), want)                    # no accumulator rounding
+    assert not np.array_equal(post(_bf16_torch(acc * L.rs[None, :])), want)       # rounding after the row scale
+    # the unrounded post equals the golden reference output, so `post` is the reference's output half
+    assert np.array_equal(post(acc * L.rs[None, :]), golden['w2i_y_bf16'].view(np.uint16))
+
+
+def _bf16_torch_bits(y):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(y, dtype=np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)

@@ -54,6 +54,10 @@ SIGNATURES = {
     'tcq_gemm_tcq': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_w8': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemm_i8': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    'tcq_post3': [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    'tcq_postg3': [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    'tcq_gemm_w8_q4': [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_gemm_tcq_q4': [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L}
 

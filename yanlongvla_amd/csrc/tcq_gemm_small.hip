@@ -42,11 +42,17 @@ struct SegPack {
     tcq_gemm_seg s[TCQ_MAX_SEGS];
 };
 
+// Activation layouts of the small-M products: q (M, K) row-major, the token-block layout, or the reference's q4 (K/4, ldq)
+// int32 words (4 consecutive inputs of one token per word, token = column; deploy/tcq_kernels/kernels.py:170-184).
+enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
+
 // grid (tile-row groups of the largest segment, segments), NW = blockDim.x / 64 waves; a workgroup takes TR consecutive tile
 // rows (the activation fragments of its chunks, the bulk of the loads, then serve TR rows). MODE 0: decode from tcq_repack
-// words; MODE 1: resident INT8 weights. ODT: output dtype (F32 scaled, BF16 scaled, I32 accumulators).
-template <int MODE, int NB, int ODT, int TR, bool QB>
-__global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
+// words (RB: from the reference word layout, 64 bytes per tile, tiles row-major); MODE 1: resident INT8 weights. ODT: output
+// dtype (F32 scaled, BF16 scaled, I32 accumulators). QL: activation layout (ldq only for QL_WORDS).
+template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false>
+__global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz,
+                                                                    int ldq) {
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
     const tcq_gemm_seg S = P.s[blockIdx.y];
@@ -58,10 +64,12 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     const int lr = lane & 15, lg = lane >> 4;
     const u32 cp4 = (u32)(lane & (SM_C - 1)) << 2;
     constexpr int ESH = SM_C == 16 ? 6 : SM_C == 8 ? 5 : SM_C == 4 ? 4 : 2;
+    const int tiles_n = K >> 4;
     rsrc_t Wr;
-    if (MODE == 0) Wr = make_rsrc(S.w, (u32)(tiles_m * nch) << 10);
+    if (MODE == 0) Wr = make_rsrc(S.w, RB ? (u32)(tiles_m * tiles_n) << 6 : (u32)(tiles_m * nch) << 10);
     else Wr = make_rsrc(S.w, (u32)S.m * (u32)K);
-    const rsrc_t Q = make_rsrc(q, QB ? (u32)((M + 15) >> 4) * 16u * (u32)K : (u32)M * (u32)K);   // QB: token-block layout
+    const rsrc_t Q = make_rsrc(q, QL == QL_BLOCKS ? (u32)((M + 15) >> 4) * 16u * (u32)K
+                                  : QL == QL_WORDS ? (u32)(K >> 2) * (u32)ldq * 4u : (u32)M * (u32)K);
 
     uint4_t wa[TR][MODE == 0 ? 1 : 4];
     int4v B[4][NB];
@@ -69,7 +77,15 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
             const int I = min(I0 + r, tiles_m - 1);                       // a row past the end reloads the last (never stored)
-            if (MODE == 0) {
+            if (MODE == 0 && RB) {                                        // dword lr of tile 16 c + 4 j + lg, halves swapped
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int J = 16 * c + 4 * j + lg;
+                    const u32 off = J < tiles_n ? (((u32)(I * tiles_n + J) << 6) | ((u32)lr << 2)) : RSRC_OOB;
+                    const u32 d = __builtin_amdgcn_raw_buffer_load_b32(Wr, off, 0, 2);
+                    wa[r][0][j] = __builtin_amdgcn_alignbit(d, d, 16);
+                }
+            } else if (MODE == 0) {
                 wa[r][0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
             } else {
 #pragma unroll
@@ -85,8 +101,15 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const int t = 16 * b + lr, k = 256 * c + 64 * j + 16 * lg;
-                const u32 off = (t < M && k < K) ? (QB ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
-                B[j][b] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
+                const bool in = t < M && k < K;
+                if (QL == QL_WORDS) {                                     // 4 words (k / 4 + i, t): 16 lanes read 64 bytes
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        B[j][b][i] = (int)__builtin_amdgcn_raw_buffer_load_b32(Q, in ? ((u32)((k >> 2) + i) * (u32)ldq + (u32)t) << 2 : RSRC_OOB, 0, 0);
+                } else {
+                    const u32 off = in ? (QL == QL_BLOCKS ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
+                    B[j][b] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
+                }
             }
     };
 
@@ -294,27 +317,27 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
 }
 
 // =========================================================================================================== C ABI
-template <int MODE, int NB, int TR, bool QB>
+template <int MODE, int NB, int TR, int QL, bool RB>
 static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
-                            int ldo, int odt) {
+                            int ldo, int ldq, int odt) {
     switch (odt) {
-        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR, QB>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
+        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
+        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
     }
 }
-template <int MODE, int TR, bool QB>
+template <int MODE, int TR, int QL, bool RB = false>
 static void launch_small_qb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
-                            int ldo, int odt) {
-    if (M <= 16) launch_small_nb<MODE, 1, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
-    else if (M <= 32) launch_small_nb<MODE, 2, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
-    else launch_small_nb<MODE, 4, TR, QB>(grid, block, st, P, q, s, M, K, ldo, odt);
+                            int ldo, int ldq, int odt) {
+    if (M <= 16) launch_small_nb<MODE, 1, TR, QL, RB>(grid, block, st, P, q, s, M, K, ldo, ldq, odt);
+    else if (M <= 32) launch_small_nb<MODE, 2, TR, QL, RB>(grid, block, st, P, q, s, M, K, ldo, ldq, odt);
+    else launch_small_nb<MODE, 4, TR, QL, RB>(grid, block, st, P, q, s, M, K, ldo, ldq, odt);
 }
 template <int MODE, int TR>
 static void launch_small_tr(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                             int ldo, int odt, bool qb) {
-    if (qb) launch_small_qb<MODE, TR, true>(grid, block, st, P, q, s, M, K, ldo, odt);
-    else launch_small_qb<MODE, TR, false>(grid, block, st, P, q, s, M, K, ldo, odt);
+    if (qb) launch_small_qb<MODE, TR, QL_BLOCKS>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
+    else launch_small_qb<MODE, TR, QL_ROWS>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
 }
 
 template <int ODT, bool QB>
@@ -414,4 +437,51 @@ extern "C" int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q,
 extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                            tcq_stream_t stream) {
     return gemm_small<1>(segs, nseg, q, s, M, K, out_dtype, ldo, stream);
+}
+
+// ------------------------------------------------------------------------------------------ reference-shaped helpers
+// The reference's small-M helpers take the activations as q4 (K/4, M) int32 words and write FP32 z (M, N)
+// (deploy/tcq_kernels/kernels.py:662-673). Both run the workgroup plan of the products above with the word layout of q4;
+// the fused decode reads the reference's own word layout (bits as stored, no repack) and picks table i of t8 (up to three
+// concatenated (512, 2) tables) for tile rows I with (I >= nb0) + (I >= nb1) == i, as k_gemm_tcq (kernels.py:403-412).
+static int small_words_check(const void* w, const int32_t* q4, int ldq, const float* s, const float* rs, const float* z, int M, int N,
+                             int K) {
+    if (!w || !q4 || !s || !rs || !z || M <= 0 || N <= 0 || K <= 0 || ldq < M) return TCQ_ERR_ARG;
+    if (N % 16 || K % 16) return TCQ_ERR_SHAPE;
+    if (M > 64) return TCQ_ERR_UNSUPPORTED;
+    if ((size_t)N * K >= ((size_t)1 << 31) || (size_t)(K / 4) * ldq * 4 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if ((uintptr_t)z % 16 || (uintptr_t)rs % 16 || (uintptr_t)q4 % 4) return TCQ_ERR_ALIGN;
+    return TCQ_OK;
+}
+
+extern "C" int tcq_gemm_w8_q4(const int8_t* W, const int32_t* q4, int ldq, const float* s, const float* rs, float* z, int M, int N,
+                              int K, tcq_stream_t stream) {
+    const int e = small_words_check(W, q4, ldq, s, rs, z, M, N, K);
+    if (e) return e;
+    SegPack P = {};
+    P.s[0] = tcq_gemm_seg{W, nullptr, rs, z, N, 0};
+    const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
+    launch_small_qb<1, 1, QL_WORDS>(dim3(N / 16, 1), dim3(64 * nw), (hipStream_t)stream, P, (const i8*)q4, s, M, K, N, ldq, TCQ_F32);
+    return launch_status();
+}
+
+extern "C" int tcq_gemm_tcq_q4(const void* bits, const int8_t* t8, const int32_t* q4, int ldq, const float* s, const float* rs,
+                               float* z, int M, int N, int K, int nb0, int nb1, tcq_stream_t stream) {
+    const int e = small_words_check(bits, q4, ldq, s, rs, z, M, N, K);
+    if (e) return e;
+    if (!t8 || nb0 < 0 || nb1 < nb0) return TCQ_ERR_ARG;
+    const int tiles = N / 16, tiles_n = K / 16;
+    const int bnd[4] = {0, nb0 < tiles ? nb0 : tiles, nb1 < tiles ? nb1 : tiles, tiles};
+    SegPack P = {};
+    int nseg = 0, max_m = 0;
+    for (int i = 0; i < 3; ++i) {
+        const int lo = bnd[i], hi = bnd[i + 1];
+        if (hi <= lo) continue;
+        P.s[nseg++] = tcq_gemm_seg{(const u16*)bits + (size_t)lo * tiles_n * 32, t8 + 1024 * i, rs + 16 * lo, z + 16 * lo, 16 * (hi - lo), 0};
+        if (16 * (hi - lo) > max_m) max_m = 16 * (hi - lo);
+    }
+    const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
+    launch_small_qb<0, 1, QL_WORDS, true>(dim3(max_m / 16, nseg), dim3(64 * nw), (hipStream_t)stream, P, (const i8*)q4, s, M, K, N, ldq,
+                                          TCQ_F32);
+    return launch_status();
 }

@@ -1417,6 +1417,38 @@ extern "C" int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype,
     return launch_status();
 }
 
+// Up to three layers whose accumulator columns, row scales, signs and biases lie side by side (layer i from column
+// n0 + ... + n(i-1)); a layer with n <= 0 ends the list. BF16 outputs, the first optionally through the GELU table.
+static int post_side_by_side(const void* acc, int acc_dtype, const float* s, const float* rs, const int8_t* sv, const float* bias,
+                             const uint16_t* gelu_lut, void* y0, void* y1, void* y2, int M, int n0, int n1, int n2, int lda,
+                             int gelu0, tcq_stream_t stream) {
+    const int n[3] = {n0, n1, n2};
+    void* ys[3] = {y0, y1, y2};
+    tcq_post_seg segs[3];
+    int nseg = 0, col = 0;
+    for (int i = 0; i < 3 && n[i] > 0; ++i) {
+        if (!ys[i]) return TCQ_ERR_ARG;
+        segs[nseg++] = tcq_post_seg{acc, rs ? rs + col : nullptr, sv ? sv + col : nullptr, bias ? bias + col : nullptr, ys[i], lda, col, n[i],
+                                    gelu0 && i == 0};
+        col += n[i];
+    }
+    if (nseg == 0) return TCQ_ERR_ARG;
+    return tcq_post_group(segs, nseg, acc_dtype, s, gelu_lut, TCQ_BF16, M, stream);
+}
+
+extern "C" int tcq_post3(const void* acc, int acc_dtype, const float* s, const float* rs, const int8_t* sv, const float* bias, void* y0,
+                         void* y1, void* y2, int M, int n0, int n1, int n2, int lda, tcq_stream_t stream) {
+    if (n0 <= 0 || n1 <= 0 || n2 <= 0) return TCQ_ERR_ARG;
+    return post_side_by_side(acc, acc_dtype, s, rs, sv, bias, nullptr, y0, y1, y2, M, n0, n1, n2, lda, 0, stream);
+}
+
+extern "C" int tcq_postg3(const void* acc, int acc_dtype, const float* s, const float* rs, const int8_t* sv, const float* bias,
+                          const uint16_t* gelu_lut, void* y0, void* y1, void* y2, int M, int n0, int n1, int n2, int lda, int gelu0,
+                          tcq_stream_t stream) {
+    if (n0 <= 0 || n1 <= 0) return TCQ_ERR_ARG;
+    return post_side_by_side(acc, acc_dtype, s, rs, sv, bias, gelu_lut, y0, y1, y2, M, n0, n1, n2 > 0 ? n2 : 0, lda, gelu0, stream);
+}
+
 static size_t norm_lds(int K) { return row_lds(K) + (size_t)(K / 16) * sizeof(float); }
 
 extern "C" int tcq_rmsnorm(const void* x, const void* w, float eps, void* y, int M, int K, tcq_stream_t stream) {

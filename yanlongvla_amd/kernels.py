@@ -107,6 +107,8 @@ def decode_bf16(bits, tb, out):
 def rht(x, su, y):
     """y = fwht(x * su) row by row (su may be None). x, y (M, n); dtypes float32 / bfloat16 / float16."""
     M, n = x.shape
+    if y.shape != x.shape or (su is not None and su.numel() != n):
+        raise ValueError(f'rht: y {tuple(y.shape)} / su must match x {tuple(x.shape)}')
     call('tcq_rht', ptr(x), _dt(x, (0, 1, 2), 'rht x'), x.stride(0), ptr(su), ptr(y), _dt(y, (0, 1, 2), 'rht y'), y.stride(0),
          M, n, stream())
     return y
@@ -140,6 +142,10 @@ def post(acc, s, rs, sv, bias, y, col0=0):
     (M, N) BF16 / FP16 / FP32 (reference kernels.py:612-615)."""
     M, N = y.shape
     _contig(acc, s, rs, sv, bias, y)
+    if acc.shape[0] < M or col0 < 0 or col0 + N > acc.shape[1]:
+        raise ValueError(f'post: accumulator {tuple(acc.shape)} does not hold columns {col0}..{col0 + N} of {M} rows')
+    if sv.numel() != N or (rs is not None and rs.numel() != N) or (bias is not None and bias.numel() != N):
+        raise ValueError('post: sv / rs / bias must have N elements')
     call('tcq_post', ptr(acc), _dt(acc, (0, 1, 3), 'post acc'), acc.shape[1], col0, ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(y),
          _dt(y, (0, 1, 2), 'post y'), M, N, stream())
 
@@ -242,15 +248,24 @@ def gemv_descriptors(layers):
         G = _groups(tlut)
         flat += [ptr(wdev), ptr(tlut), ptr(row_scale), ptr(z), 0 if G == 1 else z.shape[-1] // G]
     dev = layers[0][0].device
-    return torch.tensor(flat, dtype=torch.int64).to(dev)
+    desc = torch.tensor(flat, dtype=torch.int64).to(dev)
+    desc.rows_per_table = sorted(set(flat[4::5]))         # the launch plan needs one common value (checked by gemv_f16)
+    return desc
 
 
-def gemv_f16(desc, h16, hscale, m, n, rows_per_table=0):
-    """Batched FP16-table decode-GEMV: for every layer in desc, z (M, m) = (h16 Q^T) * hscale * row_scale (M <= 16). Layers
-    with row-group tables pass their common rows_per_table."""
+def gemv_f16(desc, h16, hscale, m, n, rows_per_table=None):
+    """Batched FP16-table decode-GEMV: for every layer in desc, z (M, m) = (h16 Q^T) * hscale * row_scale (M <= 16). The
+    rows per table come from the descriptors (all layers must agree); a rows_per_table argument must equal them."""
     M = h16.shape[0]
     _contig(h16, hscale)
-    call('tcq_gemv_f16_groups', ptr(desc), desc.numel() // 5, ptr(h16), ptr(hscale), M, m, n, rows_per_table, stream())
+    rpt = getattr(desc, 'rows_per_table', None)
+    if rpt is None:
+        raise ValueError('gemv_f16: descriptors must come from gemv_descriptors')
+    if len(rpt) != 1:
+        raise ValueError(f'gemv_f16: the layers have different rows per table {rpt}')
+    if rows_per_table is not None and rows_per_table != rpt[0]:
+        raise ValueError(f'gemv_f16: rows_per_table {rows_per_table} differs from the descriptors ({rpt[0]})')
+    call('tcq_gemv_f16_groups', ptr(desc), desc.numel() // 5, ptr(h16), ptr(hscale), M, m, n, rpt[0], stream())
 
 
 def gemv_post_descriptors(layers):
@@ -302,10 +317,48 @@ def post_segments(segs, device):
     return torch.from_numpy(a.view(np.uint8).copy()).to(device)
 
 
-def postg(desc, nseg, acc_dtype, y_dtype, s, M, maxN, gelu_lut=None):
-    """Batched epilogue over nseg segments of post_segments (reference kernels.postg / post3, kernels.py:618-628): one
-    workgroup per (token, segment). acc_dtype / y_dtype: torch dtypes shared by all segments."""
+def post_batched(desc, nseg, acc_dtype, y_dtype, s, M, maxN, gelu_lut=None):
+    """Batched epilogue over nseg segments of post_segments (a device descriptor array; the batched form of the reference's
+    kernels.postg, kernels.py:618-628): one workgroup per (token, segment). acc_dtype / y_dtype: torch dtypes shared by all
+    segments."""
     call('tcq_postg', ptr(desc), nseg, DTYPE[acc_dtype], ptr(s), ptr(gelu_lut), DTYPE[y_dtype], M, maxN, stream())
+
+
+def _side_by_side(acc, s, rs, sv, bias, ys):
+    """Checks of the reference's three-layer epilogue arguments: columns, rs / sv / bias concatenated, BF16 outputs."""
+    M = ys[0].shape[0]
+    n = [y.shape[1] for y in ys]
+    _contig(acc, s, rs, sv, bias, *ys)
+    if acc.shape[0] < M or acc.shape[1] < sum(n):
+        raise ValueError(f'accumulator {tuple(acc.shape)} does not hold {M} rows of {sum(n)} columns')
+    if sv.numel() != sum(n) or (rs is not None and rs.numel() != sum(n)) or (bias is not None and bias.numel() != sum(n)):
+        raise ValueError('rs / sv / bias must be the concatenations over the layers')
+    if any(y.dtype != torch.bfloat16 or y.shape[0] != M for y in ys):
+        raise TypeError('outputs must be (M, n) bfloat16')
+    if acc.dtype == torch.int32 and (s is None or rs is None):
+        raise ValueError('an int32 accumulator needs s and rs')
+    return M, n
+
+
+def post3(acc, s, rs, sv, bias, ys):
+    """q / k / v in one launch (reference kernels.post3, kernels.py:618-621): rs, sv, bias concatenated over the three
+    layers; ys = three (M, N_i) BF16 outputs."""
+    M, n = _side_by_side(acc, s, rs, sv, bias, ys)
+    if len(ys) != 3:
+        raise ValueError('post3 takes three outputs')
+    call('tcq_post3', ptr(acc), _dt(acc, (0, 1, 3), 'post3 acc'), ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(ys[0]), ptr(ys[1]),
+         ptr(ys[2]), M, n[0], n[1], n[2], acc.shape[1], stream())
+
+
+def postg(acc, s, rs, sv, bias, ys, gelu0=False):
+    """Two or three layers sharing the accumulator row, one workgroup per (token, layer); optional GELU on the first
+    (reference kernels.postg, kernels.py:624-628)."""
+    M, n = _side_by_side(acc, s, rs, sv, bias, ys)
+    if len(ys) not in (2, 3):
+        raise ValueError('postg takes two or three outputs')
+    y2, n2 = (ys[2], n[2]) if len(ys) == 3 else (None, 0)
+    call('tcq_postg3', ptr(acc), _dt(acc, (0, 1, 3), 'postg acc'), ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(gelu_table(acc.device)),
+         ptr(ys[0]), ptr(ys[1]), ptr(y2), M, n[0], n[1], n2, acc.shape[1], int(bool(gelu0)), stream())
 
 
 def post_group(segs, acc_dtype, y_dtype, s, M, gelu_lut=None):
@@ -347,8 +400,8 @@ class SmallProduct:
     """A prepared small-M product over 1..4 segments [(w, t8, rs, out), ...]: out is a view whose first element is the
     segment's first output column of an (M, ldo) buffer (FP32 / BF16 scaled, or int32 sums); rs (m,) FP32 gives m. The
     descriptor array is built once (keep the tensors alive); __call__(q, s) launches on the current stream.
-    resident False: w = tcq_repack words + t8 (fused decode, reference kernels.gemm_tcq, kernels.py:671-673);
-    resident True: w = (m, K) int8 weights (reference kernels.gemm_w8, kernels.py:662-668)."""
+    resident False: w = tcq_repack words + t8 (fused decode; the segment form of reference kernels.gemm_tcq,
+    kernels.py:671-673); resident True: w = (m, K) int8 weights (segment form of reference kernels.gemm_w8, kernels.py:662-668)."""
 
     def __init__(self, segs, ldo, resident=False):
         if not 1 <= len(segs) <= _lib.MAX_SEGS:
@@ -357,6 +410,7 @@ class SmallProduct:
         self.arr = (_lib.GemmSeg * len(segs))()
         self.keep = segs
         self.odt = None
+        self.K = None
         for i, (w, t8, rs, out) in enumerate(segs):
             _contig(w, t8, rs)
             d = _dt(out, (0, 1, 3), f'{self.name} out')
@@ -364,31 +418,73 @@ class SmallProduct:
                 raise TypeError('all segments need one output dtype')
             self.odt = d
             G = 1 if t8 is None else _groups(t8)
+            if resident:
+                if w.dim() != 2 or w.shape[0] != rs.numel() or w.dtype != torch.int8:
+                    raise ValueError(f'segment {i}: resident weights must be ({rs.numel()}, K) int8')
+                k = w.shape[1]
+                if self.K is not None and k != self.K:
+                    raise ValueError('all segments need one K')
+                self.K = k
             self.arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(out), rs.numel(), 0 if G == 1 else rs.numel() // G)
+        self.outs = [(o, rs.numel()) for _, _, rs, o in segs]
         self.n, self.ldo = len(segs), ldo
         self.fn = getattr(_lib.lib(), self.name)
 
     def __call__(self, q, s):
         """q (M, K) row-major, or a token-block tensor (M = s.numel() tokens; s is then required)."""
         if q.dim() == 4:
+            if s is None:
+                raise ValueError('token-block activations need s (their token count)')
             M, K, odt = s.numel(), q.shape[1] * 16, self.odt | Q_TOKEN_BLOCKS
         else:
             (M, K), odt = q.shape, self.odt
-        rc = self.fn(self.arr, self.n, q.data_ptr(), None if s is None else s.data_ptr(), M, K, odt, self.ldo, stream())
+        if self.K is not None and K != self.K:
+            raise ValueError(f'activations have K = {K}, the weights {self.K}')
+        if s is not None and s.numel() < M:
+            raise ValueError('fewer token scales than tokens')
+        for o, m in self.outs:
+            if o.storage_offset() + (M - 1) * self.ldo + m > o.untyped_storage().nbytes() // o.element_size():
+                raise ValueError(f'an output buffer does not hold {M} rows of stride {self.ldo}')
+        rc = self.fn(self.arr, self.n, ptr(q), ptr(s), M, K, odt, self.ldo, stream())
         if rc:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
 
-def gemm_tcq(segs, q, s, ldo):
+def gemm_tcq_segments(segs, q, s, ldo):
     """One-shot fused decode + product over segments (see SmallProduct)."""
     _contig(q, s)
     SmallProduct(segs, ldo)(q, s)
 
 
-def gemm_w8(segs, q, s, ldo):
+def gemm_w8_segments(segs, q, s, ldo):
     """One-shot INT8-resident product over segments (see SmallProduct)."""
     _contig(q, s)
     SmallProduct(segs, ldo, resident=True)(q, s)
+
+
+def gemm_w8(W, q4, s, rs, z):
+    """W (N, K) int8 resident, q4 (K/4, M) int32, z (M, N) FP32 = (float(acc) * s) * rs (reference kernels.gemm_w8,
+    kernels.py:662-668)."""
+    N, K = W.shape
+    M = z.shape[0]
+    _contig(W, q4, s, rs, z)
+    if q4.shape[0] != K // 4 or q4.shape[1] < M or z.shape[1] != N or rs.numel() != N or s.numel() < M:
+        raise ValueError('gemm_w8: shapes do not match')
+    call('tcq_gemm_w8_q4', ptr(W), ptr(q4), q4.shape[1], ptr(s), ptr(rs), ptr(z), M, N, K, stream())
+
+
+def gemm_tcq(bits, t8, q4, s, rs, z, K, bounds=(1 << 30, 1 << 30)):
+    """Fused decode + product over the packed words as stored: bits of up to three layers concatenated along the rows,
+    t8 their (512, 2) tables concatenated, tile rows below bounds[0] / bounds[1] / beyond on table 0 / 1 / 2; q4 (K/4, M),
+    z (M, N) FP32 (reference kernels.gemm_tcq, kernels.py:671-673)."""
+    M, N = z.shape
+    _contig(bits, t8, q4, s, rs, z)
+    if bits.numel() != (N // 16) * (K // 16) * 32 or q4.shape[0] != K // 4 or q4.shape[1] < M or rs.numel() != N:
+        raise ValueError('gemm_tcq: shapes do not match')
+    if t8.numel() < 1024 * (1 + (N // 16 > bounds[0]) + (N // 16 > bounds[1])):
+        raise ValueError('gemm_tcq: fewer tables than the bounds select')
+    call('tcq_gemm_tcq_q4', ptr(bits), ptr(t8), ptr(q4), q4.shape[1], ptr(s), ptr(rs), ptr(z), M, N, K, int(bounds[0]),
+         int(bounds[1]), stream())
 
 
 def gemm_bf16(a, w, out, sa=None, sw=None):

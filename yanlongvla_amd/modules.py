@@ -129,10 +129,10 @@ class Group:
             z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
             if self.W is not None:
                 segs = [(self.W[c:c + n], None, r, z[:, c:]) for c, n, r in zip(self.col0, self.N, self.rs_parts)]
-                kernels.gemm_w8(segs, q, b['scale'], self.Ntot)
+                kernels.gemm_w8_segments(segs, q, b['scale'], self.Ntot)
             else:
                 segs = [(L.words(), L.t8, r, z[:, c:]) for L, c, r in zip(self.layers, self.col0, self.rs_parts)]
-                kernels.gemm_tcq(segs, q, b['scale'], self.Ntot)
+                kernels.gemm_tcq_segments(segs, q, b['scale'], self.Ntot)
             return z
         W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.int8, device=dev))
         z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
