@@ -22,6 +22,7 @@
 #ifndef TCQ_API_H
 #define TCQ_API_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -231,6 +232,16 @@ int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, c
 int tcq_attend_q4(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
                   int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, int32_t* q4, int ldq, float* scale,
                   tcq_stream_t stream);
+/* tcq_attend_q4 without the workspace argument, for callers that cannot allocate device memory (code under HIP-graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The workspace is a
+ * file-scope device array of tcq_attend_static_floats() floats (8 MiB) on each device the library runs on, held until the
+ * process ends; a call that needs more (M * tcq_attend_chunks(P, M) * H * 260 floats) returns TCQ_ERR_UNSUPPORTED before
+ * launching. The call allocates nothing. Calls that overlap on one device share the array and race: order them (one stream,
+ * or events between streams). */
+int tcq_attend_q4_static(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
+                         int H, int D, int causal_offset, void* o, const int8_t* su, int8_t* q8, int32_t* q4, int ldq, float* scale,
+                         tcq_stream_t stream);
+size_t tcq_attend_static_floats(void);
 
 /* -------------------------------------------------------------------------------------------------------- products */
 

@@ -468,3 +468,45 @@ extern "C" int tcq_attend(const void* q, const void* k_cache, const void* v_cach
                           tcq_stream_t stream) {
     return tcq_attend_q4(q, k_cache, v_cache, P, k_new, v_new, M, H, D, causal_offset, part, o, su, q8, nullptr, 0, scale, stream);
 }
+
+// ------------------------------------------------------------------------------------------- allocation-free variant
+// tcq_attend_q4 with the workspace in a file-scope device array instead of a caller's buffer, for callers that cannot
+// allocate. Every (token, chunk, head) slot the combine reads is written by k_attn_part of the same call first, so the
+// array needs no clearing; calls that overlap on one device share it and race.
+constexpr size_t ATTEND_SCRATCH_FLOATS = (size_t)1 << 21;          // 8 MiB per device
+static __device__ __align__(256) float scratch[ATTEND_SCRATCH_FLOATS];
+
+namespace {
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex scratch_mu;
+float* scratch_ptr[SCRATCH_DEVICES] = {};
+
+// The device address of `scratch` on the current device (its own copy per device), looked up once per device.
+int scratch_on_current_device(float** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES) return TCQ_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        scratch_ptr[dev] = (float*)p;
+    }
+    *out = scratch_ptr[dev];
+    return TCQ_OK;
+}
+}  // namespace
+
+extern "C" size_t tcq_attend_static_floats(void) { return ATTEND_SCRATCH_FLOATS; }
+
+extern "C" int tcq_attend_q4_static(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new,
+                                    const void* v_new, int M, int H, int D, int causal_offset, void* o, const int8_t* su, int8_t* q8,
+                                    int32_t* q4, int ldq, float* scale, tcq_stream_t stream) {
+    if (M <= 0 || H <= 0 || P < 0) return TCQ_ERR_ARG;
+    if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
+    if ((size_t)M * tcq_attend_chunks(P, M) * H * PS > ATTEND_SCRATCH_FLOATS) return TCQ_ERR_UNSUPPORTED;
+    float* part = nullptr;
+    const int e = scratch_on_current_device(&part);
+    if (e) return e;
+    return tcq_attend_q4(q, k_cache, v_cache, P, k_new, v_new, M, H, D, causal_offset, part, o, su, q8, q4, ldq, scale, stream);
+}

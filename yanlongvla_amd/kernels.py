@@ -238,6 +238,20 @@ def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None,
     return o
 
 
+def attend_static(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None, su=None, q8=None, scale=None, q4=None):
+    """attend without a workspace allocation: the library's own per-device scratch array (tcq_attend_q4_static). For code
+    that must not allocate (e.g. under graph capture); calls that overlap on one device race."""
+    M = q.shape[0]
+    P = 0 if k_cache is None else k_cache.shape[0]
+    for t in (q, k_cache, v_cache, k_new, v_new, o):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError('attend_static: BF16 tensors only')
+    _contig(q, k_cache, v_cache, k_new, v_new, o, su, q8, q4, scale)
+    call('tcq_attend_q4_static', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, k_new.shape[1],
+         -1 if causal_offset is None else int(causal_offset), ptr(o), ptr(su), ptr(q8), ptr(q4), _ldq(q4), ptr(scale), stream())
+    return o
+
+
 # -------------------------------------------------------------------------------------------------------------- products
 def gemv_descriptors(layers):
     """[(wdev, tlut, row_scale, z), ...] -> device array of tcq_gemv_layer (4 pointers + rows_per_table each; z (M, m) gives
