@@ -9,9 +9,15 @@ step = the complete layer forward of every layer on the same input token:
     input rotation h = fwht(x * su) -> FP16 (tcq_pre_h16, once: the layers share the input signs, as a q/k/v group does)
     fused decode-GEMV and output rotation y_l = fwht((h Q_l^T) * r_l) * sv_l for all layers (tcq_gemv_f16_post, one launch,
     one workgroup per layer).
-value = packed-weight bytes per step / step time (GB/s). roofline = the fused decode-GEMV kernel alone, timed with HIP events
-on the stream it runs on. cpu_baseline = the oracle's restatement of the reference layer (reference_linear, FP16 table,
-unquantized activations) timed on the host over a bounded sample of the same layers.
+value = packed-weight bytes per step / step time (GB/s), after at least --warmup steps and --warmup-seconds of warm-up.
+roofline = the fused decode-GEMV kernel alone, timed with HIP events on the stream it runs on. cpu_baseline = the oracle's
+restatement of the reference layer (reference_linear, FP16 table, unquantized activations) timed on the host over a bounded
+sample of the same layers.
+
+Secondary workloads in the same line: the RHT shapes and the W8A8 GEMM (`ops`, each with a CPU baseline of the oracle), the
+pi0.5-shaped action-expert chunk (`action_chunk`) and the Gemma-2B-shaped backbone (`backbone`: prefill + 32 decode tokens,
+per-product decode rates at one token, a CPU baseline), with the device time by kernel class of each stage
+(yanlongvla_amd/harness.py).
 """
 import argparse
 import json
@@ -34,6 +40,8 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
+    p.add_argument('--warmup-seconds', type=float, default=3.0,
+                   help='minimum wall time of the headline warm-up (the clocks reach their loaded state first)')
     p.add_argument('--layers', type=int, default=1024)
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu', action='store_true')
@@ -133,13 +141,12 @@ class Stream:
             self.rotate_out()
 
 
-def timed(fn, steps, warmup):
-    """Average ms of fn over `steps` calls after `warmup` untimed calls, HIP events on the current stream (where the library
-    launches), bracketed by device synchronisation."""
+def timed(fn, steps, warmup, warm_seconds=0.0):
+    """Average ms of fn over `steps` calls after at least `warmup` untimed calls and `warm_seconds` of warm-up wall time,
+    HIP events on the current stream (where the library launches), bracketed by device synchronisation."""
     import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    from yanlongvla_amd import harness
+    harness.warm(fn, warm_seconds, warmup)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(steps):
@@ -324,6 +331,61 @@ def gemm_figures(dev, seed):
     return out
 
 
+def blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([d.get('num_threads', 1) for d in threadpool_info() if d.get('user_api') == 'blas'] or [1])
+    except Exception:
+        return 1
+
+
+def rht_cpu_baseline(seed, seconds):
+    """The oracle's fwht (tcq_format.py:44-55 restated in numpy) of x * su over BF16 rows [800, 16384] (the largest
+    RHT shape), FP32 butterflies and BF16 output, as many repeats as fit in about `seconds` (at least 3, median)."""
+    import numpy as np
+    from oracle import tcq_oracle as O
+    rng = np.random.default_rng(seed + 5)
+    M, n = 800, 16384
+    x = O.bf16_to_f32(O.bf16_bits(rng.standard_normal((M, n)).astype(np.float32)))
+    su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.float32)
+    ts, t0 = [], time.perf_counter()
+    while len(ts) < 3 or (time.perf_counter() - t0 < seconds and len(ts) < 20):
+        t1 = time.perf_counter()
+        O.bf16_bits(O.fwht(x * su))
+        ts.append(time.perf_counter() - t1)
+    med = float(np.median(ts))
+    byts = 4 * M * n + n
+    return dict(value=round(byts / med / 1e9, 4), unit='GB/s', cores=1, kind='port',
+                sample=f'{len(ts)} transforms of BF16 [{M}, {n}] through the numpy oracle (fwht of x * su, BF16 out), median '
+                       f'{med * 1e3:.1f} ms; numpy elementwise (one thread)')
+
+
+def gemm_cpu_baseline(seed, seconds):
+    """The reference's CPU path of the W8A8 product (tcq_format.py:110-122, 135): quantize_tokens of the activations,
+    int_matmul's CPU branch (FP64 matmul -> int32), then (acc * s) * s_channel -> BF16, at K = 2048, N = 16384 on as many
+    of the 800 token rows as fit in about `seconds` (per-channel weight quantization is offline and not timed)."""
+    import numpy as np
+    from oracle import tcq_oracle as O
+    rng = np.random.default_rng(seed + 6)
+    Kd, N = 2048, 16384
+    qw, sw = O.quantize_channels((rng.standard_normal((N, Kd)) * 0.02).astype(np.float32))
+
+    def run(M):
+        a = O.bf16_to_f32(O.bf16_bits(rng.standard_normal((M, Kd)).astype(np.float32)))
+        t1 = time.perf_counter()
+        q, s_ = O.quantize_tokens(a)
+        acc = O.int_matmul(q, qw)
+        O.bf16_bits((acc.astype(np.float32) * s_) * sw[None, :])
+        return time.perf_counter() - t1
+    t50 = run(50)
+    M = int(min(800, max(50, 50 * seconds / 2 / max(t50, 1e-3))))
+    el = run(M)
+    ops = 2 * M * N * Kd
+    return dict(value=round(ops / el / 1e12, 5), unit='TOPS', cores=int(blas_threads()), kind='port',
+                sample=f'{M} of the 800 token rows x K {Kd} x N {N} through the numpy oracle (quantize_tokens, FP64 int_matmul, '
+                       f'scales, BF16 out), {el:.2f} s; BLAS threads as cores')
+
+
 # ------------------------------------------------------------------------------------------------ action-expert chunk
 CHUNK_TOKENS, CHUNK_STEPS, PREFIX = 50, 10, 800
 EXPERT_PACKED_BYTES = 311_427_072 * 2 // 8      # 2-bit payload of the expert's 126 layers, per flow step
@@ -371,7 +433,8 @@ def action_chunk(args, dev):
                 med, p95 = graph_latency(chunk, replays=args.chunk_replays, warmup=10)
                 res[runtime] = {'median': round(med, 4), 'p95': round(p95, 4)}
             if runtime == 'fly':
-                keep = dict(model=model, layers=layers)
+                from yanlongvla_amd import harness
+                keep = dict(model=model, layers=layers, classes=harness.kernel_classes(harness.capture(chunk), chunk))
             else:
                 del model, layers
             torch.cuda.synchronize()
@@ -381,9 +444,29 @@ def action_chunk(args, dev):
                          f'4096x1024, down 1024x4096) 2-bit TCQ, {CHUNK_TOKENS} action tokens, {PREFIX}-row prefix KV, '
                          f'{CHUNK_STEPS} Euler steps, one HIP graph per chunk',
                 ms_per_chunk=fly, ms_per_chunk_p95=res['fly']['p95'], runtime='fly (2-bit stream decoded on every call)',
-                operating_points_ms=res, bitexact_vs_reference_runtime=exact,
+                operating_points_ms=res, bitexact_vs_reference_runtime=exact, kernel_classes_fly=keep['classes'],
                 packed_bytes_per_chunk=EXPERT_PACKED_BYTES * CHUNK_STEPS,
                 effective_packed_GBs=round(EXPERT_PACKED_BYTES * CHUNK_STEPS / (fly * 1e-3) / 1e9, 2)), keep, (ks, vs, noise)
+
+
+def oracle_linear_class():
+    """nn.Module running one quantized Linear through the oracle's reference_linear on the host (W2A8, its INT8 weight
+    decoded once at construction, untimed), as RefLinear(resident=True) runs it."""
+    import numpy as np
+    import torch
+    from oracle import tcq_oracle as O
+
+    class OracleLinear(torch.nn.Module):
+        def __init__(self, L):
+            super().__init__()
+            self.ol = O.Layer(L.name, dict(bits=L.bits.cpu().numpy(), tlut=L.tlut.cpu().numpy(),
+                                           row_scale=L.row_scale.cpu().numpy(), su=L.su.cpu().numpy(), sv=L.sv.cpu().numpy()))
+            self.w8 = L.w8_reference().cpu().numpy()
+
+        def forward(self, x):
+            y = O.reference_linear(x.float().reshape(-1, self.ol.n).numpy(), self.ol, w8=self.w8)
+            return torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).reshape(*x.shape[:-1], self.ol.m)
+    return OracleLinear
 
 
 def chunk_cpu_baseline(keep, setup, seconds):
@@ -397,17 +480,7 @@ def chunk_cpu_baseline(keep, setup, seconds):
     model, layers = keep['model'], keep['layers']
     ks, vs, noise = setup
 
-    class OracleLinear(torch.nn.Module):
-        def __init__(self, L):
-            super().__init__()
-            self.ol = O.Layer(L.name, dict(bits=L.bits.cpu().numpy(), tlut=L.tlut.cpu().numpy(),
-                                           row_scale=L.row_scale.cpu().numpy(), su=L.su.cpu().numpy(), sv=L.sv.cpu().numpy()))
-            self.w8 = L.w8_reference().cpu().numpy()             # decoded once (setup, untimed)
-
-        def forward(self, x):
-            y = O.reference_linear(x.float().reshape(-1, self.ol.n).numpy(), self.ol, w8=self.w8)
-            return torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).reshape(*x.shape[:-1], self.ol.m)
-
+    OracleLinear = oracle_linear_class()
     cpu = gemma.ExpertPolicy().bfloat16().requires_grad_(False)
     state = {k: v.cpu() for k, v in model.state_dict().items()}
     cpu.load_state_dict(state, strict=False)
@@ -448,13 +521,14 @@ def backbone(args, dev):
     import torch
     from yanlongvla_amd import gemma, modules
     img, ids, dec = backbone_setup(args.seed, dev)
-    res, outs = {}, {}
+    res, outs, products, classes, cpu = {}, {}, {}, {}, None
     with torch.inference_mode():
         for runtime in ('reference', 'fly', 'resident'):
             model = gemma.make_policy(gemma.BackbonePolicy, dev, seed=args.seed + 1)
             layers = gemma.synthetic_layers(model, args.seed + 9, dev)
             modules.install(model, runtime=runtime, layers=layers)
-            del layers
+            if runtime != 'fly':
+                del layers
             x = torch.cat([img, model.embed(ids)], 0)
             state = {}
 
@@ -477,6 +551,15 @@ def backbone(args, dev):
                 d_med, d_p95 = graph_latency(decode, replays=args.backbone_replays, warmup=2)
                 res[runtime] = {'prefill_ms': round(p_med, 3), 'decode_ms_32_tokens': round(d_med, 3),
                                 'total_ms': round(p_med + d_med, 3), 'decode_ms_per_token': round(d_med / BB_DECODE, 4)}
+                products[runtime] = decode_products(model, runtime, dev, args.seed)
+            if runtime == 'fly':
+                from yanlongvla_amd import harness
+                prefill()
+                classes['prefill'] = harness.kernel_classes(harness.capture(prefill), prefill)
+                classes['decode_32_tokens'] = harness.kernel_classes(harness.capture(decode), decode)
+                if not args.no_cpu:
+                    prefill()
+                    cpu = backbone_cpu_baseline(model, layers, x, state, [model.embed(dec[t]) for t in range(2)])
             del model, state
             torch.cuda.synchronize()
     exact = {r: bool(torch.equal(outs[r][0], outs['reference'][0]) and torch.equal(outs[r][1], outs['reference'][1]))
@@ -488,7 +571,62 @@ def backbone(args, dev):
                 prefill_int8_TOPS={r: round(2 * 800 * BACKBONE_WEIGHTS / (v['prefill_ms'] * 1e-3) / 1e12, 1) for r, v in res.items()},
                 decode_packed_bytes_per_token=BACKBONE_WEIGHTS // 4,
                 decode_effective_packed_GBs_fly=round(BACKBONE_WEIGHTS / 4 / (tok_fly * 1e-3) / 1e9, 1),
-                decode_effective_int8_GBs_resident=round(BACKBONE_WEIGHTS / (res['resident']['decode_ms_per_token'] * 1e-3) / 1e9, 1))
+                decode_effective_int8_GBs_resident=round(BACKBONE_WEIGHTS / (res['resident']['decode_ms_per_token'] * 1e-3) / 1e9, 1),
+                decode_products_M1=products, kernel_classes_fly=classes, cpu_baseline=cpu)
+
+
+def decode_products(model, runtime, dev, seed):
+    """Device time and weight-stream rate of each product of decoder layer 0 at one token (the decode step's GEMVs), per
+    call from back-to-back graph replays: fly reads the 2-bit words (m * n / 4 bytes), resident the INT8 weights."""
+    import torch
+    groups = {g.layers[0].name: g for g in model._tcq_groups}
+    pre = 'paligemma_with_expert.paligemma.language_model.layers.0.'
+    g0 = torch.Generator(device=dev).manual_seed(seed + 11)
+    out = {}
+    for tag, key in (('q/k/v', 'self_attn.q_proj'), ('o', 'self_attn.o_proj'), ('gate/up', 'mlp.gate_proj'), ('down', 'mlp.down_proj')):
+        g = groups[pre + key]
+        b = g.quantize(torch.randn(1, g.K, generator=g0, device=dev).bfloat16())
+        ms = graph_per_call(lambda: g.product(b))
+        byts = g.Ntot * g.K // 4 if runtime == 'fly' else g.Ntot * g.K
+        gbs = byts / (ms * 1e-3) / 1e9
+        out[tag] = {'shape': f'{g.Ntot}x{g.K}', 'bytes': byts, 'us': round(ms * 1e3, 2), 'GBs': round(gbs, 1),
+                    'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def backbone_cpu_baseline(model, layers, x, state, dec_x):
+    """The backbone on the host, every quantized Linear through the oracle's reference_linear (INT8 weights decoded once,
+    untimed), norms and attention by PyTorch on the CPU: decoder layer 0 over the 800-row prefill (times 18) and one decode
+    token through all 18 layers against the prefill's KV rows (times 32)."""
+    import torch
+    from yanlongvla_amd import gemma, modules
+    OracleLinear = oracle_linear_class()
+    with torch.device('meta'):
+        cpu = gemma.BackbonePolicy()
+    cpu.embed_tokens = torch.nn.Identity()
+    for n, L in layers.items():
+        modules.set_submodule(cpu, n, OracleLinear(L))
+    cpu = cpu.to_empty(device='cpu').bfloat16().requires_grad_(False)
+    for n, p in model.named_parameters():
+        if n.endswith('layernorm.weight') or n == 'paligemma_with_expert.paligemma.language_model.norm.weight':
+            cpu.get_parameter(n).copy_(p.cpu())
+    nl = len(cpu.stack.layers)
+    with torch.inference_mode():
+        xc = x.cpu()
+        t0 = time.perf_counter()
+        cpu.stack.layers[0](xc, causal_offset=0)
+        t_pre = time.perf_counter() - t0
+        ks, vs = [k.cpu() for k in state['ks']], [v.cpu() for v in state['vs']]
+        t0 = time.perf_counter()
+        cpu.decode_step(dec_x[0].cpu(), ks, vs)
+        t_tok = time.perf_counter() - t0
+    total = (t_pre * nl + t_tok * BB_DECODE) * 1e3
+    return dict(value=round(total, 1), unit='ms (800-token prefill + 32 decode tokens)', cores=torch.get_num_threads(),
+                kind='port', prefill_layer_s=round(t_pre, 3), decode_token_s=round(t_tok, 3),
+                sample=f'decoder layer 0 of the 800-token prefill ({t_pre:.2f} s, times {nl}) and one decode token through all '
+                       f'{nl} layers ({t_tok:.2f} s, times {BB_DECODE}): every quantized Linear through the numpy oracle '
+                       f'(reference_linear, INT8 weights decoded once), PyTorch CPU for norms and attention; host affinity '
+                       f'{len(os.sched_getaffinity(0))} cores')
 
 
 def note(msg):
@@ -522,8 +660,8 @@ def main():
         raise SystemExit(f'decode-GEMV output differs from the oracle: relative L2 {err}')
     note(f'layer stream checked against the oracle (relative L2 {err:.2e})')
 
-    ms_step = timed(S.step, args.steps, args.warmup)
-    ms_gemv = timed(S.gemv, args.steps, args.warmup)
+    ms_step = timed(S.step, args.steps, args.warmup, args.warmup_seconds)
+    ms_gemv = timed(S.gemv, args.steps, args.warmup, 0.5)
     byts = nl * PACKED_BYTES
     achieved = byts / (ms_gemv * 1e-3) / 1e9
     note(f'layer stream timed: {ms_step:.4f} ms per step, {ms_gemv:.4f} ms per decode-GEMV launch')
@@ -540,6 +678,10 @@ def main():
     if not args.no_ops:
         ops = {'rht_bf16': rht_figures(dev, args.seed), 'w8a8_gemm_K2048_N16384': gemm_figures(dev, args.seed)}
         note('RHT and W8A8 GEMM shapes timed')
+        if not args.no_cpu:
+            ops['rht_bf16']['cpu_baseline'] = rht_cpu_baseline(args.seed, args.cpu_seconds / 2)
+            ops['w8a8_gemm_K2048_N16384']['cpu_baseline'] = gemm_cpu_baseline(args.seed, args.cpu_seconds / 2)
+            note('RHT and W8A8 GEMM CPU baselines timed')
     chunk = None
     if not args.no_chunk:
         del S1, L1
@@ -554,7 +696,7 @@ def main():
         'metric': 'TCQ-2bit decode-GEMV GB/s (% HBM peak) + ms per action chunk, 1 GPU',
         'value': round(byts / (ms_step * 1e-3) / 1e9, 2),
         'unit': 'GB/s',
-        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'warmup_seconds_min': args.warmup_seconds,
         'ms_per_step': round(ms_step, 5),
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
         'dtype': 'fp16',
