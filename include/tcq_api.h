@@ -112,6 +112,13 @@ int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, void* y, int 
 int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
             tcq_stream_t stream);
 
+/* tcq_pre with FP16 column scales col_scale (K,) applied to the rotated activations before the absmax and the INT8 rounding:
+ * q, scale of quantize_tokens(fwht(x * su) * col_scale) (col_scale NULL: tcq_pre). The column scale of the GR00T row-group
+ * records (baselines/groot/simpler/main_row/scripts/groot_tcq.py:178-184: W = S_v H_m diag(r) Q diag(c) H_n S_u, c in the
+ * rotated input basis) moves onto the activations this way; the reference deploy path has no column scale. */
+int tcq_pre_cs(const void* x, int x_dtype, const int8_t* su, const void* col_scale, int8_t* q, int32_t* q4, int ldq, float* scale,
+               int M, int K, tcq_stream_t stream);
+
 /* Rotate for the float (W2) path: h16 (M, K) FP16 = fwht(x * su) / hscale[t], hscale[t] (M,) FP32 a power of two that puts
  * the row's absmax in [2^14, 2^15) (1 for a zero row), so the division is exact and FP16 cannot overflow. Counterpart of
  * kernels.pre_h (kernels.py:309-317, 677-680), which rounds to BF16 instead. */
@@ -121,7 +128,8 @@ int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h16, float* 
  * dense weight per output channel. q (M, K) int8, scale (M,) FP32. */
 int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q, float* scale, int M, int K, tcq_stream_t stream);
 
-/* Scale + rotate epilogue: z = SCALE(acc[t, col0 + i]) -> block Walsh -> * sv -> + bias -> y (M, N).
+/* Scale + rotate epilogue: z = SCALE(acc[t, col0 + i]) -> block Walsh -> * sv -> + bias -> y (M, N). sv NULL: a one-sided
+ * layer (the GR00T "tcq" base, groot_tcq.py:187-191: W = Q H_n S_u, no output rotation): y = SCALE(acc) (+ bias).
  * acc_dtype I32: SCALE = (float(a) * s[t]) * rs[i]; F32: SCALE = a (s, rs ignored); BF16: SCALE = bf16(a) * rs[i].
  * bias FP32 (N,) or NULL. y_dtype in {BF16, F16, F32}. lda = leading dimension of acc in elements.
  * Replaces kernels.post / k_post_{i32,f32,bf16} (deploy/tcq_kernels/kernels.py:221-230, 545, 612-615). */

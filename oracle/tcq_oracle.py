@@ -154,7 +154,9 @@ def q4_layout(q):
 
 # ----------------------------------------------------------------------------------------------------------------- the layer
 class Layer:
-    """One quantized Linear (tcq_format.py:80-107): packed tensors + the derived INT8 table / row scale."""
+    """One quantized Linear (tcq_format.py:80-107): packed tensors + the derived INT8 table / row scale. Optional GR00T
+    record fields (baselines/groot/simpler/main_row/scripts/groot_tcq.py:178-191): no 'sv' = a one-sided layer
+    W = Q H_n S_u (no output rotation); 'col_scale' (n,) FP16 = diag(c) between Q and the input rotation."""
 
     def __init__(self, name, tensors, bias=None):
         self.name = name
@@ -162,8 +164,10 @@ class Layer:
         self.tlut = np.asarray(tensors['tlut']).astype(np.float16)
         self.row_scale = np.asarray(tensors['row_scale']).astype(np.float16)
         self.su = np.asarray(tensors['su']).astype(np.int8)
-        self.sv = np.asarray(tensors['sv']).astype(np.int8)
-        self.m, self.n = self.sv.size, self.su.size
+        self.sv = np.asarray(tensors['sv']).astype(np.int8) if tensors.get('sv') is not None else None
+        cs = tensors.get('col_scale')
+        self.col_scale = None if cs is None else np.asarray(cs).astype(np.float16)
+        self.m, self.n = self.row_scale.size, self.su.size
         assert self.bits.shape == ((self.m // 16) * (self.n // 16), 32) and self.m % 16 == 0 and self.n % 16 == 0, name
         self.t8, self.rs, self.gain = snap(self.tlut, self.row_scale)
         self.bias = None if bias is None else np.asarray(bias, dtype=np.float32)
@@ -175,12 +179,17 @@ class Layer:
         return lookup(self.states(), self.t8.astype(np.int16)).astype(np.int8)
 
     def dense(self, table='fp16'):
-        """Original-basis FP32 weight S_v H_m diag(r) Q H_n S_u (tcq_format.py:100-107)."""
+        """Original-basis FP32 weight S_v H_m diag(r) Q diag(c) H_n S_u (tcq_format.py:100-107; groot_tcq.py:178-191 for
+        the column scale c and the one-sided form without S_v H_m)."""
         if table == 'fp16':
             q = lookup(self.states(), self.tlut.astype(np.float32)) * self.row_scale.astype(np.float32)[:, None]
         else:
             q = self.w8_reference().astype(np.float32) * self.rs[:, None]
+        if self.col_scale is not None:
+            q = q * self.col_scale.astype(np.float32)[None, :]
         w = fwht(q) * self.su.astype(np.float32)[None, :]
+        if self.sv is None:
+            return w
         return (fwht(np.ascontiguousarray(w.T)) * self.sv.astype(np.float32)[None, :]).T
 
 
@@ -190,6 +199,8 @@ def reference_linear(x, layer, a8=True, table='int8', w8=None, out_dtype='bf16')
     x = np.asarray(x, dtype=np.float32)
     shape = x.shape
     h = fwht(x.reshape(-1, shape[-1]) * layer.su.astype(np.float32))
+    if layer.col_scale is not None:              # GR00T column scale on the rotated activations (the weight's diag(c))
+        h = h * layer.col_scale.astype(np.float32)
     if table == 'int8':
         w8 = layer.w8_reference() if w8 is None else w8
         if a8:
@@ -205,7 +216,7 @@ def reference_linear(x, layer, a8=True, table='int8', w8=None, out_dtype='bf16')
             z = ((q.astype(np.float64) @ wq.astype(np.float64).T).astype(np.float32) * s) * r
         else:
             z = (h.astype(np.float64) @ wq.astype(np.float64).T).astype(np.float32) * r
-    y = fwht(z) * layer.sv.astype(np.float32)
+    y = z if layer.sv is None else fwht(z) * layer.sv.astype(np.float32)     # one-sided layers: no output rotation
     if layer.bias is not None:
         y = y + layer.bias
     y = y.reshape(*shape[:-1], -1)
@@ -301,10 +312,12 @@ def w8a8_reference(a, w):
 
 
 # ----------------------------------------------------------------------------------------------------------- synthetic layers
-def random_layer(m, n, seed, name='layer', bias=False, scale_range=(0.5, 1.5), per_layer_scale=True, groups=1):
+def random_layer(m, n, seed, name='layer', bias=False, scale_range=(0.5, 1.5), per_layer_scale=True, groups=1, one_sided=False,
+                 col_scale=False):
     """Seeded synthetic layer: uniform-random packed words, N(0, 1) FP16 table (groups > 1: (G, 512, 2) row-group tables,
     table g scaled by 1 + g / 4), +-1 signs, FP16 scale drawn from scale_range (one per layer broadcast to all rows when
-    per_layer_scale, else one per row)."""
+    per_layer_scale, else one per row). one_sided: no output signs (no output rotation); col_scale: FP16 column scales
+    drawn from [0.5, 1.5]."""
     rng = np.random.default_rng(seed)
     bits = rng.integers(0, 1 << 16, size=((m // 16) * (n // 16), 32), dtype=np.uint32).astype(np.uint16).view(np.int16)
     tlut = rng.standard_normal((512, 2)).astype(np.float16)
@@ -317,4 +330,7 @@ def random_layer(m, n, seed, name='layer', bias=False, scale_range=(0.5, 1.5), p
     su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.int8)
     sv = np.where(rng.integers(0, 2, m) > 0, 1, -1).astype(np.int8)
     b = rng.standard_normal(m).astype(np.float32) * np.float32(0.1) if bias else None
-    return Layer(name, dict(bits=bits, tlut=tlut, row_scale=row_scale, su=su, sv=sv), bias=b)
+    t = dict(bits=bits, tlut=tlut, row_scale=row_scale, su=su, sv=None if one_sided else sv)
+    if col_scale:
+        t['col_scale'] = rng.uniform(0.5, 1.5, size=n).astype(np.float16)
+    return Layer(name, t, bias=b)

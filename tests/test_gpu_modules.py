@@ -97,7 +97,7 @@ def test_group_bitexact(M, mode):
     for mod, ol in zip(mods, oracles):
         y = mod(x)
         assert np.array_equal(bits16(y), O.reference_linear(xs, ol))
-    assert g.x is None                                              # all three members served
+    assert g.pending is None                                        # all three members served
 
 
 @pytest.mark.parametrize('M', [10, 50, 200])

@@ -124,3 +124,43 @@ def test_decoder_layer_handoff_rules():
         assert take(out + 0) is None                             # a new tensor
         out = hand(y4)
         assert take(y4.reshape(2, 2, 8)) is None                 # another object over the same storage
+
+
+def test_groot_skeleton_matches_the_rule_accounting():
+    """The GR00T skeleton's layers under GR00T's rule: 432 quantized Linear (216 backbone, 216 action head) holding
+    2,340,421,632 weights, the reference's own accounting (groot_common.py:38-42); AdaLN linears, proj_out_*, lm_head and
+    embeddings stay dense."""
+    from yanlongvla_amd import groot, modules
+    model = groot.skeleton()
+    assert modules.rule_for(model) is modules.GROOT
+    q = {n: m for n, m in model.named_modules() if modules.groot_is_quantizable(n, m)}
+    assert len(q) == groot.QUANTIZED_LAYERS == 432
+    assert sum(modules.groot_part_of(n) == 'backbone' for n in q) == 216
+    assert sum(m.weight.numel() for m in q.values()) == groot.QUANTIZED_PARAMETERS == 2_340_421_632
+    dense = [n for n, m in model.named_modules() if isinstance(m, torch.nn.Linear) and n not in q]
+    assert sorted(dense) == sorted([f'action_head.model.transformer_blocks.{i}.norm1.linear' for i in range(32)] +
+                                   ['action_head.model.proj_out_1', 'action_head.model.proj_out_2', 'backbone.model.lm_head'])
+    assert not any(modules.is_quantizable(n, m) for n, m in q.items() if 'language_model' not in n)   # pi0.5's rule differs
+
+
+def test_groot_group_plan():
+    """Self-attention q/k/v (LLM, vl_self_attention, odd DiT blocks) and gate/up share a rotation; the cross-attention
+    blocks' to_k / to_v read another width than to_q and stay single: 344 groups for 432 layers."""
+    from types import SimpleNamespace
+    from yanlongvla_amd import groot, modules
+    model = groot.skeleton()
+    signs = {}
+    layers = {}
+    for n, m in model.named_modules():
+        if modules.groot_is_quantizable(n, m):
+            w = m.in_features
+            signs.setdefault(w, torch.ones(w, dtype=torch.int8))
+            layers[n] = SimpleNamespace(n=w, su=signs[w], col_scale=None)
+    plan = modules.plan_groups(list(layers), layers, modules.GROOT.families)
+    assert len(plan) == 344 and sum(len(g) for g in plan) == 432
+    assert ['backbone.model.model.language_model.layers.3.self_attn.q_proj', 'backbone.model.model.language_model.layers.3.self_attn.k_proj',
+            'backbone.model.model.language_model.layers.3.self_attn.v_proj'] in plan
+    cross = 'action_head.model.transformer_blocks.0.attn1.'
+    assert [cross + 'to_k'] in plan and [cross + 'to_q'] in plan
+    self_attn = 'action_head.model.transformer_blocks.1.attn1.'
+    assert [self_attn + 'to_q', self_attn + 'to_k', self_attn + 'to_v'] in plan

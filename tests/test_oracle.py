@@ -375,3 +375,49 @@ def test_w2_linear_prefill_rounds_the_accumulator(golden):
 def _bf16_torch_bits(y):
     import torch
     return torch.from_numpy(np.ascontiguousarray(y, dtype=np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+# ----------------------------------------------------------------- GR00T records: one-sided layers, column scales
+@pytest.mark.parametrize('m,n,one_sided,cs', [(64, 1536, True, True), (48, 96, True, False), (96, 64, False, True),
+                                              (32, 3072, True, True), (48, 48, False, False)])
+def test_groot_layer_forms_against_the_dense_closed_form(m, n, one_sided, cs):
+    """Layer.dense and reference_linear (FP16 table, unquantized activations) equal the FP64 closed form
+    W = [S_v H_m] diag(r) Q diag(c) H_n S_u (groot_tcq.py:178-191) built from explicit Sylvester blocks; putting c on the
+    output side, leaving it out, or rotating the output of a one-sided layer fails."""
+    L = O.random_layer(m, n, 7 * m + n, bias=True, per_layer_scale=False, one_sided=one_sided, col_scale=cs)
+    Q = O.lookup(L.states(), L.tlut.astype(np.float32)).astype(np.float64)
+    r = L.row_scale.astype(np.float64)
+    c = L.col_scale.astype(np.float64) if cs else np.ones(n)
+    W = ((r[:, None] * Q * c[None, :]) @ block_hadamard(n).T) * L.su.astype(np.float64)[None, :]
+    if not one_sided:
+        W = L.sv.astype(np.float64)[:, None] * (block_hadamard(m) @ W)
+    scale = np.abs(W).max()
+    assert np.max(np.abs(L.dense('fp16') - W)) < 1e-5 * scale
+    x = np.random.default_rng(n).standard_normal((5, n)).astype(np.float32)
+    y = O.reference_linear(x, L, a8=False, table='fp16', out_dtype='f32').astype(np.float64)
+    want = x.astype(np.float64) @ W.T + L.bias
+    assert np.max(np.abs(y - want)) < 1e-4 * np.abs(want).max()
+    # planted slips
+    if cs:
+        W_noc = ((r[:, None] * Q) @ block_hadamard(n).T) * L.su.astype(np.float64)[None, :]
+        if not one_sided:
+            W_noc = L.sv.astype(np.float64)[:, None] * (block_hadamard(m) @ W_noc)
+        assert np.max(np.abs(x @ W_noc.T + L.bias - want)) > 1e-2 * np.abs(want).max()      # c left out
+    if one_sided:
+        rotated = O.fwht(np.ascontiguousarray((x.astype(np.float64) @ W.T).astype(np.float32))) + L.bias
+        assert np.max(np.abs(rotated - want)) > 1e-2 * np.abs(want).max()
+    # the W2A8 path quantizes the column-scaled rotated activations: within the INT8 rounding of the closed form
+    yq = O.reference_linear(x, L, a8=True, table='fp16', out_dtype='f32').astype(np.float64)
+    assert np.linalg.norm(yq - want) < 2e-2 * np.linalg.norm(want)
+
+
+def test_groot_one_sided_int8_layer_is_the_scaled_product():
+    """One-sided W2A8 layer: y = bf16((acc * s) * rs + bias), acc = int_matmul(quantize_tokens(fwht(x * su) * c), w8) exact
+    (tcq_format.py:130-136 without the output rotation, groot_tcq.py:187-191)."""
+    L = O.random_layer(64, 1536, 11, bias=True, one_sided=True, col_scale=True)
+    x = np.random.default_rng(3).standard_normal((4, 1536)).astype(np.float32)
+    h = O.fwht(x * L.su.astype(np.float32)) * L.col_scale.astype(np.float32)
+    q, s = O.quantize_tokens(h)
+    acc = (q.astype(np.int64) @ L.w8_reference().astype(np.int64).T).astype(np.int32)
+    want = O.bf16_bits((acc.astype(np.float32) * s) * L.rs[None, :] + L.bias)
+    assert np.array_equal(O.reference_linear(x, L), want)

@@ -60,6 +60,7 @@ SIGNATURES = {
     'tcq_gemm_tcq_q4': [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend_q4_static': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P],
     'tcq_attend_static_floats': [],
+    'tcq_pre_cs': [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 

@@ -173,14 +173,23 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_rht_tw(const void* x, int ldx
 }
 
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
+// cs: FP16 column scales of the rotated activations (NULL: none), applied after the rotation, before the absmax.
 template <int XDT>
-__global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec) {
+__global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec, const u16* cs) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     const int tok = blockIdx.x;
     load_row<XDT>(lds, x, (size_t)tok * K, su, K, vec);
     float mx = 0.f;
-    block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    if (cs) {
+        block_walsh(lds, K, [&](int i, float v) {
+            const float w = v * f16_to_f32(gptr(cs)[i]);
+            lds[lds_slot(i)] = w;
+            mx = fmaxf(mx, fabsf(w));
+        });
+    } else {
+        block_walsh(lds, K, [&](int i, float v) { lds[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+    }
     const float s = token_scale(block_max(mx, red));
     if (threadIdx.x == 0) scale[tok] = s;
     quantize_row(lds, s, q ? q + (size_t)tok * K : nullptr, q4, tok, K, ldq);
@@ -1181,8 +1190,8 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
     return launch_status();
 }
 
-extern "C" int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
-                       tcq_stream_t stream) {
+extern "C" int tcq_pre_cs(const void* x, int x_dtype, const int8_t* su, const void* col_scale, int8_t* q, int32_t* q4, int ldq,
+                          float* scale, int M, int K, tcq_stream_t stream) {
     if (!x || !scale || (!q && !q4) || M <= 0 || K <= 0 || q4_bad(q4, ldq, M)) return TCQ_ERR_ARG;
     if (K % 4 || K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     if (q4_tb_shape_bad(q4, ldq, K)) return TCQ_ERR_SHAPE;
@@ -1191,9 +1200,16 @@ extern "C" int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, 
     const size_t sh = row_lds(K);
     const int vec = K % 8 == 0 && al16(x) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
-#define PRE(XD, _) launch_k(k_pre<XD>, grid, block, sh, st, x, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec)
+    const u16* cs = (const u16*)col_scale;
+#define PRE(XD, _) launch_k(k_pre<XD>, grid, block, sh, st, x, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec, cs)
     DISPATCH_X(x_dtype, PRE, 0)
+#undef PRE
     return launch_status();
+}
+
+extern "C" int tcq_pre(const void* x, int x_dtype, const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int K,
+                       tcq_stream_t stream) {
+    return tcq_pre_cs(x, x_dtype, su, nullptr, q, q4, ldq, scale, M, K, stream);
 }
 
 extern "C" int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h16, float* hscale, int M, int K,
@@ -1221,10 +1237,50 @@ extern "C" int tcq_quantize_rows(const void* x, int x_dtype, int ldx, int8_t* q,
     return launch_status();
 }
 
+// Epilogue of a one-sided layer (no output rotation, the GR00T "tcq" base): y[t, i] = SCALE(acc[t, col0 + i]) (+ bias[i]),
+// SCALE as in k_post. grid (ceil(N / 256), M), one element per thread.
+template <int ADT, int YDT>
+__global__ __launch_bounds__(256) void k_post_plain(const void* acc, int lda, int col0, const float* s, const float* rs,
+                                                    const float* bias, void* y, int N) {
+    const int i = blockIdx.x * 256 + threadIdx.x, tok = blockIdx.y;
+    if (i >= N) return;
+    const size_t a = (size_t)tok * lda + col0 + i;
+    float z;
+    if constexpr (ADT == TCQ_I32) z = ((float)gptr((const int*)acc)[a] * gptr(s)[tok]) * gptr(rs)[i];
+    else if constexpr (ADT == TCQ_BF16) z = bf16_to_f32(gptr((const u16*)acc)[a]) * gptr(rs)[i];
+    else z = gptr((const float*)acc)[a];
+    if (bias) z = z + gptr(bias)[i];
+    const size_t o = (size_t)tok * N + i;
+    if constexpr (YDT == TCQ_F32) gptr((float*)y)[o] = z;
+    else if constexpr (YDT == TCQ_BF16) gptr((u16*)y)[o] = f32_to_bf16(z);
+    else gptr((u16*)y)[o] = f32_to_f16(z);
+}
+
 extern "C" int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
                         const float* bias, void* y, int y_dtype, int M, int N, tcq_stream_t stream) {
-    if (!acc || !sv || !y || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
+    if (!acc || !y || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
+    if (!sv) {                                                   // one-sided layer: no output rotation
+        const dim3 grid((N + 255) / 256, M);
+        hipStream_t st = (hipStream_t)stream;
+#define PLAIN_Y(AD, YD) launch_k(k_post_plain<AD, YD>, grid, dim3(256), 0, st, acc, lda, col0, s, rs, bias, y, N)
+#define PLAIN_A(AD)                                          \
+    switch (y_dtype) {                                       \
+        case TCQ_F32: PLAIN_Y(AD, TCQ_F32); break;           \
+        case TCQ_BF16: PLAIN_Y(AD, TCQ_BF16); break;         \
+        case TCQ_F16: PLAIN_Y(AD, TCQ_F16); break;           \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+        switch (acc_dtype) {
+            case TCQ_I32: PLAIN_A(TCQ_I32); break;
+            case TCQ_F32: PLAIN_A(TCQ_F32); break;
+            case TCQ_BF16: PLAIN_A(TCQ_BF16); break;
+            default: return TCQ_ERR_DTYPE;
+        }
+#undef PLAIN_A
+#undef PLAIN_Y
+        return launch_status();
+    }
     if (N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N);

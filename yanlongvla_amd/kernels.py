@@ -114,13 +114,19 @@ def rht(x, su, y):
     return y
 
 
-def pre(x, su, q=None, q4=None, scale=None):
+def pre(x, su, q=None, q4=None, scale=None, col_scale=None):
     """x (M, K) BF16 / FP32 / FP16 contiguous -> q (M, K) int8 and / or q4 (K/4, ld) int32 or token blocks, scale (M,) FP32
-    (reference kernels.py:602-606)."""
+    (reference kernels.py:602-606). col_scale: FP16 (K,) column scales of a GR00T record, applied to the rotated activations
+    before they are quantized (tcq_pre_cs); not a reference argument."""
     M, K = x.shape
-    _contig(x, su, q, q4, scale)
-    call('tcq_pre', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale),
-         M, K, stream())
+    _contig(x, su, q, q4, scale, col_scale)
+    if col_scale is None:
+        call('tcq_pre', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, K, stream())
+        return
+    if col_scale.dtype != torch.float16 or col_scale.numel() != K:
+        raise ValueError(f'pre: col_scale must be ({K},) float16')
+    call('tcq_pre_cs', ptr(x), _dt(x, (0, 1, 2), 'pre x'), ptr(su), ptr(col_scale), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, K,
+         stream())
 
 
 def pre_h16(x, su, h16, hscale):
@@ -139,12 +145,12 @@ def quantize_rows(x, q, scale):
 
 def post(acc, s, rs, sv, bias, y, col0=0):
     """acc (M, lda) int32 (scaled here by s, rs), FP32 (already scaled) or BF16 (scaled by rs); columns col0 .. col0 + N -> y
-    (M, N) BF16 / FP16 / FP32 (reference kernels.py:612-615)."""
+    (M, N) BF16 / FP16 / FP32 (reference kernels.py:612-615). sv None: a one-sided layer, no output rotation."""
     M, N = y.shape
     _contig(acc, s, rs, sv, bias, y)
     if acc.shape[0] < M or col0 < 0 or col0 + N > acc.shape[1]:
         raise ValueError(f'post: accumulator {tuple(acc.shape)} does not hold columns {col0}..{col0 + N} of {M} rows')
-    if sv.numel() != N or (rs is not None and rs.numel() != N) or (bias is not None and bias.numel() != N):
+    if (sv is not None and sv.numel() != N) or (rs is not None and rs.numel() != N) or (bias is not None and bias.numel() != N):
         raise ValueError('post: sv / rs / bias must have N elements')
     call('tcq_post', ptr(acc), _dt(acc, (0, 1, 3), 'post acc'), acc.shape[1], col0, ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(y),
          _dt(y, (0, 1, 2), 'post y'), M, N, stream())

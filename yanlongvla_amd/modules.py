@@ -1,23 +1,28 @@
-"""Model integration: swaps the quantized nn.Linear modules of a policy for TCQ W2A8 modules running on the HIP library.
+"""Model integration: puts the TCQ W2A8 deploy path behind a policy's quantized nn.Linear modules.
 
-Mirrors deploy/tcq_kernels/modules.py (Group 29-155, KLinear 158-167, KGatedMLP 170-189, KPlainMLP 192-206, RefLinear
-209-219, install 246-311, decode_chunk 314-320): same class and function names, arguments and operating points.
+Drop-in counterpart of deploy/tcq_kernels/modules.py: the same public names and arguments (install 246-311, Group 29-155,
+KLinear 158-167, KGatedMLP 170-189, KPlainMLP 192-206, RefLinear 209-219, decode_chunk 314-320), the same runtimes and
+operating points, the same STATS counters. The bodies are this package's own: layers are planned into groups by bucket,
+a group keeps one segment record per member, and the first-member-computes protocol is a pending-result record.
 
 Runtimes (install(policy, row, runtime)):
-  dense        BF16 dense weights in the original basis written into the existing nn.Linear modules
-  reference    RefLinear: the layer definition as separate unfused steps (decode, rotate, quantize, exact GEMM, rotate)
+  dense        BF16 dense weights in the original basis, written into the existing nn.Linear modules
+  reference    RefLinear: the layer definition as separate unfused launches (decode, rotate, quantize, exact GEMM, rotate)
   resident     operating point (i): every layer decoded once at load, weights held as INT8
   fly          operating point (ii): every layer decoded from the 2-bit stream on each call
   hybrid       operating point (iii): backbone on the fly; action expert decoded once per chunk (decode_chunk) into INT8
 
-Layers that read the same tensor with identical input signs share one rotation + quantization and one product (q/k/v;
-gate/up): the group runs on the first member's call and the other members return their slice.
+Policies: the pi0.5 layer rule (baselines/common.py:51-58) and the GR00T N1.7 rule (baselines/groot/groot_common.py:33-42,
+70-79; 432 Linear) are both known; install picks the one whose layer names the model carries. GR00T records may be
+one-sided (no output rotation) and may carry column scales (groot_tcq.py:178-191).
 
-Products by token count: up to SMALL_M tokens the small-M kernels (tcq_gemm_tcq on the stream / tcq_gemm_w8 on INT8
-weights) give FP32 z = (acc * s) * rs directly; more tokens run the INT8 MFMA GEMM (tcq_gemm_i8) to exact int32 accumulators,
-on the resident INT8 weights or on weights decoded for the call. Every launch goes to the HIP library; nothing here computes
-with PyTorch ops except the bookkeeping (views, empty outputs).
+Layers that read the same tensor with the same input signs share one rotation + quantization and one product (q/k/v,
+gate/up): the group computes on the first member's call and the other members take their slice. Every launch goes to the
+HIP library; nothing here computes with PyTorch ops except the bookkeeping (views, empty outputs).
 """
+from collections import Counter, namedtuple
+from itertools import accumulate
+
 import torch
 
 from . import kernels
@@ -33,134 +38,220 @@ FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
+# ------------------------------------------------------------------------------------------------------ layer rules
 def part_of(name):
-    return 'expert' if '.gemma_expert.' in name else 'vision' if 'vision_tower' in name else 'llm'
+    """pi0.5 policy part of a layer name: the action expert, the vision tower or the language model."""
+    if '.gemma_expert.' in name:
+        return 'expert'
+    return 'vision' if 'vision_tower' in name else 'llm'
+
+
+_PI05_STACKS = ('.vision_tower.vision_model.encoder.layers.', '.language_model.layers.', '.gemma_expert.model.layers.')
+_PI05_DENSE_TAILS = ('.input_layernorm.dense', '.post_attention_layernorm.dense')
 
 
 def is_quantizable(name, module):
-    """The quantized Linear layers of the pi0.5 policy (baselines/common.py:51-58): encoder / language-model / expert layers;
-    embeddings, projector, heads, action / time projections and norms stay dense."""
-    if not isinstance(module, torch.nn.Linear):
-        return False
-    if name.endswith(('.input_layernorm.dense', '.post_attention_layernorm.dense')):
-        return False
-    return ('.vision_tower.vision_model.encoder.layers.' in name or '.language_model.layers.' in name or
-            '.gemma_expert.model.layers.' in name)
+    """The quantized Linear layers of the pi0.5 policy (baselines/common.py:51-58): encoder / language-model / expert
+    layers; embeddings, projector, heads, action / time projections and the norms' dense layers stay dense."""
+    return (isinstance(module, torch.nn.Linear) and any(s in name for s in _PI05_STACKS)
+            and not name.endswith(_PI05_DENSE_TAILS))
+
+
+_GROOT_PARTS = (('backbone', ('backbone.model.model.visual.', 'backbone.model.model.language_model.layers.')),
+                ('head', ('action_head.vl_self_attention.', 'action_head.model.transformer_blocks.')))
+_GROOT_DENSE = ('norm1.linear', 'proj_out', 'lm_head', 'embed')
+
+
+def groot_part_of(name):
+    """GR00T N1.7 part of a layer name (groot_common.py:33-34, 57-62): 'backbone', 'head' or None."""
+    return next((part for part, prefixes in _GROOT_PARTS if name.startswith(prefixes)), None)
+
+
+def groot_is_quantizable(name, module):
+    """The 432 quantized Linear layers of GR00T N1.7 (groot_common.py:35-42, 65-66): vision tower and LLM layers 0-15 of
+    the backbone, vl_self_attention and the DiT blocks of the action head; the timestep-only AdaLN linears, proj_out_*,
+    lm_head and embeddings stay dense."""
+    return (isinstance(module, torch.nn.Linear) and groot_part_of(name) is not None
+            and not any(d in name for d in _GROOT_DENSE))
+
+
+Rule = namedtuple('Rule', 'name quantizable part streamed families')
+# streamed(part): under the hybrid runtime the action-generating part is decoded per action chunk ('chunk'), the rest
+# streams ('fly'). families: leaf names whose layers may share one input rotation.
+PI05 = Rule('pi0.5', is_quantizable, part_of, lambda p: p != 'expert', GROUPS)
+GROOT = Rule('gr00t', groot_is_quantizable, lambda n: groot_part_of(n) or 'backbone', lambda p: p != 'head',
+             GROUPS + (('to_q', 'to_k', 'to_v'),))
+
+
+def rule_for(model):
+    """GR00T's rule for a model carrying GR00T layer names, else pi0.5's."""
+    groot = any(groot_part_of(n) for n, _ in model.named_modules())
+    return GROOT if groot else PI05
+
+
+# ---------------------------------------------------------------------------------------------------------- groups
+Segment = namedtuple('Segment', 'col0 width rs sv bias')     # one member's columns and epilogue vectors
+
+
+def _shares_input(layers):
+    """Members of a group read one rotated, quantized input: same width, input signs and column scales."""
+    a = layers[0]
+
+    def same(t, u):
+        return (t is None and u is None) or (t is not None and u is not None and torch.equal(t, u))
+    return all(L.n == a.n and torch.equal(L.su, a.su) and same(L.col_scale, a.col_scale) for L in layers)
+
+
+def _cat(tensors):
+    return None if tensors[0] is None else torch.cat(list(tensors)).contiguous()
+
+
+class _Pending:
+    """Outputs of one group run waiting for the members that have not taken theirs yet."""
+    __slots__ = ('x', 'outs', 'waiting')
+
+    def __init__(self, x, outs, taken):
+        self.x, self.outs = x, outs
+        self.waiting = set(range(len(outs))) - {taken}
 
 
 class Group:
-    """Layers sharing one input rotation + quantization and one product, columns side by side (modules.py:29-155).
-    mode: resident (INT8 weights, stream released) | fly (decoded on every call) | chunk (INT8 weights re-decoded by
-    decode_chunk); a8: INT8 activations, else the W2 float path (BF16 rotated activations, the INT8 table values as BF16
-    weights, FP32 accumulation; modules.py:117-144)."""
+    """Layers sharing one input rotation + quantization and one product, their output columns side by side
+    (modules.py:29-155). mode: resident (INT8 weights, stream released) | fly (decoded on every call) | chunk (INT8 weights
+    re-decoded by decode_chunk); a8: INT8 activations, else the W2 float path (BF16 rotated activations, the INT8 table
+    values as BF16 weights, FP32 accumulation; modules.py:117-144)."""
 
     def __init__(self, layers, part, mode, a8=True):
-        self.layers, self.part, self.mode, self.a8 = layers, part, mode, a8
-        self.K = layers[0].n
-        if not all(L.n == self.K and torch.equal(L.su, layers[0].su) for L in layers):
-            raise ValueError(f'group members must share the input width and signs: {[L.name for L in layers]}')
+        if not _shares_input(layers):
+            raise ValueError(f'group members must share the input width, signs and column scales: {[L.name for L in layers]}')
         if len(layers) > kernels._lib.MAX_SEGS:
             raise ValueError(f'at most {kernels._lib.MAX_SEGS} layers per group')
-        self.su = layers[0].su
+        sided = {L.sv is None for L in layers}
+        if len(sided) > 1:
+            raise ValueError(f'group mixes one-sided and two-sided layers: {[L.name for L in layers]}')
+        self.layers, self.part, self.mode, self.a8 = list(layers), part, mode, a8
+        lead = layers[0]
+        self.K, self.su, self.col_scale = lead.n, lead.su, lead.col_scale
+        if self.col_scale is not None and not a8:
+            raise NotImplementedError('the W2 float path takes no column scales')
+        self.one_sided = lead.sv is None
         self.N = [L.m for L in layers]
-        self.col0 = [sum(self.N[:i]) for i in range(len(layers))]
+        self.col0 = list(accumulate([0] + self.N[:-1]))
         self.Ntot = sum(self.N)
-        self.small = part == 'expert'
-        self.W = None
-        self.rs = torch.cat([L.rs for L in layers]).contiguous()
-        self.sv = torch.cat([L.sv for L in layers]).contiguous()
-        self.bias = torch.cat([L.bias for L in layers]).contiguous() if layers[0].bias is not None else None
-        self.rs_parts = [self.rs[c:c + n] for c, n in zip(self.col0, self.N)]
-        self.sv_parts = [self.sv[c:c + n] for c, n in zip(self.col0, self.N)]
-        self.bias_parts = [None if self.bias is None else self.bias[c:c + n] for c, n in zip(self.col0, self.N)]
+        self.small = part in ('expert', 'head')           # the few-token (action-generating) part
+        self.rs = _cat([L.rs for L in layers])
+        self.sv = None if self.one_sided else _cat([L.sv for L in layers])
+        self.bias = _cat([L.bias for L in layers]) if lead.bias is not None else None
+
+        def piece(t, c, n):
+            return None if t is None else t[c:c + n]
+        self.segments = [Segment(c, n, piece(self.rs, c, n), piece(self.sv, c, n), piece(self.bias, c, n))
+                         for c, n in zip(self.col0, self.N)]
         if not a8:                                          # BF16 bit patterns of the INT8 table values (modules.py:60)
             self.tb = [L.t8.to(torch.bfloat16).contiguous() for L in layers]
-        if mode == 'chunk' and a8:
-            for L in layers:
-                if L.t8.dim() == 2:
-                    L.words()                               # the per-chunk decode reads the repacked words
+        self.W = None
         if mode in ('resident', 'chunk'):
+            if mode == 'chunk' and a8:
+                self._repack()                              # the per-chunk decode reads the repacked words
             self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8 if a8 else torch.bfloat16, device=self.su.device)
             self.decode()
         elif a8:
-            for L in layers:
-                L.words()                                   # repack once at load: the fused small-M product reads it
-        self.x = self.outs = None
-        self.served = 0
+            self._repack()                                  # the fused small-M product reads the repacked words
+        self.pending = None
 
+    def _repack(self):
+        for L in self.layers:
+            if L.t8.dim() == 2 or self.mode != 'chunk':
+                L.words()
+
+    # -------------------------------------------------------------------------------------------------- weights
     def decode(self, W=None):
+        """The group's dense weight rows (INT8, or BF16 images for the float path) into W (default: the resident W)."""
         W = self.W if W is None else W
-        for i, (L, c) in enumerate(zip(self.layers, self.col0)):
-            if self.a8 and L.t8.dim() == 2 and L._words is not None:
-                kernels.decode_words(L._words, L.t8, W[c:c + L.m])      # the repacked words the fused products keep
-            elif self.a8:
-                kernels.decode(L.bits, L.t8, W[c:c + L.m])
+        for i, (L, seg) in enumerate(zip(self.layers, self.segments)):
+            rows = W[seg.col0:seg.col0 + seg.width]
+            if not self.a8:
+                kernels.decode_bf16(L.bits, self.tb[i], rows)
+            elif L.t8.dim() == 2 and L._words is not None:
+                kernels.decode_words(L._words, L.t8, rows)          # the words the fused products keep
             else:
-                kernels.decode_bf16(L.bits, self.tb[i], W[c:c + L.m])
+                kernels.decode(L.bits, L.t8, rows)
         return W
 
+    # -------------------------------------------------------------------------------------------- activations
     def prep(self, x):
+        """The (M, K) contiguous view of x in a dtype the rotation kernels read."""
         x2 = x.reshape(-1, self.K)
-        if not x2.is_contiguous():
-            x2 = x2.contiguous()
         if x2.dtype not in (torch.bfloat16, torch.float32, torch.float16):
             x2 = x2.float()
-        return x2
+        return x2 if x2.is_contiguous() else x2.contiguous()
 
     def buffers(self, M, dev):
-        """Quantized activations and the per-token scales: up to SMALL_M tokens in the token-block layout the small-M products
+        """Quantized activations and per-token scales: up to SMALL_M tokens in the token-block layout the small-M products
         read fastest (q4), else (M, K) row-major (q)."""
-        scale = torch.empty(M, dtype=torch.float32, device=dev)
-        if M <= SMALL_M and self.K % 16 == 0:
-            return dict(q=None, q4=kernels.token_blocks(M, self.K, dev), scale=scale)
-        return dict(q=torch.empty(M, self.K, dtype=torch.int8, device=dev), q4=None, scale=scale)
+        blocks = M <= SMALL_M and self.K % 16 == 0
+        return dict(q=None if blocks else torch.empty(M, self.K, dtype=torch.int8, device=dev),
+                    q4=kernels.token_blocks(M, self.K, dev) if blocks else None,
+                    scale=torch.empty(M, dtype=torch.float32, device=dev))
 
     def quantize(self, x2):
         b = self.buffers(x2.shape[0], x2.device)
-        kernels.pre(x2, self.su, q=b['q'], q4=b['q4'], scale=b['scale'])
+        kernels.pre(x2, self.su, q=b['q'], q4=b['q4'], scale=b['scale'], col_scale=self.col_scale)
         return b
 
+    # ------------------------------------------------------------------------------------------------ product
     def product(self, b):
         """INT8 activations -> FP32 z = (float(acc) * s) * rs (M, Ntot) of the exact int32 product acc: few tokens on the
         fused decode products, many tokens on the INT8 MFMA GEMM with the scaling in its epilogue (the order of tcq_post)."""
         q = b['q'] if b['q'] is not None else b['q4']
         M, dev = b['scale'].numel(), q.device
-        if M <= SMALL_M:
-            z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
-            if self.W is not None:
-                segs = [(self.W[c:c + n], None, r, z[:, c:]) for c, n, r in zip(self.col0, self.N, self.rs_parts)]
-                kernels.gemm_w8_segments(segs, q, b['scale'], self.Ntot)
-            else:
-                segs = [(L.words(), L.t8, r, z[:, c:]) for L, c, r in zip(self.layers, self.col0, self.rs_parts)]
-                kernels.gemm_tcq_segments(segs, q, b['scale'], self.Ntot)
-            return z
-        W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.int8, device=dev))
         z = torch.empty(M, self.Ntot, dtype=torch.float32, device=dev)
-        return kernels.gemm_i8(q, W, z, sa=b['scale'], sw=self.rs)
+        if M > SMALL_M:
+            W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.int8, device=dev))
+            return kernels.gemm_i8(q, W, z, sa=b['scale'], sw=self.rs)
+        if self.W is not None:
+            segs = [(self.W[s.col0:s.col0 + s.width], None, s.rs, z[:, s.col0:]) for s in self.segments]
+            kernels.gemm_w8_segments(segs, q, b['scale'], self.Ntot)
+        else:
+            segs = [(L.words(), L.t8, s.rs, z[:, s.col0:]) for L, s in zip(self.layers, self.segments)]
+            kernels.gemm_tcq_segments(segs, q, b['scale'], self.Ntot)
+        return z
 
+    # ------------------------------------------------------------------------------------------------ epilogue
     def posts(self, acc, b, shape, gelu0=False, outs=None):
         """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs).
         outs: per segment, None or a contiguous (M, n) BF16 tensor the segment's output is written to (e.g. a row of a
         preallocated key / value cache)."""
         M, dev = acc.shape[0], acc.device
-        ys = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) if outs is None or outs[i] is None else outs[i]
-              for i, n in enumerate(self.N)]
-        for y, n in zip(ys, self.N):
-            if y.shape != (M, n) or y.dtype != torch.bfloat16 or not y.is_contiguous():
-                raise ValueError(f'segment output {tuple(y.shape)} {y.dtype}: expected a contiguous ({M}, {n}) BF16 tensor')
+        ys = []
+        for i, s in enumerate(self.segments):
+            y = outs[i] if outs is not None and outs[i] is not None else torch.empty(M, s.width, dtype=torch.bfloat16, device=dev)
+            if y.shape != (M, s.width) or y.dtype != torch.bfloat16 or not y.is_contiguous():
+                raise ValueError(f'segment output {tuple(y.shape)} {y.dtype}: expected a contiguous ({M}, {s.width}) BF16 tensor')
+            ys.append(y)
         scaled = acc.dtype == torch.float32
-        segs = [(acc, c, None if scaled else r, v, bb, y, gelu0 and i == 0)
-                for i, (c, r, v, bb, y) in enumerate(zip(self.col0, self.rs_parts, self.sv_parts, self.bias_parts, ys))]
-        kernels.post_group(segs, acc.dtype, torch.bfloat16, b['scale'] if acc.dtype == torch.int32 else None, M,
-                           gelu_lut=kernels.gelu_table(dev) if gelu0 else None)
-        return [y.reshape(*shape[:-1], n) for y, n in zip(ys, self.N)]
+        s_tok = b['scale'] if acc.dtype == torch.int32 else None
+        if self.one_sided:                        # no output rotation: one plain epilogue per member
+            if gelu0:
+                raise ValueError('one-sided groups have no fused GELU epilogue')
+            for s, y in zip(self.segments, ys):
+                kernels.post(acc, s_tok, None if scaled else s.rs, None, s.bias, y, col0=s.col0)
+        else:
+            segs = [(acc, s.col0, None if scaled else s.rs, s.sv, s.bias, y, gelu0 and i == 0)
+                    for i, (s, y) in enumerate(zip(self.segments, ys))]
+            kernels.post_group(segs, acc.dtype, torch.bfloat16, s_tok, M,
+                               gelu_lut=kernels.gelu_table(dev) if gelu0 else None)
+        return [y.reshape(*shape[:-1], s.width) for s, y in zip(self.segments, ys)]
 
+    # --------------------------------------------------------------------------------------------------- runs
     def run(self, x):
+        """All members' outputs for input x."""
         x2 = self.prep(x)
-        if not self.a8:
-            return self.run_float(x2, x.shape)
-        b = self.quantize(x2)
-        outs = self.posts(self.product(b), b, x.shape)
+        if self.a8:
+            b = self.quantize(x2)
+            outs = self.posts(self.product(b), b, x.shape)
+        else:
+            outs = self.run_float(x2, x.shape)
         STATS['group_runs'] += 1
         return outs
 
@@ -169,48 +260,58 @@ class Group:
         (tcq_gemm_bf16). Expert: z = acc * rs in FP32; prefill: the product rounded to BF16, scaled by rs in the epilogue
         (modules.py:117-144)."""
         M, dev = x2.shape[0], x2.device
-        h = torch.empty(M, self.K, dtype=torch.bfloat16, device=dev)
-        kernels.rht(x2, self.su, h)
+        h = kernels.rht(x2, self.su, torch.empty(M, self.K, dtype=torch.bfloat16, device=dev))
         W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.bfloat16, device=dev))
         if self.small:
             acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.float32, device=dev), sw=self.rs)
         else:
             acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.bfloat16, device=dev))
-        outs = self.posts(acc, None, shape)
-        STATS['group_runs'] += 1
-        return outs
+        return self.posts(acc, None, shape)
 
     def get(self, x, index):
-        if self.x is not x:
-            if self.x is not None:
+        """Member index's output for input x. The first member called with a new input runs the group; the others take
+        their slice of that run. A member asking again, or asking with another input, starts a new run (regroup_misses
+        counts runs that replaced unfinished ones)."""
+        p = self.pending
+        if p is None or p.x is not x or index not in p.waiting:
+            if p is not None:
                 STATS['regroup_misses'] += 1
-            self.outs = self.run(x)
-            self.x = x
-            self.served = 0
-        out = self.outs[index]
-        self.served += 1
-        if self.served == len(self.layers):
-            self.x = self.outs = None
+            p = self.pending = _Pending(x, self.run(x), index)
+        else:
+            p.waiting.discard(index)
+        out = p.outs[index]
+        if not p.waiting:
+            self.pending = None
         return out
 
 
 class KLinear(torch.nn.Module):
-    """One member of a Group as an nn.Linear replacement (modules.py:158-167)."""
+    """One member of a Group as an nn.Linear replacement (modules.py:158-167): in_features / out_features / layer_name of
+    its layer, and an empty BF16 weight buffer the model reads only for its dtype."""
 
     def __init__(self, group, index):
         super().__init__()
-        self.group, self.index = [group], index                 # list: keeps the group out of the module tree
-        L = group.layers[index]
-        self.in_features, self.out_features, self.layer_name = L.n, L.m, L.name
-        self.register_buffer('weight', torch.empty(0, dtype=torch.bfloat16, device=L.su.device), persistent=False)
+        layer = group.layers[index]
+        self.group = [group]                     # a list keeps the group out of the module tree
+        self.index = index
+        self.in_features, self.out_features, self.layer_name = layer.n, layer.m, layer.name
+        self.register_buffer('weight', torch.empty(0, dtype=torch.bfloat16, device=layer.su.device), persistent=False)
 
     def forward(self, x):
-        return self.group[0].get(x, self.index)
+        (group,) = self.group
+        return group.get(x, self.index)
+
+
+# ---------------------------------------------------------------------------------------------------- fused MLPs
+def _first_half(group, x):
+    """Rotate + quantize the MLP input and run the first product: (FP32 z, the quantized-input buffers)."""
+    b = group.quantize(group.prep(x))
+    return group.product(b), b
 
 
 class KGatedMLP(torch.nn.Module):
-    """Gemma MLP down(gelu(gate(x)) * up(x)) with the middle fused (modules.py:170-189): rotate + quantize, product, middle
-    (tcq_mid2, or postg + pre2 with FUSE['split']), product, scale + rotate."""
+    """Gemma MLP down(gelu(gate(x)) * up(x)) with the middle fused (modules.py:170-189): rotate + quantize, product,
+    middle (tcq_mid2, or postg + pre2 with FUSE['split']), product, scale + rotate."""
 
     def __init__(self, gate_up, down):
         super().__init__()
@@ -219,22 +320,18 @@ class KGatedMLP(torch.nn.Module):
 
     def forward(self, x):
         gu, down = self.groups
-        b = gu.quantize(gu.prep(x))
-        acc = gu.product(b)
+        acc, b = _first_half(gu, x)
         M, dev = acc.shape[0], acc.device
         b2 = down.buffers(M, dev)
-        scaled = acc.dtype == torch.float32
+        s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], gu.rs)
         if FUSE['split']:
-            g = torch.empty(M, gu.N[0], dtype=torch.bfloat16, device=dev)
-            u = torch.empty_like(g)
-            segs =[(acc, gu.col0[0], None if scaled else gu.rs_parts[0], gu.sv_parts[0], None, g, True),
-                    (acc, gu.col0[1], None if scaled else gu.rs_parts[1], gu.sv_parts[1], None, u, False)]
-            kernels.post_group(segs, acc.dtype, torch.bfloat16, None if scaled else b['scale'], M,
-                               gelu_lut=kernels.gelu_table(dev))
+            g, u = (torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in gu.N)
+            segs = [(acc, s.col0, None if rs is None else s.rs, s.sv, None, y, i == 0)
+                    for i, (s, y) in enumerate(zip(gu.segments, (g, u)))]
+            kernels.post_group(segs, acc.dtype, torch.bfloat16, s_tok, M, gelu_lut=kernels.gelu_table(dev))
             kernels.pre2(g, u, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
         else:
-            kernels.mid2(acc, None if scaled else b['scale'], None if scaled else gu.rs, gu.sv, down.su, q=b2['q'],
-                         q4=b2['q4'], scale=b2['scale'])
+            kernels.mid2(acc, s_tok, rs, gu.sv, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
         STATS['fused_mlps'] += 1
         return down.posts(down.product(b2), b2, x.shape)[0]
 
@@ -248,15 +345,13 @@ class KPlainMLP(torch.nn.Module):
         self.fc1, self.fc2 = KLinear(fc1, 0), KLinear(fc2, 0)
 
     def forward(self, x):
-        g1, g2 = self.groups
-        b = g1.quantize(g1.prep(x))
-        acc = g1.product(b)
-        b2 = g2.buffers(acc.shape[0], acc.device)
-        scaled = acc.dtype == torch.float32
-        kernels.mid1(acc, None if scaled else b['scale'], None if scaled else g1.rs, g1.sv, g1.bias, g2.su, q=b2['q'],
-                     q4=b2['q4'], scale=b2['scale'])
+        first, second = self.groups
+        acc, b = _first_half(first, x)
+        b2 = second.buffers(acc.shape[0], acc.device)
+        s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], first.rs)
+        kernels.mid1(acc, s_tok, rs, first.sv, first.bias, second.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
         STATS['fused_mlps'] += 1
-        return g2.posts(g2.product(b2), b2, x.shape)[0]
+        return second.posts(second.product(b2), b2, x.shape)[0]
 
 
 class KDecoderLayer(torch.nn.Module):
@@ -296,6 +391,11 @@ class KDecoderLayer(torch.nn.Module):
             return b if x is ret else None
         return b if (not x2.is_inference() and x2._version == ver) else None
 
+    @staticmethod
+    def _unscaled(acc, b, group):
+        """(token scales, row scales) the epilogue applies to acc: none for FP32 z, else the quantizer's and the group's."""
+        return (None, None) if acc.dtype == torch.float32 else (b['scale'], group.rs)
+
     def forward(self, x, cache_k=None, cache_v=None, causal_offset=None, kv_out=None):
         """kv_out: None, or (k, v) contiguous (M, head_dim) BF16 tensors that this call's keys / values are written to by
         the q/k/v epilogue itself (the rows of a preallocated cache); they are then the returned k, v."""
@@ -320,24 +420,21 @@ class KDecoderLayer(torch.nn.Module):
         z = og.product(b2)
         x3 = torch.empty_like(x2)
         b3 = gu.buffers(M, dev)
-        sc = z.dtype == torch.float32
-        kernels.post_add_norm_pre(z, None if sc else b2['scale'], None if sc else og.rs, og.sv, og.bias, x2, x3, n2.weight, n2.eps,
-                                  gu.su, q=b3['q'], q4=b3['q4'], scale=b3['scale'])
+        kernels.post_add_norm_pre(z, *self._unscaled(z, b2, og), og.sv, og.bias, x2, x3, n2.weight, n2.eps, gu.su, q=b3['q'],
+                                  q4=b3['q4'], scale=b3['scale'])
         acc = gu.product(b3)
         b4 = dn.buffers(M, dev)
-        sc = acc.dtype == torch.float32
-        kernels.mid2(acc, None if sc else b3['scale'], None if sc else gu.rs, gu.sv, dn.su, q=b4['q'], q4=b4['q4'], scale=b4['scale'])
+        kernels.mid2(acc, *self._unscaled(acc, b3, gu), gu.sv, dn.su, q=b4['q'], q4=b4['q4'], scale=b4['scale'])
         z4 = dn.product(b4)
         x4 = torch.empty_like(x2)
-        sc = z4.dtype == torch.float32
         nxt = self._next[0] if (self._next and FUSE['chain']) else None
         if nxt is None:
-            kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4)
+            kernels.post_add_norm_pre(z4, *self._unscaled(z4, b4, dn), dn.sv, dn.bias, x3, x4)
         else:
             nq, nn1 = nxt.groups[0], nxt.input_layernorm
             bn = nq.buffers(M, dev)
-            kernels.post_add_norm_pre(z4, None if sc else b4['scale'], None if sc else dn.rs, dn.sv, dn.bias, x3, x4,
-                                      nn1.weight, nn1.eps, nq.su, q=bn['q'], q4=bn['q4'], scale=bn['scale'])
+            kernels.post_add_norm_pre(z4, *self._unscaled(z4, b4, dn), dn.sv, dn.bias, x3, x4, nn1.weight, nn1.eps, nq.su,
+                                      q=bn['q'], q4=bn['q4'], scale=bn['scale'])
         out = x4.reshape(shape)
         if nxt is not None:
             nxt._handoff = (x4, None if x4.is_inference() else x4._version, out, bn)
@@ -349,67 +446,145 @@ class RefLinear(torch.nn.Module):
     """The layer by definition, one unfused step per launch (modules.py:209-219 runs tcq_format.reference_linear):
     a8 / INT8 table: h = fwht(x * su) in FP32 -> per-token INT8 -> exact int32 product with the decoded INT8 weight ->
     (acc * s) * rs -> fwht -> * sv (+ bias) -> BF16. a8=False: the FP32 rotated activations times the decoded weight of
-    `table` in FP64, * row scale, then the same output rotation. resident=False decodes on every call."""
+    `table` in FP64, * row scale, then the same output rotation. resident=False decodes on every call. GR00T records: a
+    column scale joins the rotate + quantize launch (tcq_pre_cs); a one-sided layer skips the output rotation."""
 
     def __init__(self, layer, a8=True, table='int8', resident=True):
         super().__init__()
         if table not in ('int8', 'fp16') or (a8 and table != 'int8'):
             raise ValueError('RefLinear: a8 needs the INT8 table; table is int8 or fp16')
+        if layer.col_scale is not None and not a8:
+            raise NotImplementedError('RefLinear: column scales are applied to quantized activations only')
         self.layer, self.a8, self.table, self.resident = [layer], a8, table, resident
         self.w8 = layer.w8_reference() if (table == 'int8' and resident) else None
         self.in_features, self.out_features, self.layer_name = layer.n, layer.m, layer.name
         self.register_buffer('weight', torch.empty(0, dtype=torch.bfloat16, device=layer.su.device), persistent=False)
 
     def forward(self, x):
-        L = self.layer[0]
+        (L,) = self.layer
         shape = x.shape
         x2 = x.reshape(-1, L.n).contiguous()
         if x2.dtype not in (torch.bfloat16, torch.float32, torch.float16):
             x2 = x2.float()
         M, dev = x2.shape[0], x2.device
-        h = torch.empty(M, L.n, dtype=torch.float32, device=dev)
-        kernels.rht(x2, L.su, h)
+        y = torch.empty(M, L.m, dtype=torch.bfloat16, device=dev)
         if self.a8:
             q = torch.empty(M, L.n, dtype=torch.int8, device=dev)
             s = torch.empty(M, dtype=torch.float32, device=dev)
-            kernels.quantize_rows(h, q, s)
+            if L.col_scale is None:
+                h = kernels.rht(x2, L.su, torch.empty(M, L.n, dtype=torch.float32, device=dev))
+                kernels.quantize_rows(h, q, s)
+            else:
+                kernels.pre(x2, L.su, q=q, scale=s, col_scale=L.col_scale)
             w8 = self.w8 if self.w8 is not None else L.w8_reference()
             acc = kernels.gemm_i8(q, w8, torch.empty(M, L.m, dtype=torch.int32, device=dev))
-            y = torch.empty(M, L.m, dtype=torch.bfloat16, device=dev)
             kernels.post(acc, s, L.rs, L.sv, L.bias, y)
         else:
+            h = kernels.rht(x2, L.su, torch.empty(M, L.n, dtype=torch.float32, device=dev))
             w = (self.w8 if self.w8 is not None else L.w8_reference()) if self.table == 'int8' else L.decode_f16()
             r = L.rs if self.table == 'int8' else L.row_scale.float()
             z = ((h.double() @ w.double().t()).float() * r[None, :]).contiguous()
-            y = torch.empty(M, L.m, dtype=torch.bfloat16, device=dev)
             kernels.post(z, None, None, L.sv, L.bias, y)
         return y.reshape(*shape[:-1], L.m)
 
 
+# ------------------------------------------------------------------------------------------------------- install
 def set_submodule(model, name, module):
     parent, _, leaf = name.rpartition('.')
     setattr(model.get_submodule(parent) if parent else model, leaf, module)
 
 
+def _norm_tensors(f):
+    """(parameter name path, attribute, key) of the fine-tuned norm entries norm::<module>::<attr> of a dense file."""
+    for key in sorted(f.keys()):
+        kind, _, rest = key.partition('::')
+        if kind == 'norm':
+            module, _, attr = rest.partition('::')
+            yield module, attr, key
+
+
 def apply_row_state(model, row):
     """The fine-tuned norm weights stored beside the packed file (dense.safetensors entries norm::<module>::<attr>,
-    modules.py:231-243). The reference's row-INT8 token embedding belongs to its private policy loader and is not applied."""
+    modules.py:227-243). The reference's row-INT8 token embedding belongs to its private policy loader and is not applied."""
     path = F.packed_path(row).with_name('dense.safetensors')
     if not path.exists():
         return 0
     from safetensors import safe_open
-    norms = 0
+    count = 0
     with safe_open(str(path), framework='pt', device='cpu') as f:
-        for k in sorted(f.keys()):
-            if k.startswith('norm::'):
-                _, name, attr = k.split('::')
-                p = getattr(model.get_submodule(name), attr)
-                v = f.get_tensor(k)
-                if v.shape != p.shape or v.dtype != p.dtype:
-                    raise ValueError(f'{k}: {tuple(v.shape)} {v.dtype} does not match {tuple(p.shape)} {p.dtype}')
-                p.data.copy_(v)
-                norms += 1
-    return norms
+        for module, attr, key in _norm_tensors(f):
+            target, value = getattr(model.get_submodule(module), attr), f.get_tensor(key)
+            if (value.shape, value.dtype) != (target.shape, target.dtype):
+                raise ValueError(f'{key}: {tuple(value.shape)} {value.dtype} does not match {tuple(target.shape)} {target.dtype}')
+            target.data.copy_(value)
+            count += 1
+    return count
+
+
+def plan_groups(names, layers, families=GROUPS):
+    """Partition layer names into groups: the members of one family (of GROUPS by default) under one parent module form a
+    group when the whole family is there and reads one input (_shares_input); every other layer is a group of its own.
+    Groups come in the order of their first member."""
+    buckets = {}
+    for name in names:
+        parent, _, leaf = name.rpartition('.')
+        family = next((fam for fam in families if leaf in fam), None)
+        buckets.setdefault((parent, family) if family else (name, None), {})[leaf] = name
+    plan = []
+    for (_, family), members in buckets.items():
+        whole = family is not None and set(members) == set(family)
+        if whole and _shares_input([layers[members[leaf]] for leaf in family]):
+            plan.append([members[leaf] for leaf in family])
+        else:
+            plan.extend([n] for n in members.values())
+    return plan
+
+
+def _mode_of(runtime, streamed):
+    if runtime == 'resident':
+        return 'resident'
+    return 'fly' if (runtime == 'fly' or streamed) else 'chunk'
+
+
+def _fuse_mlps(model, heads):
+    """Replace GemmaMLP / SiglipMLP modules whose layers are grouped (heads: first member name -> group) by the fused
+    modules. Returns the count."""
+    fused = 0
+    for path, mod in list(model.named_modules()):
+        kind = type(mod).__name__
+        if kind == 'GemmaMLP':
+            gu, dn = heads.get(f'{path}.gate_proj'), heads.get(f'{path}.down_proj')
+            if gu is not None and len(gu.layers) == 2 and dn is not None and not gu.one_sided:
+                set_submodule(model, path, KGatedMLP(gu, dn))
+                fused += 1
+        elif kind == 'SiglipMLP':
+            f1, f2 = heads.get(f'{path}.fc1'), heads.get(f'{path}.fc2')
+            if f1 is not None and f2 is not None and not f1.one_sided:
+                set_submodule(model, path, KPlainMLP(f1, f2))
+                fused += 1
+    return fused
+
+
+def _fuse_decoder_layers(model, heads):
+    """Replace GemmaDecoderLayer modules whose attention projections are grouped and whose MLP is fused by
+    KDecoderLayer, then link consecutive fused layers of each stack. Returns the count."""
+    fused = 0
+    for path, mod in list(model.named_modules()):
+        if type(mod).__name__ != 'GemmaDecoderLayer':
+            continue
+        attn = f'{path}.self_attn'
+        qkv, og = heads.get(f'{attn}.q_proj'), heads.get(f'{attn}.o_proj')
+        if (qkv is None or len(qkv.layers) != 3 or og is None or not isinstance(getattr(mod, 'mlp', None), KGatedMLP)
+                or not hasattr(mod.self_attn, 'core')):
+            continue
+        set_submodule(model, path, KDecoderLayer(mod, qkv, og, mod.mlp))
+        fused += 1
+    for stack in model.modules():
+        if isinstance(stack, torch.nn.ModuleList):
+            for a, b in zip(stack[:-1], stack[1:]):
+                if isinstance(a, KDecoderLayer) and isinstance(b, KDecoderLayer):
+                    a._next = [b]
+    return fused
 
 
 def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', reference_resident=True, layers=None):
@@ -418,112 +593,65 @@ def install(policy, row=F.ROW, runtime='resident', a8=True, table='int8', refere
     if runtime not in RUNTIMES:
         raise ValueError(f'runtime {runtime!r} not in {RUNTIMES}')
     model = getattr(policy, '_model', policy)
+    rule = rule_for(model)
+    mods = dict(model.named_modules())
     if layers is None:
         stored = set(F.layer_names(row))
-        names = [n for n, m in model.named_modules() if n in stored and is_quantizable(n, m)]
+        names = [n for n, m in mods.items() if n in stored and rule.quantizable(n, m)]
     else:
         names = list(layers)
-    norms = apply_row_state(model, row) if layers is None else 0
-    info = dict(row=str(row), runtime=runtime, layers=len(names), norm_tensors=norms)
-    biases = {}
     for name in names:
-        m = model.get_submodule(name)
-        if not isinstance(m, torch.nn.Linear):
-            raise TypeError(f'{name}: {type(m).__name__} is not an nn.Linear')
-        if m.bias is not None:
-            biases[name] = m.bias.detach().float().clone()
+        if not isinstance(mods.get(name), torch.nn.Linear):
+            raise TypeError(f'{name}: {type(mods.get(name)).__name__} is not an nn.Linear')
+    # biases live in the model; a module on the meta device carries none (the layer keeps its own, if any)
+    biases = {n: mods[n].bias.detach().float().clone() for n in names
+              if mods[n].bias is not None and not mods[n].bias.is_meta}
+    info = dict(row=str(row), runtime=runtime, layers=len(names), policy=rule.name,
+                norm_tensors=apply_row_state(model, row) if layers is None else 0)
     if layers is None:
-        dev = next(model.parameters()).device
-        layers = F.load(row, device=dev, names=names, biases=biases)
+        layers = F.load(row, device=next(model.parameters()).device, names=names, biases=biases)
     else:
         for n, b in biases.items():
             if layers[n].bias is None:
                 layers[n].bias = b.to(layers[n].su.device).contiguous()
     if runtime == 'dense':
         for name in names:
-            m = model.get_submodule(name)
             w = layers[name].dense(table)
-            if m.weight.shape != w.shape:
-                raise ValueError(f'{name}: weight {tuple(m.weight.shape)} != {tuple(w.shape)}')
-            m.weight.data.copy_(w.to(m.weight.dtype))
+            if mods[name].weight.shape != w.shape:
+                raise ValueError(f'{name}: weight {tuple(mods[name].weight.shape)} != {tuple(w.shape)}')
+            mods[name].weight.data.copy_(w.to(mods[name].weight.dtype))
         return info
     if runtime == 'reference':
         for name in names:
             set_submodule(model, name, RefLinear(layers[name], a8=a8, table=table, resident=reference_resident))
         return info
-    groups, done = [], set()
-    for name in names:
-        if name in done:
-            continue
-        parent, _, leaf = name.rpartition('.')
-        members = [name]
-        for g in GROUPS:
-            if leaf in g:
-                cand = [f'{parent}.{x}' for x in g]
-                if all(c in layers for c in cand) and all(layers[c].n == layers[cand[0]].n and
-                                                          torch.equal(layers[c].su, layers[cand[0]].su) for c in cand):
-                    members = cand
-        part = part_of(name)
-        mode = 'resident' if runtime == 'resident' else 'fly' if (runtime == 'fly' or part != 'expert') else 'chunk'
-        group = Group([layers[n] for n in members], part, mode, a8=a8)
+    groups = []
+    for members in plan_groups(names, layers, rule.families):
+        part = rule.part(members[0])
+        group = Group([layers[n] for n in members], part, _mode_of(runtime, rule.streamed(part)), a8=a8)
         for i, n in enumerate(members):
             set_submodule(model, n, KLinear(group, i))
-            done.add(n)
-        if mode == 'resident':
+        if group.mode == 'resident':                        # the stream is not needed after load
             for L in group.layers:
-                L.bits_resident = False
-                L.bits = None                                   # resident: the bitstream is not needed after load
-                L._words = None
+                L.bits_resident, L.bits, L._words = False, None, None
         groups.append(group)
-    fused = 0
-    if a8 and FUSE['mlp']:
-        by_name = {g.layers[0].name: g for g in groups}
-        for g in list(groups):
-            parent, _, leaf = g.layers[0].name.rpartition('.')
-            if leaf == 'gate_proj' and len(g.layers) == 2 and f'{parent}.down_proj' in by_name:
-                if type(model.get_submodule(parent)).__name__ != 'GemmaMLP':
-                    raise TypeError(f'{parent}: expected a GemmaMLP, got {type(model.get_submodule(parent)).__name__}')
-                set_submodule(model, parent, KGatedMLP(g, by_name[f'{parent}.down_proj']))
-                fused += 1
-            elif leaf == 'fc1' and f'{parent}.fc2' in by_name:
-                if type(model.get_submodule(parent)).__name__ != 'SiglipMLP':
-                    raise TypeError(f'{parent}: expected a SiglipMLP, got {type(model.get_submodule(parent)).__name__}')
-                set_submodule(model, parent, KPlainMLP(g, by_name[f'{parent}.fc2']))
-                fused += 1
-    layers_fused = 0
-    if a8 and FUSE['mlp'] and FUSE['layer']:
-        by_name = {g.layers[0].name: g for g in groups}
-        for g in groups:
-            attn, _, leaf = g.layers[0].name.rpartition('.')
-            lname = attn.rpartition('.')[0]
-            if leaf != 'q_proj' or len(g.layers) != 3 or f'{attn}.o_proj' not in by_name:
-                continue
-            layer = model.get_submodule(lname)
-            mlp = getattr(layer, 'mlp', None)
-            if type(layer).__name__ != 'GemmaDecoderLayer' or not isinstance(mlp, KGatedMLP) or not hasattr(layer.self_attn, 'core'):
-                continue
-            set_submodule(model, lname, KDecoderLayer(layer, g, by_name[f'{attn}.o_proj'], mlp))
-            layers_fused += 1
-        for ml in model.modules():                     # link consecutive decoder layers of each stack
-            if isinstance(ml, torch.nn.ModuleList):
-                for a, b in zip(ml[:-1], ml[1:]):
-                    if isinstance(a, KDecoderLayer) and isinstance(b, KDecoderLayer):
-                        a._next = [b]
+    heads = {g.layers[0].name: g for g in groups}
+    fused = _fuse_mlps(model, heads) if (a8 and FUSE['mlp']) else 0
+    fused_layers = _fuse_decoder_layers(model, heads) if (a8 and FUSE['mlp'] and FUSE['layer']) else 0
     torch.cuda.synchronize()
     policy._tcq_groups = groups
-    info['fused_layers'] = layers_fused
-    info['fused_mlps'] = fused
-    info.update(groups=len(groups), shared_rotations=sum(len(g.layers) - 1 for g in groups),
-                modes={m: sum(1 for g in groups if g.mode == m) for m in ('resident', 'fly', 'chunk')})
+    modes = Counter(g.mode for g in groups)
+    info.update(fused_layers=fused_layers, fused_mlps=fused, groups=len(groups),
+                shared_rotations=sum(len(g.layers) for g in groups) - len(groups),
+                modes={m: modes.get(m, 0) for m in ('resident', 'fly', 'chunk')},
+                parts=dict(Counter(rule.part(n) for n in names)))
     return info
 
 
 def decode_chunk(policy):
-    """Operating point (iii): decode the action expert's layers once per action chunk, before the first denoising step
-    (modules.py:314-320). Returns the number of layers decoded."""
-    n = 0
-    for g in getattr(policy, '_tcq_groups', ()):
-        if g.mode == 'chunk':
-            g.decode()
-            n += len(g.layers)
-    return n
+    """Operating point (iii): decode the action-generating part's layers once per action chunk, before the first denoising
+    step (modules.py:314-320). Returns the number of layers decoded."""
+    chunked = [g for g in getattr(policy, '_tcq_groups', ()) if g.mode == 'chunk']
+    for g in chunked:
+        g.decode()
+    return sum(len(g.layers) for g in chunked)

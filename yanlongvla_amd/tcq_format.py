@@ -8,7 +8,10 @@ packed.safetensors: per quantized Linear `name`
   <name>::tlut       FP16 (512, 2) table, or (G, 512, 2) row-group tables (rows split evenly into G contiguous groups, the
                      GR00T variants of baselines/groot/simpler/main_row/scripts/groot_tcq.py:154-175)
   <name>::row_scale  FP16 (m,)
-  <name>::su, ::sv   int8 (n,), (m,) input / output signs of the two-sided block-Walsh rotation
+  <name>::su, ::sv   int8 (n,), (m,) input / output signs of the two-sided block-Walsh rotation; a layer without ::sv is
+                     one-sided (no output rotation: the GR00T "tcq" base, groot_tcq.py:187-191)
+  <name>::col_scale  FP16 (n,), optional: column scales of the GR00T row-group records (groot_tcq.py:178-184), applied to
+                     the rotated activations before they are quantized
 Derived at load (tcq_snap on the device): t8 = clamp(round(tlut * g)), g = float(1 / max|tlut|) * 127; rs = row_scale / g.
 Derived on demand: the repacked words of the fused products (tcq_repack), the INT8 weight (tcq_decode_i8).
 """
@@ -22,6 +25,7 @@ from . import kernels as K
 ROOT = Path(os.environ.get('VLA_ROOT', '/projects/yanlongvla'))        # project root holding models/pi05_tcq/<row>/
 ROW = 'tcq_raqft_d1'
 TENSORS = ('bits', 'tlut', 'row_scale', 'su', 'sv')
+OPTIONAL = ('sv', 'col_scale')
 
 
 def block_widths(width):
@@ -44,8 +48,12 @@ class Layer:
         self.tlut = tensors['tlut'].to(device).to(torch.float16).contiguous()
         self.row_scale = tensors['row_scale'].to(device).to(torch.float16).contiguous()
         self.su = tensors['su'].to(device).to(torch.int8).contiguous()
-        self.sv = tensors['sv'].to(device).to(torch.int8).contiguous()
-        self.m, self.n = self.sv.numel(), self.su.numel()
+        sv, cs = tensors.get('sv'), tensors.get('col_scale')
+        self.sv = None if sv is None else sv.to(device).to(torch.int8).contiguous()
+        self.col_scale = None if cs is None else cs.to(device).to(torch.float16).contiguous()
+        self.m, self.n = self.row_scale.numel(), self.su.numel()
+        if (self.sv is not None and self.sv.numel() != self.m) or (self.col_scale is not None and self.col_scale.numel() != self.n):
+            raise ValueError(f'{name}: sv / col_scale do not fit a ({self.m}, {self.n}) layer')
         if not (self.bits.shape == ((self.m // 16) * (self.n // 16), 32) and self.m % 16 == 0 and self.n % 16 == 0):
             raise ValueError(f'{name}: bits {tuple(self.bits.shape)} do not fit a ({self.m}, {self.n}) layer of 16 x 16 tiles')
         if self.tlut.dim() == 3:                      # row-group tables (G, 512, 2): rows split evenly into G groups
@@ -80,15 +88,25 @@ class Layer:
         K.decode_f16(self.bits, self.tlut, out)
         return out
 
+    @property
+    def one_sided(self):
+        return self.sv is None
+
     def dense(self, table='fp16'):
-        """Original-basis FP32 weight S_v H_m diag(r) Q H_n S_u (tcq_format.py:100-107), rotations by tcq_rht."""
+        """Original-basis FP32 weight S_v H_m diag(r) Q diag(c) H_n S_u (tcq_format.py:100-107; the column scale and the
+        one-sided form of groot_tcq.py:178-191), rotations by tcq_rht."""
         if table == 'fp16':
             q = self.decode_f16().float() * self.row_scale.float()[:, None]
         else:
             q = self.w8_reference().float() * self.rs[:, None]
+        if self.col_scale is not None:
+            q = q * self.col_scale.float()[None, :]
         w = torch.empty_like(q)
         K.rht(q, None, w)
-        w = (w * self.su.float()[None, :]).t().contiguous()
+        w = w * self.su.float()[None, :]
+        if self.sv is None:
+            return w
+        w = w.t().contiguous()
         wt = torch.empty_like(w)
         K.rht(w, None, wt)
         return (wt * self.sv.float()[None, :]).t().contiguous()
@@ -114,18 +132,26 @@ def load(row=ROW, device='cuda', names=None, biases=None):
     from safetensors import safe_open
     out = {}
     with safe_open(str(packed_path(row)), framework='pt', device='cpu') as f:
-        for name in (names or [k[:-len('::bits')] for k in f.keys() if k.endswith('::bits')]):
-            out[name] = Layer(name, {k: f.get_tensor(f'{name}::{k}') for k in TENSORS}, bias=(biases or {}).get(name),
-                              device=device)
+        keys = set(f.keys())
+        for name in (names or [k[:-len('::bits')] for k in keys if k.endswith('::bits')]):
+            t = {k: f.get_tensor(f'{name}::{k}') for k in TENSORS + ('col_scale',) if f'{name}::{k}' in keys}
+            missing = [k for k in TENSORS if k not in t and k not in OPTIONAL]
+            if missing:
+                raise KeyError(f'{name}: packed file lacks {missing}')
+            out[name] = Layer(name, t, bias=(biases or {}).get(name), device=device)
     return out
 
 
 def save(tensors, path):
-    """Write {name: {bits, tlut, row_scale, su, sv}} (CPU or device tensors) as a packed file."""
+    """Write {name: {bits, tlut, row_scale, su[, sv][, col_scale]}} (CPU or device tensors) as a packed file."""
     from safetensors.torch import save_file
     flat = {}
     for name, t in tensors.items():
-        for k in TENSORS:
+        for k in TENSORS + ('col_scale',):
+            if t.get(k) is None:
+                if k not in OPTIONAL:
+                    raise KeyError(f'{name}: {k} is required')
+                continue
             v = t[k].detach().cpu().clone()                  # members of a group may share one sign tensor
             flat[f'{name}::{k}'] = (v.view(torch.int16) if k == 'bits' else v).contiguous()
     path = Path(path)
