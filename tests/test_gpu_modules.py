@@ -68,6 +68,19 @@ def test_reflinear_float_activations(table):
     assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 4e-3            # BF16 output of an FP32 result
 
 
+def test_reflinear_int8_activations_fp16_table():
+    """a8 with the FP16 table (tcq_format.py:139-141): INT8 activations and scales bit-exact, FP64 sums on both sides in
+    their own orders, so the BF16 outputs agree to within one BF16 rounding of a few elements."""
+    from yanlongvla_amd.modules import RefLinear
+    L, ol = device_layer(256, 512, 22)
+    x = torch.randn(9, 512, device=DEV).bfloat16()
+    ref = O.reference_linear(x.float().cpu().numpy(), ol, a8=True, table='fp16')
+    y = bits16(RefLinear(L, a8=True, table='fp16')(x))
+    close = O.bf16_to_f32(ref)
+    assert np.mean(y == ref) > 0.99
+    assert np.linalg.norm(O.bf16_to_f32(y) - close) / np.linalg.norm(close) < 2e-3
+
+
 def qkv_layers(seed, K=1024, widths=(2048, 256, 256), bias=False):
     from yanlongvla_amd import tcq_format as F
     layers, oracles = [], []

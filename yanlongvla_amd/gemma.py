@@ -1,7 +1,9 @@
 """Gemma-shaped decoder stacks carrying the pi0.5 policy's module names, so that modules.install finds and swaps their
 quantized Linear layers exactly as in the policy (baselines/common.py:51-58 names; GemmaMLP class name asserted by install,
-modules.py:299-300). They drive the deploy path at the policy's shapes with synthetic weights; the layers between the
-quantized Linears (RMSNorm, attention, residuals) are plain PyTorch on the device.
+modules.py:299-300). They drive the deploy path at the policy's shapes with synthetic weights. Between the quantized
+Linears, RMSNorm and attention of BF16 device tensors run on this library's kernels (tcq_rmsnorm, tcq_attend), and the
+residual adds, GELU and products of the unfused MLP are PyTorch; host tensors (CPU twins in tests) take the same formulas
+in PyTorch.
 
   ExpertPolicy: the action expert (Gemma-300M-style: width 1024, MLP 4096 GeGLU, 8 query heads / 1 KV head of dim 256),
       action tokens attend to a fixed prefix KV cache and to each other; `sample_chunk` runs the flow-matching Euler steps.

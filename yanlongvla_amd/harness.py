@@ -76,6 +76,26 @@ def warm(fn, seconds, min_calls=1):
     return calls, time.perf_counter() - t0
 
 
+def action_table(actions, reference):
+    """Action agreement of every row with the reference row (parity.py:92-99): `actions` maps a row name to an array of
+    shape (observations, ...). Per row: observations whose actions are identical, the largest absolute difference, and the
+    relative error ||A - A_ref|| / ||A_ref|| per observation (max, mean) and pooled over all observations."""
+    ref = np.asarray(actions[reference], dtype=np.float64)
+    n = len(ref)
+    ref_norm = np.linalg.norm(ref.reshape(n, -1), axis=1)
+    table = {}
+    for row, a in actions.items():
+        a = np.asarray(a, dtype=np.float64)
+        if a.shape != ref.shape:
+            raise ValueError(f'{row}: actions {a.shape} != reference {ref.shape}')
+        d = a - ref
+        per = np.linalg.norm(d.reshape(n, -1), axis=1) / ref_norm
+        table[row] = dict(identical_observations=int(sum(np.array_equal(x, y) for x, y in zip(a, ref))),
+                          max_abs=float(np.abs(d).max()), rel_err_max=float(per.max()), rel_err_mean=float(per.mean()),
+                          rel_err_pooled=float(np.linalg.norm(d) / np.linalg.norm(ref)))
+    return table
+
+
 def classify(name):
     return next(c for c, pat in CLASSES if re.search(pat, name))
 

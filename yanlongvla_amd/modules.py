@@ -445,14 +445,15 @@ class KDecoderLayer(torch.nn.Module):
 class RefLinear(torch.nn.Module):
     """The layer by definition, one unfused step per launch (modules.py:209-219 runs tcq_format.reference_linear):
     a8 / INT8 table: h = fwht(x * su) in FP32 -> per-token INT8 -> exact int32 product with the decoded INT8 weight ->
-    (acc * s) * rs -> fwht -> * sv (+ bias) -> BF16. a8=False: the FP32 rotated activations times the decoded weight of
-    `table` in FP64, * row scale, then the same output rotation. resident=False decodes on every call. GR00T records: a
+    (acc * s) * rs -> fwht -> * sv (+ bias) -> BF16. a8 / FP16 table: the INT8 activations times the FP16-table weight in
+    FP64, then (z * s) * row scale. a8=False: the FP32 rotated activations times the decoded weight of `table` in FP64,
+    * row scale, then the same output rotation (tcq_format.py:130-148). resident=False decodes on every call. GR00T records: a
     column scale joins the rotate + quantize launch (tcq_pre_cs); a one-sided layer skips the output rotation."""
 
     def __init__(self, layer, a8=True, table='int8', resident=True):
         super().__init__()
-        if table not in ('int8', 'fp16') or (a8 and table != 'int8'):
-            raise ValueError('RefLinear: a8 needs the INT8 table; table is int8 or fp16')
+        if table not in ('int8', 'fp16'):
+            raise ValueError('RefLinear: table is int8 or fp16')
         if layer.col_scale is not None and not a8:
             raise NotImplementedError('RefLinear: column scales are applied to quantized activations only')
         self.layer, self.a8, self.table, self.resident = [layer], a8, table, resident
@@ -476,9 +477,13 @@ class RefLinear(torch.nn.Module):
                 kernels.quantize_rows(h, q, s)
             else:
                 kernels.pre(x2, L.su, q=q, scale=s, col_scale=L.col_scale)
-            w8 = self.w8 if self.w8 is not None else L.w8_reference()
-            acc = kernels.gemm_i8(q, w8, torch.empty(M, L.m, dtype=torch.int32, device=dev))
-            kernels.post(acc, s, L.rs, L.sv, L.bias, y)
+            if self.table == 'int8':
+                w8 = self.w8 if self.w8 is not None else L.w8_reference()
+                acc = kernels.gemm_i8(q, w8, torch.empty(M, L.m, dtype=torch.int32, device=dev))
+                kernels.post(acc, s, L.rs, L.sv, L.bias, y)
+            else:                                           # INT8 activations times the FP16-table weights, FP64 sums
+                z = (q.double() @ L.decode_f16().double().t()).float() * s[:, None] * L.row_scale.float()[None, :]
+                kernels.post(z.contiguous(), None, None, L.sv, L.bias, y)
         else:
             h = kernels.rht(x2, L.su, torch.empty(M, L.n, dtype=torch.float32, device=dev))
             w = (self.w8 if self.w8 is not None else L.w8_reference()) if self.table == 'int8' else L.decode_f16()
