@@ -670,7 +670,22 @@ def main():
     S1 = Stream(L1, x, fused=False)            # a single layer runs the latency plan (128 workgroups) and a separate rotation
     lat_med, lat_p95 = graph_latency(S1.step)
     am_med, am_p95 = graph_latency(S1.step, replays=50, warmup=5, per_graph=100)
-    note(f'single-layer latency timed: {lat_med:.4f} ms per graph replay')
+    # the same layer in one launch (tcq_layer_f16: rotation, decode-GEMV and rotation in one kernel), equal bit for bit
+    from yanlongvla_amd import kernels as K
+    y1 = torch.empty(1, M_DIM, dtype=torch.float16, device=dev)
+    z1 = torch.empty(1, M_DIM, dtype=torch.float32, device=dev)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def one_launch():
+        K.layer_f16(x, L1['su'], L1['wdev'], L1['tlut'][0], L1['row_scale'][0], L1['sv'][0], None, y1, z1, counter)
+    one_launch()
+    S1.step()
+    torch.cuda.synchronize()
+    if not torch.equal(y1, S1.y[0]):
+        raise SystemExit('the one-launch layer differs from the three-launch chain')
+    one_med, one_p95 = graph_latency(one_launch)
+    one_am_med, one_am_p95 = graph_latency(one_launch, replays=50, warmup=5, per_graph=100)
+    note(f'single-layer latency timed: {lat_med:.4f} ms per graph replay (three launches), {one_med:.4f} (one launch)')
     cpu = None if args.no_cpu else cpu_baseline(L, x, args.cpu_seconds)
     if cpu:
         note(f'CPU baseline timed: {cpu["value"]} {cpu["unit"]}')
@@ -708,9 +723,14 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1, 1024, true, tcq_gemv_post_layer, 2> (layer stream, output rotation fused)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_from_profile(nl),
                      'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
-        'single_layer_ms': {'graph_replay_median': round(lat_med, 5), 'graph_replay_p95': round(lat_p95, 5),
-                            'per_step_in_100_step_graph_median': round(am_med, 5),
-                            'per_step_in_100_step_graph_p95': round(am_p95, 5)},
+        'single_layer_ms': {'kernel': 'tcq_layer_f16 (one launch: input rotation, decode-GEMV, output rotation)',
+                            'graph_replay_median': round(one_med, 5), 'graph_replay_p95': round(one_p95, 5),
+                            'per_step_in_100_step_graph_median': round(one_am_med, 5),
+                            'per_step_in_100_step_graph_p95': round(one_am_p95, 5),
+                            'three_launches': {'graph_replay_median': round(lat_med, 5), 'graph_replay_p95': round(lat_p95, 5),
+                                               'per_step_in_100_step_graph_median': round(am_med, 5),
+                                               'per_step_in_100_step_graph_p95': round(am_p95, 5)},
+                            'one_launch_equals_three_launches': True},
         'max_rel_l2_vs_oracle': err,
         'cpu_baseline': cpu,
         'action_chunk': chunk,

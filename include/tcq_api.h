@@ -294,6 +294,20 @@ typedef struct tcq_gemv_post_layer {
 int tcq_gemv_f16_post(const tcq_gemv_post_layer* layers, int nlayers, const void* h16, const float* hscale, int M, int m, int n,
                       int y_dtype, tcq_stream_t stream);
 
+/* One whole layer in one launch, the FP16-table float path for a few tokens: y = walsh(walsh(x * su) Q^T * row_scale) * sv
+ * (+ bias), i.e. tcq_pre_h16 + tcq_gemv_f16 (its latency plan) + tcq_post step for step, so y equals that three-launch chain
+ * bit for bit. Replaces, for one layer, tcq_format.reference_linear(x, layer, a8=False, table='fp16')
+ * (tcq_format.py:125-148, the float definition the reference's parity checks use).
+ * x (M, n) F32 / BF16 / F16, M <= 16; wdev: tcq_repack words; tlut (512, 2) FP16; row_scale (m,) FP16; sv (m,); bias (m,)
+ * FP32 or NULL; y (M, m) of y_dtype (F16 / BF16 / F32).
+ * Workspace: z (M, m) FP32, 16-byte aligned (left holding walsh(x * su) Q^T * row_scale, the layer before its output
+ * rotation; row_scale must be 8-byte aligned) and
+ * *counter, one int that must be zero before the first call; every call leaves it zero, so the call can be captured in a
+ * graph and replayed. Calls that share a workspace must not overlap. */
+int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                  const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
+                  tcq_stream_t stream);
+
 /* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
  * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
 typedef struct tcq_gemm_seg {

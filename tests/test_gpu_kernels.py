@@ -300,6 +300,74 @@ def test_gemv_f16_layer(m, n, M, nl):
         assert rel_l2(y16.cpu().float().numpy(), ref) < 2e-3
 
 
+# one launch of a whole layer: the latency plan's split (4 / 8 / 16 waves per tile row), non-power-of-two widths (block
+# Walsh), several tokens, every input and output type
+@pytest.mark.parametrize('m,n,M,xdt,ydt', [(2048, 2048, 1, torch.float16, torch.float16), (2048, 2048, 4, torch.bfloat16, torch.float32),
+                                           (1024, 4096, 1, torch.float32, torch.bfloat16), (4096, 1024, 2, torch.float16, torch.float16),
+                                           (64, 1152, 3, torch.float16, torch.float32), (1536, 512, 1, torch.bfloat16, torch.bfloat16),
+                                           (256, 16384, 1, torch.float16, torch.float16)])
+def test_layer_f16_one_launch(m, n, M, xdt, ydt):
+    """tcq_layer_f16 equals the three-launch chain pre_h16 -> gemv_f16 -> post bit for bit (y and z), twice in a row on
+    different inputs (the second call finds the counter the first left at zero), and is within 2e-3 of the oracle's
+    reference_linear(table='fp16', a8=False)."""
+    from yanlongvla_amd import kernels as K
+    L = O.random_layer(m, n, 300 + m + M)
+    d = dev_layer(L)
+    bias = torch.randn(m, device=DEV) * 0.1
+    wdev = K.repack(d['bits'], m, n)
+    z = torch.empty(M, m, dtype=torch.float32, device=DEV)
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    rng = np.random.default_rng(m + n)
+    for call in range(2):
+        x = torch.from_numpy(rng.standard_normal((M, n)).astype(np.float32)).to(DEV).to(xdt)
+        y = torch.empty(M, m, dtype=ydt, device=DEV)
+        K.layer_f16(x, d['su'], wdev, d['tlut'], d['row_scale'], d['sv'], bias, y, z, counter)
+        h16 = torch.empty(M, n, dtype=torch.float16, device=DEV)
+        hs = torch.empty(M, dtype=torch.float32, device=DEV)
+        K.pre_h16(x, d['su'], h16, hs)
+        z3 = torch.empty(M, m, dtype=torch.float32, device=DEV)
+        K.gemv_f16(K.gemv_descriptors([(wdev, d['tlut'], d['row_scale'], z3)]), h16, hs, m, n)
+        y3 = torch.empty(M, m, dtype=ydt, device=DEV)
+        K.post(z3, None, None, d['sv'], bias, y3)
+        assert torch.equal(z, z3), call
+        assert torch.equal(y.view(torch.int16) if ydt != torch.float32 else y, y3.view(torch.int16) if ydt != torch.float32 else y3), call
+        assert int(counter.item()) == 0
+        ref = O.reference_linear(x.float().cpu().numpy(), L, a8=False, table='fp16', out_dtype='f32') + bias.cpu().numpy()
+        assert rel_l2(y.float().cpu().numpy(), ref) < 2e-3
+
+
+def test_layer_f16_graph_replays():
+    """A captured one-launch layer replays to the eager result several times, with eager calls in between."""
+    from yanlongvla_amd import kernels as K
+    L = O.random_layer(2048, 2048, 77)
+    d = dev_layer(L)
+    wdev = K.repack(d['bits'], 2048, 2048)
+    x = torch.randn(1, 2048, device=DEV).half()
+    z = torch.empty(1, 2048, device=DEV)
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    y = torch.empty(1, 2048, dtype=torch.float16, device=DEV)
+    step = lambda: K.layer_f16(x, d['su'], wdev, d['tlut'], d['row_scale'], d['sv'], None, y, z, counter)
+    step()
+    eager = y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(3):
+            step()
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager) and int(counter.item()) == 0
+        step()
+        assert torch.equal(y, eager)
+
+
 def test_gemv_f16_deterministic():
     from yanlongvla_amd import kernels as K
     L = O.random_layer(512, 2048, 7)

@@ -356,3 +356,338 @@ extern "C" int tcq_gemv_f16_post(const tcq_gemv_post_layer* layers, int nlayers,
     }
     return launch_status();
 }
+
+// --------------------------------------------------------------------------------------------------- one-launch layer
+// The whole FP16-table layer of a few tokens in one launch: the operations of tcq_pre_h16, tcq_gemv_f16 (latency plan: one
+// tile row per workgroup, KS waves splitting its chunks) and tcq_post, step for step and in the same order, so y equals the
+// three-launch chain bit for bit. Every workgroup issues the loads of its words, rotates the M input rows itself (a few KiB;
+// no workgroup waits for another), decodes and multiplies its tile row, stores its 16 rows of z with device-coherent
+// stores and counts itself in *counter. The workgroup whose count completes the grid reads the whole z after an acquire
+// fence, rotates it, writes y and sets the counter back to zero, so a graph replays it without any reset.
+// Rows of a power of two from 256 to 16 x (threads) run on registers (thread t owns elements [16 t, 16 t + 16), loaded and
+// stored as 16-byte vectors when VEC); other widths run the LDS block Walsh.
+struct LayerArgs {
+    const void* x;
+    const i8* su;
+    const void* wdev;
+    const u16* tlut;
+    const u16* row_scale;
+    const i8* sv;
+    const float* bias;
+    void* y;
+    float* z;
+    int* counter;
+};
+
+constexpr int LAYER_MAXCW = 4;      // chunks per wave: n <= 16384 with 16 waves
+
+template <int XDT>
+__device__ __forceinline__ float layer_x(const void* x, size_t i) {
+    if constexpr (XDT == TCQ_F32) return gptr((const float*)x)[i];
+    else if constexpr (XDT == TCQ_BF16) return bf16_to_f32(gptr((const u16*)x)[i]);
+    else return f16_to_f32(gptr((const u16*)x)[i]);
+}
+
+// 16 consecutive elements of a 16-byte aligned row as FP32 (exact for every input type)
+template <int XDT>
+__device__ __forceinline__ void layer_x16(const void* x, size_t i, float (&v)[16]) {
+    if constexpr (XDT == TCQ_F32) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const uint4_t a = gptr((const uint4_t*)((const float*)x + i))[h];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * h + k] = __uint_as_float(a[k]);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4_t a = gptr((const uint4_t*)((const u16*)x + i))[h];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const u16 b = (u16)(a[k >> 1] >> (16 * (k & 1)));
+                v[8 * h + k] = XDT == TCQ_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+            }
+        }
+    }
+}
+
+// reg_walsh16 for a row of K = 16 nt values held by threads t < nt of a possibly wider workgroup: the same stages in the
+// same order (lanes through shuffles, waves through xs); threads from nt on hold no values but meet every barrier.
+__device__ __forceinline__ void layer_walsh16(float (&v)[16], int K, float* xs) {
+    butterflies<4>(v);
+    const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
+    const bool on = t < nt;
+    // waves past the row skip the lane stages (their shuffles would only load the LDS crossbar)
+    const bool wave_on = __builtin_amdgcn_readfirstlane(t & ~63) < nt;
+    for (int m = 1; wave_on && m < nt && m < 64; m <<= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float p = __shfl_xor(v[k], m, 64);
+            v[k] = upper ? p - v[k] : v[k] + p;
+        }
+    }
+    for (int m = 64; m < nt; m <<= 1) {
+        if (on) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) xs[k * nt + t] = v[k];
+        }
+        __syncthreads();
+        if (on) {
+            const bool upper = t & m;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float p = xs[k * nt + (t ^ m)];
+                v[k] = upper ? p - v[k] : v[k] + p;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ bool reg_row(int K) { return (K & (K - 1)) == 0 && K >= 256 && K <= 16 * (int)blockDim.x; }
+
+template <int KS, int XDT, int YDT>
+__global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m, int n, int vec) {
+    constexpr int C = LAT_C, NE = 1024, ESH = 2 + ilog2(C);
+    __shared__ __attribute__((aligned(16))) u32 tab[NE * C];
+    __shared__ float red[16], hsl[16];
+    __shared__ int last;
+    extern __shared__ __attribute__((aligned(16))) u32 dyn[];
+    const int tiles_m = m >> 4, nch = (n + 255) >> 8, np = nch << 8, I = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const bool tok = lr < M;
+    const u32 cp4 = (u32)(lane & (C - 1)) << 2;
+    const int nchw = wave < nch ? (nch - 1 - wave) / KS + 1 : 0;
+    const rsrc_t W = make_rsrc(A.wdev, (u32)(tiles_m * nch) << 10);
+    uint4_t buf[LAYER_MAXCW];
+#pragma unroll
+    for (int j = 0; j < LAYER_MAXCW; ++j)
+        if (j < nchw)
+            buf[j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, (u32)lane << 4, (u32)(I * nch + wave + j * KS) << 10, 2));
+    const bool rin = vec && reg_row(n), rout = vec && reg_row(m);
+    const bool on_in = tid < (n >> 4), on_out = tid < (m >> 4);
+    // token 0's input, the input signs and the output signs / bias of the final rotation (used only by the workgroup that
+    // completes the count), all issued before the table fill
+    uint4_t xr[4], s4 = {0, 0, 0, 0}, sv4 = {0, 0, 0, 0};
+    float4_t b4[4];
+    if (rin && on_in) {
+#pragma unroll
+        for (int h = 0; h < (XDT == TCQ_F32 ? 4 : 2); ++h) xr[h] = gptr((const uint4_t*)((const char*)A.x + (size_t)16 * tid * (XDT == TCQ_F32 ? 4 : 2)))[h];
+        s4 = gptr((const uint4_t*)(A.su + 16 * tid))[0];
+    }
+    if (rout && on_out) {
+        sv4 = gptr((const uint4_t*)(A.sv + 16 * tid))[0];
+        if (A.bias) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) b4[h] = gptr((const float4_t*)(A.bias + 16 * tid))[h];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);                            // keep these loads ahead of the table fill
+
+    u16* hl = (u16*)dyn;                                          // h16 rows (M, np), zero from n on
+    float* row = (float*)(dyn + (M * np >> 1));                   // one FP32 row (input rotation, then output rotation)
+    float4_t* part = (float4_t*)(row + lds_words(max(n, m)));     // the KS waves' partial sums
+    fill_table<C, NE>(tab, A.tlut);
+    // input rotation of every token row, as tcq_pre_h16: h = walsh(x * su), hscale = 2^e with amax / 2^e in [2^14, 2^15)
+    for (int t = 0; t < M; ++t) {
+        float mx = 0.f;
+        if (rin) {
+            float v[16];
+            if (t > 0 && on_in) {
+                layer_x16<XDT>(A.x, (size_t)t * n + 16 * tid, v);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const u32 w = XDT == TCQ_F32 ? xr[k >> 2][k & 3] : xr[k >> 3][(k >> 1) & 3] >> (16 * (k & 1));
+                    v[k] = XDT == TCQ_F32 ? __uint_as_float(w) : XDT == TCQ_BF16 ? bf16_to_f32((u16)w) : f16_to_f32((u16)w);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v[k] * (float)(i8)(s4[k >> 2] >> (8 * (k & 3)));
+            layer_walsh16(v, n, row);
+            const float c = (float)(1.0 / __builtin_sqrt((double)n));
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                v[k] = v[k] * c;
+                if (on_in) mx = fmaxf(mx, fabsf(v[k]));
+            }
+            const float amax = block_max(mx, red);
+            int e = 0;
+            if (amax > 0.f && amax < __builtin_inff()) {
+                frexpf(amax, &e);
+                e -= 15;
+            }
+            if (tid == 0) hsl[t] = ldexpf(1.f, e);
+            if (on_in) {
+                uint4_t h[2];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) h[k >> 2][k & 3] = (u32)f32_to_f16(ldexpf(v[2 * k], -e)) | ((u32)f32_to_f16(ldexpf(v[2 * k + 1], -e)) << 16);
+                *(uint4_t*)(hl + t * np + 16 * tid) = h[0];
+                *(uint4_t*)(hl + t * np + 16 * tid + 8) = h[1];
+            }
+        } else {
+            for (int i = tid; i < n; i += blockDim.x) row[lds_slot(i)] = layer_x<XDT>(A.x, (size_t)t * n + i) * (float)gptr(A.su)[i];
+            __syncthreads();
+            block_walsh(row, n, [&](int i, float v) { row[lds_slot(i)] = v; mx = fmaxf(mx, fabsf(v)); });
+            const float amax = block_max(mx, red);
+            int e = 0;
+            if (amax > 0.f && amax < __builtin_inff()) {
+                frexpf(amax, &e);
+                e -= 15;
+            }
+            if (tid == 0) hsl[t] = ldexpf(1.f, e);
+            for (int i = tid; i < np; i += blockDim.x) hl[t * np + i] = i < n ? f32_to_f16(ldexpf(row[lds_slot(i)], -e)) : (u16)0;
+        }
+        __syncthreads();
+    }
+    const float hs = hsl[tok ? lr : 0];
+    const char* hb = (const char*)hl + (size_t)(lr * np + 16 * lg) * 2;
+
+    float4_t acc[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < LAYER_MAXCW; ++j) {
+        if (j >= nchw) break;
+        const int c = wave + j * KS;
+        half8_t B[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            B[q][0] = tok ? *(const half8_t*)(hb + 512 * c + 128 * q) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            B[q][1] = tok ? *(const half8_t*)(hb + 512 * c + 128 * q + 16) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32 hi = buf[j][q];
+            const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+            u32 v[8];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                v[p] = *(const u32*)((const char*)tab + ((((x >> 22) & (NE - 1)) << ESH) | cp4));
+                v[4 + p] = *(const u32*)((const char*)tab + ((((x >> 6) & (NE - 1)) << ESH) | cp4));
+            }
+            const uint4_t A0 = {v[0], v[1], v[2], v[3]}, A1 = {v[4], v[5], v[6], v[7]};
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A0), B[q][0], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A1), B[q][1], acc[1], 0, 0, 0);
+        }
+    }
+    part[wave * 64 + lane] = acc[0] + acc[1];
+    __syncthreads();
+    if (wave == 0 && tok) {                                       // sum the chunk phases in wave order, then the epilogue
+        float4_t a = part[lane];
+        for (int k = 1; k < KS; ++k) a += part[k * 64 + lane];
+        const int r0 = 16 * I + 4 * lg;
+        const u64 rs4 = *gptr((const u64*)(A.row_scale + r0));
+        uint4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = __float_as_uint((a[e] * hs) * f16_to_f32((u16)(rs4 >> (16 * e))));
+        // device-coherent store (sc1): visible to the workgroup that completes the count, wherever it runs
+        __builtin_amdgcn_raw_buffer_store_b128(o, make_rsrc(A.z, (u32)(M * m) * 4), (u32)(lr * m + r0) * 4, 0, 16);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) last = __hip_atomic_fetch_add(A.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;                                            // uniform over the workgroup
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (tid == 0) __hip_atomic_store(A.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // output rotation of every token row, as tcq_post: y = walsh(z) * sv (+ bias)
+    const rsrc_t Z = make_rsrc(A.z, (u32)(M * m) * 4);
+    for (int t = 0; t < M; ++t) {
+        if (rout) {
+            float v[16];
+            if (on_out) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint4_t a = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Z, (u32)(t * m + 16 * tid + 4 * h) * 4, 0, 16));
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) v[4 * h + k] = __uint_as_float(a[k]);
+                }
+            }
+            layer_walsh16(v, m, row);
+            if (on_out) {
+                const float c = (float)(1.0 / __builtin_sqrt((double)m));
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    v[k] = (v[k] * c) * (float)(i8)(sv4[k >> 2] >> (8 * (k & 3)));
+                    if (A.bias) v[k] = v[k] + b4[k >> 2][k & 3];
+                }
+                const size_t o = (size_t)t * m + 16 * tid;
+                if constexpr (YDT == TCQ_F32) {
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) gptr((float4_t*)((float*)A.y + o))[h] = float4_t{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                } else {
+                    uint4_t w[2];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const u32 a = YDT == TCQ_BF16 ? f32_to_bf16(v[2 * k]) : f32_to_f16(v[2 * k]);
+                        const u32 b = YDT == TCQ_BF16 ? f32_to_bf16(v[2 * k + 1]) : f32_to_f16(v[2 * k + 1]);
+                        w[k >> 2][k & 3] = a | (b << 16);
+                    }
+                    gptr((uint4_t*)((u16*)A.y + o))[0] = w[0];
+                    gptr((uint4_t*)((u16*)A.y + o))[1] = w[1];
+                }
+            }
+        } else {
+            for (int i = tid; i < m; i += blockDim.x)
+                row[lds_slot(i)] = __hip_atomic_load(A.z + (size_t)t * m + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            block_walsh(row, m, [&](int i, float v) { row[lds_slot(i)] = v; });
+            __syncthreads();
+            for (int i = tid; i < m; i += blockDim.x) {
+                float v = row[lds_slot(i)] * (float)gptr(A.sv)[i];
+                if (A.bias) v = v + gptr(A.bias)[i];
+                const size_t o = (size_t)t * m + i;
+                if constexpr (YDT == TCQ_F32) gptr((float*)A.y)[o] = v;
+                else if constexpr (YDT == TCQ_BF16) gptr((u16*)A.y)[o] = f32_to_bf16(v);
+                else gptr((u16*)A.y)[o] = f32_to_f16(v);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+extern "C" int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                             const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
+                             tcq_stream_t stream) {
+    if (!x || !su || !wdev || !tlut || !row_scale || !sv || !y || !z || !counter || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+    if (m % 16 || n % 16 || m > TCQ_MAX_WIDTH || n > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (M > 16 || m / 16 > 65535) return TCQ_ERR_UNSUPPORTED;
+    if ((size_t)(m / 16) * ((n + 255) / 256) * 1024 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    const int nch = (n + 255) / 256, ks = nch >= 16 ? 16 : nch >= 8 ? 8 : 4;   // the latency plan's split of a tile row
+    if (nch > ks * LAYER_MAXCW) return TCQ_ERR_UNSUPPORTED;
+    if ((uintptr_t)z % 16 || (uintptr_t)row_scale % 8) return TCQ_ERR_ALIGN;
+    const size_t dyn = (size_t)M * nch * 256 * 2 + (size_t)lds_words(n > m ? n : m) * 4 + (size_t)ks * 64 * 16;
+    if (dyn + 4096 * LAT_C + 256 > 160 * 1024) return TCQ_ERR_UNSUPPORTED;
+    const LayerArgs a{x, su, wdev, (const u16*)tlut, (const u16*)row_scale, sv, bias, y, z, counter};
+    const int xs = x_dtype == TCQ_F32 ? 4 : 2, ys = y_dtype == TCQ_F32 ? 4 : 2;
+    const int vec = (uintptr_t)x % 16 == 0 && (uintptr_t)su % 16 == 0 && (uintptr_t)sv % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+                    (uintptr_t)z % 16 == 0 && (uintptr_t)bias % 16 == 0 && (size_t)n * xs % 16 == 0 && (size_t)m * ys % 16 == 0;
+    const dim3 grid(m / 16), block(64 * ks);
+    const hipStream_t st = (hipStream_t)stream;
+#define LAYER_K(KS, XD, YD) launch_k(k_layer_f16<KS, XD, YD>, grid, block, dyn, st, a, M, m, n, vec)
+#define LAYER_Y(KS, XD)                                      \
+    switch (y_dtype) {                                       \
+        case TCQ_F16: LAYER_K(KS, XD, TCQ_F16); break;       \
+        case TCQ_BF16: LAYER_K(KS, XD, TCQ_BF16); break;     \
+        case TCQ_F32: LAYER_K(KS, XD, TCQ_F32); break;       \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+#define LAYER_X(KS)                                          \
+    switch (x_dtype) {                                       \
+        case TCQ_F16: LAYER_Y(KS, TCQ_F16); break;           \
+        case TCQ_BF16: LAYER_Y(KS, TCQ_BF16); break;         \
+        case TCQ_F32: LAYER_Y(KS, TCQ_F32); break;           \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+    switch (ks) {
+        case 4: LAYER_X(4); break;
+        case 8: LAYER_X(8); break;
+        default: LAYER_X(16); break;
+    }
+#undef LAYER_X
+#undef LAYER_Y
+#undef LAYER_K
+    return launch_status();
+}

@@ -308,6 +308,23 @@ def gemv_f16_post(desc, h16, hscale, m, n, y_dtype):
     call('tcq_gemv_f16_post', ptr(desc), desc.numel() // 7, ptr(h16), ptr(hscale), M, m, n, DTYPE[y_dtype], stream())
 
 
+def layer_f16(x, su, wdev, tlut, row_scale, sv, bias, y, z, counter):
+    """One launch of a whole FP16-table layer (tcq_layer_f16): y (M, m) = walsh(walsh(x * su) Q^T * row_scale) * sv (+ bias),
+    bit-identical to pre_h16 -> gemv_f16 -> post. z (M, m) float32 and counter (one int32, zero before the first call, left
+    zero) are its workspace."""
+    M, n = x.shape
+    m = row_scale.numel()
+    _contig(x, su, wdev, tlut, row_scale, sv, bias, y, z, counter)
+    if tuple(y.shape) != (M, m) or z.dtype != torch.float32 or z.numel() < M * m:
+        raise ValueError(f'layer_f16: y must be ({M}, {m}) and z hold {M * m} float32')
+    if su.numel() != n or sv.numel() != m or (bias is not None and bias.numel() != m) or _groups(tlut) != 1:
+        raise ValueError('layer_f16: su (n,), sv (m,), bias (m,) and one (512, 2) table')
+    if counter.dtype != torch.int32 or counter.numel() < 1:
+        raise ValueError('layer_f16: counter must be an int32 tensor')
+    call('tcq_layer_f16', ptr(x), _dt(x, (0, 1, 2), 'layer_f16 x'), ptr(su), ptr(wdev), ptr(tlut), ptr(row_scale), ptr(sv),
+         ptr(bias), ptr(y), DTYPE[y.dtype], M, m, n, ptr(z), ptr(counter), stream())
+
+
 _SEG = None
 
 
