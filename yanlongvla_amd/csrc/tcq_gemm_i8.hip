@@ -57,8 +57,10 @@ template <> struct MfmaOf<2> {                 // BF16
     }
 };
 
-// ESZ: element size (1 INT8, 2 BF16); K in elements.
-template <int ESZ, int TN, int TM, int WN, int WM, int NS, int ODT>
+// ESZ: element size (1 INT8, 2 BF16); K in elements. WAUX: cache policy of the weight loads, non-temporal (2) when a single
+// tile row of tokens reads every weight once, temporal (0) when several token tiles reread them (measured at M = 800,
+// N = 16384, K = 2048: 40.6 against 46.3 us per launch; the four token tiles of a weight tile run on one XCD and share its L2).
+template <int ESZ, int TN, int TM, int WN, int WM, int NS, int ODT, int WAUX = 2>
 __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const void* w_, const float* sa, const float* sw, void* out,
                                                           int ldo, int M, int N, int K_) {
     typedef typename MfmaOf<ESZ>::acc_t acc_t;
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const 
             if (blk < WBLK) {
                 const int row = n0 + 16 * blk + prow;
                 const u32 off = (row < N && k < K) ? (u32)row * (u32)K + (u32)k : RSRC_OOB;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(RW, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(RW, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, WAUX);
             } else {
                 const int row = m0 + 16 * (blk - WBLK) + prow;
                 const u32 off = (row < M && k < K) ? (u32)row * (u32)K + (u32)k : RSRC_OOB;
@@ -217,6 +219,12 @@ template <int ESZ, int TN, int TM, int WN, int WM, int NS>
 static void launch_gemm(int odt, hipStream_t st, const void* a, const void* w, const float* sa, const float* sw, void* out, int ldo,
                         int M, int N, int K) {
     const dim3 grid((N + TN - 1) / TN, (M + TM - 1) / TM), block(64 * WN * WM);
+    if (grid.y > 1) {                                   // token tiles share each weight tile: keep the weights in L2
+        if (odt == TCQ_I32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_I32, 0>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+        else if (odt == TCQ_F32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_F32, 0>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+        else launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_BF16, 0>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
+        return;
+    }
     if (odt == TCQ_I32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_I32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
     else if (odt == TCQ_F32) launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_F32>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
     else launch_k(k_gemm_i8<ESZ, TN, TM, WN, WM, NS, TCQ_BF16>, grid, block, 0, st, a, w, sa, sw, out, ldo, M, N, K);
