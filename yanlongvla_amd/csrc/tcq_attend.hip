@@ -136,7 +136,7 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
                 const int k0 = 32 * ks + lg + 8 * k2;                   // elements 2 k2, 2 k2 + 1: keys k0, k0 + 4
-                w[k2] = (u32)f32_to_bf16(ps[16 * rb + lr][k0]) | ((u32)f32_to_bf16(ps[16 * rb + lr][k0 + 4]) << 16);
+                w[k2] = bf16x2(ps[16 * rb + lr][k0], ps[16 * rb + lr][k0 + 4]);
             }
             A[rb][ks] = uint4_t{w[0], w[1], w[2], w[3]};
         }

@@ -23,12 +23,16 @@ typedef u16 u16x2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------------------------------------------------ conversions
 __device__ __forceinline__ float bf16_to_f32(u16 b) { return __uint_as_float(((u32)b) << 16); }
-__device__ __forceinline__ u16 f32_to_bf16(float f) {
-    u32 u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)0x7fc0;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (u16)(u >> 16);
+// FP32 -> BF16, round to nearest even, every NaN -> 0x7fc0 (reference kernels.py:20-25). The rounded word is formed
+// unconditionally and replaced for NaN (an unordered compare and a select): fewer instructions than testing the bits first.
+__device__ __forceinline__ u32 bf16_round_word(float f) {
+    const u32 u = __float_as_uint(f);
+    const u32 r = u + 0x7fffu + ((u >> 16) & 1u);
+    return __builtin_isnan(f) ? 0x7fc00000u : r;                 // the BF16 value sits in the high half
 }
+__device__ __forceinline__ u16 f32_to_bf16(float f) { return (u16)(bf16_round_word(f) >> 16); }
+// two values -> one word of two BF16 (a in the low half), the halves picked by one byte permute
+__device__ __forceinline__ u32 bf16x2(float a, float b) { return __builtin_amdgcn_perm(bf16_round_word(b), bf16_round_word(a), 0x07060302u); }
 __device__ __forceinline__ float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 // FP32 -> FP16 of an FP32 value. The value is pinned in a register first: otherwise the compiler may fuse a preceding multiply
 // and this conversion into one mixed-precision FMA (v_fma_mixlo_f16), a single rounding of the exact product, where the
@@ -522,9 +526,10 @@ __device__ __forceinline__ void tw_span_put(const Span<LE, ESZ>& r, float* xs, F
             d[m] = f(j, m, ESZ == 4 ? r.p[j][m] : (r.p[j][m >> 1] >> (16 * (m & 1))) & 0xffffu);
     }
 }
-// the span from its row slots to memory; g(v) gives the raw bits of value v (ESZ = 2: in the low 16 bits)
-template <int LE, int ESZ, class G>
-__device__ __forceinline__ void tw_span_store(void* row, float* xs, G&& g) {
+// the span from its row slots to memory as YDT (F32, BF16 or F16)
+template <int LE, int YDT>
+__device__ __forceinline__ void tw_span_store(void* row, float* xs) {
+    constexpr int ESZ = YDT == TCQ_F32 ? 4 : 2;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint4_t* o = (uint4_t*)((char*)row + ((size_t)w << (LE + 6)) * ESZ);
 #pragma unroll
@@ -533,7 +538,9 @@ __device__ __forceinline__ void tw_span_store(void* row, float* xs, G&& g) {
         uint4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            v[e] = ESZ == 4 ? g(d[e]) : (g(d[2 * e]) & 0xffffu) | (g(d[2 * e + 1]) << 16);
+            v[e] = YDT == TCQ_F32 ? __float_as_uint(d[e])
+                 : YDT == TCQ_BF16 ? bf16x2(d[2 * e], d[2 * e + 1])
+                                   : (u32)f32_to_f16(d[2 * e]) | ((u32)f32_to_f16(d[2 * e + 1]) << 16);
         *gptr(o + 64 * j + lane) = v;
     }
 }

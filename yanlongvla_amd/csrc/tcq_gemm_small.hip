@@ -194,8 +194,8 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
                     if (ODT == TCQ_F32) {
                         *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
                     } else {
-                        const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
-                        const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
+                        const u32 lo = bf16x2(v[0], v[1]);
+                        const u32 hi = bf16x2(v[2], v[3]);
                         *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
                     }
                 }
@@ -309,8 +309,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
         if (ODT == TCQ_F32) {
             *gptr((float4_t*)((float*)S.out + o)) = float4_t{v[0], v[1], v[2], v[3]};
         } else {
-            const u32 lo = (u32)f32_to_bf16(v[0]) | ((u32)f32_to_bf16(v[1]) << 16);
-            const u32 hi = (u32)f32_to_bf16(v[2]) | ((u32)f32_to_bf16(v[3]) << 16);
+            const u32 lo = bf16x2(v[0], v[1]);
+            const u32 hi = bf16x2(v[2], v[3]);
             *gptr((u64*)((u16*)S.out + o)) = (u64)lo | ((u64)hi << 32);
         }
     }

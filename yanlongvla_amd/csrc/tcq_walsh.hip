@@ -40,7 +40,7 @@ template <int DT> struct Elem16 {
     static __device__ __forceinline__ void st8(void* p, size_t i, const float (&v)[8]) {
         uint4_t a;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a[k] = (u32)cv(v[2 * k]) | ((u32)cv(v[2 * k + 1]) << 16);
+        for (int k = 0; k < 4; ++k) a[k] = DT == TCQ_BF16 ? bf16x2(v[2 * k], v[2 * k + 1]) : (u32)cv(v[2 * k]) | ((u32)cv(v[2 * k + 1]) << 16);
         gptr((uint4_t*)((u16*)p + i))[0] = a;
     }
 };
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_rht_tw(const void* x, int ldx
     for (int k = 0; k < E; ++k) v[k] = v[k] * c;
     tw_put<L, LE, 2>(v, xs);
     __syncthreads();
-    tw_span_store<LE, YS>((char*)y + tok * ldy * YS, xs, [](float f) { return f32_to_bits<YDT>(f); });
+    tw_span_store<LE, YDT>((char*)y + tok * ldy * YS, xs);
 }
 
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
