@@ -37,6 +37,12 @@ def bits16(y):
     return y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def differ(a, b):
+    """Where two bit arrays differ: count, first positions, their values (for the assertion message)."""
+    d = np.argwhere(a != b)
+    return f'{len(d)} of {a.size} differ; first {d[:6].tolist()}: {a[tuple(d[:6].T)].tolist()} vs {b[tuple(d[:6].T)].tolist()}'
+
+
 def test_layer_derived_tensors_and_dense():
     L, ol = device_layer(256, 1024, 3)
     assert np.array_equal(L.t8.cpu().numpy(), ol.t8)
@@ -137,7 +143,7 @@ def test_gated_mlp_bitexact(M, split):
     ub = O.reference_linear(xs, ou)
     prod = O.bf16_bits(O.bf16_to_f32(O.gelu_tanh_bf16(gb)) * O.bf16_to_f32(ub))
     ref = O.reference_linear(O.bf16_to_f32(prod), od)
-    assert np.array_equal(bits16(y), ref)
+    assert np.array_equal(bits16(y), ref), differ(bits16(y), ref)
 
 
 def small_expert(layers=2, prefix=64, seed=0):

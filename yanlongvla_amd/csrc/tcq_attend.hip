@@ -56,6 +56,13 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     auto visible_end = [&](int t) { return min(T, causal >= 0 ? causal + t + 1 : T); };   // keys j < end are visible to t
     const int jend = visible_end(min(t0 + TPB, M) - 1);                 // the group's last token sees the most keys
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
+    if (j0 >= jend) {                                                   // no key of the chunk is visible to the group: what the
+        for (int i = tid; i < AR * (AD + 2); i += AT) {                 // full computation gives, m = -inf, l = 0, o = 0
+            const int r = i / (AD + 2), d = i - r * (AD + 2), t = t0 + (r >> 3), h = r & 7;
+            if (h < H && t < M) part[(((size_t)t * NC + c) * H + h) * PS + d] = d == AD ? -__builtin_inff() : 0.f;
+        }
+        return;
+    }
     // value stage (64 rows x 256 dims, 8 granules of 16 bytes per thread) and query rows (AR x 256), issued first
     uint4_t vg[8];
 #pragma unroll
