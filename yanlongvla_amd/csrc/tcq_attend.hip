@@ -56,13 +56,8 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     auto visible_end = [&](int t) { return min(T, causal >= 0 ? causal + t + 1 : T); };   // keys j < end are visible to t
     const int jend = visible_end(min(t0 + TPB, M) - 1);                 // the group's last token sees the most keys
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
-    if (j0 >= jend) {                                                   // no key of the chunk is visible to the group: what the
-        for (int i = tid; i < AR * (AD + 2); i += AT) {                 // full computation gives, m = -inf, l = 0, o = 0
-            const int r = i / (AD + 2), d = i - r * (AD + 2), t = t0 + (r >> 3), h = r & 7;
-            if (h < H && t < M) part[(((size_t)t * NC + c) * H + h) * PS + d] = d == AD ? -__builtin_inff() : 0.f;
-        }
-        return;
-    }
+    if (j0 >= jend) return;                                             // no key of the chunk is visible to the group; the
+                                                                        // combine never reads its slots (visible_chunks)
     // value stage (64 rows x 256 dims, 8 granules of 16 bytes per thread) and query rows (AR x 256), issued first
     uint4_t vg[8];
 #pragma unroll
@@ -178,6 +173,13 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     }
 }
 
+// Chunks of token t that hold a key it sees: the combine merges only these. A chunk past them has m = -inf, l = 0 and o = 0
+// for t (weight 0), and adding 0 * 0 to a sum that starts at +0 changes no bit, so skipping them gives the same result;
+// k_attn_part does not compute the chunks no token of its group sees.
+__device__ __forceinline__ int visible_chunks(int NC, int T, int causal, int t) {
+    return causal >= 0 ? min(NC, (min(T, causal + t + 1) + KC - 1) / KC) : NC;
+}
+
 // grid M, CT = 1024 threads: thread (d, g) = (tid % 256, tid / 256) sums dim d of every head over the chunks c = g (mod 4);
 // wave h < H first merges head h's chunk statistics (lane = chunk). The four partial sums of a head add in the fixed order
 // ((g0 + g1) + g2) + g3, so the result depends only on NC. With su set, the BF16 row (H x 256) is rotated and quantized
@@ -185,8 +187,8 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 constexpr int MAXC = 256;        // most chunks a token may have in the combine (16384 keys)
 constexpr int CT = 1024, CG = CT / AD, CB = 4;   // threads, chunk groups, chunks per group held in registers per batch
 
-__global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4, int ldq,
-                                                     float* scale) {
+__global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su, i8* q8,
+                                                     int* q4, int ldq, float* scale) {
     extern __shared__ float lds[];
     __shared__ float red[CT / 64];
     __shared__ float wts[AH][MAXC];
@@ -195,14 +197,15 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     const int t = blockIdx.x, tid = threadIdx.x, d = tid & (AD - 1), g = tid / AD, lane = tid & 63, wave = tid >> 6, K = H * AD;
     const size_t cs = (size_t)H * PS;                          // stride between chunks
     const float* tb = part + (size_t)t * NC * cs;
+    const int NV = visible_chunks(NC, T, causal, t);
     constexpr int SR = MAXC / 64;
     float mv[SR], lv[SR];
     if (wave < H) {
 #pragma unroll
         for (int r = 0; r < SR; ++r) {
             const int c = 64 * r + lane;
-            mv[r] = c < NC ? tb[c * cs + wave * PS + AD] : -__builtin_inff();
-            lv[r] = c < NC ? tb[c * cs + wave * PS + AD + 1] : 0.f;
+            mv[r] = c < NV ? tb[c * cs + wave * PS + AD] : -__builtin_inff();
+            lv[r] = c < NV ? tb[c * cs + wave * PS + AD + 1] : 0.f;
         }
     }
     float v[CB][AH];
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
         for (int i = 0; i < CB; ++i) {
             const int c = c0 + g + CG * i;
 #pragma unroll
-            for (int h = 0; h < AH; ++h) v[i][h] = c < NC && h < H ? tb[c * cs + h * PS + d] : 0.f;
+            for (int h = 0; h < AH; ++h) v[i][h] = c < NV && h < H ? tb[c * cs + h * PS + d] : 0.f;
         }
     };
     load(0);
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
         for (int r = 0; r < SR; ++r) {
             const int c = 64 * r + lane;
             const float w = mv[r] == -__builtin_inff() ? 0.f : expf(mv[r] - mx);
-            if (c < NC) wts[wave][c] = w;
+            if (c < NV) wts[wave][c] = w;
             L = __builtin_fmaf(w, lv[r], L);
         }
 #pragma unroll
@@ -236,12 +239,12 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     float acc[AH];
 #pragma unroll
     for (int h = 0; h < AH; ++h) acc[h] = 0.f;
-    for (int c0 = 0; c0 < NC; c0 += CG * CB) {
+    for (int c0 = 0; c0 < NV; c0 += CG * CB) {
         if (c0) load(c0);
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
             const int c = c0 + g + CG * i;
-            if (c < NC) {
+            if (c < NV) {
 #pragma unroll
                 for (int h = 0; h < AH; ++h)
                     if (h < H) acc[h] = __builtin_fmaf(wts[h][c], v[i][h], acc[h]);
@@ -278,25 +281,26 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
 // chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
 // register engine) and quantized.
 constexpr int CW = 16;
-__global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4,
-                                                        int ldq, float* scale) {
+__global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su,
+                                                        i8* q8, int* q4, int ldq, float* scale) {
     extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
     const int t = blockIdx.x, tid = threadIdx.x, h = tid >> 6, lane = tid & 63, g = lane & 15, d0 = 4 * lane, K = H * AD;
     const size_t cs = (size_t)H * PS;
     const float* hb = part + (size_t)t * NC * cs + (size_t)h * PS;      // head h of chunk 0
+    const int NV = visible_chunks(NC, T, causal, t);
     constexpr int SC = MAXC / 16;
     typedef float f2_t __attribute__((ext_vector_type(2)));
     f2_t ml[SC];
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
         const int c = g + 16 * r;
-        ml[r] = c < NC ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
+        ml[r] = c < NV ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
     }
     float4_t v[CW];
 #pragma unroll
-    for (int i = 0; i < CW; ++i) v[i] = i < NC ? gptr((const float4_t*)(hb + i * cs + d0))[0] : float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < CW; ++i) v[i] = i < NV ? gptr((const float4_t*)(hb + i * cs + d0))[0] : float4_t{0.f, 0.f, 0.f, 0.f};
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
         const int c = g + 16 * r;
-        if (c < NC) {
+        if (c < NV) {
             const float w = ml[r].x == -__builtin_inff() ? 0.f : expf(ml[r].x - mx);
             if (lane < 16) wts[h][c] = w;                                // read back by this wave only: LDS keeps its order
             L = __builtin_fmaf(w, ml[r].y, L);
@@ -317,13 +321,13 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < CW; ++i) {
-        if (i < NC) {
+        if (i < NV) {
             const float w = wts[h][i];
 #pragma unroll
             for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, v[i][k], acc[k]);
         }
     }
-    for (int c = CW; c < NC; ++c) {
+    for (int c = CW; c < NV; ++c) {
         const float4_t vc = gptr((const float4_t*)(hb + c * cs + d0))[0];
         const float w = wts[h][c];
 #pragma unroll
@@ -349,14 +353,15 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
 // chunks straight from the partials; the 16 lanes of head h first merge its chunk statistics (lane = chunk mod 16, a
 // butterfly over the 16 lanes, so every lane holds the same total). With su, the BF16 row goes through the register Walsh
 // engine and the quantizer of the output projection's prologue.
-__global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int NC, int H, u16* o, const i8* su, i8* q8, int* q4,
-                                                          int ldq, float* scale) {
+__global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su,
+                                                          i8* q8, int* q4, int ldq, float* scale) {
     extern __shared__ float xs[];                                        // H * AD floats: cross-wave exchange
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
     const int t = blockIdx.x, tid = threadIdx.x, h = tid >> 4, g = tid & 15, d0 = 16 * g, K = H * AD;
     const size_t cs = (size_t)H * PS;
     const float* hb = part + (size_t)t * NC * cs + (size_t)h * PS;      // head h of chunk 0
+    const int NV = visible_chunks(NC, T, causal, t);
     // every load issued at entry: this lane's chunk statistics (chunks g, g + 16, ...) and the first 8 chunks' values
     constexpr int SC = MAXC / 16, VB = 8;
     typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -364,13 +369,13 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
         const int c = g + 16 * r;
-        ml[r] = c < NC ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
+        ml[r] = c < NV ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
     }
     float4_t v0[VB][4];
 #pragma unroll
     for (int i = 0; i < VB; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v0[i][q] = i < NC ? gptr((const float4_t*)(hb + i * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < 4; ++q) v0[i][q] = i < NV ? gptr((const float4_t*)(hb + i * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
@@ -380,7 +385,7 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
         const int c = g + 16 * r;
-        if (c < NC) {
+        if (c < NV) {
             const float w = ml[r].x == -__builtin_inff() ? 0.f : expf(ml[r].x - mx);
             wts[h][c] = w;                                               // read back by this wave only: LDS keeps its order
             L = __builtin_fmaf(w, ml[r].y, L);
@@ -393,21 +398,21 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
     for (int k = 0; k < 16; ++k) acc[k] = 0.f;
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-        if (i >= NC) break;
+        if (i >= NV) break;
         const float w = wts[h][i];
 #pragma unroll
         for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(w, v0[i][k >> 2][k & 3], acc[k]);
     }
-    for (int c0 = VB; c0 < NC; c0 += 4) {
+    for (int c0 = VB; c0 < NV; c0 += 4) {
         float4_t v[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                v[i][q] = c0 + i < NC ? gptr((const float4_t*)(hb + (c0 + i) * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
+                v[i][q] = c0 + i < NV ? gptr((const float4_t*)(hb + (c0 + i) * cs + d0))[q] : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (c0 + i >= NC) break;
+            if (c0 + i >= NV) break;
             const float w = wts[h][c0 + i];
 #pragma unroll
             for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(w, v[i][k >> 2][k & 3], acc[k]);
@@ -460,13 +465,13 @@ extern "C" int tcq_attend_q4(const void* q, const void* k_cache, const void* v_c
     const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
     if ((!o || (uintptr_t)o % 8 == 0) && (!su || (uintptr_t)su % 4 == 0))
         launch_k(k_attn_combine_w, dim3(M), dim3(H * 64), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part,
-                 NC, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
+                 NC, P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     else if ((H == 4 || H == 8) && oal)
-        launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC, H,
-                 (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
+        launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC,
+                 P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     else
-        launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC, H,
-                 (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
+        launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC,
+                 P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
     return launch_status();
 }
 
