@@ -207,6 +207,40 @@ __device__ __forceinline__ void reg_walsh16(float (&v)[16], int K, float* xs) {
     }
 }
 
+// reg_walsh16 for a row of K = 16 nt values held by threads t < nt of a possibly wider workgroup: the same stages in the
+// same order (lanes through shuffles, waves through xs); threads from nt on hold no values but meet every barrier.
+__device__ __forceinline__ void reg_walsh16_part(float (&v)[16], int K, float* xs) {
+    butterflies<4>(v);
+    const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
+    const bool on = t < nt;
+    // waves past the row skip the lane stages (their shuffles would only load the LDS crossbar)
+    const bool wave_on = __builtin_amdgcn_readfirstlane(t & ~63) < nt;
+    for (int m = 1; wave_on && m < nt && m < 64; m <<= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float p = __shfl_xor(v[k], m, 64);
+            v[k] = upper ? p - v[k] : v[k] + p;
+        }
+    }
+    for (int m = 64; m < nt; m <<= 1) {
+        if (on) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) xs[k * nt + t] = v[k];
+        }
+        __syncthreads();
+        if (on) {
+            const bool upper = t & m;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float p = xs[k * nt + (t ^ m)];
+                v[k] = upper ? p - v[k] : v[k] + p;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // Register + transpose Walsh engine: a power-of-two row of 2^L values held 2^LE per thread by 2^(L - LE) threads
 // (2 LE <= L <= 3 LE). Three layouts give the row index of register k in thread t:
 //   A (natural):  (t << LE) | k                                              -- register bits = index bits [0, LE)
@@ -421,19 +455,22 @@ __device__ __forceinline__ void cv16(const Raw16<4>& a, float (&v)[16]) {
 }
 
 // Rotate + quantize of a register row (values already signed): walsh, * c, per-token absmax, INT8 words (as k_pre).
+// Threads from N / 16 on (a workgroup wider than the row) hold no values: they meet the barriers and store nothing.
 __device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float* xs, float* red, i8* q, int* q4, int ldq,
                                                     float* scale, int tok) {
     const int t = threadIdx.x;
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
-    reg_walsh16(v, N, xs);
+    reg_walsh16_part(v, N, xs);
     float mx = 0.f;
+    const bool on = t < (N >> 4);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
         v[k] = v[k] * c;
-        mx = fmaxf(mx, fabsf(v[k]));
+        if (on) mx = fmaxf(mx, fabsf(v[k]));
     }
     const float sc = token_scale(block_max(mx, red));
     if (t == 0) scale[tok] = sc;
+    if (!on) return;
     u32 words[4];
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4)

@@ -411,40 +411,6 @@ __device__ __forceinline__ void layer_x16(const void* x, size_t i, float (&v)[16
     }
 }
 
-// reg_walsh16 for a row of K = 16 nt values held by threads t < nt of a possibly wider workgroup: the same stages in the
-// same order (lanes through shuffles, waves through xs); threads from nt on hold no values but meet every barrier.
-__device__ __forceinline__ void layer_walsh16(float (&v)[16], int K, float* xs) {
-    butterflies<4>(v);
-    const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
-    const bool on = t < nt;
-    // waves past the row skip the lane stages (their shuffles would only load the LDS crossbar)
-    const bool wave_on = __builtin_amdgcn_readfirstlane(t & ~63) < nt;
-    for (int m = 1; wave_on && m < nt && m < 64; m <<= 1) {
-        const bool upper = lane & m;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const float p = __shfl_xor(v[k], m, 64);
-            v[k] = upper ? p - v[k] : v[k] + p;
-        }
-    }
-    for (int m = 64; m < nt; m <<= 1) {
-        if (on) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) xs[k * nt + t] = v[k];
-        }
-        __syncthreads();
-        if (on) {
-            const bool upper = t & m;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const float p = xs[k * nt + (t ^ m)];
-                v[k] = upper ? p - v[k] : v[k] + p;
-            }
-        }
-        __syncthreads();
-    }
-}
-
 __device__ __forceinline__ bool reg_row(int K) { return (K & (K - 1)) == 0 && K >= 256 && K <= 16 * (int)blockDim.x; }
 
 template <int KS, int XDT, int YDT>
@@ -506,7 +472,7 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
             }
 #pragma unroll
             for (int k = 0; k < 16; ++k) v[k] = v[k] * (float)(i8)(s4[k >> 2] >> (8 * (k & 3)));
-            layer_walsh16(v, n, row);
+            reg_walsh16_part(v, n, row);
             const float c = (float)(1.0 / __builtin_sqrt((double)n));
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
@@ -605,7 +571,7 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
                     for (int k = 0; k < 4; ++k) v[4 * h + k] = __uint_as_float(a[k]);
                 }
             }
-            layer_walsh16(v, m, row);
+            reg_walsh16_part(v, m, row);
             if (on_out) {
                 const float c = (float)(1.0 / __builtin_sqrt((double)m));
 #pragma unroll
