@@ -368,6 +368,27 @@ def test_layer_f16_graph_replays():
         assert torch.equal(y, eager)
 
 
+@pytest.mark.parametrize('K,M,xdt', [(256, 1, torch.float16), (1024, 3, torch.bfloat16), (2048, 1, torch.float16),
+                                     (16384, 2, torch.float32), (1152, 2, torch.float16), (2048, 5, torch.bfloat16)])
+def test_pre_h16_bitexact(K, M, xdt):
+    """The float path's input rotation (register engine for power-of-two rows, LDS engine otherwise) against the oracle:
+    h = fwht(x * su), hscale = 2^e with amax / 2^e in [2^14, 2^15), h16 = FP16(h / hscale), bit for bit."""
+    from yanlongvla_amd import kernels as K_
+    rng = np.random.default_rng(K + M)
+    x32 = rng.standard_normal((M, K)).astype(np.float32)
+    su = (rng.integers(0, 2, K) * 2 - 1).astype(np.int8)
+    x = torch.from_numpy(x32).to(DEV).to(xdt)
+    h16 = torch.empty(M, K, dtype=torch.float16, device=DEV)
+    hs = torch.empty(M, dtype=torch.float32, device=DEV)
+    K_.pre_h16(x, T(su), h16, hs)
+    h = O.fwht(x.float().cpu().numpy() * su.astype(np.float32))
+    for t in range(M):
+        e = int(np.frexp(np.abs(h[t]).max())[1]) - 15
+        assert hs[t].item() == 2.0 ** e
+        want = np.ldexp(h[t], -e).astype(np.float16).view(np.uint16)
+        assert np.array_equal(h16[t].cpu().numpy().view(np.uint16), want), t
+
+
 def test_gemv_f16_deterministic():
     from yanlongvla_amd import kernels as K
     L = O.random_layer(512, 2048, 7)

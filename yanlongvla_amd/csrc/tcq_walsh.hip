@@ -217,6 +217,64 @@ __global__ void k_pre_h16(const void* x, const i8* su, u16* h16, float* hscale, 
     }, [&](int, float v) { return ldexpf(v, -e); });
 }
 
+// k_pre_h16 on the register engine for power-of-two rows of 256 .. 16384 (thread t < K / 16 owns elements [16 t, 16 t + 16),
+// 16-byte loads and stores): the same sign products, butterflies, constant, maximum and scaling as k_pre_h16.
+template <int XDT>
+__global__ __launch_bounds__(1024) void k_pre_h16_reg(const void* x, const i8* su, u16* h16, float* hscale, int K) {
+    extern __shared__ float xs[];                                      // K floats: the engine's exchange buffer
+    __shared__ float red[16];
+    const int tok = blockIdx.x, t = threadIdx.x;
+    const bool on = t < (K >> 4);
+    float v[16];
+    if (on) {
+        const size_t i0 = (size_t)tok * K + 16 * t;
+        if constexpr (XDT == TCQ_F32) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint4_t a = gptr((const uint4_t*)((const float*)x + i0))[h];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[4 * h + k] = __uint_as_float(a[k]);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint4_t a = gptr((const uint4_t*)((const u16*)x + i0))[h];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[8 * h + k] = Elem16<XDT>::cv((u16)(a[k >> 1] >> (16 * (k & 1))));
+            }
+        }
+        if (su) {
+            float sg[16];
+            cv16(raw16<1>(su + 16 * t, true), sg);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v[k] * sg[k];
+        }
+    }
+    reg_walsh16_part(v, K, xs);
+    const float c = (float)(1.0 / __builtin_sqrt((double)K));
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        v[k] = v[k] * c;
+        if (on) mx = fmaxf(mx, fabsf(v[k]));
+    }
+    const float amax = block_max(mx, red);
+    int e = 0;
+    if (amax > 0.f && amax < __builtin_inff()) {
+        frexpf(amax, &e);
+        e -= 15;
+    }
+    if (t == 0) hscale[tok] = ldexpf(1.f, e);
+    if (!on) return;
+    uint4_t o[2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        o[k >> 2][k & 3] = (u32)f32_to_f16(ldexpf(v[2 * k], -e)) | ((u32)f32_to_f16(ldexpf(v[2 * k + 1], -e)) << 16);
+    uint4_t* out = (uint4_t*)(h16 + (size_t)tok * K + 16 * t);
+    gptr(out)[0] = o[0];
+    gptr(out)[1] = o[1];
+}
+
 // ------------------------------------------------------------------------------------------------- per-row INT8 (no RHT)
 template <int XDT>
 __global__ void k_quantize_rows(const void* x, int ldx, i8* q, float* scale, int K, int vec) {
@@ -1220,6 +1278,13 @@ extern "C" int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h
     const size_t sh = row_lds(K);
     const int vec = K % 8 == 0 && al16(x) && al16(h16) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
+    if ((K & (K - 1)) == 0 && K >= 256 && vec && (!su || al16(su))) {     // register engine
+        const int nt = K / 16 < 64 ? 64 : K / 16;
+#define PREHR(XD, _) launch_k(k_pre_h16_reg<XD>, grid, dim3(nt), (size_t)K * sizeof(float), st, x, (const i8*)su, (u16*)h16, hscale, K)
+        DISPATCH_X(x_dtype, PREHR, 0)
+#undef PREHR
+        return launch_status();
+    }
 #define PREH(XD, _) launch_k(k_pre_h16<XD>, grid, block, sh, st, x, (const i8*)su, (u16*)h16, hscale, K, vec)
     DISPATCH_X(x_dtype, PREH, 0)
     return launch_status();
