@@ -482,7 +482,7 @@ def test_gelu_table_vs_cpu():
     nan = torch.isnan(allb)
     assert bool((torch.isnan(dev) == torch.isnan(cpu))[nan].all())
     diff = (dev.view(torch.int16) != cpu.view(torch.int16)) & ~nan
-    print(f'GELU table: {int(diff.sum())} of {int((~nan).sum())} finite BF16 inputs differ between device and CPU')
+    print(f'GELU table: {int(diff.sum())} of {int((~nan).sum())} finite BF16 inputs differ between device and CPU', flush=True)
     assert int(diff.sum()) < 65536 // 100
 
 
