@@ -52,6 +52,15 @@ enum tcq_dtype { TCQ_F32 = 0, TCQ_BF16 = 1, TCQ_F16 = 2, TCQ_I32 = 3, TCQ_I8 = 4
 #define TCQ_LDQ_TOKEN_BLOCKS (-16)
 #define TCQ_Q_TOKEN_BLOCKS 0x100
 
+/* K parts: the int32 sums of a small-M product split over P = 2 or 4 consecutive ranges of its 256-column K chunks (chunks
+ * [p * ceil(nch / P), ...) for part p), each written whole, part p at out + p * M * ldo elements. Flag of out_dtype
+ * (with TCQ_I32) for tcq_gemm_tcq / tcq_gemm_w8, and of acc_dtype (with TCQ_I32) for tcq_post_add_norm_pre, which adds the
+ * P parts (exact int32; part p at acc + p * M * lda) before scaling. A product of few tile rows then spreads over P times
+ * as many workgroups, and the consumer reads P partial rows instead of one. No reference counterpart (the reference's
+ * small-M products cover K in one block, kernels.py:365-427). */
+#define TCQ_K_PARTS2 0x200
+#define TCQ_K_PARTS4 0x400
+
 /* Library version string and the widest row the block-Walsh kernels take (16384). */
 const char* tcq_version(void);
 int tcq_max_width(void);
@@ -218,7 +227,8 @@ int tcq_norm_pre(const void* x, const void* w, float eps, const int8_t* su, int8
 /* Epilogue + residual + next prologue of a decoder layer, one launch: a = the tcq_post output of columns col0 .. col0 + N
  * (BF16 rounding), xout = bf16(x + a) (x, xout (M, N) BF16); then, when w is given, q / q4 / scale of
  * fwht(RMSNorm(xout) * su) as tcq_norm_pre. Extends kernels.post (deploy/tcq_kernels/kernels.py:221-230) with the residual
- * add and the following norm. N % 16 == 0. */
+ * add and the following norm. N % 16 == 0. acc_dtype TCQ_I32 may carry TCQ_K_PARTS2 / TCQ_K_PARTS4 (power-of-two N of
+ * 1024 .. 16384, 16-byte aligned operands; else TCQ_ERR_UNSUPPORTED). */
 int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, const float* s, const float* rs, const int8_t* sv,
                           const float* bias, const void* x, void* xout, const void* w, float eps, const int8_t* su, int8_t* q,
                           int32_t* q4, int ldq, float* scale, int M, int N, tcq_stream_t stream);
@@ -321,8 +331,8 @@ typedef struct tcq_gemm_seg {
 
 /* W2A8 fused decode + product for M <= 64 tokens: acc[t, i] = sum_k q[t, k] * w8[i, k], exact in int32, with w8 = sign *
  * t8[hash(state)] decoded from the words on the fly. out_dtype F32: z = (float(acc) * s[t]) * rs[i]; BF16: its rounding;
- * I32: acc. q (M, K) int8 row-major (or in the token-block layout when out_dtype carries TCQ_Q_TOKEN_BLOCKS), s (M,) FP32,
- * K a multiple of 16. segs: HOST array of nseg <= TCQ_MAX_SEGS descriptors
+ * I32: acc (with TCQ_K_PARTS2 / TCQ_K_PARTS4: its K parts, M <= 64). q (M, K) int8 row-major (or in the token-block
+ * layout when out_dtype carries TCQ_Q_TOKEN_BLOCKS), s (M,) FP32, K a multiple of 16. segs: HOST array of nseg <= TCQ_MAX_SEGS descriptors
  * (copied into the launch). Replaces kernels.gemm_tcq / k_gemm_tcq (deploy/tcq_kernels/kernels.py:403-427, 671-673),
  * which takes at most three concatenated layers (q/k/v or gate/up, table chosen by tile-row bounds) and MT <= 10 tokens. */
 int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,

@@ -565,6 +565,43 @@ def test_gemm_tcq_streaming_row_group_tables(G, M):
     assert np.array_equal(bits_of(z), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize('shapes,M,parts', [([(2048, 16384)], 1, 2), ([(2048, 2048)], 1, 2), ([(1024, 2048)], 50, 4),
+                                            ([(1024, 4096)], 50, 4), ([(256, 512)], 3, 4), ([(2048, 1024), (256, 1024)], 17, 2),
+                                            ([(2048, 16384)], 16, 4)])
+def test_gemm_k_parts(shapes, M, parts):
+    """K parts of the fused and the INT8-resident small-M products (streaming and workgroup plans): the int32 parts sum
+    to the exact product; a part whose chunk range is empty (K = 512 in 4 parts: 2 chunks) writes zeros."""
+    from yanlongvla_amd import kernels as K
+    layers, dev, t8s, q, s, ldz, ref = _small_product_case(shapes, M, 7 * M + parts)
+    n = layers[0].n
+    qd, sd = T(q), T(s)
+    exact = np.concatenate([O.int_matmul(q, L.w8_reference()) for L in layers], 1)
+    wdevs = [K.repack(d['bits'], L.m, n) for L, d in zip(layers, dev)]
+    w8s = []
+    for L, d, (t8, _) in zip(layers, dev, t8s):
+        w = torch.empty(L.m, n, dtype=torch.int8, device=DEV)
+        K.decode(d['bits'], t8, w)
+        w8s.append(w)
+    cols = np.cumsum([0] + [L.m for L in layers])[:-1]
+    nch = (n + 255) // 256
+    per = (nch + parts - 1) // parts
+    for resident in (False, True):
+        acc = torch.full((parts, M, ldz), -12345, dtype=torch.int32, device=DEV)
+        if resident:
+            K.gemm_w8_segments([(w, None, rs, acc[0, :, c:]) for w, (_, rs), c in zip(w8s, t8s, cols)], qd, sd, ldz, parts)
+        else:
+            K.gemm_tcq_segments([(w, t8, rs, acc[0, :, c:]) for w, (t8, rs), c in zip(wdevs, t8s, cols)], qd, sd, ldz, parts)
+        a = acc.cpu().numpy().astype(np.int64)
+        assert np.array_equal(a.sum(0), exact), resident
+        for p in range(parts):                                   # each part is the product over its own chunks
+            k0, k1 = min(n, 256 * per * p), min(n, 256 * per * (p + 1))
+            want = np.concatenate([O.int_matmul(q[:, k0:k1], L.w8_reference()[:, k0:k1]) if k1 > k0 else
+                                   np.zeros((M, L.m), np.int64) for L in layers], 1)
+            assert np.array_equal(a[p], want), (resident, p)
+    with pytest.raises(ValueError):                              # K parts are int32 sums only
+        K.gemm_tcq_segments([(wdevs[0], t8s[0][0], t8s[0][1], torch.empty(parts, M, ldz, device=DEV)[0])], qd, sd, ldz, parts)
+
+
 def test_gemm_small_rejects_bad_sizes():
     from yanlongvla_amd import kernels as K, _lib
     L = O.random_layer(32, 64, 1)

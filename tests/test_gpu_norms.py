@@ -60,6 +60,36 @@ def test_norm_pre_bitexact(M, K):
     assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr[:, 0])
 
 
+@pytest.mark.parametrize('M,N,parts', [(1, 2048, 2), (50, 1024, 4), (3, 4096, 2), (2, 8192, 4), (1, 16384, 2)])
+def test_post_add_norm_pre_k_parts(M, N, parts):
+    """int32 K parts in: the same outputs as their int32 sum in one accumulator (register + transpose engine up to 4096,
+    register engine beyond); a row the LDS path would take (N = 1152) is refused."""
+    from yanlongvla_amd import kernels as Kn, _lib
+    rng = np.random.default_rng(M + N + parts)
+    lda = N + 64
+    part = rng.integers(-2 ** 16, 2 ** 16, size=(parts, M, lda)).astype(np.int32)
+    s = T((rng.random(M) * 1e-3 + 1e-4).astype(np.float32))
+    rs = T((rng.random(N) * 1e-2).astype(np.float32))
+    sv, su = T(signs(rng, N)), T(signs(rng, N))
+    bias = T((rng.standard_normal(N) * 0.1).astype(np.float32))
+    x = bf16_dev(O.bf16_bits(rng.standard_normal((M, N)).astype(np.float32)))
+    w = bf16_dev(O.bf16_bits(rng.standard_normal(N).astype(np.float32) * 0.2))
+    outs = []
+    for acc in (T(part), T(part.sum(0, dtype=np.int32))):
+        xo = torch.empty_like(x)
+        q = torch.empty(M, N, dtype=torch.int8, device=DEV)
+        sc = torch.empty(M, dtype=torch.float32, device=DEV)
+        Kn.post_add_norm_pre(acc, s, rs, sv, bias, x, xo, w, 1e-6, su, q=q, scale=sc, col0=16)
+        outs.append((xo, q, sc))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    with pytest.raises(_lib.TcqError):
+        N2 = 1152
+        acc = torch.zeros(parts, M, N2, dtype=torch.int32, device=DEV)
+        xx = torch.zeros(M, N2, dtype=torch.bfloat16, device=DEV)
+        Kn.post_add_norm_pre(acc, s, torch.ones(N2, device=DEV), T(signs(rng, N2)), None, xx, torch.empty_like(xx))
+
+
 @pytest.mark.parametrize('kind', ['f32', 'i32'])
 @pytest.mark.parametrize('M,N,col0', [(1, 1024, 16), (50, 1024, 16), (300, 2048, 16), (5, 4096, 16), (2, 16384, 16),
                                       (50, 1024, 2), (3, 4096, 2)])

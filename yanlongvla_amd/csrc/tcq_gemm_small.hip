@@ -50,13 +50,17 @@ enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
 // rows (the activation fragments of its chunks, the bulk of the loads, then serve TR rows). MODE 0: decode from tcq_repack
 // words (RB: from the reference word layout, 64 bytes per tile, tiles row-major); MODE 1: resident INT8 weights. ODT: output
 // dtype (F32 scaled, BF16 scaled, I32 accumulators). QL: activation layout (ldq only for QL_WORDS).
-template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false>
+// KS > 1 (I32 only): K parts, blockIdx.z = part p takes chunks [p * ceil(nch / KS), ...) and writes at out + p * M * ldz.
+template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1>
 __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz,
                                                                     int ldq) {
+    static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
     const tcq_gemm_seg S = P.s[blockIdx.y];
-    const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
+    const int tiles_m = S.m >> 4, nch_all = (K + 255) >> 8;
+    const int c0 = KS > 1 ? (int)blockIdx.z * ((nch_all + KS - 1) / KS) : 0;
+    const int nch = KS > 1 ? min(nch_all, c0 + (nch_all + KS - 1) / KS) : nch_all;   // chunks c0 .. nch - 1
     const int I0 = blockIdx.x * TR;
     if (I0 >= tiles_m) return;                                            // uniform
     const int nw = blockDim.x >> 6;
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     constexpr int ESH = SM_C == 16 ? 6 : SM_C == 8 ? 5 : SM_C == 4 ? 4 : 2;
     const int tiles_n = K >> 4;
     rsrc_t Wr;
-    if (MODE == 0) Wr = make_rsrc(S.w, RB ? (u32)(tiles_m * tiles_n) << 6 : (u32)(tiles_m * nch) << 10);
+    if (MODE == 0) Wr = make_rsrc(S.w, RB ? (u32)(tiles_m * tiles_n) << 6 : (u32)(tiles_m * nch_all) << 10);
     else Wr = make_rsrc(S.w, (u32)S.m * (u32)K);
     const rsrc_t Q = make_rsrc(q, QL == QL_BLOCKS ? (u32)((M + 15) >> 4) * 16u * (u32)K
                                   : QL == QL_WORDS ? (u32)(K >> 2) * (u32)ldq * 4u : (u32)M * (u32)K);
@@ -86,7 +90,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
                     wa[r][0][j] = __builtin_amdgcn_alignbit(d, d, 16);
                 }
             } else if (MODE == 0) {
-                wa[r][0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
+                wa[r][0] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     for (int r = 0; r < TR; ++r)
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
-    if (wave < nch) load(wave);
+    if (c0 + wave < nch) load(c0 + wave);
     // epilogue scales, loaded with the operands (wave 0 stores)
     float4_t rsv[TR];
     float sv[NB];
@@ -134,8 +138,8 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     }
     if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
     __syncthreads();
-    for (int c = wave; c < nch; c += nw) {
-        if (c != wave) load(c);
+    for (int c = c0 + wave; c < nch; c += nw) {
+        if (c != c0 + wave) load(c);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -185,7 +189,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
             if (t < M) {
                 const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
                 if (ODT == TCQ_I32) {
-                    *gptr((int4v*)((int*)S.out + o)) = acc[r][b];
+                    *gptr((int4v*)((int*)S.out + (KS > 1 ? (size_t)blockIdx.z * M * ldz : 0) + o)) = acc[r][b];
                 } else {
                     const float st = sv[b];
                     float v[4];
@@ -214,12 +218,15 @@ constexpr int GV_C = 16;
 constexpr int GV_CMAX = 8;
 constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table fill per 16 waves)
 
-template <int ODT, bool QB, int WPR, int NW>
+template <int ODT, bool QB, int WPR, int NW, int KS = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
+    static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     constexpr int RPW = NW / WPR;
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
     const tcq_gemm_seg S = P.s[blockIdx.y];
-    const int tiles_m = S.m >> 4, nch = (K + 255) >> 8;
+    const int tiles_m = S.m >> 4, nch_all = (K + 255) >> 8;
+    const int c0 = KS > 1 ? (int)blockIdx.z * ((nch_all + KS - 1) / KS) : 0;
+    const int nch = KS > 1 ? min(nch_all, c0 + (nch_all + KS - 1) / KS) : nch_all;   // chunks c0 .. nch - 1 (K part z)
     const int I0 = blockIdx.x * RPW;
     if (I0 >= tiles_m) return;                                            // uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -227,13 +234,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     const int I = min(I0 + slot, tiles_m - 1);                            // a row past the end decodes the last (never stored)
     const int lr = lane & 15, lg = lane >> 4;
     const u32 cp4 = (u32)(lane & (GV_C - 1)) << 2;
-    const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch) << 10);
+    const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch_all) << 10);
     const rsrc_t Q = make_rsrc(q, QB ? 16u * (u32)K : (u32)M * (u32)K);
     uint4_t wa[GV_CMAX];
 #pragma unroll
     for (int i = 0; i < GV_CMAX; ++i) {
-        const int c = part + WPR * i;
-        if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch + c) << 10, 2));
+        const int c = c0 + part + WPR * i;
+        if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
     }
     auto loadB = [&](int c, int4v* B) {
 #pragma unroll
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
         }
     };
     int4v Bf[2][4];                                                        // activation fragments, two chunks in turn
-    loadB(part, Bf[0]);
+    loadB(c0 + part, Bf[0]);
     float4_t rsv = float4_t{0.f, 0.f, 0.f, 0.f};
     float sv = 0.f;
     if (ODT != TCQ_I32 && part == 0) {
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     int4v acc = int4v{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < GV_CMAX; ++i) {
-        const int c = part + WPR * i;
+        const int c = c0 + part + WPR * i;
         if (c >= nch) continue;                                            // uniform
         if (i + 1 < GV_CMAX && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
 #pragma unroll
@@ -301,7 +308,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     if (t >= M) return;
     const size_t o = (size_t)t * ldz + 16 * I + 4 * lg;
     if (ODT == TCQ_I32) {
-        *gptr((int4v*)((int*)S.out + o)) = acc;
+        *gptr((int4v*)((int*)S.out + (KS > 1 ? (size_t)blockIdx.z * M * ldz : 0) + o)) = acc;
     } else {
         float v[4];
 #pragma unroll
@@ -354,6 +361,40 @@ static void launch_gv(int wpr, int rows, int nseg, hipStream_t st, const SegPack
     }
 }
 
+// K parts (int32 sums only): grid.z = KS parts
+template <int MODE, int KS, int QL>
+static void launch_small_parts(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                               int ldo) {
+    if (M <= 16) launch_k(k_gemm_small<MODE, 1, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
+    else if (M <= 32) launch_k(k_gemm_small<MODE, 2, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
+    else launch_k(k_gemm_small<MODE, 4, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
+}
+template <bool QB, int KS>
+static void launch_gv_parts(int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
+                            int ldo) {
+    const int rpw = GV_NW / wpr;
+    const dim3 grid((rows + rpw - 1) / rpw, nseg, KS), block(64 * GV_NW);
+    switch (wpr) {
+        case 1: launch_k(k_gemv_tcq<TCQ_I32, QB, 1, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 2: launch_k(k_gemv_tcq<TCQ_I32, QB, 2, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 4: launch_k(k_gemv_tcq<TCQ_I32, QB, 4, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 8: launch_k(k_gemv_tcq<TCQ_I32, QB, 8, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemv_tcq<TCQ_I32, QB, 16, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+    }
+}
+template <int MODE, int KS>
+static void launch_parts(bool qb, int wpr, int rows, int nseg, int nw, hipStream_t st, const SegPack& P, const i8* q, const float* s,
+                         int M, int K, int ldo) {
+    if (MODE == 0 && wpr > 0) {
+        if (qb) launch_gv_parts<true, KS>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
+        else launch_gv_parts<false, KS>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
+        return;
+    }
+    const dim3 grid(rows, nseg, KS), block(64 * nw);
+    if (qb) launch_small_parts<MODE, KS, QL_BLOCKS>(grid, block, st, P, q, s, M, K, ldo);
+    else launch_small_parts<MODE, KS, QL_ROWS>(grid, block, st, P, q, s, M, K, ldo);
+}
+
 template <bool QB>
 static void launch_gv_odt(int odt, int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s,
                           int M, int K, int ldo) {
@@ -383,8 +424,11 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
                       tcq_stream_t stream) {
     if (!segs || !q || nseg <= 0 || M <= 0 || K <= 0 || ldo <= 0) return TCQ_ERR_ARG;
     const bool qb = odt & TCQ_Q_TOKEN_BLOCKS;                          // q in the token-block layout
-    odt &= ~TCQ_Q_TOKEN_BLOCKS;
+    if ((odt & TCQ_K_PARTS2) && (odt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
+    const int parts = (odt & TCQ_K_PARTS4) ? 4 : (odt & TCQ_K_PARTS2) ? 2 : 1;
+    odt &= ~(TCQ_Q_TOKEN_BLOCKS | TCQ_K_PARTS2 | TCQ_K_PARTS4);
     if (odt != TCQ_F32 && odt != TCQ_BF16 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
+    if (parts > 1 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (odt != TCQ_I32 && !s) return TCQ_ERR_ARG;
     if (nseg > TCQ_MAX_SEGS || M > 64) return TCQ_ERR_UNSUPPORTED;
     if (K % 16) return TCQ_ERR_SHAPE;
@@ -403,9 +447,19 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
         if (g.m > max_m) max_m = g.m;
     }
     if ((size_t)M * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if (parts > 1 && (size_t)parts * M * ldo >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
     hipStream_t st = (hipStream_t)stream;
     const i8* qq = (const i8*)q;
+    if (parts > 1) {                                   // K parts: each part a product over its chunks, int32 out
+        const int nchp = (nch + parts - 1) / parts, nwp = nchp < SM_MAXW ? nchp : SM_MAXW;
+        int tiles = 0;
+        for (int i = 0; i < nseg; ++i) tiles += segs[i].m / 16;
+        const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, M, nchp, tiles * parts) : 0;
+        if (parts == 2) launch_parts<MODE, 2>(qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
+        else launch_parts<MODE, 4>(qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
+        return launch_status();
+    }
     // two tile rows per workgroup when there are many (their activation fragments are then loaded once for both), at most 8
     // waves (the partial sums of both rows fit the LDS) and row-group tables that never split a pair
     int tiles = 0;

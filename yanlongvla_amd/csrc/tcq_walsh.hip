@@ -793,9 +793,11 @@ __global__ __launch_bounds__(512) void k_post_add_norm_pre(const void* acc, int 
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
 }
 
-// Accumulator chunk 16 t .. 16 t + 15 of a row (scaled like load_acc_row), loaded at kernel entry.
+// Accumulator chunk 16 t .. 16 t + 15 of a row (scaled like load_acc_row), loaded at kernel entry. int32 K parts (parts > 1,
+// part p at acc + p * pstride) are added in int32 first: the same sum as one part.
 template <int ADT>
-__device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st, const float* rs, float (&v)[16]) {
+__device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st, const float* rs, float (&v)[16], int parts = 1,
+                                          size_t pstride = 0) {
     if (ADT == TCQ_BF16) {
         const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
         const Raw16<4> r4 = raw16<4>(rs, true);
@@ -805,9 +807,19 @@ __device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st
 #pragma unroll
         for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
     } else {
-        const Raw16<4> a = raw16<4>((const u32*)acc + base, true);
+        Raw16<4> a = raw16<4>((const u32*)acc + base, true);
         if (ADT == TCQ_I32) {
+            Raw16<4> ap[3];
+#pragma unroll
+            for (int p = 1; p < 4; ++p)
+                if (p < parts) ap[p - 1] = raw16<4>((const u32*)acc + base + p * pstride, true);
             const Raw16<4> r4 = raw16<4>(rs, true);
+#pragma unroll
+            for (int p = 1; p < 4; ++p)
+                if (p < parts) {
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) a.r[k >> 2][k & 3] = (u32)((int)a.r[k >> 2][k & 3] + (int)ap[p - 1].r[k >> 2][k & 3]);
+                }
             float r[16];
             cv16(r4, r);
 #pragma unroll
@@ -1064,7 +1076,8 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw2(const void* acc, int
 template <int ADT>
 __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc, int lda, int col0, const float* s, const float* rs,
                                                                 const i8* sv, const float* bias, const u16* x, u16* xout, const u16* w,
-                                                                float eps, const i8* su, i8* q, int* q4, int ldq, float* scale, int N) {
+                                                                float eps, const i8* su, i8* q, int* q4, int ldq, float* scale, int N,
+                                                                int parts) {
     extern __shared__ float xs[];                                      // N floats: cross-wave exchange and chunk sums
     __shared__ float red[16];
     const int tok = blockIdx.x, t = threadIdx.x, i0 = 16 * t;
@@ -1081,7 +1094,7 @@ __global__ __launch_bounds__(1024) void k_post_add_norm_pre_reg(const void* acc,
         su0 = raw16<1>(su + i0, true);
     }
     float v[16];
-    acc_chunk<ADT>(acc, base, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 : nullptr, v);
+    acc_chunk<ADT>(acc, base, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 : nullptr, v, parts, (size_t)gridDim.x * lda);
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
     reg_walsh16(v, N, xs);
     float sg[16], b[16], xv[16];
@@ -1117,7 +1130,7 @@ template <int ADT, int L, int LE>
 __global__ __launch_bounds__(1 << (L - LE)) void k_post_add_norm_pre_tw(const void* acc, int lda, int col0, const float* s,
                                                                        const float* rs, const i8* sv, const float* bias, const u16* x,
                                                                        u16* xout, const u16* w, float eps, const i8* su, i8* q,
-                                                                       int* q4, int ldq, float* scale) {
+                                                                       int* q4, int ldq, float* scale, int parts) {
     constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
     extern __shared__ float xs[];                                      // lds_words(N) floats for the transposes, then N / 16 sums
     float* part = xs + lds_words(N);
@@ -1139,7 +1152,9 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_post_add_norm_pre_tw(const vo
     }
     float v[E];
 #pragma unroll
-    for (int h = 0; h < NP; ++h) acc_chunk<ADT>(acc, base + 16 * h, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 + 16 * h : nullptr, part16(v, h));
+    for (int h = 0; h < NP; ++h)
+        acc_chunk<ADT>(acc, base + 16 * h, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 + 16 * h : nullptr, part16(v, h), parts,
+                       (size_t)gridDim.x * lda);
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
     tw_walsh<L, LE>(v, xs);
     tw_to_natural<L, LE>(v, xs);
@@ -1597,6 +1612,11 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
                                      const int8_t* sv, const float* bias, const void* x, void* xout, const void* w, float eps,
                                      const int8_t* su, int8_t* q, int32_t* q4, int ldq, float* scale, int M, int N,
                                      tcq_stream_t stream) {
+    if ((acc_dtype & TCQ_K_PARTS2) && (acc_dtype & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
+    const int parts = (acc_dtype & TCQ_K_PARTS4) ? 4 : (acc_dtype & TCQ_K_PARTS2) ? 2 : 1;
+    acc_dtype &= ~(TCQ_K_PARTS2 | TCQ_K_PARTS4);
+    if (parts > 1 && acc_dtype != TCQ_I32) return TCQ_ERR_DTYPE;
+    if (parts > 1 && (size_t)parts * M * lda >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     if (!acc || !sv || !x || !xout || M <= 0 || N <= 0 || col0 < 0 || lda < col0 + N) return TCQ_ERR_ARG;
     if ((acc_dtype == TCQ_I32 && (!s || !rs)) || (acc_dtype == TCQ_BF16 && !rs)) return TCQ_ERR_ARG;
     if (w && (!su || !scale || (!q && !q4) || q4_bad(q4, ldq, M))) return TCQ_ERR_ARG;
@@ -1614,7 +1634,7 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     if ((N == 1024 || N == 2048 || N == 4096) && vec && svec && (!q || al16(q))) {
         const size_t tsh = (size_t)(lds_words(N) + N / 16) * sizeof(float);
 #define PANT(AD, L, LE) launch_k(k_post_add_norm_pre_tw<AD, L, LE>, dim3(M), dim3(1 << (L - LE)), tsh, st, acc, lda, col0, s, rs, \
-                                 (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale)
+                                 (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, parts)
 #define PANW(L, LE)                                      \
     switch (acc_dtype) {                                 \
         case TCQ_I32: PANT(TCQ_I32, L, LE); break;       \
@@ -1634,7 +1654,7 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     // register path: power-of-two rows of 1024 .. 16384 (one 16-element chunk per thread, at least one full wave), aligned
     if ((N & (N - 1)) == 0 && N >= 1024 && vec && svec && (!q || al16(q))) {
 #define PANR(AD) launch_k(k_post_add_norm_pre_reg<AD>, dim3(M), dim3(N / 16), (size_t)N * sizeof(float), st, acc, lda, col0, s, rs, \
-                          (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N)
+                          (const i8*)sv, bias, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, N, parts)
         switch (acc_dtype) {
             case TCQ_I32: PANR(TCQ_I32); break;
             case TCQ_F32: PANR(TCQ_F32); break;
@@ -1644,6 +1664,7 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
 #undef PANR
         return launch_status();
     }
+    if (parts > 1) return TCQ_ERR_UNSUPPORTED;         // K parts: register paths only
     // 512 threads at most: the side vectors the kernel loads ahead need more than the 128 registers of 1024-thread groups
     const dim3 grid(M), block(row_threads(M, N) < 512 ? row_threads(M, N) : 512);
     const size_t sh = norm_lds(N);

@@ -26,6 +26,9 @@ def _contig(*ts):
 # small-M products read it (out_dtype | Q_TOKEN_BLOCKS): every 16-token x 64-column activation fragment is one contiguous KiB.
 LDQ_TOKEN_BLOCKS = -16
 Q_TOKEN_BLOCKS = 0x100
+# K parts of a small-M product (include/tcq_api.h): int32 sums over 2 or 4 consecutive ranges of the 256-column K chunks, part
+# p at out + p * M * ldo; the fused epilogue post_add_norm_pre adds them. A product of few tile rows then fills the chip.
+K_PARTS = {2: 0x200, 4: 0x400}
 
 
 def token_blocks(M, K, device):
@@ -214,13 +217,23 @@ def norm_pre(x, w, eps, su, q=None, q4=None, scale=None):
 
 
 def post_add_norm_pre(acc, s, rs, sv, bias, x, xout, w=None, eps=0.0, su=None, q=None, q4=None, scale=None, col0=0):
-    """xout = bf16(x + post(acc ...)) and, with w, q / q4 / scale of fwht(RMSNorm(xout) * su), one launch. acc as post."""
+    """xout = bf16(x + post(acc ...)) and, with w, q / q4 / scale of fwht(RMSNorm(xout) * su), one launch. acc as post, or
+    an int32 (P, M, lda) tensor of P = 2 / 4 K parts of one product (summed in int32 before scaling)."""
     M, N = x.shape
     _bf16(x, 'post_add_norm_pre x'), _bf16(xout, 'post_add_norm_pre xout')
     _contig(acc, s, rs, sv, bias, x, xout, w, su, q, q4, scale)
-    call('tcq_post_add_norm_pre', ptr(acc), _dt(acc, (0, 1, 3), 'post_add_norm_pre acc'), acc.shape[1], col0, ptr(s), ptr(rs),
-         ptr(sv), ptr(bias), ptr(x), ptr(xout), ptr(w), float(eps), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, N,
-         stream())
+    adt = _dt(acc, (0, 1, 3), 'post_add_norm_pre acc')
+    if acc.dim() == 3:
+        if acc.dtype != torch.int32 or acc.shape[0] not in K_PARTS or acc.shape[1] != M:
+            raise ValueError(f'post_add_norm_pre: K parts must be int32 (2 or 4, {M}, lda), got {tuple(acc.shape)} {acc.dtype}')
+        adt |= K_PARTS[acc.shape[0]]
+    elif acc.shape[0] < M:
+        raise ValueError(f'post_add_norm_pre: accumulator {tuple(acc.shape)} has fewer than {M} rows')
+    lda = acc.shape[-1]
+    if col0 < 0 or col0 + N > lda:
+        raise ValueError(f'post_add_norm_pre: columns {col0}..{col0 + N} exceed the accumulator width {lda}')
+    call('tcq_post_add_norm_pre', ptr(acc), adt, lda, col0, ptr(s), ptr(rs), ptr(sv), ptr(bias), ptr(x), ptr(xout), ptr(w),
+         float(eps), ptr(su), ptr(q), ptr(q4), _ldq(q4), ptr(scale), M, N, stream())
     return xout
 
 
@@ -467,36 +480,41 @@ class SmallProduct:
         self.n, self.ldo = len(segs), ldo
         self.fn = getattr(_lib.lib(), self.name)
 
-    def __call__(self, q, s):
-        """q (M, K) row-major, or a token-block tensor (M = s.numel() tokens; s is then required)."""
+    def __call__(self, q, s, parts=1):
+        """q (M, K) row-major, or a token-block tensor (M = s.numel() tokens; s is then required). parts 2 / 4: int32 outputs
+        only, K parts written at out + p * M * ldo (see K_PARTS)."""
         if q.dim() == 4:
             if s is None:
                 raise ValueError('token-block activations need s (their token count)')
             M, K, odt = s.numel(), q.shape[1] * 16, self.odt | Q_TOKEN_BLOCKS
         else:
             (M, K), odt = q.shape, self.odt
+        if parts != 1:
+            if parts not in K_PARTS or self.odt != 3:
+                raise ValueError('K parts: 2 or 4, int32 outputs only')
+            odt |= K_PARTS[parts]
         if self.K is not None and K != self.K:
             raise ValueError(f'activations have K = {K}, the weights {self.K}')
         if s is not None and s.numel() < M:
             raise ValueError('fewer token scales than tokens')
         for o, m in self.outs:
-            if o.storage_offset() + (M - 1) * self.ldo + m > o.untyped_storage().nbytes() // o.element_size():
-                raise ValueError(f'an output buffer does not hold {M} rows of stride {self.ldo}')
+            if o.storage_offset() + ((parts - 1) * M + M - 1) * self.ldo + m > o.untyped_storage().nbytes() // o.element_size():
+                raise ValueError(f'an output buffer does not hold {parts} x {M} rows of stride {self.ldo}')
         rc = self.fn(self.arr, self.n, ptr(q), ptr(s), M, K, odt, self.ldo, stream())
         if rc:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
 
-def gemm_tcq_segments(segs, q, s, ldo):
+def gemm_tcq_segments(segs, q, s, ldo, parts=1):
     """One-shot fused decode + product over segments (see SmallProduct)."""
     _contig(q, s)
-    SmallProduct(segs, ldo)(q, s)
+    SmallProduct(segs, ldo)(q, s, parts)
 
 
-def gemm_w8_segments(segs, q, s, ldo):
+def gemm_w8_segments(segs, q, s, ldo, parts=1):
     """One-shot INT8-resident product over segments (see SmallProduct)."""
     _contig(q, s)
-    SmallProduct(segs, ldo, resident=True)(q, s)
+    SmallProduct(segs, ldo, resident=True)(q, s, parts)
 
 
 def gemm_w8(W, q4, s, rs, z):
