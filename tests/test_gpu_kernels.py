@@ -472,6 +472,41 @@ def test_postg_matches_post_and_oracle(M):
         assert np.array_equal(bits_of(y), ref.view(np.uint32))
 
 
+def test_bf16_conversion_of_every_exponent_and_payload():
+    """FP32 -> BF16 of the kernels (round to nearest even, NaN -> 0x7fc0) over every high half-word with low halves at and
+    around the rounding tie (0x7fff, 0x8000, 0x8001), the extremes and two payloads: infinities, subnormals, overflow to
+    infinity and NaNs of every sign and payload. One-sided plain epilogue, FP32 in, BF16 out (a conversion only)."""
+    from yanlongvla_amd import kernels as K
+    hi = np.arange(65536, dtype=np.uint32) << 16
+    lo = np.array([0x0000, 0x0001, 0x4000, 0x7fff, 0x8000, 0x8001, 0xc000, 0xffff], dtype=np.uint32)
+    u = (hi[:, None] | lo[None, :]).reshape(64, -1)
+    x = T(u.view(np.int32)).view(torch.float32)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=DEV)
+    K.post(x, None, None, None, None, y)
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(u.view(np.float32)))
+
+
+def test_rht_bf16_output_of_nan_and_inf_rows():
+    """BF16 outputs of the rotation for rows holding a NaN (any payload), opposite infinities or one infinity, against the
+    oracle: a NaN reaches every output of its row and converts to 0x7fc0 (the packed two-value conversion with its NaN
+    rule); inf - inf gives NaN at half the positions of its row."""
+    from yanlongvla_amd import kernels as K
+    n = 1024
+    x = np.zeros((4, n), np.float32)
+    x[0, 5] = np.uint32(0x7f812345).view(np.float32)      # signalling-style payload
+    x[1, 9] = np.uint32(0xffc00001).view(np.float32)      # negative quiet NaN with payload
+    x[2, 0], x[2, 1] = np.inf, -np.inf
+    x[3, 3] = np.inf
+    y = torch.empty(4, n, dtype=torch.bfloat16, device=DEV)
+    K.rht(T(x), None, y)
+    b = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert (b[:2] == 0x7fc0).all()
+    with np.errstate(invalid='ignore'):
+        ref = O.bf16_bits(O.fwht(x))
+    assert np.array_equal(b, ref)
+    assert (b[2] == 0x7fc0).sum() == n // 2
+
+
 def test_gelu_table_vs_cpu():
     """The device GELU table against PyTorch's CPU routine over all 65,536 BF16 inputs (NaN inputs: both NaN). Records the
     number of differing finite entries; the fused kernels use the device table, as the reference does."""
