@@ -901,8 +901,10 @@ __global__ void k_postg_tw(SEGS segs, const float* s, const u16* gelu_lut, int m
 // k_mid2 on the register + transpose engine for N = 2^L (2^LE values per thread, 2^(L - LE) threads, aligned): the gate half
 // is loaded at entry and the up half during the gate's transform, each transform returns to the natural layout through LDS,
 // so signs, GELU and rounding points are applied exactly as in k_mid2.
+// At most 128 registers (4 waves per SIMD): two 512-thread rows of 16384 per CU, as their LDS allows (139 registers left one
+// row per CU: 800 x 16384 72.4 -> 51.5 us on MI355X, bit-identical).
 template <int ADT, int L, int LE>
-__global__ __launch_bounds__(1 << (L - LE)) void k_mid2_tw(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
+__global__ __launch_bounds__(1 << (L - LE), 4) void k_mid2_tw(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
                                                            const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale) {
     constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
     extern __shared__ float xs[];
