@@ -149,11 +149,20 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_rht_tw(const void* x, int ldx
 #pragma unroll
         for (int h = 0; h < E / 16; ++h) s0[h] = raw16<1>(su + i0 + 16 * h, true);
     }
-    const Span<LE, XS> xa = tw_span_load<LE, XS>((const char*)x + tok * ldx * XS);
-    tw_span_put<LE, XS>(xa, xs, [](int, int, u32 b) { return bits_to_f32<XDT>(b); });
-    __syncthreads();
+    // the thread's 2^LE contiguous inputs (layout 0) straight from memory: each lane reads its own 16-byte pieces, which
+    // costs the address unit more lines per instruction than lane-contiguous loads but saves the LDS round trip that would
+    // bring lane-contiguous pieces into layout 0 (MI355X, BF16, 800 x 16384: 18.85 -> 15.87 us; FP32 20.7 -> 18.4 us)
     float v[E];
-    tw_get<L, LE, 0>(v, xs);
+    {
+        constexpr int NQ = E * XS / 16;
+        const uint4_t* src = (const uint4_t*)((const char*)x + tok * ldx * XS + (size_t)i0 * XS);
+        uint4_t raw[NQ];
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) raw[j] = *gptr(src + j);
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+            v[k] = XS == 4 ? bits_to_f32<XDT>(raw[k >> 2][k & 3]) : bits_to_f32<XDT>((raw[k >> 3][(k & 7) >> 1] >> (16 * (k & 1))) & 0xffffu);
+    }
     if (su) {
 #pragma unroll
         for (int h = 0; h < E / 16; ++h) {
