@@ -108,15 +108,15 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) m[rr] = sv[rr] = ps[4 * rr + wave][lane];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
+    for (int rr = 0; rr < RW; ++rr) m[rr] = row16_max(m[rr]);
 #pragma unroll
-        for (int rr = 0; rr < RW; ++rr) m[rr] = fmaxf(m[rr], __shfl_xor(m[rr], o, 64));
+    for (int rr = 0; rr < RW; ++rr) m[rr] = rows_max(m[rr]);
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) l[rr] = e[rr] = m[rr] == -__builtin_inff() ? 0.f : expf(sv[rr] - m[rr]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
+    for (int rr = 0; rr < RW; ++rr) l[rr] = row16_sum(l[rr]);
 #pragma unroll
-        for (int rr = 0; rr < RW; ++rr) l[rr] = l[rr] + __shfl_xor(l[rr], o, 64);
+    for (int rr = 0; rr < RW; ++rr) l[rr] = rows_sum(l[rr]);
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) {
         const int r = 4 * rr + wave, t = t0 + (r >> 3), h = r & 7;
@@ -231,8 +231,7 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
             if (c < NV) wts[wave][c] = w;
             L = __builtin_fmaf(w, lv[r], L);
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) L = L + __shfl_xor(L, off, 64);
+        L = wave_sum(L);
         if (lane == 0) inv[wave] = L;
     }
     __syncthreads();
@@ -304,8 +303,7 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    mx = row16_max(mx);
     float L = 0.f;
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
@@ -316,8 +314,7 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
             L = __builtin_fmaf(w, ml[r].y, L);
         }
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) L = L + __shfl_xor(L, m, 64);
+    L = row16_sum(L);
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < CW; ++i) {
@@ -379,8 +376,7 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    mx = row16_max(mx);
     float L = 0.f;
 #pragma unroll
     for (int r = 0; r < SC; ++r) {
@@ -391,8 +387,7 @@ __global__ __launch_bounds__(128) void k_attn_combine_reg(const float* part, int
             L = __builtin_fmaf(w, ml[r].y, L);
         }
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) L = L + __shfl_xor(L, m, 64);
+    L = row16_sum(L);
     float acc[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] = 0.f;

@@ -62,11 +62,40 @@ __device__ __forceinline__ void store_from_f32(void* p, size_t i, float v, int d
 }
 
 // ------------------------------------------------------------------------------------------------- wave / block reductions
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// Cross-lane moves inside 16-lane rows by DPP (a modifier of the consuming instruction, no trip through the LDS crossbar):
+// dpp<C>(v) returns, in lane i, v of lane: quad_perm 0xB1 -> i ^ 1, 0x4E -> i ^ 2; row_ror:N (0x120 + N) -> row lane
+// (i - N) mod 16; row_shl:N (0x100 + N) -> i + N within the row (0 past the row's end). Checked on MI355X lane by lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+__device__ __forceinline__ float lane_value(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// max over the 16 lanes of each row, in every lane of the row (max is exact in any order)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    return fmaxf(v, dpp<0x128>(v));
+}
+// sum over the 16 lanes of each row, the same bits in every lane of the row: each step adds the partial sum of a disjoint
+// class of lanes (shifts 8, 4, 2, 1), and the two lanes of every pair add the same two values
+__device__ __forceinline__ float row16_sum(float v) {
+    v = v + dpp<0x128>(v);
+    v = v + dpp<0x124>(v);
+    v = v + dpp<0x4E>(v);
+    return v + dpp<0xB1>(v);
+}
+// the four rows' values (lanes 0, 16, 32, 48) combined into one wave-uniform value
+__device__ __forceinline__ float rows_max(float v) {
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+// wave-wide max / sum, uniform across the wave
+__device__ __forceinline__ float wave_max(float v) { return rows_max(row16_max(v)); }
+__device__ __forceinline__ float wave_sum(float v) { return rows_sum(row16_sum(v)); }
 
 // max over the workgroup; red: >= 16 floats of LDS. Ends with a barrier (red may be reused after it).
 __device__ __forceinline__ float block_max(float v, float* red) {

@@ -534,11 +534,13 @@ __device__ __forceinline__ float tree_total(const float* part, float* red, int K
     for (int g = wid; g < groups; g += nw) {
         const int j = (g << 6) + lane;
         float v = j < C ? part[j] : 0.f;
-#pragma unroll
-        for (int h = 1; h < 64; h <<= 1) {
-            const float o = __shfl_down(v, h, 64);
-            if ((lane & (2 * h - 1)) == 0) v = v + o;
-        }
+        // pairwise tree over the 64 lanes (stride 1, 2, 4, 8 inside the rows, then 16 and 32): lane l adds lane l + h for l
+        // a multiple of 2h; the other lanes compute values no kept lane reads
+        v = v + dpp<0x101>(v);
+        v = v + dpp<0x102>(v);
+        v = v + dpp<0x104>(v);
+        v = v + dpp<0x108>(v);
+        v = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
         if (lane == 0) red[g] = v;
     }
     __syncthreads();
