@@ -97,6 +97,18 @@ __device__ __forceinline__ float rows_sum(float v) {
 __device__ __forceinline__ float wave_max(float v) { return rows_max(row16_max(v)); }
 __device__ __forceinline__ float wave_sum(float v) { return rows_sum(row16_sum(v)); }
 
+// v of lane (lane ^ m): DPP for m = 1, 2, 4, 8 (4: row_ror:4 for lanes with bit 2 set, row_ror:12 for the others), the LDS
+// crossbar (ds_bpermute) for 16 and 32
+__device__ __forceinline__ float lane_xor(float v, int m, int lane) {
+    switch (m) {
+        case 1: return dpp<0xB1>(v);
+        case 2: return dpp<0x4E>(v);
+        case 4: { const float a = dpp<0x124>(v), b = dpp<0x12C>(v); return (lane & 4) ? a : b; }
+        case 8: return dpp<0x128>(v);
+        default: return __shfl_xor(v, m, 64);
+    }
+}
+
 // max over the workgroup; red: >= 16 floats of LDS. Ends with a barrier (red may be reused after it).
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
@@ -214,11 +226,13 @@ __device__ __forceinline__ void block_walsh(float* lds, int K, Out&& out) {
 __device__ __forceinline__ void reg_walsh16(float (&v)[16], int K, float* xs) {
     butterflies<4>(v);
     const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
-    for (int m = 1; m < nt && m < 64; m <<= 1) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        if (m >= nt) break;
         const bool upper = lane & m;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float p = __shfl_xor(v[k], m, 64);
+            const float p = lane_xor(v[k], m, lane);
             v[k] = upper ? p - v[k] : v[k] + p;
         }
     }
@@ -244,11 +258,13 @@ __device__ __forceinline__ void reg_walsh16_part(float (&v)[16], int K, float* x
     const bool on = t < nt;
     // waves past the row skip the lane stages (their shuffles would only load the LDS crossbar)
     const bool wave_on = __builtin_amdgcn_readfirstlane(t & ~63) < nt;
-    for (int m = 1; wave_on && m < nt && m < 64; m <<= 1) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        if (!wave_on || m >= nt) break;
         const bool upper = lane & m;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float p = __shfl_xor(v[k], m, 64);
+            const float p = lane_xor(v[k], m, lane);
             v[k] = upper ? p - v[k] : v[k] + p;
         }
     }
