@@ -97,15 +97,18 @@ __device__ __forceinline__ float rows_sum(float v) {
 __device__ __forceinline__ float wave_max(float v) { return rows_max(row16_max(v)); }
 __device__ __forceinline__ float wave_sum(float v) { return rows_sum(row16_sum(v)); }
 
-// v of lane (lane ^ m): DPP for m = 1, 2, 4, 8 (4: row_ror:4 for lanes with bit 2 set, row_ror:12 for the others), the LDS
-// crossbar (ds_bpermute) for 16 and 32
+// v of lane (lane ^ m): DPP for m = 1, 2, 4, 8 (4: row_ror:4 for lanes with bit 2 set, row_ror:12 for the others); for 16
+// and 32 gfx950's v_permlane16_swap / v_permlane32_swap of v with itself, whose two results hold, lane by lane, the rows
+// (16) or halves (32) of v unchanged and exchanged (checked on MI355X lane by lane).
 __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
+    const int b = __float_as_int(v);
     switch (m) {
         case 1: return dpp<0xB1>(v);
         case 2: return dpp<0x4E>(v);
-        case 4: { const float a = dpp<0x124>(v), b = dpp<0x12C>(v); return (lane & 4) ? a : b; }
+        case 4: { const float a = dpp<0x124>(v), c = dpp<0x12C>(v); return (lane & 4) ? a : c; }
         case 8: return dpp<0x128>(v);
-        default: return __shfl_xor(v, m, 64);
+        case 16: { const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false); return __int_as_float((lane & 16) ? r[0] : r[1]); }
+        default: { const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false); return __int_as_float((lane & 32) ? r[0] : r[1]); }
     }
 }
 
