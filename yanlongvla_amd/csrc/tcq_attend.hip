@@ -280,8 +280,16 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
 // chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
 // register engine) and quantized.
 constexpr int CW = 16;
+// rotate + quantize of the combined row (2^L values in xs, natural layout) on the register + transpose engine, 16 values per
+// thread on threads 0 .. 2^(L - 4) - 1; the rest of the workgroup meets the barriers
+template <int L>
+__device__ __forceinline__ void combine_rotate_quantize(float* xs, float* red, i8* q8, int* q4, int ldq, float* scale, int t) {
+    float v[16];
+    tw_get<L, 4, 0>(v, xs);
+    tw_rotate_quantize<L, 4>(v, xs, red, q8, q4, ldq, scale, t);
+}
 __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su,
-                                                        i8* q8, int* q4, int ldq, float* scale) {
+                                                        i8* q8, int* q4, int ldq, float* scale, int tw_ok) {
     extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
@@ -339,6 +347,16 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
 #pragma unroll
     for (int k = 0; k < 4; ++k) xs[lds_slot(h * AD + d0 + k)] = bf16_to_f32(b[k]) * (float)(i8)(sg >> (8 * k));
     __syncthreads();
+    // power-of-two rows (H = 1, 2, 4, 8) and 16-byte aligned INT8 outputs: the register + transpose engine on the first K / 16
+    // threads (16 values each, read from the LDS row in layout 0); the same stages in the same order as the LDS engine, so
+    // the same bits
+    switch (tw_ok ? H : 0) {
+        case 8: combine_rotate_quantize<11>(xs, red, q8, q4, ldq, scale, t); return;
+        case 4: combine_rotate_quantize<10>(xs, red, q8, q4, ldq, scale, t); return;
+        case 2: combine_rotate_quantize<9>(xs, red, q8, q4, ldq, scale, t); return;
+        case 1: combine_rotate_quantize<8>(xs, red, q8, q4, ldq, scale, t); return;
+        default: break;
+    }
     float amx = 0.f;
     block_walsh(xs, K, [&](int i, float x) { xs[lds_slot(i)] = x; amx = fmaxf(amx, fabsf(x)); });
     const float sc = token_scale(block_max(amx, red));
@@ -460,7 +478,8 @@ extern "C" int tcq_attend_q4(const void* q, const void* k_cache, const void* v_c
     const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
     if ((!o || (uintptr_t)o % 8 == 0) && (!su || (uintptr_t)su % 4 == 0))
         launch_k(k_attn_combine_w, dim3(M), dim3(H * 64), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part,
-                 NC, P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
+                 NC, P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale,
+                 (int)((!q8 || (uintptr_t)q8 % 16 == 0) && (!q4 || ldq != TCQ_LDQ_TOKEN_BLOCKS || (uintptr_t)q4 % 16 == 0)));
     else if ((H == 4 || H == 8) && oal)
         launch_k(k_attn_combine_reg, dim3(M), dim3(H * 16), su ? (size_t)H * AD * sizeof(float) : 0, st, (const float*)part, NC,
                  P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);

@@ -539,22 +539,25 @@ __device__ __forceinline__ float (&part16(float (&v)[E], int h))[16] { return *r
 
 // reg_rotate_quantize on the register + transpose engine: v holds the natural-layout values 2^LE t .. 2^LE t + 2^LE - 1 of
 // the row (N = 2^L); the same operations in the same order (Walsh, * c, row max, per-token INT8, q and / or q4 words).
+// Threads from 2^(L - LE) on (a workgroup wider than the row) hold no values: they meet the barriers and store nothing.
 template <int L, int LE>
 __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* xs, float* red, i8* q, int* q4, int ldq,
                                                    float* scale, int tok) {
     constexpr int N = 1 << L, E = 1 << LE;
     const int t = threadIdx.x;
+    const bool on = t < (N >> LE);
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
     tw_walsh<L, LE>(v, xs);
     float mx = 0.f;
 #pragma unroll
     for (int k = 0; k < E; ++k) {
         v[k] = v[k] * c;
-        mx = fmaxf(mx, fabsf(v[k]));
+        if (on) mx = fmaxf(mx, fabsf(v[k]));
     }
     const float sc = token_scale(block_max(mx, red));
     if (t == 0) scale[tok] = sc;
     tw_to_natural<L, LE>(v, xs);
+    if (!on) return;
     u32 words[E / 4];
 #pragma unroll
     for (int k4 = 0; k4 < E / 4; ++k4)
