@@ -577,7 +577,8 @@ def backbone(args, dev):
 
 def decode_products(model, runtime, dev, seed):
     """Device time and weight-stream rate of each product of decoder layer 0 at one token (the decode step's GEMVs), per
-    call from back-to-back graph replays: fly reads the 2-bit words (m * n / 4 bytes), resident the INT8 weights."""
+    call from back-to-back graph replays: fly reads the 2-bit words (m * n / 4 bytes), resident the INT8 weights. The o and
+    down products run in the K parts the decoder layer uses for them (Group.k_parts; their epilogue adds the parts)."""
     import torch
     groups = {g.layers[0].name: g for g in model._tcq_groups}
     pre = 'paligemma_with_expert.paligemma.language_model.layers.0.'
@@ -586,11 +587,12 @@ def decode_products(model, runtime, dev, seed):
     for tag, key in (('q/k/v', 'self_attn.q_proj'), ('o', 'self_attn.o_proj'), ('gate/up', 'mlp.gate_proj'), ('down', 'mlp.down_proj')):
         g = groups[pre + key]
         b = g.quantize(torch.randn(1, g.K, generator=g0, device=dev).bfloat16())
-        ms = graph_per_call(lambda: g.product(b))
+        parts = g.k_parts(1) if tag in ('o', 'down') else 1
+        ms = graph_per_call(lambda: g.product(b, parts))
         byts = g.Ntot * g.K // 4 if runtime == 'fly' else g.Ntot * g.K
         gbs = byts / (ms * 1e-3) / 1e9
         out[tag] = {'shape': f'{g.Ntot}x{g.K}', 'bytes': byts, 'us': round(ms * 1e3, 2), 'GBs': round(gbs, 1),
-                    'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
+                    'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'k_parts': parts}
     return out
 
 
