@@ -653,7 +653,9 @@ def test_gemm_small_rejects_bad_sizes():
 
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM
 @pytest.mark.parametrize('M,K,N', [(800, 2048, 16384), (50, 2048, 16384), (1, 2048, 16384), (33, 80, 48), (130, 1152, 260),
-                                   (17, 16, 4)])
+                                   (17, 16, 4),
+                                   # 256-token tiles whose last tile holds 1 to 64 rows, K not a multiple of the 64-byte step
+                                   (801, 256, 32768), (832, 64, 16384), (769, 208, 16384)])
 def test_gemm_i8_bitexact(M, K, N):
     """INT32 accumulators equal the exact integer product; FP32 / BF16 epilogues equal (acc * sa) * sw bit for bit."""
     from yanlongvla_amd import kernels as Kk
