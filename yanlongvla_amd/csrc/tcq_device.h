@@ -229,14 +229,18 @@ __device__ __forceinline__ void block_walsh(float* lds, int K, Out&& out) {
 __device__ __forceinline__ void reg_walsh16(float (&v)[16], int K, float* xs) {
     butterflies<4>(v);
     const int t = threadIdx.x, nt = K >> 4, lane = t & 63;
+    // the six lane stages unrolled with a guard rather than a loop exit (an exit left the loop rolled in some kernels, with
+    // lane_xor's choice of cross-lane move made at run time for every value)
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        if (m >= nt) break;
-        const bool upper = lane & m;
+    for (int s = 0; s < 6; ++s) {
+        const int m = 1 << s;
+        if (m < nt) {
+            const bool upper = lane & m;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const float p = lane_xor(v[k], m, lane);
-            v[k] = upper ? p - v[k] : v[k] + p;
+            for (int k = 0; k < 16; ++k) {
+                const float p = lane_xor(v[k], m, lane);
+                v[k] = upper ? p - v[k] : v[k] + p;
+            }
         }
     }
     for (int m = 64; m < nt; m <<= 1) {
