@@ -191,11 +191,13 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const 
                     if (ODT == TCQ_F32) *(float*)dst = v;
                     else *(u16*)dst = f32_to_bf16(v);
                 }
+            constexpr int NG = (32 * GPR + 63) / 64;                     // 16-byte pieces per lane (a fixed count: unrolled)
 #pragma unroll
-            for (int g = lane; g < 32 * GPR; g += 64) {
+            for (int it = 0; it < NG; ++it) {
+                const int g = lane + 64 * it;
                 const int tr = g / GPR, cg = g - tr * GPR;
                 const int m = mb + tr, n = nw0 + cg * EPG;
-                if (m >= M || n >= N) continue;
+                if (g >= 32 * GPR || m >= M || n >= N) continue;
                 const uint4_t v = *(const uint4_t*)(slice + tr * RB + cg * 16);
                 char* o = (char*)out + ((size_t)m * ldo + n) * OSZ;
                 if (vec && n + EPG <= N) {
