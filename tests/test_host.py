@@ -164,3 +164,28 @@ def test_groot_group_plan():
     assert [cross + 'to_k'] in plan and [cross + 'to_q'] in plan
     self_attn = 'action_head.model.transformer_blocks.1.attn1.'
     assert [self_attn + 'to_q', self_attn + 'to_k', self_attn + 'to_v'] in plan
+
+
+def test_k_parts_rule():
+    """K parts of a small-M product (Group.k_parts): doubled, up to 4, while the workgroups (one per tile row and part) stay
+    below the 256 CUs and every part would keep at least 4 of the 256-column chunks; one part for many tokens or when off."""
+    class G:
+        pass
+
+    def parts(n_out, k, m):
+        g = G()
+        g.Ntot, g.K = n_out, k
+        return modules.Group.k_parts(g, m)
+    assert parts(2048, 16384, 1) == 2           # backbone down: 128 tile rows x 2 parts = 256 workgroups
+    assert parts(2048, 2048, 1) == 2            # backbone o
+    assert parts(1024, 4096, 50) == 4           # expert down: 64 tile rows, 16 chunks
+    assert parts(1024, 2048, 50) == 2           # expert o: 8 chunks allow one split
+    assert parts(32768, 2048, 1) == 1           # gate/up: 2048 tile rows already fill the chip
+    assert parts(256, 512, 3) == 1              # 2 chunks: no part would keep enough
+    assert parts(2048, 16384, modules.SMALL_M + 1) == 1
+    old = modules.FUSE['k_parts']
+    modules.FUSE['k_parts'] = False
+    try:
+        assert parts(2048, 16384, 1) == 1
+    finally:
+        modules.FUSE['k_parts'] = old
