@@ -429,6 +429,37 @@ def test_gemv_post_fused_equals_unfused(nl, M, m, n, ydt):
             assert ((y.double() - ref.double()).norm() / ref.double().norm()).item() < (2e-3 if ydt != torch.float32 else 1e-6)
 
 
+def test_layer_stream_2048_against_the_oracle():
+    """The benchmarked pass itself against the oracle: 256 distinct 2048 x 2048 layers (one FP16 scale per layer, N(0, 1)
+    FP16 tables, random signs), one FP16 token x ~ N(0, 1), input rotation by pre_h16, then one gemv_f16_post launch over
+    the whole stream (the layer-stream plan, output rotation fused, FP16 y). Every 8th layer and the last one are checked
+    against the oracle's reference_linear(table='fp16', a8=False) (tcq_format.py:125-148): relative L2 <= 2e-3."""
+    from yanlongvla_amd import kernels as K
+    nl, m, n = 256, 2048, 2048
+    layers = [O.random_layer(m, n, 900 + i) for i in range(nl)]
+    su = layers[0].su
+    for L in layers:                                   # one stream shares the input signs (one input rotation)
+        L.su = su
+    devs = [dev_layer(L) for L in layers]
+    x = np.random.default_rng(901).standard_normal((1, n)).astype(np.float16)
+    h16 = torch.empty(1, n, dtype=torch.float16, device=DEV)
+    hs = torch.empty(1, dtype=torch.float32, device=DEV)
+    K.pre_h16(T(x), T(su), h16, hs)
+    ws = [K.repack(d['bits'], m, n) for d in devs]
+    ys = [torch.empty(1, m, dtype=torch.float16, device=DEV) for _ in range(nl)]
+    desc = K.gemv_post_descriptors([(w, d['tlut'], d['row_scale'], d['sv'], None, y) for w, d, y in zip(ws, devs, ys)])
+    K.gemv_f16_post(desc, h16, hs, m, n, torch.float16)
+    torch.cuda.synchronize()
+    errs = {}
+    for i in sorted(set(range(0, nl, 8)) | {nl - 1}):
+        ref = O.reference_linear(x.astype(np.float32), layers[i], a8=False, table='fp16', out_dtype='f32')
+        y = ys[i].float().cpu().numpy()
+        errs[i] = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+    worst = max(errs, key=errs.get)
+    print(f'layer stream 256 x 2048^2: max rel L2 {errs[worst]:.2e} (layer {worst}) over {len(errs)} layers', flush=True)
+    assert errs[worst] <= 2e-3, (worst, errs[worst])
+
+
 # ------------------------------------------------------------------------------------------------------ batched epilogue
 @pytest.mark.parametrize('M', [1, 10, 50])
 def test_postg_matches_post_and_oracle(M):
@@ -508,17 +539,26 @@ def test_rht_bf16_output_of_nan_and_inf_rows():
 
 
 def test_gelu_table_vs_cpu():
-    """The device GELU table against PyTorch's CPU routine over all 65,536 BF16 inputs (NaN inputs: both NaN). Records the
-    number of differing finite entries; the fused kernels use the device table, as the reference does."""
+    """The device GELU table against PyTorch's CPU routine over all 65,536 BF16 inputs: NaN at the same inputs (NaN inputs,
+    and -inf, whose x * (1 + tanh(..)) is -inf * 0). Measured on MI355X, the two routines differ at 4 other inputs, -5.0625
+    .. -5.15625 (0xc0a2 .. 0xc0a5), where 1 + tanh(..) cancels: the CPU result is -0, the device's about -1.5e-7. At most
+    4 entries may differ, all at inputs below -5, each by at most 2^-22 in absolute value. The fused kernels use the
+    device table, as the reference does."""
     from yanlongvla_amd import kernels as K
     dev = K.gelu_table(DEV).cpu()
     allb = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     cpu = torch.nn.functional.gelu(allb, approximate='tanh')
-    nan = torch.isnan(allb)
-    assert bool((torch.isnan(dev) == torch.isnan(cpu))[nan].all())
-    diff = (dev.view(torch.int16) != cpu.view(torch.int16)) & ~nan
-    print(f'GELU table: {int(diff.sum())} of {int((~nan).sum())} finite BF16 inputs differ between device and CPU', flush=True)
-    assert int(diff.sum()) < 65536 // 100
+    nan = torch.isnan(cpu)
+    assert torch.equal(torch.isnan(dev), nan)
+    db = dev.view(torch.int16).numpy().view(np.uint16).astype(np.int64)
+    cb = cpu.view(torch.int16).numpy().view(np.uint16).astype(np.int64)
+    diff = np.flatnonzero((db != cb) & ~nan.numpy())
+    print(f'GELU table: {diff.size} of {int((~nan).sum())} non-NaN BF16 results differ between device and CPU '
+          f'(inputs {[hex(int(i)) for i in diff]})', flush=True)
+    assert diff.size <= 4, diff.size
+    x, d, c = allb.float().numpy(), dev.float().numpy(), cpu.float().numpy()
+    assert (x[diff] < -5).all() and (np.abs(d[diff] - c[diff]) <= 2.0 ** -22).all(), \
+        [(hex(int(i)), hex(int(db[i])), hex(int(cb[i]))) for i in diff]
 
 
 # ------------------------------------------------------------------------------------------------- small-M INT8 products

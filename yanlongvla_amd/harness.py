@@ -1,16 +1,21 @@
-"""Stage timing and kernel-class accounting of the deploy path (the reference's runner.capture / timed / kernel_classes,
-deploy/tcq_kernels/runner.py:204-266): capture a stage as a HIP graph, time its replays with events, and split the device
-time of one replay by kernel class from a profiler trace.
+"""Stage timing and kernel-class accounting of the deploy path. It reports what the reference's harness reports
+(deploy/tcq_kernels/runner.py:214-266: 20 + 200 graph replays, median / p95; device time per kernel class of one stage;
+parity.py:92-99: action agreement per row), under the same result keys so that figures can be set side by side.
 
-The class patterns name this library's kernels (include/tcq_api.h); anything else falls through to the library classes.
+  capture(fn, per_graph)    a HIP graph of per_graph back-to-back calls of fn
+  timed(graph)              isolated replays: each starts on an idle device and is bracketed by its own pair of events
+  warm(fn, seconds)         calls until the clocks have settled
+  kernel_classes(graph, fn) one stage's device time folded from per-kernel totals into classes of this library's kernels
+  action_table(actions, r)  agreement of every runtime's actions with runtime r, per observation and pooled
 """
 import re
 import time
-from collections import Counter, defaultdict
 
 import numpy as np
 import torch
 
+# (class, pattern) pairs, first match wins; the patterns name this library's kernels (include/tcq_api.h), then the
+# library kernels PyTorch launches between them.
 CLASSES = [
     ('tcq decode', r'k_decode'),
     ('tcq scale+rotate', r'k_post'),
@@ -19,12 +24,20 @@ CLASSES = [
     ('tcq decode+product', r'k_gemm_small<0|k_gemv_tcq|k_gemv_f16'),
     ('tcq product (INT8 weights)', r'k_gemm_small<1'),
     ('int8 matrix product', r'k_gemm_i8'),
-    ('bf16 matrix product', r'k_gemm_bf16'),
+    ('bf16 matrix product', r'k_gemm_bf16|k_gemm_small<2|k_gemm_small<3'),
     ('attention', r'k_attn'),
     ('norm', r'rmsnorm'),
     ('copies / casts', r'copy|cast|Copy|fill|zero|memset|Memset|memcpy|Memcpy|elementwise|vectorized'),
     ('other', r'.*'),
 ]
+_COMPILED = [(c, re.compile(p)) for c, p in CLASSES]
+
+
+def classify(name):
+    for cls, pat in _COMPILED:
+        if pat.search(name):
+            return cls
+    return 'other'
 
 
 def capture(fn, per_graph=1):
@@ -42,22 +55,29 @@ def capture(fn, per_graph=1):
     return g
 
 
+def _quantile(ordered, q):
+    """q-quantile of an ascending list, interpolating linearly between the two nearest ranks."""
+    pos = q * (len(ordered) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(ordered) - 1)
+    return ordered[lo] + (ordered[hi] - ordered[lo]) * (pos - lo)
+
+
 def timed(graph, warmup=20, n=200):
-    """Replay statistics in ms: `warmup` untimed replays, then `n` replays each bracketed by events (runner.py:214-224)."""
+    """Replay statistics in ms over n isolated replays after `warmup` untimed ones. The event pairs are made before the
+    first replay; every timed replay starts on an idle device, so each figure includes the graph's submission."""
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for _ in range(warmup):
         graph.replay()
-    torch.cuda.synchronize()
-    values = []
-    for _ in range(n):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
+    for start, end in marks:
+        torch.cuda.synchronize()
+        start.record()
         graph.replay()
-        b.record()
-        b.synchronize()
-        values.append(a.elapsed_time(b))
-    v = np.array(values)
-    return dict(median_ms=float(np.median(v)), p95_ms=float(np.percentile(v, 95)), mean_ms=float(v.mean()),
-                min_ms=float(v.min()), n=n, warmup=warmup)
+        end.record()
+    torch.cuda.synchronize()
+    ms = sorted(start.elapsed_time(end) for start, end in marks)
+    return dict(median_ms=float(_quantile(ms, 0.5)), p95_ms=float(_quantile(ms, 0.95)), mean_ms=float(sum(ms) / n),
+                min_ms=float(ms[0]), n=n, warmup=warmup)
 
 
 def warm(fn, seconds, min_calls=1):
@@ -77,62 +97,62 @@ def warm(fn, seconds, min_calls=1):
 
 
 def action_table(actions, reference):
-    """Action agreement of every row with the reference row (parity.py:92-99): `actions` maps a row name to an array of
-    shape (observations, ...). Per row: observations whose actions are identical, the largest absolute difference, and the
-    relative error ||A - A_ref|| / ||A_ref|| per observation (max, mean) and pooled over all observations."""
+    """Agreement of every row's actions with the reference row's. `actions` maps a row name to an array of shape
+    (observations, ...). Per row: the observations whose actions are identical, the largest absolute difference, and the
+    relative L2 error ||A - A_ref|| / ||A_ref|| per observation (max, mean) and over all observations at once."""
     ref = np.asarray(actions[reference], dtype=np.float64)
-    n = len(ref)
-    ref_norm = np.linalg.norm(ref.reshape(n, -1), axis=1)
+    axes = tuple(range(1, ref.ndim))
+    ref_sq = np.square(ref).sum(axis=axes)
     table = {}
     for row, a in actions.items():
         a = np.asarray(a, dtype=np.float64)
         if a.shape != ref.shape:
             raise ValueError(f'{row}: actions {a.shape} != reference {ref.shape}')
         d = a - ref
-        per = np.linalg.norm(d.reshape(n, -1), axis=1) / ref_norm
-        table[row] = dict(identical_observations=int(sum(np.array_equal(x, y) for x, y in zip(a, ref))),
-                          max_abs=float(np.abs(d).max()), rel_err_max=float(per.max()), rel_err_mean=float(per.mean()),
-                          rel_err_pooled=float(np.linalg.norm(d) / np.linalg.norm(ref)))
+        d_sq = np.square(d).sum(axis=axes)
+        rel = np.sqrt(d_sq / ref_sq)
+        table[row] = dict(identical_observations=int(np.count_nonzero((a == ref).all(axis=axes))),
+                          max_abs=float(np.abs(d).max()), rel_err_max=float(rel.max()), rel_err_mean=float(rel.mean()),
+                          rel_err_pooled=float(np.sqrt(d_sq.sum() / ref_sq.sum())))
     return table
 
 
-def classify(name):
-    return next(c for c, pat in CLASSES if re.search(pat, name))
+def _kernel_totals(run):
+    """(wall ms of one traced call of run, [(kernel name, launches, device ms)]) from the profiler's per-name averages."""
+    from torch.autograd import DeviceType
+    from torch.profiler import ProfilerActivity, profile
+    run()
+    run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        start.record()
+        run()
+        end.record()
+        torch.cuda.synchronize()
+    rows = [(k.key, k.count, k.device_time_total / 1e3) for k in prof.key_averages() if k.device_type == DeviceType.CUDA]
+    return start.elapsed_time(end), rows
 
 
 def kernel_classes(graph=None, fn=None):
-    """Device time per kernel class of one replay of `graph` (or one eager call of `fn`), launches, wall time and the
-    gaps between kernels, from a torch.profiler trace (ROCm tracer). If a graph replay yields no kernel records, the eager
-    call is traced instead (same kernels; launches then include host submission)."""
-    from torch.profiler import profile, ProfilerActivity
-
-    def trace(run):
-        for _ in range(3):
-            run()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with profile(activities=[ProfilerActivity.CUDA, ProfilerActivity.CPU]) as prof:
-            a.record()
-            run()
-            b.record()
-            b.synchronize()
-        kern = [e for e in prof.events() if e.device_type.name == 'CUDA']
-        return a.elapsed_time(b), kern
-
-    mode = 'graph replay'
-    wall, kern = trace(graph.replay) if graph is not None else (0.0, [])
-    if not kern and fn is not None:
+    """Device time per kernel class of one replay of `graph` (or one eager call of `fn`), with launches, the wall time of
+    the traced call and the time between kernels. On ROCm the tracer records no kernels inside graph replays; the eager
+    call of the same stage is then traced (same kernels; its wall time includes host submission)."""
+    mode, wall, rows = 'graph replay', 0.0, []
+    if graph is not None:
+        wall, rows = _kernel_totals(graph.replay)
+    if not rows and fn is not None:
         mode = 'eager call'
-        wall, kern = trace(fn)
-    by, launches, top = defaultdict(float), Counter(), Counter()
-    for e in kern:
-        dur = e.time_range.elapsed_us() / 1000
-        cls = classify(e.name)
-        by[cls] += dur
-        launches[cls] += 1
-        top[e.name.split('(')[0][:90]] += dur
-    total = sum(by.values())
+        wall, rows = _kernel_totals(fn)
+    classes = {}
+    for name, count, ms in rows:
+        c = classes.setdefault(classify(name), [0, 0.0])
+        c[0] += count
+        c[1] += ms
+    total = sum(ms for _, ms in classes.values())
+    ordered = sorted(classes.items(), key=lambda kv: kv[1][1], reverse=True)
+    top = sorted(((name.split('(')[0][:90], ms) for name, _, ms in rows), key=lambda r: r[1], reverse=True)[:8]
     return dict(traced=mode, wall_ms=round(wall, 4), kernel_ms=round(total, 4), gaps_ms=round(max(wall - total, 0.0), 4),
-                launches=sum(launches.values()),
-                by_class_ms={k: round(v, 4) for k, v in sorted(by.items(), key=lambda kv: -kv[1])},
-                launches_by_class=dict(launches), top=[(n, round(d, 4)) for n, d in top.most_common(8)])
+                launches=sum(c for c, _ in classes.values()),
+                by_class_ms={k: round(ms, 4) for k, (_, ms) in ordered},
+                launches_by_class={k: c for k, (c, _) in ordered}, top=[(n, round(ms, 4)) for n, ms in top])
