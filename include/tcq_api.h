@@ -366,13 +366,45 @@ int tcq_gemm_tcq_q4(const void* bits, const int8_t* t8, const int32_t* q4, int l
 int tcq_gemm_i8(const int8_t* a, const int8_t* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
                 int K, tcq_stream_t stream);
 
-/* BF16 GEMM of the W2 float path: acc = sum_k a[m, k] w[n, k] with FP32 accumulation, a (M, K) BF16 (rotated activations),
- * w (N, K) BF16 (the INT8 table values as BF16, tcq_decode_f16 with the BF16 table); out = (acc * sa[m]) * sw[n] as FP32 or
- * BF16 (sa / sw may be NULL: factor 1). K % 16 == 0, N % 4 == 0; a, w, out 16-byte aligned. Replaces the BF16 product of
- * Group.run_float (`h @ W.t()` on decoded BF16 weights, deploy/tcq_kernels/modules.py:125-130) and the float small-M
- * products kernels.gemmf_w8 / gemmf_tcq (kernels.py:442-489, 686-696) with sw = rs, FP32 output. */
+/* BF16 GEMM on dense BF16 weights: acc = sum_k a[m, k] w[n, k] with FP32 accumulation, a (M, K) BF16, w (N, K) BF16 (e.g.
+ * the INT8 table values as BF16 from tcq_decode_f16 with the BF16 table); out = (acc * sa[m]) * sw[n] as FP32 or BF16
+ * (sa / sw may be NULL: factor 1). K % 16 == 0, N % 4 == 0; a, w, out 16-byte aligned. Replaces the prefill product of the
+ * reference's Group.run_float, `h @ W.t()` on BF16 weights decoded by kernels.decode_bf16 (deploy/tcq_kernels/modules.py:
+ * 120-126), for callers that hold such dense weights; the module layer runs tcq_gemmf_* instead (no dense copy). */
 int tcq_gemm_bf16(const void* a, const void* w, const float* sa, const float* sw, void* out, int out_dtype, int ldo, int M, int N,
                   int K, tcq_stream_t stream);
+
+/* W2 float path prologue: bf16(fwht(x * su)) per token (x (M, K) of x_dtype F32 / BF16 / F16, contiguous) into h (M, K)
+ * row-major and / or hT (K, ldh) with token = column (ldh >= M); either may be NULL, not both. Replaces kernels.pre_h /
+ * k_preh_{bf16,f32} (deploy/tcq_kernels/kernels.py:309-317, 677-680), argument for argument. */
+int tcq_pre_h(const void* x, int x_dtype, const int8_t* su, uint16_t* h, uint16_t* hT, int ldh, int M, int K, tcq_stream_t stream);
+
+/* 1 when tcq_mid2 takes a gated-MLP middle of width N (N % 16 == 0, N <= 16384), else 0. Replaces kernels.mid2_available
+ * (deploy/tcq_kernels/kernels.py:636-638), whose answer depends on the shared-memory limit of the reference's kernels. */
+int tcq_mid2_available(int N);
+
+/* W2 float path products over up to TCQ_MAX_SEGS layers side by side (segments as tcq_gemm_tcq): acc[t, i] = sum_k w[i, k]
+ * h[t, k] with FP32 sums (MFMA blocks), the weights the INT8 table values taken as BF16, h (M, K) BF16 rotated activations
+ * (tcq_pre_h / tcq_rht), any M (groups of 64 tokens over grid.z). out_dtype F32: out = acc * rs[i] (the expert's z,
+ * kernels.py:430-439); BF16: out = bf16(acc), unscaled (the prefill product rounded to BF16, modules.py:126, scaled by rs
+ * in tcq_post with a BF16 accumulator). ldo % 4 == 0, h 16-byte aligned, FP32 out / rs 16-byte aligned.
+ * tcq_gemmf_tcq decodes the tcq_repack words of each segment on the fly (w = words, t8 its table or row-group tables);
+ * tcq_gemmf_w8 reads resident INT8 weights (w = (m, K) int8, t8 unused). Replace kernels.gemmf_tcq / k_gemmf_tcq and
+ * kernels.gemmf_w8 / k_gemmf_w8 (deploy/tcq_kernels/kernels.py:442-489, 689-696) in the module layer, and the prefill
+ * product of Group.run_float (decode_bf16 + `h @ W.t()`, modules.py:120-126) without a dense BF16 copy. */
+int tcq_gemmf_tcq(const tcq_gemm_seg* segs, int nseg, const void* h, int M, int K, int out_dtype, int ldo, tcq_stream_t stream);
+int tcq_gemmf_w8(const tcq_gemm_seg* segs, int nseg, const void* h, int M, int K, int out_dtype, int ldo, tcq_stream_t stream);
+
+/* kernels.gemmf_w8 / k_gemmf_w8 (deploy/tcq_kernels/kernels.py:442-463, 689-691), argument for argument: W (N, K) int8 resident
+ * weights, hT (K, ldh) BF16 with token = column (the reference passes hT (K, M), ldh = M, from pre_h), rs (N,) FP32, z (M, N)
+ * FP32 = acc * rs. N and K multiples of 16; z and rs 16-byte aligned; any M <= ldh. */
+int tcq_gemmf_w8_hT(const int8_t* W, const void* hT, int ldh, const float* rs, float* z, int M, int N, int K, tcq_stream_t stream);
+/* kernels.gemmf_tcq / k_gemmf_tcq (deploy/tcq_kernels/kernels.py:465-489, 694-696), argument for argument: the fused decode +
+ * float product over the packed words as stored (bits (N/16 * K/16, 32) uint16, up to three layers concatenated along the
+ * rows), t8 up to three concatenated (512, 2) INT8 tables, tile row I decoded with table (I >= nb0) + (I >= nb1); hT, rs, z
+ * as tcq_gemmf_w8_hT. */
+int tcq_gemmf_tcq_hT(const void* bits, const int8_t* t8, const void* hT, int ldh, const float* rs, float* z, int M, int N, int K,
+                     int nb0, int nb1, tcq_stream_t stream);
 
 #ifdef __cplusplus
 }

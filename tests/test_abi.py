@@ -57,3 +57,15 @@ def test_argument_errors_are_reported_before_launch():
     assert lib.tcq_rht(P(16), 0, 32768, None, P(16), 0, 32768, 1, 32768, None) == -2
     assert lib.tcq_pre(P(16), 1, None, P(16), None, 0, P(16), 1, 18, None) == -2
     assert lib.tcq_gemv_f16(P(16), 1, P(16), P(16), 17, 16, 16, None) == -4
+    assert lib.tcq_pre_h(P(16), 1, None, None, None, 0, 1, 16, None) == -1          # neither h nor hT
+    assert lib.tcq_pre_h(P(16), 1, None, None, P(16), 1, 2, 16, None) == -1         # ldh < M
+    assert lib.tcq_gemmf_w8_hT(P(16), P(16), 1, P(16), P(16), 2, 16, 16, None) == -1
+    assert lib.tcq_gemmf_tcq_hT(P(16), P(16), P(16), 1, P(16), P(16), 1, 24, 16, 0, 0, None) == -2
+    assert lib.tcq_gemmf_tcq_hT(P(16), P(16), P(16), 1, P(16), P(8), 1, 16, 16, 0, 0, None) == -5
+    assert lib.tcq_gemmf_tcq(P(16), 1, P(16), 1, 16, 3, 16, None) == -3               # int32 out: not a float product
+
+
+@pytest.mark.skipif(not LIB.exists(), reason='libtcq.so not built')
+def test_mid2_available_without_gpu():
+    lib = ctypes.CDLL(str(LIB))
+    assert [lib.tcq_mid2_available(n) for n in (1024, 4096, 4304, 16384, 16400, 24, 0)] == [1, 1, 1, 1, 0, 0, 0]

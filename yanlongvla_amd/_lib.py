@@ -62,6 +62,12 @@ SIGNATURES = {
     'tcq_attend_q4_static': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P],
     'tcq_attend_static_floats': [],
     'tcq_pre_cs': [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P],
+    'tcq_pre_h': [_P, _I, _P, _P, _P, _I, _I, _I, _P],
+    'tcq_mid2_available': [_I],
+    'tcq_gemmf_tcq': [_P, _I, _P, _I, _I, _I, _I, _P],
+    'tcq_gemmf_w8': [_P, _I, _P, _I, _I, _I, _I, _P],
+    'tcq_gemmf_w8_hT': [_P, _P, _I, _P, _P, _I, _I, _I, _P],
+    'tcq_gemmf_tcq_hT': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 

@@ -124,6 +124,22 @@ __global__ void k_rht(const void* x, int ldx, const i8* su, void* y, int ldy, in
     store_row<YDT>(lds, y, tok * ldy, K, vec, [](int, float(&)[8]) {}, [](int, float v) { return v; });
 }
 
+// W2 float path prologue with the transposed output: bf16(fwht(x * su)) of token `tok` into column tok of hT (K, ldh) and,
+// when h is given, into row tok of h (M, K) (the reference's k_preh, deploy/tcq_kernels/kernels.py:309-317). The hT stores
+// of one row are ldh elements apart; a token's values stay in one workgroup.
+template <int XDT>
+__global__ void k_pre_hT(const void* x, const i8* su, u16* h, u16* hT, int K, int ldh, int vec) {
+    extern __shared__ float lds[];
+    const size_t tok = blockIdx.x;
+    load_row<XDT>(lds, x, tok * K, su, K, vec);
+    walsh_inplace(lds, K);
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        const u16 b = f32_to_bf16(lds[lds_slot(i)]);
+        gptr(hT)[(size_t)i * ldh + tok] = b;
+        if (h) gptr(h)[tok * K + i] = b;
+    }
+}
+
 // raw element bits <-> FP32 for FP32 / BF16 / FP16 rows (2-byte types in the low 16 bits)
 template <int DT>
 __device__ __forceinline__ float bits_to_f32(u32 b) {
@@ -1275,6 +1291,23 @@ extern "C" int tcq_rht(const void* x, int x_dtype, int ldx, const int8_t* su, vo
     DISPATCH_X(x_dtype, RHT_X, 0)
     return launch_status();
 }
+
+extern "C" int tcq_pre_h(const void* x, int x_dtype, const int8_t* su, uint16_t* h, uint16_t* hT, int ldh, int M, int K,
+                         tcq_stream_t stream) {
+    if (!x || (!h && !hT) || M <= 0 || K <= 0 || (hT && ldh < M)) return TCQ_ERR_ARG;
+    if (K > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    if (hT && (size_t)K * ldh >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if (!hT) return tcq_rht(x, x_dtype, K, su, h, TCQ_BF16, K, M, K, stream);      // row-major only: the rotation engines
+    const dim3 grid(M), block(row_threads(M, K));
+    const int vec = K % 8 == 0 && al16(x) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
+    hipStream_t st = (hipStream_t)stream;
+#define PREH(XD, _) launch_k(k_pre_hT<XD>, grid, block, row_lds(K), st, x, (const i8*)su, (u16*)h, (u16*)hT, K, ldh, vec)
+    DISPATCH_X(x_dtype, PREH, 0)
+#undef PREH
+    return launch_status();
+}
+
+extern "C" int tcq_mid2_available(int N) { return N > 0 && N % 16 == 0 && N <= TCQ_MAX_WIDTH; }
 
 extern "C" int tcq_pre_cs(const void* x, int x_dtype, const int8_t* su, const void* col_scale, int8_t* q, int32_t* q4, int ldq,
                           float* scale, int M, int K, tcq_stream_t stream) {

@@ -557,6 +557,83 @@ def gemm_bf16(a, w, out, sa=None, sw=None):
     return out
 
 
+# ------------------------------------------------------------------------------------------------------- W2 float path
+def pre_h(x, su, h=None, hT=None):
+    """Rotated activations as BF16: h (M, K) row-major and / or hT (K, ldh) with token = column, bf16(fwht(x * su))
+    (reference kernels.pre_h, kernels.py:677-680). x (M, K) float32 / bfloat16 / float16."""
+    M, K = x.shape
+    if h is None and hT is None:
+        raise ValueError('pre_h: give h and / or hT')
+    _contig(x, su, h, hT)
+    if any(t is not None and t.dtype != torch.bfloat16 for t in (h, hT)):
+        raise TypeError('pre_h: h / hT must be bfloat16')
+    if h is not None and tuple(h.shape) != (M, K):
+        raise ValueError(f'pre_h: h {tuple(h.shape)} != {(M, K)}')
+    if hT is not None and (hT.shape[0] != K or hT.shape[1] < M):
+        raise ValueError(f'pre_h: hT {tuple(hT.shape)} does not hold ({K}, >= {M})')
+    call('tcq_pre_h', ptr(x), _dt(x, (0, 1, 2), 'pre_h x'), ptr(su), ptr(h), ptr(hT), 0 if hT is None else hT.shape[1], M, K,
+         stream())
+
+
+def mid2_available(N):
+    """Whether mid2 takes a gated-MLP middle of width N (reference kernels.mid2_available, kernels.py:636-638)."""
+    return bool(_lib.lib().tcq_mid2_available(int(N)))
+
+
+def gemmf_segments(segs, h, ldo, resident=False):
+    """W2 float product over 1..4 segments [(w, t8, rs, out), ...] side by side: h (M, K) BF16 rotated activations; out a
+    view whose first element is the segment's first output column of an (M, ldo) buffer, FP32 (= acc * rs) or BF16
+    (= bf16(acc), the prefill rounding). resident False: w = tcq_repack words + t8 (fused decode, the segment form of
+    reference kernels.gemmf_tcq); True: w = (m, K) int8 weights (segment form of kernels.gemmf_w8, kernels.py:689-696)."""
+    if not 1 <= len(segs) <= _lib.MAX_SEGS:
+        raise ValueError(f'1 to {_lib.MAX_SEGS} segments')
+    if h.dtype != torch.bfloat16 or h.dim() != 2:
+        raise TypeError('gemmf: h must be (M, K) bfloat16')
+    _contig(h)
+    M, K = h.shape
+    arr = (_lib.GemmSeg * len(segs))()
+    odt = None
+    for i, (w, t8, rs, out) in enumerate(segs):
+        _contig(w, t8, rs)
+        d = _dt(out, (0, 1), 'gemmf out')
+        if odt is not None and d != odt:
+            raise TypeError('all segments need one output dtype')
+        odt = d
+        m = rs.numel()
+        if resident and (w.dtype != torch.int8 or tuple(w.shape) != (m, K)):
+            raise ValueError(f'segment {i}: resident weights must be ({m}, {K}) int8')
+        if out.storage_offset() + (M - 1) * ldo + m > out.untyped_storage().nbytes() // out.element_size():
+            raise ValueError(f'segment {i}: the output buffer does not hold {M} rows of stride {ldo}')
+        G = 1 if t8 is None else _groups(t8)
+        arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(out), m, 0 if G == 1 else m // G)
+    call('tcq_gemmf_w8' if resident else 'tcq_gemmf_tcq', arr, len(segs), ptr(h), M, K, odt, ldo, stream())
+
+
+def gemmf_w8(W, hT, rs, z):
+    """W (N, K) int8 resident, hT (K, >= M) BF16 (token = column), z (M, N) FP32 = acc * rs with FP32 sums (reference
+    kernels.gemmf_w8, kernels.py:689-691)."""
+    N, K = W.shape
+    M = z.shape[0]
+    _contig(W, hT, rs, z)
+    if hT.dtype != torch.bfloat16 or hT.shape[0] != K or hT.shape[1] < M or z.shape[1] != N or rs.numel() != N:
+        raise ValueError('gemmf_w8: shapes do not match')
+    call('tcq_gemmf_w8_hT', ptr(W), ptr(hT), hT.shape[1], ptr(rs), ptr(z), M, N, K, stream())
+
+
+def gemmf_tcq(bits, t8, hT, rs, z, K, bounds=(1 << 30, 1 << 30)):
+    """Fused decode + float product over the packed words as stored (bits and tables of up to three layers, bounds as
+    gemm_tcq); hT (K, >= M) BF16, z (M, N) FP32 = acc * rs (reference kernels.gemmf_tcq, kernels.py:694-696)."""
+    M, N = z.shape
+    _contig(bits, t8, hT, rs, z)
+    if bits.numel() != (N // 16) * (K // 16) * 32 or hT.dtype != torch.bfloat16 or hT.shape[0] != K or hT.shape[1] < M \
+            or rs.numel() != N:
+        raise ValueError('gemmf_tcq: shapes do not match')
+    if t8.numel() < 1024 * (1 + (N // 16 > bounds[0]) + (N // 16 > bounds[1])):
+        raise ValueError('gemmf_tcq: fewer tables than the bounds select')
+    call('tcq_gemmf_tcq_hT', ptr(bits), ptr(t8), ptr(hT), hT.shape[1], ptr(rs), ptr(z), M, N, K, int(bounds[0]), int(bounds[1]),
+         stream())
+
+
 # ----------------------------------------------------------------------------------------------------------- W8A8 GEMM
 def gemm_i8(a, w, out, sa=None, sw=None):
     """acc = a w^T exact in int32; out (M, ldo) int32 (acc), FP32 ((acc * sa) * sw) or BF16 of that. a (M, K), w (N, K) int8.

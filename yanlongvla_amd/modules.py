@@ -119,7 +119,8 @@ class Group:
     """Layers sharing one input rotation + quantization and one product, their output columns side by side
     (modules.py:29-155). mode: resident (INT8 weights, stream released) | fly (decoded on every call) | chunk (INT8 weights
     re-decoded by decode_chunk); a8: INT8 activations, else the W2 float path (BF16 rotated activations, the INT8 table
-    values as BF16 weights, FP32 accumulation; modules.py:117-144)."""
+    values as BF16 weights, FP32 accumulation; modules.py:117-144). Both paths keep the same weights: the packed words
+    (fly), or INT8 weights (resident, chunk)."""
 
     def __init__(self, layers, part, mode, a8=True):
         if not _shares_input(layers):
@@ -147,16 +148,14 @@ class Group:
             return None if t is None else t[c:c + n]
         self.segments = [Segment(c, n, piece(self.rs, c, n), piece(self.sv, c, n), piece(self.bias, c, n))
                          for c, n in zip(self.col0, self.N)]
-        if not a8:                                          # BF16 bit patterns of the INT8 table values (modules.py:60)
-            self.tb = [L.t8.to(torch.bfloat16).contiguous() for L in layers]
         self.W = None
         if mode in ('resident', 'chunk'):
-            if mode == 'chunk' and a8:
+            if mode == 'chunk':
                 self._repack()                              # the per-chunk decode reads the repacked words
-            self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8 if a8 else torch.bfloat16, device=self.su.device)
+            self.W = torch.empty(self.Ntot, self.K, dtype=torch.int8, device=self.su.device)
             self.decode()
-        elif a8:
-            self._repack()                                  # the fused small-M product reads the repacked words
+        else:
+            self._repack()                                  # the fused products read the repacked words
         self.pending = None
 
     def _repack(self):
@@ -166,13 +165,11 @@ class Group:
 
     # -------------------------------------------------------------------------------------------------- weights
     def decode(self, W=None):
-        """The group's dense weight rows (INT8, or BF16 images for the float path) into W (default: the resident W)."""
+        """The group's dense INT8 weight rows into W (default: the resident W)."""
         W = self.W if W is None else W
-        for i, (L, seg) in enumerate(zip(self.layers, self.segments)):
+        for L, seg in zip(self.layers, self.segments):
             rows = W[seg.col0:seg.col0 + seg.width]
-            if not self.a8:
-                kernels.decode_bf16(L.bits, self.tb[i], rows)
-            elif L.t8.dim() == 2 and L._words is not None:
+            if L.t8.dim() == 2 and L._words is not None:
                 kernels.decode_words(L._words, L.t8, rows)          # the words the fused products keep
             else:
                 kernels.decode(L.bits, L.t8, rows)
@@ -282,16 +279,18 @@ class Group:
         return outs
 
     def run_float(self, x2, shape):
-        """W2: BF16 rotated activations (kernels.rht), BF16 weights decoded from the INT8 table values, FP32 accumulation
-        (tcq_gemm_bf16). Expert: z = acc * rs in FP32; prefill: the product rounded to BF16, scaled by rs in the epilogue
-        (modules.py:117-144)."""
+        """W2: BF16 rotated activations (kernels.rht = the reference's pre_h), the INT8 table values as BF16 weights, FP32
+        sums, on the fused products (kernels.gemmf_segments: the packed words decoded on the fly, or the resident INT8
+        weights; no dense BF16 copy). Expert: z = acc * rs in FP32; prefill: the product rounded to BF16, scaled by rs in
+        the epilogue (modules.py:117-144)."""
         M, dev = x2.shape[0], x2.device
         h = kernels.rht(x2, self.su, torch.empty(M, self.K, dtype=torch.bfloat16, device=dev))
-        W = self.W if self.W is not None else self.decode(torch.empty(self.Ntot, self.K, dtype=torch.bfloat16, device=dev))
-        if self.small:
-            acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.float32, device=dev), sw=self.rs)
+        acc = torch.empty(M, self.Ntot, dtype=torch.float32 if self.small else torch.bfloat16, device=dev)
+        if self.W is not None:
+            segs = [(self.W[s.col0:s.col0 + s.width], None, s.rs, acc[:, s.col0:]) for s in self.segments]
         else:
-            acc = kernels.gemm_bf16(h, W, torch.empty(M, self.Ntot, dtype=torch.bfloat16, device=dev))
+            segs = [(L.words(), L.t8, s.rs, acc[:, s.col0:]) for L, s in zip(self.layers, self.segments)]
+        kernels.gemmf_segments(segs, h, self.Ntot, resident=self.W is not None)
         return self.posts(acc, None, shape)
 
     def get(self, x, index):
