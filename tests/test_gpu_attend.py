@@ -66,19 +66,24 @@ def test_causal_rows_ignore_later_keys():
     assert torch.equal(o1[:100], o2[:100]) and not torch.equal(o1[100:], o2[100:])
 
 
-@pytest.mark.parametrize('M,P', [(50, 800), (1, 800), (300, 0)])
-def test_fused_prologue_bitexact(M, P):
+@pytest.mark.parametrize('H', [1, 2, 4, 8])
+@pytest.mark.parametrize('M,P,causal', [(50, 800, None), (1, 800, None), (300, 0, 0), (7, 0, 0), (20, 40, 40)])
+def test_fused_prologue_bitexact(M, P, causal, H):
+    """The o-projection prologue fused into attention (rotate + quantize of the BF16 attention output, every engine width
+    H * 256 = 256 .. 2048) equals attention followed by kernels.pre bit for bit: q8, the token-block q4 and the scales.
+    Cases: a prefix without masking, a causal prefill with no prefix, and causal rows over a prefix (causal offset P)."""
     from yanlongvla_amd import kernels as K
-    q, kc, vc, kn, vn = inputs(M, P, 8, 7 + M)
-    su = (torch.randint(0, 2, (2048,), device=DEV) * 2 - 1).to(torch.int8)
-    causal = 0 if P == 0 else None
-    o = torch.empty(M, 2048, dtype=torch.bfloat16, device=DEV)
-    K.attend(q, kc, vc, kn, vn, 8, causal, o=o)
-    q1, s1 = torch.empty(M, 2048, dtype=torch.int8, device=DEV), torch.empty(M, device=DEV)
-    K.pre(o, su, q=q1, scale=s1)
-    q2, s2 = torch.empty_like(q1), torch.empty_like(s1)
-    K.attend(q, kc, vc, kn, vn, 8, causal, su=su, q8=q2, scale=s2)
+    q, kc, vc, kn, vn = inputs(M, P, H, 7 + M + H)
+    W = H * 256
+    su = (torch.randint(0, 2, (W,), generator=torch.Generator(device=DEV).manual_seed(H), device=DEV) * 2 - 1).to(torch.int8)
+    o = torch.empty(M, W, dtype=torch.bfloat16, device=DEV)
+    K.attend(q, kc, vc, kn, vn, H, causal, o=o)
+    q1, s1, tb1 = torch.empty(M, W, dtype=torch.int8, device=DEV), torch.empty(M, device=DEV), K.token_blocks(M, W, DEV)
+    K.pre(o, su, q=q1, q4=tb1, scale=s1)
+    q2, s2, tb2 = torch.empty_like(q1), torch.empty_like(s1), K.token_blocks(M, W, DEV)
+    K.attend(q, kc, vc, kn, vn, H, causal, su=su, q8=q2, scale=s2, q4=tb2)
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    assert torch.equal(K.rows_of_token_blocks(tb1, M), K.rows_of_token_blocks(tb2, M))
     o2 = torch.empty_like(o)
-    K.attend(q, kc, vc, kn, vn, 8, causal, o=o2)
+    K.attend(q, kc, vc, kn, vn, H, causal, o=o2)
     assert torch.equal(o, o2)

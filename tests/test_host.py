@@ -183,6 +183,9 @@ def test_k_parts_rule():
     assert parts(32768, 2048, 1) == 1           # gate/up: 2048 tile rows already fill the chip
     assert parts(256, 512, 3) == 1              # 2 chunks: no part would keep enough
     assert parts(2048, 16384, modules.SMALL_M + 1) == 1
+    assert parts(1536, 6144, 1) == 1            # not a power of two: the epilogue takes no K parts at this width
+    assert parts(512, 8192, 1) == 1             # below the epilogue's 1024-wide rows
+    assert parts(1024, 8192, 1) == 4            # 64 tile rows, 32 chunks
     old = modules.FUSE['k_parts']
     modules.FUSE['k_parts'] = False
     try:

@@ -70,3 +70,55 @@ def test_static_scratch_refuses_sizes_beyond_the_array():
     c = _case(800, 0, 0, 3)                        # 800 causal rows: 800 * 13 chunks * 8 heads * 260 floats > the array
     assert 800 * lib.tcq_attend_chunks(0, 800) * H * (D + 4) > cap
     assert _call(lib, c, _outputs(800)) == -4
+
+
+FRESH_PROCESS = r'''
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + '/tests')
+from yanlongvla_amd import _lib
+from test_zz_no_alloc import _case, _outputs, _call, H, D
+lib = _lib.lib()
+torch.cuda.init()
+c = _case(50, 800, -1, 4)
+nc = lib.tcq_attend_chunks(c['P'], c['M'])
+part = torch.empty(c['M'] * nc * H * (D + 4), dtype=torch.float32, device='cuda')
+ref, out = _outputs(c['M']), _outputs(c['M'])
+assert _call(lib, c, ref, part) == 0
+torch.cuda.synchronize()
+print('step: capture with the first static call of the process', flush=True)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    rc = _call(lib, c, out)
+assert rc == 0, rc
+for replay in range(3):
+    for k, v in _outputs(c['M']).items():
+        out[k].copy_(v)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    for k in ('o', 'q8', 'q4', 'scale'):
+        assert torch.equal(ref[k].view(torch.uint8), out[k].view(torch.uint8)), (replay, k)
+print('step: allocation check', flush=True)
+torch.cuda.synchronize()
+a0, f0 = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
+assert _call(lib, c, out) == 0
+torch.cuda.synchronize()
+a1, f1 = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
+assert (a0, f0) == (a1, f1), ((a0, f0), (a1, f1))
+print('FRESH_PROCESS_OK', flush=True)
+'''
+
+
+def test_static_scratch_first_call_under_graph_capture():
+    """In a fresh process, the first call of tcq_attend_q4_static (the per-device scratch lookup included) is recorded in a
+    HIP graph; three replays, each after eager writes over the outputs, equal the caller-workspace call bit for bit; and
+    an eager call changes neither PyTorch's allocated bytes nor the device's free memory."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, '-c', FRESH_PROCESS, str(root)], capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and 'FRESH_PROCESS_OK' in r.stdout

@@ -507,15 +507,22 @@ constexpr int SCRATCH_DEVICES = 64;
 std::mutex scratch_mu;
 float* scratch_ptr[SCRATCH_DEVICES] = {};
 
-// The device address of `scratch` on the current device (its own copy per device), looked up once per device.
+// The device address of `scratch` on the current device (its own copy per device), looked up once per device. The first
+// call on a device may come while the caller captures a graph: the lookup is no stream work, so this thread's capture
+// mode is relaxed around it (and restored), which lets it run under any capture mode.
 int scratch_on_current_device(float** out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES) return TCQ_ERR_UNSUPPORTED;
     std::lock_guard<std::mutex> lock(scratch_mu);
     if (!scratch_ptr[dev]) {
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess) return (int)e;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t r = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return (int)e;
+        if (r != hipSuccess) return (int)r;
         scratch_ptr[dev] = (float*)p;
     }
     *out = scratch_ptr[dev];

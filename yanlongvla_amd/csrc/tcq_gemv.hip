@@ -361,9 +361,10 @@ extern "C" int tcq_gemv_f16_post(const tcq_gemv_post_layer* layers, int nlayers,
 // The whole FP16-table layer of a few tokens in one launch: the operations of tcq_pre_h16, tcq_gemv_f16 (latency plan: one
 // tile row per workgroup, KS waves splitting its chunks) and tcq_post, step for step and in the same order, so y equals the
 // three-launch chain bit for bit. Every workgroup issues the loads of its words, rotates the M input rows itself (a few KiB;
-// no workgroup waits for another), decodes and multiplies its tile row, stores its 16 rows of z with device-coherent
-// stores and counts itself in *counter. The workgroup whose count completes the grid reads the whole z after an acquire
-// fence, rotates it, writes y and sets the counter back to zero, so a graph replays it without any reset.
+// no workgroup waits for another), decodes and multiplies its tile row, stores its 16 rows of z and counts itself in
+// *counter with an agent-scope acquire-release add (after a workgroup barrier, so the count releases the whole workgroup's
+// stores). The workgroup whose count completes the grid reads the whole z after an agent-scope acquire fence, rotates it,
+// writes y and sets the counter back to zero, so a graph replays it without any reset.
 // Rows of a power of two from 256 to 16 x (threads) run on registers (thread t owns elements [16 t, 16 t + 16), loaded and
 // stored as 16-byte vectors when VEC); other widths run the LDS block Walsh.
 struct LayerArgs {
@@ -548,12 +549,13 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
         uint4_t o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = __float_as_uint((a[e] * hs) * f16_to_f32((u16)(rs4 >> (16 * e))));
-        // device-coherent store (sc1): visible to the workgroup that completes the count, wherever it runs
-        __builtin_amdgcn_raw_buffer_store_b128(o, make_rsrc(A.z, (u32)(M * m) * 4), (u32)(lr * m + r0) * 4, 0, 16);
+        gptr((uint4_t*)(A.z + (size_t)lr * m + r0))[0] = o;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // hand-off: the barrier orders the workgroup's z stores before the count; the count is an agent-scope release (the
+    // stores reach the level every XCD reads) and acquire; the workgroup that completes it reads every z row after an
+    // agent-scope acquire fence
     __syncthreads();
-    if (tid == 0) last = __hip_atomic_fetch_add(A.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+    if (tid == 0) last = __hip_atomic_fetch_add(A.counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
     __syncthreads();
     if (!last) return;                                            // uniform over the workgroup
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");

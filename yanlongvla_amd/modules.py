@@ -202,8 +202,10 @@ class Group:
         product's workgroups (one per tile row and part) stay below the 256 CUs and every part keeps at least 4 of the
         256-column chunks; 1 for many tokens or when FUSE['k_parts'] is off. Measured on MI355X, product + epilogue:
         2048 x 16384 at one token 13.6 -> 12.4 us (fly), 19.3 -> 14.3 (resident INT8); 1024 x 4096 at 50 tokens (4 parts)
-        12.4 -> 10.6 / 12.5 -> 9.7; 2048 x 2048 at one token unchanged."""
-        if not FUSE['k_parts'] or M > SMALL_M:
+        12.4 -> 10.6 / 12.5 -> 9.7; 2048 x 2048 at one token unchanged. The epilogue adds K parts only for power-of-two
+        rows of 1024 .. 16384 (its register engines), so every other output width keeps one part."""
+        w = self.Ntot
+        if not FUSE['k_parts'] or M > SMALL_M or w & (w - 1) or not 1024 <= w <= 16384:
             return 1
         tiles, nch = self.Ntot // 16, (self.K + 255) // 256
         parts = 1
