@@ -79,3 +79,38 @@ def test_groot_layers_bitexact(one_sided, runtime, M):
         y = mod(x)
         want = O.reference_linear(x.float().cpu().numpy(), oracle[name])
         assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), want), name
+
+
+@pytest.mark.parametrize('one_sided', [True, False])
+def test_groot_fit_records_load_and_run(one_sided, tmp_path):
+    """GR00T fit records as groot_tcq.py writes them (torch.save of {w_hat, tensors: trellis (uint16), tlut, row_scale,
+    signs[, signs_out], col_scale, tcq}, 341-347 / 470-472), loaded by tcq_format.load_groot and installed: the layers'
+    outputs at 10 tokens equal the oracle's reference_linear of the same records bit for bit (fly runtime)."""
+    from yanlongvla_amd import groot, modules, tcq_format as F
+    model = groot.skeleton()
+    src = groot.synthetic_layers(model, 31, DEV, one_sided=one_sided, names=SAMPLE)
+    files = {}
+    for name, L in src.items():
+        t = dict(trellis=L.bits.cpu().view(torch.uint16).reshape(-1), tlut=L.tlut.cpu(), row_scale=L.row_scale.cpu(),
+                 signs=L.su.cpu(), col_scale=L.col_scale.cpu())
+        if L.sv is not None:
+            t['signs_out'] = L.sv.cpu()
+        files[name] = tmp_path / f'{name}.pt'
+        torch.save(dict(w_hat=torch.zeros(1), tensors=t, tcq=dict(L=16, K=2, V=2, td=16, rotation='one' if one_sided else 'two')),
+                   files[name])
+    oracle = {n: oracle_layer(L) for n, L in src.items()}
+    biases = {n: L.bias for n, L in src.items() if L.bias is not None}      # the model's biases (records hold none)
+    del src
+    layers = F.load_groot(files, device=DEV, biases=biases)
+    assert all((L.sv is None) == one_sided and L.col_scale is not None for L in layers.values())
+    modules.install(model, runtime='fly', layers=layers)
+    rng = np.random.default_rng(3)
+    inputs = {}
+    for name in SAMPLE:
+        mod = model.get_submodule(name)
+        key = (name.rpartition('.')[0], mod.in_features)
+        if key not in inputs:
+            inputs[key] = torch.from_numpy(rng.standard_normal((10, mod.in_features)).astype(np.float32)).bfloat16().to(DEV)
+        y = mod(inputs[key])
+        want = O.reference_linear(inputs[key].float().cpu().numpy(), oracle[name])
+        assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), want), name

@@ -188,3 +188,56 @@ def convert_qtip(files, path):
     """{layer name: QTIP-official per-layer .safetensors} -> one packed file at path."""
     from safetensors.torch import load_file
     return save({name: from_qtip(load_file(str(f))) for name, f in files.items()}, path)
+
+
+# ------------------------------------------------------------------------------------------- GR00T fit records
+def from_groot(rec):
+    """One GR00T TCQ fit record -> the packed tensors {bits, tlut, row_scale, su[, sv][, col_scale]} (CPU tensors).
+
+    The records (baselines/groot/simpler/main_row/scripts/groot_tcq.py:341-343 for the one- and two-sided bases, 470 for the
+    row-group variants) hold `trellis` (QTIP pack_trellis of the 16 x 16 tiles in row-major tile order, state 8 r + p = row
+    r, pair p of a tile: groot_tcq.pack / unpack, 218-228), `tlut` (512, 2) or (G, 512, 2) FP16, `row_scale` (m,) FP16,
+    `signs` (n,) and optionally `signs_out` (m,) int8 and `col_scale` (n,) FP16, with the decoded weight
+    W = [S_out H_m] diag(r) Q diag(c) H_n S_in (groot_tcq.decode / inverse_rotation, 178-191; inverse_rht = block Walsh then
+    signs, groot_ptq.py:155-159). That is the deploy format's layer with bits = the trellis words (the same pack and tile
+    order the reference's own packer copies unchanged for the pi0.5 records, deploy/tcq_kernels/tcq_format.py:204-207),
+    su = signs, sv = signs_out (absent: one-sided) and the column scale kept. `rec` is the record or its `tensors` dict."""
+    t = rec.get('tensors', rec)
+    info = rec.get('tcq') if isinstance(rec.get('tcq'), dict) else None
+    if info is not None and (info.get('L'), info.get('K'), info.get('V'), info.get('td')) not in ((16, 2, 2, 16), (None, None, None, None)):
+        raise ValueError(f"record format {info}: the deploy path takes L = 16, K = 2, V = 2, 16 x 16 tiles")
+    su = t['signs'].to(torch.int8).reshape(-1)
+    rsc = t['row_scale'].to(torch.float16).reshape(-1)
+    m, n = rsc.numel(), su.numel()
+    bits = t['trellis'].contiguous().view(torch.int16).reshape(-1, 32)
+    if bits.shape[0] != (m // 16) * (n // 16) or m % 16 or n % 16:
+        raise ValueError(f'trellis holds {bits.shape[0]} tiles, a {m} x {n} layer has {(m // 16) * (n // 16)}')
+    out = dict(bits=bits, tlut=t['tlut'].to(torch.float16).contiguous(), row_scale=rsc.contiguous(), su=su.contiguous())
+    if t.get('signs_out') is not None:
+        out['sv'] = t['signs_out'].to(torch.int8).reshape(-1).contiguous()
+    if t.get('col_scale') is not None:
+        out['col_scale'] = t['col_scale'].to(torch.float16).reshape(-1).contiguous()
+    for k in ('su', 'sv'):
+        if k in out and not torch.all(out[k].abs() == 1):
+            raise ValueError(f'{k} must hold +-1')
+    return out
+
+
+def _read_record(path):
+    """A record file: torch.save'd dicts of tensors (read without unpickling code) or safetensors."""
+    path = Path(path)
+    if path.suffix == '.safetensors':
+        from safetensors.torch import load_file
+        return load_file(str(path))
+    return torch.load(str(path), map_location='cpu', weights_only=True)
+
+
+def load_groot(files, device='cuda', biases=None):
+    """{layer name: GR00T fit record file} -> {name: Layer}."""
+    return {name: Layer(name, from_groot(_read_record(f)), bias=(biases or {}).get(name), device=device)
+            for name, f in files.items()}
+
+
+def convert_groot(files, path):
+    """{layer name: GR00T fit record file} -> one packed file at path (sv / col_scale entries where the records hold them)."""
+    return save({name: from_groot(_read_record(f)) for name, f in files.items()}, path)
