@@ -263,8 +263,38 @@ def graph_per_call(fn, calls=20, replays=20):
     return a.elapsed_time(b) / (replays * calls)
 
 
+ROTATE_BYTES = 512 << 20        # distinct operands per timed graph: twice the 256 MB last-level cache
+ROTATE_MAX_SETS = 512
+
+
+def rotating_sets(bytes_per_set):
+    """How many distinct operand sets of this size one timed graph cycles through: enough for ROTATE_BYTES (each call
+    then finds its operands outside the last-level cache), at most ROTATE_MAX_SETS."""
+    return max(2, min(ROTATE_MAX_SETS, -(-ROTATE_BYTES // bytes_per_set)))
+
+
+def rotating_per_call(fns, replays=5):
+    """Device ms per call of a list of calls on distinct operands, captured in order as one graph (graph_per_call)."""
+    def run():
+        for f in fns:
+            f()
+    return graph_per_call(run, calls=1, replays=replays) / len(fns)
+
+
+def hbm_figure(byts, ms, sets):
+    """The rate of a call over distinct operands: an HBM fraction when the sets exceed the last-level cache."""
+    gbs = byts / (ms * 1e-3) / 1e9
+    r = {'us': round(ms * 1e3, 2), 'GBs': round(gbs, 1), 'distinct_operand_MB': round(sets * byts / 2 ** 20, 1), 'sets': sets}
+    if sets * byts > 256 << 20:
+        r['hbm_frac'] = round(gbs / HBM_PEAK_GBS, 4)
+    else:
+        r['note'] = 'operands fit the last-level cache even across sets: launch / latency bound, no HBM figure'
+    return r
+
+
 def rht_figures(dev, seed):
-    """Randomized block-Walsh transform of BF16 rows [M, n] (tcq_rht, BF16 in and out), per call; bytes = 4 M n + n."""
+    """Randomized block-Walsh transform of BF16 rows [M, n] (tcq_rht, BF16 in and out), per call; bytes = 4 M n + n. Timed
+    over distinct input / output rows (rotating_sets) and, labelled cache-resident, on one set."""
     import torch
     from yanlongvla_amd import kernels as K
     g = torch.Generator(device=dev).manual_seed(seed + 5)
@@ -272,18 +302,23 @@ def rht_figures(dev, seed):
     for n in (1024, 2048, 4096, 16384):
         su = (torch.randint(0, 2, (n,), generator=g, device=dev) * 2 - 1).to(torch.int8)
         for M in (1, 16, 50, 800):
-            x = torch.randn(M, n, generator=g, device=dev).bfloat16()
-            y = torch.empty_like(x)
-            ms = graph_per_call(lambda: K.rht(x, su, y))
             byts = 4 * M * n + n
-            out[f'{M}x{n}'] = {'us': round(ms * 1e3, 2), 'GBs': round(byts / (ms * 1e-3) / 1e9, 1),
-                               'hbm_frac': round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            S = rotating_sets(byts)
+            xs = torch.randn(S, M, n, generator=g, device=dev).bfloat16()
+            ys = torch.empty_like(xs)
+            ms = rotating_per_call([lambda i=i: K.rht(xs[i], su, ys[i]) for i in range(S)])
+            r = hbm_figure(byts, ms, S)
+            r['us_cache_resident'] = round(graph_per_call(lambda: K.rht(xs[0], su, ys[0])) * 1e3, 2)
+            out[f'{M}x{n}'] = r
+            del xs, ys
+    torch.cuda.empty_cache()
     return out
 
 
 def gemm_figures(dev, seed):
     """W8A8 GEMM, K = 2048, N = 16384: A = per-token INT8 of N(0,1) BF16 activations, B = per-channel INT8 of N(0, 0.02)
-    weights (tcq_quantize_rows); timed: the exact int32 product and the BF16 output (acc * s_token) * s_channel. The
+    weights (tcq_quantize_rows); timed: the exact int32 product and the BF16 output (acc * s_token) * s_channel, over
+    distinct weight / activation sets (rotating_sets; the same-operand times are reported as cache-resident). The
     M = 50 product is checked bit-exact against the oracle's integer matmul."""
     import numpy as np
     import torch
@@ -291,43 +326,59 @@ def gemm_figures(dev, seed):
     from yanlongvla_amd import kernels as K
     g = torch.Generator(device=dev).manual_seed(seed + 6)
     Kd, N = 2048, 16384
-    w = (torch.randn(N, Kd, generator=g, device=dev) * 0.02).bfloat16()
-    qw = torch.empty(N, Kd, dtype=torch.int8, device=dev)
-    sw = torch.empty(N, dtype=torch.float32, device=dev)
-    K.quantize_rows(w, qw, sw)
+    wbytes = N * Kd + 4 * N
+    SW = rotating_sets(wbytes)
+    qw = torch.empty(SW, N, Kd, dtype=torch.int8, device=dev)
+    sw = torch.empty(SW, N, dtype=torch.float32, device=dev)
+    for i in range(SW):
+        w = (torch.randn(N, Kd, generator=g, device=dev) * 0.02).bfloat16()
+        K.quantize_rows(w, qw[i], sw[i])
+    del w
     out = {}
     for M in (800, 50, 1):
-        a = torch.randn(M, Kd, generator=g, device=dev).bfloat16()
-        qa = torch.empty(M, Kd, dtype=torch.int8, device=dev)
-        sa = torch.empty(M, dtype=torch.float32, device=dev)
-        K.quantize_rows(a, qa, sa)
+        a = torch.randn(SW, M, Kd, generator=g, device=dev).bfloat16()
+        qa = torch.empty(SW, M, Kd, dtype=torch.int8, device=dev)
+        sa = torch.empty(SW, M, dtype=torch.float32, device=dev)
+        for i in range(SW):
+            K.quantize_rows(a[i], qa[i], sa[i])
         acc = torch.empty(M, N, dtype=torch.int32, device=dev)
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        t_i32 = graph_per_call(lambda: K.gemm_i8(qa, qw, acc))
-        t_bf16 = graph_per_call(lambda: K.gemm_i8(qa, qw, y, sa, sw))
+        t_i32 = rotating_per_call([lambda i=i: K.gemm_i8(qa[i], qw[i], acc) for i in range(SW)])
+        t_bf16 = rotating_per_call([lambda i=i: K.gemm_i8(qa[i], qw[i], y, sa[i], sw[i]) for i in range(SW)])
+        c_i32 = graph_per_call(lambda: K.gemm_i8(qa[0], qw[0], acc))
+        c_bf16 = graph_per_call(lambda: K.gemm_i8(qa[0], qw[0], y, sa[0], sw[0]))
         ops = 2 * M * N * Kd
         byts = M * Kd + N * Kd + 4 * M + 4 * N + 2 * M * N
         r = {'us_int32': round(t_i32 * 1e3, 2), 'us_bf16': round(t_bf16 * 1e3, 2),
-             'TOPS_bf16': round(ops / (t_bf16 * 1e-3) / 1e12, 1), 'GBs_bf16': round(byts / (t_bf16 * 1e-3) / 1e9, 1)}
+             'TOPS_bf16': round(ops / (t_bf16 * 1e-3) / 1e12, 1), 'GBs_bf16': round(byts / (t_bf16 * 1e-3) / 1e9, 1),
+             'distinct_weight_sets': SW, 'distinct_operand_MB': round(SW * (byts - 2 * M * N) / 2 ** 20, 1),
+             'us_int32_cache_resident': round(c_i32 * 1e3, 2), 'us_bf16_cache_resident': round(c_bf16 * 1e3, 2)}
         if M == 800:
             r['mfma_frac_bf16'] = round(r['TOPS_bf16'] / MFMA_I8_PEAK_TOPS, 4)
             r['mfma_frac_int32'] = round(ops / (t_i32 * 1e-3) / 1e12 / MFMA_I8_PEAK_TOPS, 4)
-            # the reference's own prefill product (torch._int_mm, hipBLASLt on ROCm) on the same operands and box
+            # the reference's own prefill product (torch._int_mm, hipBLASLt on ROCm) on the same operand sets and box
             try:
-                wt = qw.t()
-                same = bool(torch.equal(torch._int_mm(qa, wt), acc))
-                r['torch_int_mm_us_int32'] = round(graph_per_call(lambda: torch._int_mm(qa, wt)) * 1e3, 2)
+                K.gemm_i8(qa[0], qw[0], acc)
+                same = bool(torch.equal(torch._int_mm(qa[0], qw[0].t()), acc))
+                r['torch_int_mm_us_int32'] = round(rotating_per_call([lambda i=i: torch._int_mm(qa[i], qw[i].t())
+                                                                      for i in range(SW)]) * 1e3, 2)
                 r['torch_int_mm_equal'] = same
             except RuntimeError as e:
                 r['torch_int_mm_us_int32'] = f'unavailable: {e}'[:120]
         else:
             r['hbm_frac_bf16'] = round(r['GBs_bf16'] / HBM_PEAK_GBS, 4)
+            r['hbm_frac_int32'] = round((byts - 2 * M * N + 4 * M * N) / (t_i32 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         if M == 50:
-            ref = O.int_matmul(qa.cpu().numpy(), qw.cpu().numpy())
+            K.gemm_i8(qa[0], qw[0], acc)
+            K.gemm_i8(qa[0], qw[0], y, sa[0], sw[0])
+            ref = O.int_matmul(qa[0].cpu().numpy(), qw[0].cpu().numpy())
             r['int32_bitexact'] = bool(np.array_equal(acc.cpu().numpy(), ref))
-            yb = O.bf16_bits((ref.astype(np.float32) * sa.cpu().numpy()[:, None]) * sw.cpu().numpy()[None, :])
+            yb = O.bf16_bits((ref.astype(np.float32) * sa[0].cpu().numpy()[:, None]) * sw[0].cpu().numpy()[None, :])
             r['bf16_bitexact'] = bool(np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), yb))
         out[f'M={M}'] = r
+        del a, qa, sa
+    del qw, sw
+    torch.cuda.empty_cache()
     return out
 
 
@@ -575,10 +626,55 @@ def backbone(args, dev):
                 decode_products_M1=products, kernel_classes_fly=classes, cpu_baseline=cpu)
 
 
+class _Calls(list):
+    """A list of calls that also keeps their tensors alive."""
+    keep = None
+
+
+def product_sets(widths, Kd, resident, parts, dev, g):
+    """Calls of one small-M product shape (segments of the given widths side by side, K = Kd, one token in the token-block
+    layout) over distinct synthetic weight sets (rotating_sets): repacked 2-bit words (fly) or INT8 weights (resident),
+    each set its own tables and row scales. Returns (calls, bytes per call, sets)."""
+    import torch
+    from yanlongvla_amd import kernels as K
+    Ntot = sum(widths)
+    byts = Ntot * Kd if resident else Ntot * Kd // 4
+    S = rotating_sets(byts)
+    col0 = [sum(widths[:i]) for i in range(len(widths))]
+    if parts > 1:
+        out = torch.empty(parts, 1, Ntot, dtype=torch.int32, device=dev)
+        outs = [out[0, :, c:] for c in col0]
+    else:
+        out = torch.empty(1, Ntot, dtype=torch.float32, device=dev)
+        outs = [out[:, c:] for c in col0]
+    x = torch.randn(1, Kd, generator=g, device=dev).bfloat16()
+    su = (torch.randint(0, 2, (Kd,), generator=g, device=dev) * 2 - 1).to(torch.int8)
+    q4, sc = K.token_blocks(1, Kd, dev), torch.empty(1, dtype=torch.float32, device=dev)
+    K.pre(x, su, q4=q4, scale=sc)
+    calls, keep = _Calls(), [out, q4, sc]
+    for _ in range(S):
+        segs = []
+        for m, o in zip(widths, outs):
+            rs = torch.rand(m, generator=g, device=dev) * 1e-3
+            if resident:
+                w, t8 = torch.randint(-127, 128, (m, Kd), generator=g, device=dev, dtype=torch.int8), None
+            else:
+                w = torch.randint(-2 ** 31, 2 ** 31 - 1, (K.repack_words(m, Kd),), generator=g, device=dev, dtype=torch.int32)
+                t8 = torch.randint(-127, 128, (512, 2), generator=g, device=dev, dtype=torch.int8)
+            segs.append((w, t8, rs, o))
+        prod = K.SmallProduct(segs, Ntot, resident=resident)
+        calls.append(lambda prod=prod: prod(q4, sc, parts))
+        keep.append(prod)
+    calls.keep = keep
+    return calls, byts, S
+
+
 def decode_products(model, runtime, dev, seed):
-    """Device time and weight-stream rate of each product of decoder layer 0 at one token (the decode step's GEMVs), per
-    call from back-to-back graph replays: fly reads the 2-bit words (m * n / 4 bytes), resident the INT8 weights. The o and
-    down products run in the K parts the decoder layer uses for them (Group.k_parts; their epilogue adds the parts)."""
+    """Device time and weight-stream rate of each product of the decode step at one token (q/k/v, o, gate/up, down of a
+    decoder layer), per call: over distinct weight sets of the layer's shapes (product_sets, more than 256 MB in all, so
+    every call streams its weights from HBM; fly reads the 2-bit words, m * n / 4 bytes, resident the INT8 weights), and,
+    labelled cache-resident, on decoder layer 0's own group replayed in place. The o and down products run in the K parts
+    the decoder layer uses for them (Group.k_parts; their epilogue adds the parts)."""
     import torch
     groups = {g.layers[0].name: g for g in model._tcq_groups}
     pre = 'paligemma_with_expert.paligemma.language_model.layers.0.'
@@ -586,13 +682,16 @@ def decode_products(model, runtime, dev, seed):
     out = {}
     for tag, key in (('q/k/v', 'self_attn.q_proj'), ('o', 'self_attn.o_proj'), ('gate/up', 'mlp.gate_proj'), ('down', 'mlp.down_proj')):
         g = groups[pre + key]
+        resident = runtime != 'fly'
         b = g.quantize(torch.randn(1, g.K, generator=g0, device=dev).bfloat16())
         parts = g.k_parts(1) if tag in ('o', 'down') else 1
-        ms = graph_per_call(lambda: g.product(b, parts))
-        byts = g.Ntot * g.K // 4 if runtime == 'fly' else g.Ntot * g.K
-        gbs = byts / (ms * 1e-3) / 1e9
-        out[tag] = {'shape': f'{g.Ntot}x{g.K}', 'bytes': byts, 'us': round(ms * 1e3, 2), 'GBs': round(gbs, 1),
-                    'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'k_parts': parts}
+        ms_cache = graph_per_call(lambda: g.product(b, parts))
+        calls, byts, S = product_sets(g.N, g.K, resident, parts, dev, g0)
+        r = hbm_figure(byts, rotating_per_call(calls), S)
+        r.update(shape=f'{g.Ntot}x{g.K}', bytes=byts, k_parts=parts, us_cache_resident=round(ms_cache * 1e3, 2))
+        out[tag] = r
+        del calls
+        torch.cuda.empty_cache()
     return out
 
 
