@@ -51,6 +51,13 @@ def parse():
     p.add_argument('--no-ops', action='store_true', help='skip the RHT and W8A8 GEMM measurements')
     p.add_argument('--no-backbone', action='store_true', help='skip the Gemma-2B-shaped backbone measurement')
     p.add_argument('--backbone-replays', type=int, default=10)
+    p.add_argument('--probe', choices=('gate_up', 'qkv', 'mid2', 'gemm', 'prefill'),
+                   help='only run one kernel kind --probe-reps times (for rocprofv3 counter passes): the fused decode '
+                        'product of one token at the backbone gate/up (32768 x 2048, k_gemv_tcq) or q/k/v (2560 x 2048, '
+                        'k_gemm_small) shape over distinct weight sets, the one-token GeGLU middle (16384 wide, '
+                        'k_mid2_tw2), the W8A8 GEMM 800 x 2048 x 16384 (k_gemm_i8, int32 out) over distinct weights, or '
+                        'the backbone\'s 800-token prefill (fly) as one graph')
+    p.add_argument('--probe-reps', type=int, default=10)
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
                         'FETCH_SIZE / WRITE_SIZE counters into bytes)')
@@ -730,6 +737,42 @@ def backbone_cpu_baseline(model, layers, x, state, dec_x):
                        f'{len(os.sched_getaffinity(0))} cores')
 
 
+def probe(kind, reps, dev):
+    """Run one kernel kind `reps` times (see --probe); prints what ran, nothing else."""
+    import torch
+    from yanlongvla_amd import kernels as K
+    g = torch.Generator(device=dev).manual_seed(1)
+    if kind in ('gate_up', 'qkv'):
+        calls, _, _ = product_sets([16384, 16384] if kind == 'gate_up' else [2048, 256, 256], 2048, False, 1, dev, g)
+    elif kind == 'mid2':
+        N = 16384
+        acc = torch.randn(1, 2 * N, generator=g, device=dev) * 0.01
+        sv = (torch.randint(0, 2, (2 * N,), generator=g, device=dev) * 2 - 1).to(torch.int8)
+        su = (torch.randint(0, 2, (N,), generator=g, device=dev) * 2 - 1).to(torch.int8)
+        q4, sc, lut = K.token_blocks(1, N, dev), torch.empty(1, device=dev), K.gelu_table(dev)
+        calls = [lambda: K.mid2(acc, None, None, sv, su, q4=q4, scale=sc, gelu_lut=lut)] * 64
+    elif kind == 'prefill':
+        from yanlongvla_amd import gemma, harness, modules
+        img, ids, _ = backbone_setup(0, dev)
+        with torch.inference_mode():
+            model = gemma.make_policy(gemma.BackbonePolicy, dev, seed=1)
+            modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 9, dev))
+            x = torch.cat([img, model.embed(ids)], 0)
+            g = harness.capture(lambda: model.prefill(x))
+        calls = [g.replay]
+    else:
+        SW, M, N, Kd = 8, 800, 16384, 2048
+        qw = torch.randint(-127, 128, (SW, N, Kd), generator=g, device=dev, dtype=torch.int8)
+        qa = torch.randint(-127, 128, (M, Kd), generator=g, device=dev, dtype=torch.int8)
+        acc = torch.empty(M, N, dtype=torch.int32, device=dev)
+        calls = [lambda i=i: K.gemm_i8(qa, qw[i], acc) for i in range(SW)]
+    for _ in range(reps):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    note(f'probe {kind}: {reps} x {len(calls)} calls')
+
+
 def note(msg):
     """Progress line of a finished stage, on stderr (the JSON result line stays alone on stdout)."""
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
@@ -743,6 +786,13 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.probe:
+        import torch
+        from yanlongvla_amd import _lib
+        _lib.lib()
+        torch.cuda.set_device(0)
+        probe(args.probe, args.probe_reps, torch.device('cuda:0'))
         return
     import torch
     from yanlongvla_amd import _lib
