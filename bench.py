@@ -51,12 +51,12 @@ def parse():
     p.add_argument('--no-ops', action='store_true', help='skip the RHT and W8A8 GEMM measurements')
     p.add_argument('--no-backbone', action='store_true', help='skip the Gemma-2B-shaped backbone measurement')
     p.add_argument('--backbone-replays', type=int, default=10)
-    p.add_argument('--probe', choices=('gate_up', 'qkv', 'mid2', 'gemm', 'prefill'),
+    p.add_argument('--probe', choices=('gate_up', 'qkv', 'mid2', 'gemm', 'prefill', 'decode'),
                    help='only run one kernel kind --probe-reps times (for rocprofv3 counter passes): the fused decode '
                         'product of one token at the backbone gate/up (32768 x 2048, k_gemv_tcq) or q/k/v (2560 x 2048, '
                         'k_gemm_small) shape over distinct weight sets, the one-token GeGLU middle (16384 wide, '
                         'k_mid2_tw2), the W8A8 GEMM 800 x 2048 x 16384 (k_gemm_i8, int32 out) over distinct weights, or '
-                        'the backbone\'s 800-token prefill (fly) as one graph')
+                        'the backbone\'s 800-token prefill (fly) or its 32 decode steps as one graph')
     p.add_argument('--probe-reps', type=int, default=10)
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
@@ -751,14 +751,24 @@ def probe(kind, reps, dev):
         su = (torch.randint(0, 2, (N,), generator=g, device=dev) * 2 - 1).to(torch.int8)
         q4, sc, lut = K.token_blocks(1, N, dev), torch.empty(1, device=dev), K.gelu_table(dev)
         calls = [lambda: K.mid2(acc, None, None, sv, su, q4=q4, scale=sc, gelu_lut=lut)] * 64
-    elif kind == 'prefill':
+    elif kind in ('prefill', 'decode'):
         from yanlongvla_amd import gemma, harness, modules
-        img, ids, _ = backbone_setup(0, dev)
+        img, ids, dec = backbone_setup(0, dev)
         with torch.inference_mode():
             model = gemma.make_policy(gemma.BackbonePolicy, dev, seed=1)
             modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 9, dev))
             x = torch.cat([img, model.embed(ids)], 0)
-            g = harness.capture(lambda: model.prefill(x))
+            if kind == 'prefill':
+                g = harness.capture(lambda: model.prefill(x))
+            else:
+                _, ks, vs = model.prefill(x)
+                cache = gemma.KVCache(ks, vs, BB_DECODE)
+
+                def steps():
+                    cache.rewind()
+                    for t in range(BB_DECODE):
+                        model.decode_step_cached(model.embed(dec[t]), cache)
+                g = harness.capture(steps)
         calls = [g.replay]
     else:
         SW, M, N, Kd = 8, 800, 16384, 2048

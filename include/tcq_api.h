@@ -61,6 +61,13 @@ enum tcq_dtype { TCQ_F32 = 0, TCQ_BF16 = 1, TCQ_F16 = 2, TCQ_I32 = 3, TCQ_I8 = 4
 #define TCQ_K_PARTS2 0x200
 #define TCQ_K_PARTS4 0x400
 
+/* Stage-split gated-MLP input (flag of out_dtype, with TCQ_F32, for tcq_gemm_tcq at M <= 16, K <= 4096, every segment m a
+ * multiple of 128): each segment's FP32 z = (float(acc) s) rs goes through the first seven stages of its block Walsh
+ * (h = 1 .. 64, which stay inside blocks of 128 rows, in the reference's stage order) inside the product, and is stored
+ * block-transposed, out (M, 128, m / 128): row 128 b + o of token t at out[(t * 128 + o) * (m / 128) + b]. tcq_glu_split
+ * finishes the middle from it. No reference counterpart: it splits tcq_mid2 (kernels.py:263-278) over many CUs. */
+#define TCQ_Z_W128T 0x1000
+
 /* Library version string and the widest row the block-Walsh kernels take (16384). */
 const char* tcq_version(void);
 int tcq_max_width(void);
@@ -382,6 +389,13 @@ int tcq_pre_h(const void* x, int x_dtype, const int8_t* su, uint16_t* h, uint16_
 /* 1 when tcq_mid2 takes a gated-MLP middle of width N (N % 16 == 0, N <= 16384), else 0. Replaces kernels.mid2_available
  * (deploy/tcq_kernels/kernels.py:636-638), whose answer depends on the shared-memory limit of the reference's kernels. */
 int tcq_mid2_available(int N);
+
+/* The gated-MLP middle after a TCQ_Z_W128T product of gate | up (zt: gate's (M, 128, N / 128) block-transposed rows, then
+ * up's), N = 16384, M <= 16: the remaining block Walsh stages (h = 128 .. N / 2), then as tcq_mid2 (* c, signs sv (2N,)
+ * gate | up, BF16 roundings, GELU by the table, the product): p (M, N) BF16 = bf16(gelu(g) * u), natural order. tcq_pre
+ * of p with the down projection's signs then gives tcq_mid2's q / q4 / scale bit for bit. Replaces, with the product's
+ * epilogue, the one-workgroup tcq_mid2 of few tokens (kernels.py:263-278, 640-643) by work spread over many CUs. */
+int tcq_glu_split(const float* zt, int N, const int8_t* sv, const uint16_t* gelu_lut, uint16_t* p, int M, tcq_stream_t stream);
 
 /* W2 float path products over up to TCQ_MAX_SEGS layers side by side (segments as tcq_gemm_tcq): acc[t, i] = sum_k w[i, k]
  * h[t, k] with FP32 sums (MFMA blocks), the weights the INT8 table values taken as BF16, h (M, K) BF16 rotated activations

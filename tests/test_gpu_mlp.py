@@ -184,3 +184,51 @@ def test_mid2_many_rows_bitexact(kind, M, N):
     assert np.array_equal(sc.cpu().numpy(), sr[:, 0]) and np.array_equal(sc2.cpu().numpy(), sr[:, 0])
     assert np.array_equal(q4.cpu().numpy(), O.q4_layout(qr))
     assert np.array_equal(K.rows_of_token_blocks(qb, M).cpu().numpy(), qr)
+
+
+@pytest.mark.parametrize('M', [1, 3, 16])
+def test_spread_middle_equals_mid2_and_oracle(M):
+    """The 16384-wide GeGLU middle of few tokens spread over many CUs: the gate/up product with the first seven Walsh
+    stages in its epilogue (gemm_tcq_w128t), glu_split, then pre with the down projection's signs. Pinned three ways:
+    the stage-split product's output equals the product's FP32 z after Walsh stages h = 1 .. 64 within 128-row blocks
+    (computed on the host in the oracle's butterfly order), block-transposed, bit for bit; the INT8 rows and scales equal
+    the one-launch mid2's bit for bit; and both equal the oracle's mlp_middle."""
+    from yanlongvla_amd import kernels as K
+    from yanlongvla_amd import tcq_format as F
+    rng = np.random.default_rng(600 + M)
+    n, N = 2048, 16384
+    ols = [O.random_layer(N, n, 700 + M + i, per_layer_scale=False) for i in range(2)]
+    ols[1].su = ols[0].su
+    devs = [F.Layer(f'l{i}', dict(bits=T(ol.bits), tlut=T(ol.tlut), row_scale=T(ol.row_scale), su=T(ol.su), sv=T(ol.sv)),
+                    device=DEV) for i, ol in enumerate(ols)]
+    x = T(rng.standard_normal((M, n)).astype(np.float32)).bfloat16()
+    tb, s = K.token_blocks(M, n, DEV), torch.empty(M, device=DEV)
+    K.pre(x, devs[0].su, q4=tb, scale=s)
+    z = torch.empty(M, 2 * N, device=DEV)
+    K.gemm_tcq_segments([(L.words(), L.t8, L.rs, z[:, i * N:]) for i, L in enumerate(devs)], tb, s, 2 * N)
+    zt = torch.empty(2, M, 128, 128, device=DEV)
+    K.gemm_tcq_w128t([(L.words(), L.t8, L.rs, zt[i]) for i, L in enumerate(devs)], tb, s)
+    # the first seven stages, on the host: (M, 2, 128 blocks, 128) -> butterflies h = 1 .. 64 within each block
+    blocks = z.cpu().numpy().reshape(M, 2, 128, 128)
+    h = 1
+    while h < 128:
+        v = blocks.reshape(M, 2, 128, 128 // (2 * h), 2, h)
+        a, b = v[..., 0, :], v[..., 1, :]
+        blocks = np.stack((a + b, a - b), axis=-2).reshape(M, 2, 128, 128)
+        h *= 2
+    want_zt = blocks.transpose(1, 0, 3, 2)                         # (2, M, offset, block)
+    assert np.array_equal(zt.cpu().numpy().view(np.uint32), np.ascontiguousarray(want_zt).view(np.uint32))
+    sv = torch.cat([L.sv for L in devs]).contiguous()
+    su = T(signs(rng, N))
+    lut = K.gelu_table(DEV)
+    q1, s1 = K.token_blocks(M, N, DEV), torch.empty(M, device=DEV)
+    K.mid2(z, None, None, sv, su, q4=q1, scale=s1, gelu_lut=lut)
+    p = K.glu_split(zt, sv, lut, torch.empty(M, N, dtype=torch.bfloat16, device=DEV))
+    q2, s2 = K.token_blocks(M, N, DEV), torch.empty(M, device=DEV)
+    K.pre(p, su, q4=q2, scale=s2)
+    assert torch.equal(K.rows_of_token_blocks(q1, M), K.rows_of_token_blocks(q2, M)) and torch.equal(s1, s2)
+    zz = z.cpu().numpy()
+    lut_h = lut.view(torch.int16).cpu().numpy().view(np.uint16)
+    qr, sr, _, _ = O.mlp_middle(zz[:, :N], zz[:, N:], sv.cpu().numpy()[:N], sv.cpu().numpy()[N:], su.cpu().numpy(),
+                                gelu=lambda b: lut_h[b])
+    assert np.array_equal(K.rows_of_token_blocks(q2, M).cpu().numpy(), qr) and np.array_equal(s2.cpu().numpy(), sr[:, 0])

@@ -68,6 +68,7 @@ SIGNATURES = {
     'tcq_gemmf_w8': [_P, _I, _P, _I, _I, _I, _I, _P],
     'tcq_gemmf_w8_hT': [_P, _P, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemmf_tcq_hT': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P],
+    'tcq_glu_split': [_P, _I, _P, _P, _P, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 

@@ -218,9 +218,13 @@ constexpr int GV_C = 16;
 constexpr int GV_CMAX = 8;
 constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table fill per 16 waves)
 
-template <int ODT, bool QB, int WPR, int NW, int KS = 1>
+// LO (TCQ_Z_W128T, FP32 scaled z, RPW = 8): the workgroup's 128 rows are one 128-row block of the segment; the first seven
+// stages of the block Walsh of the whole segment (h = 1 .. 64, which stay inside such a block) run here, in the reference's
+// stage order, and the block is stored transposed: zt[(t * 128 + o) * (m / 128) + blk] for row 128 blk + o of token t.
+template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
+    static_assert(!LO || (ODT == TCQ_F32 && KS == 1 && NW / WPR == 8), "stage-split output: FP32 z, 8 tile rows per workgroup");
     constexpr int RPW = NW / WPR;
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
     const tcq_gemm_seg S = P.s[blockIdx.y];
@@ -299,9 +303,56 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
         __syncthreads();
         if (part > 0) red[((slot * (WPR - 1)) + part - 1) * 64 + lane] = acc;
         __syncthreads();
-        if (part != 0) return;
+        if (part != 0 && !LO) return;
+        if (part == 0) {
 #pragma unroll
-        for (int w = 0; w < WPR - 1; ++w) acc += red[(slot * (WPR - 1) + w) * 64 + lane];
+            for (int w = 0; w < WPR - 1; ++w) acc += red[(slot * (WPR - 1) + w) * 64 + lane];
+        }
+    }
+    if constexpr (LO) {                                                    // every wave reaches the barrier below
+        float* zb = (float*)tab + 4096;                                    // past the reduction slots: M rows of 128
+        if (part == 0) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = ((float)acc[e] * sv) * rsv[e];
+            float a = v[0], b = v[1];                                      // h = 1, 2: row pairs in the lane's 4 rows
+            v[0] = a + b; v[1] = a - b;
+            a = v[2]; b = v[3];
+            v[2] = a + b; v[3] = a - b;
+            a = v[0]; b = v[2];
+            v[0] = a + b; v[2] = a - b;
+            a = v[1]; b = v[3];
+            v[1] = a + b; v[3] = a - b;
+#pragma unroll
+            for (int m = 16; m <= 32; m *= 2)                              // h = 4, 8: rows 4 lg + e, lanes 16 lg + lr
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pv = lane_xor(v[e], m, lane);
+                    v[e] = (lane & m) ? pv - v[e] : v[e] + pv;
+                }
+            if (lr < M) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) zb[lr * 128 + 16 * slot + 4 * lg + e] = v[e];
+            }
+        }
+        __syncthreads();
+        if (wave < M) {                                                    // h = 16, 32, 64: token `wave`, rows l and l + 64
+            float a = zb[wave * 128 + lane], b = zb[wave * 128 + 64 + lane];
+#pragma unroll
+            for (int m = 16; m <= 32; m *= 2) {
+                const float pa = lane_xor(a, m, lane), pb = lane_xor(b, m, lane);
+                a = (lane & m) ? pa - a : a + pa;
+                b = (lane & m) ? pb - b : b + pb;
+            }
+            const float x = a;
+            a = x + b;
+            b = x - b;
+            const int nb = S.m >> 7, blk = I0 >> 3;
+            float* zt = (float*)S.out + (size_t)wave * 128 * nb;
+            gptr(zt)[(size_t)lane * nb + blk] = a;
+            gptr(zt)[(size_t)(lane + 64) * nb + blk] = b;
+        }
+        return;
     }
     if (I0 + slot >= tiles_m) return;
     const int t = lr;
@@ -426,7 +477,9 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     const bool qb = odt & TCQ_Q_TOKEN_BLOCKS;                          // q in the token-block layout
     if ((odt & TCQ_K_PARTS2) && (odt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
     const int parts = (odt & TCQ_K_PARTS4) ? 4 : (odt & TCQ_K_PARTS2) ? 2 : 1;
-    odt &= ~(TCQ_Q_TOKEN_BLOCKS | TCQ_K_PARTS2 | TCQ_K_PARTS4);
+    const bool w128 = odt & TCQ_Z_W128T;
+    odt &= ~(TCQ_Q_TOKEN_BLOCKS | TCQ_K_PARTS2 | TCQ_K_PARTS4 | TCQ_Z_W128T);
+    if (w128 && (MODE != 0 || odt != TCQ_F32 || parts > 1 || M > 16 || K > 256 * 2 * GV_CMAX)) return TCQ_ERR_UNSUPPORTED;
     if (odt != TCQ_F32 && odt != TCQ_BF16 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (parts > 1 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (odt != TCQ_I32 && !s) return TCQ_ERR_ARG;
@@ -451,6 +504,14 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
     hipStream_t st = (hipStream_t)stream;
     const i8* qq = (const i8*)q;
+    if (w128) {                                        // stage-split gated-MLP input: the streaming plan, 8 tile rows per workgroup
+        for (int i = 0; i < nseg; ++i)
+            if (segs[i].m % 128 || (segs[i].rows_per_table > 0 && segs[i].rows_per_table % 128)) return TCQ_ERR_SHAPE;
+        const dim3 grid(max_m / 128, nseg), block(64 * GV_NW);
+        if (qb) launch_k(k_gemv_tcq<TCQ_F32, true, 2, GV_NW, 1, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
+        else launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
+        return launch_status();
+    }
     if (parts > 1) {                                   // K parts: each part a product over its chunks, int32 out
         const int nchp = (nch + parts - 1) / parts, nwp = nchp < SM_MAXW ? nchp : SM_MAXW;
         int tiles = 0;
@@ -537,5 +598,50 @@ extern "C" int tcq_gemm_tcq_q4(const void* bits, const int8_t* t8, const int32_t
     const int nch = (K + 255) / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
     launch_small_qb<0, 1, QL_WORDS, true>(dim3(max_m / 16, nseg), dim3(64 * nw), (hipStream_t)stream, P, (const i8*)q4, s, M, K, N, ldq,
                                           TCQ_F32);
+    return launch_status();
+}
+
+// ------------------------------------------------------------------------------------------------ stage-split middle
+// The rest of the gated-MLP middle after a TCQ_Z_W128T product of gate | up (zt: gate's (M, 128, N / 128) block-transposed
+// rows, then up's; N = 16384): block Walsh stages h = 128 .. N / 2 across the 128 blocks (h = 128 h_b), then, as tcq_mid2
+// (deploy/tcq_kernels/kernels.py:263-278), * c, the signs, BF16 roundings, GELU by table and the product:
+// p = bf16(gelu(bf16(g c sg)) * bf16(u c su)) (M, N) BF16 in natural order, the input of tcq_pre with the down projection's
+// signs. One wave per (offset o, token t): lane l holds blocks l and l + 64 of gate and of up.
+__global__ __launch_bounds__(256) void k_glu_split(const float* zt, const i8* sv, const u16* lut, u16* p, int M, int N) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + wave, t = blockIdx.y;
+    const size_t row = ((size_t)t * 128 + o) * 128;
+    const float* zg = zt + row;
+    const float* zu = zt + (size_t)M * N + row;
+    float v[4] = {gptr(zg)[lane], gptr(zg)[lane + 64], gptr(zu)[lane], gptr(zu)[lane + 64]};
+#pragma unroll
+    for (int m = 1; m <= 32; m *= 2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float pv = lane_xor(v[e], m, lane);
+            v[e] = (lane & m) ? pv - v[e] : v[e] + pv;
+        }
+    float a = v[0];
+    v[0] = a + v[1];
+    v[1] = a - v[1];
+    a = v[2];
+    v[2] = a + v[3];
+    v[3] = a - v[3];
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = (lane + 64 * k) * 128 + o;
+        const u16 gv = gptr(lut)[f32_to_bf16(v[k] * c * (float)gptr(sv)[i])];
+        const float uu = bf16_to_f32(f32_to_bf16((v[2 + k] * c) * (float)gptr(sv)[N + i]));
+        gptr(p)[(size_t)t * N + i] = f32_to_bf16(bf16_to_f32(gv) * uu);
+    }
+}
+
+extern "C" int tcq_glu_split(const float* zt, int N, const int8_t* sv, const uint16_t* gelu_lut, uint16_t* p, int M,
+                             tcq_stream_t stream) {
+    if (!zt || !sv || !gelu_lut || !p || M <= 0) return TCQ_ERR_ARG;
+    if (N != 16384) return TCQ_ERR_UNSUPPORTED;
+    if (M > 16) return TCQ_ERR_UNSUPPORTED;
+    launch_k(k_glu_split, dim3(32, M), dim3(256), 0, (hipStream_t)stream, zt, (const i8*)sv, (const u16*)gelu_lut, (u16*)p, M, N);
     return launch_status();
 }

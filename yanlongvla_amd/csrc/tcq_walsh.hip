@@ -198,6 +198,40 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_rht_tw(const void* x, int ldx
 }
 
 // ------------------------------------------------------------------------------------------------------ rotate + quantize
+// k_pre on the register + transpose engine for rows of 2^L without column scales (rows, signs and q 16-byte aligned): the
+// thread's 2^LE contiguous inputs straight into registers as k_rht_tw loads them, * su, then tw_rotate_quantize (Walsh, * c,
+// row max, INT8): the operations of k_pre in the same order.
+template <int XDT, int L, int LE>
+__global__ __launch_bounds__(1 << (L - LE)) void k_pre_tw(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale) {
+    constexpr int E = 1 << LE, XS = XDT == TCQ_F32 ? 4 : 2, NQ = E * XS / 16;
+    extern __shared__ float xs[];
+    __shared__ float red[16];
+    const int tok = blockIdx.x, i0 = E * threadIdx.x;
+    Raw16<1> s0[E / 16];
+    if (su) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) s0[h] = raw16<1>(su + i0 + 16 * h, true);
+    }
+    const uint4_t* src = (const uint4_t*)((const char*)x + ((size_t)tok << L) * XS + (size_t)i0 * XS);
+    uint4_t raw[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) raw[j] = *gptr(src + j);
+    float v[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k)
+        v[k] = XS == 4 ? bits_to_f32<XDT>(raw[k >> 2][k & 3]) : bits_to_f32<XDT>((raw[k >> 3][(k & 7) >> 1] >> (16 * (k & 1))) & 0xffffu);
+    if (su) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) {
+            float sg[16];
+            cv16(s0[h], sg);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[16 * h + k] = v[16 * h + k] * sg[k];
+        }
+    }
+    tw_rotate_quantize<L, LE>(v, xs, red, q, q4, ldq, scale, tok);
+}
+
 // cs: FP16 column scales of the rotated activations (NULL: none), applied after the rotation, before the absmax.
 template <int XDT>
 __global__ void k_pre(const void* x, const i8* su, i8* q, int* q4, int ldq, float* scale, int K, int vec, const u16* cs) {
@@ -1320,6 +1354,27 @@ extern "C" int tcq_pre_cs(const void* x, int x_dtype, const int8_t* su, const vo
     const int vec = K % 8 == 0 && al16(x) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
     const u16* cs = (const u16*)col_scale;
+    // register + transpose engine: power-of-two rows of 1024 .. 16384 without column scales, aligned
+    if (!cs && (K & (K - 1)) == 0 && K >= 1024 && al16(x) && (!su || al16(su)) && (!q || al16(q)) &&
+        (!q4 || ldq != TCQ_LDQ_TOKEN_BLOCKS || al16(q4))) {
+        const size_t tsh = (size_t)lds_words(K) * sizeof(float);
+        i8* qq = (i8*)q;
+        int* q4p = (int*)q4;
+        const i8* sp = (const i8*)su;
+#define PRE_TW(XD, L, LE, T) launch_k(k_pre_tw<XD, L, LE>, grid, dim3(T), tsh, st, x, sp, qq, q4p, ldq, scale)
+#define PRE_TWX(XD, _)                                                        \
+    switch (K) {                                                              \
+        case 1024: PRE_TW(XD, 10, 4, 64); break;                              \
+        case 2048: PRE_TW(XD, 11, 4, 128); break;                             \
+        case 4096: PRE_TW(XD, 12, 4, 256); break;                             \
+        case 8192: PRE_TW(XD, 13, 5, 256); break;                             \
+        default: PRE_TW(XD, 14, 5, 512); break;                               \
+    }
+        DISPATCH_X(x_dtype, PRE_TWX, 0)
+#undef PRE_TWX
+#undef PRE_TW
+        return launch_status();
+    }
 #define PRE(XD, _) launch_k(k_pre<XD>, grid, block, sh, st, x, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, K, vec, cs)
     DISPATCH_X(x_dtype, PRE, 0)
 #undef PRE

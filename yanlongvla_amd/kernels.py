@@ -517,6 +517,38 @@ def gemm_w8_segments(segs, q, s, ldo, parts=1):
     SmallProduct(segs, ldo, resident=True)(q, s, parts)
 
 
+Z_W128T = 0x1000
+
+
+def gemm_tcq_w128t(segs, q, s):
+    """Fused decode + product of up to 4 segments [(words, t8, rs, zt), ...] at M <= 16 tokens whose FP32 z leaves the
+    kernel after the first seven block-Walsh stages of each segment, block-transposed: zt (M, 128, m / 128) float32
+    (TCQ_Z_W128T in include/tcq_api.h). q: token blocks (M = s.numel()) or (M, K) rows. No reference counterpart."""
+    arr = (_lib.GemmSeg * len(segs))()
+    M = s.numel()
+    for i, (w, t8, rs, zt) in enumerate(segs):
+        _contig(w, t8, rs, zt)
+        m = rs.numel()
+        if zt.dtype != torch.float32 or tuple(zt.shape) != (M, 128, m // 128):
+            raise ValueError(f'segment {i}: zt must be ({M}, 128, {m // 128}) float32')
+        arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(zt), m, 0 if _groups(t8) == 1 else m // _groups(t8))
+    blocks = q.dim() == 4
+    K = q.shape[1] * 16 if blocks else q.shape[1]
+    _contig(q, s)
+    call('tcq_gemm_tcq', arr, len(segs), ptr(q), ptr(s), M, K, 0 | Z_W128T | (Q_TOKEN_BLOCKS if blocks else 0), 128, stream())
+
+
+def glu_split(zt, sv, gelu_lut, p):
+    """The gated-MLP middle after gemm_tcq_w128t of gate | up: zt (2, M, 128, N / 128) float32, sv (2N,) int8 signs of
+    gate | up -> p (M, N) BF16 = bf16(gelu(g) * u); kernels.pre(p, down_su, ...) then equals mid2 bit for bit. N = 16384."""
+    M, N = p.shape
+    _contig(zt, sv, gelu_lut, p)
+    if tuple(zt.shape) != (2, M, 128, N // 128) or zt.dtype != torch.float32 or p.dtype != torch.bfloat16 or sv.numel() != 2 * N:
+        raise ValueError('glu_split: shapes do not match')
+    call('tcq_glu_split', ptr(zt), N, ptr(sv), ptr(gelu_lut), ptr(p), M, stream())
+    return p
+
+
 def gemm_w8(W, q4, s, rs, z):
     """W (N, K) int8 resident, q4 (K/4, M) int32, z (M, N) FP32 = (float(acc) * s) * rs (reference kernels.gemm_w8,
     kernels.py:662-668)."""

@@ -30,11 +30,12 @@ from . import tcq_format as F
 
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
-STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0)
+STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
-# layer's norm + rotate + quantize prologue
-FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True)
+# layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
+# (the first Walsh stages in the gate/up product, the rest in glu_split, then the down projection's pre) instead of mid2
+FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -242,6 +243,29 @@ class Group:
             kernels.gemm_tcq_segments(segs, q, b['scale'], self.Ntot)
         return z
 
+    def spreads(self, M):
+        """Whether this gate | up group's middle at M tokens runs spread over many CUs (gemm_tcq_w128t + glu_split + pre):
+        the fused decode of two 16384-wide members with one table each, K <= 4096, at most 16 tokens."""
+        return (FUSE['spread'] and self.W is None and M <= 16 and self.K <= 4096 and self.N == [16384, 16384]
+                and not self.one_sided and self.col_scale is None and all(L.t8.dim() == 2 for L in self.layers))
+
+    def gated_middle(self, b, down, b2):
+        """This gate | up group's product and the GeGLU middle (tcq_mid2's operations) into the down projection's quantized
+        input buffers b2: spread over many CUs when self.spreads(M), else one product launch and one mid2 launch."""
+        M, dev = b['scale'].numel(), b['scale'].device
+        if self.spreads(M):
+            q = b['q'] if b['q'] is not None else b['q4']
+            zt = torch.empty(2, M, 128, 128, dtype=torch.float32, device=dev)
+            kernels.gemm_tcq_w128t([(L.words(), L.t8, s.rs, zt[i]) for i, (L, s) in enumerate(zip(self.layers, self.segments))],
+                                   q, b['scale'])
+            p = kernels.glu_split(zt, self.sv, kernels.gelu_table(dev), torch.empty(M, 16384, dtype=torch.bfloat16, device=dev))
+            kernels.pre(p, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
+            STATS['spread_middles'] += 1
+            return
+        acc = self.product(b)
+        s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], self.rs)
+        kernels.mid2(acc, s_tok, rs, self.sv, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
+
     # ------------------------------------------------------------------------------------------------ epilogue
     def posts(self, acc, b, shape, gelu0=False, outs=None):
         """acc: FP32 z (already scaled), INT32 (scaled here by the token scales of b and rs) or BF16 (scaled by rs).
@@ -347,8 +371,14 @@ class KGatedMLP(torch.nn.Module):
 
     def forward(self, x):
         gu, down = self.groups
+        x2 = gu.prep(x)
+        M, dev = x2.shape[0], x2.device
+        if not FUSE['split'] and gu.spreads(M):
+            b, b2 = gu.quantize(x2), down.buffers(M, dev)
+            gu.gated_middle(b, down, b2)
+            STATS['fused_mlps'] += 1
+            return down.posts(down.product(b2), b2, x.shape)[0]
         acc, b = _first_half(gu, x)
-        M, dev = acc.shape[0], acc.device
         b2 = down.buffers(M, dev)
         s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], gu.rs)
         if FUSE['split']:
@@ -449,9 +479,8 @@ class KDecoderLayer(torch.nn.Module):
         b3 = gu.buffers(M, dev)
         kernels.post_add_norm_pre(z, *self._unscaled(z, b2, og), og.sv, og.bias, x2, x3, n2.weight, n2.eps, gu.su, q=b3['q'],
                                   q4=b3['q4'], scale=b3['scale'])
-        acc = gu.product(b3)
         b4 = dn.buffers(M, dev)
-        kernels.mid2(acc, *self._unscaled(acc, b3, gu), gu.sv, dn.su, q=b4['q'], q4=b4['q4'], scale=b4['scale'])
+        gu.gated_middle(b3, dn, b4)
         z4 = dn.product(b4, dn.k_parts(M))
         x4 = torch.empty_like(x2)
         nxt = self._next[0] if (self._next and FUSE['chain']) else None
