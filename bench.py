@@ -51,7 +51,7 @@ def parse():
     p.add_argument('--no-ops', action='store_true', help='skip the RHT and W8A8 GEMM measurements')
     p.add_argument('--no-backbone', action='store_true', help='skip the Gemma-2B-shaped backbone measurement')
     p.add_argument('--backbone-replays', type=int, default=10)
-    p.add_argument('--probe', choices=('gate_up', 'qkv', 'mid2', 'gemm', 'prefill', 'decode'),
+    p.add_argument('--probe', choices=('gate_up', 'qkv', 'gate_up_dot4', 'qkv_dot4', 'mid2', 'gemm', 'prefill', 'decode'),
                    help='only run one kernel kind --probe-reps times (for rocprofv3 counter passes): the fused decode '
                         'product of one token at the backbone gate/up (32768 x 2048, k_gemv_tcq) or q/k/v (2560 x 2048, '
                         'k_gemm_small) shape over distinct weight sets, the one-token GeGLU middle (16384 wide, '
@@ -638,10 +638,11 @@ class _Calls(list):
     keep = None
 
 
-def product_sets(widths, Kd, resident, parts, dev, g):
+def product_sets(widths, Kd, resident, parts, dev, g, dot=None):
     """Calls of one small-M product shape (segments of the given widths side by side, K = Kd, one token in the token-block
     layout) over distinct synthetic weight sets (rotating_sets): repacked 2-bit words (fly) or INT8 weights (resident),
-    each set its own tables and row scales. Returns (calls, bytes per call, sets)."""
+    each set its own tables and row scales; dot: the product's arithmetic (SmallProduct). Returns (calls, bytes per call,
+    sets)."""
     import torch
     from yanlongvla_amd import kernels as K
     Ntot = sum(widths)
@@ -670,7 +671,7 @@ def product_sets(widths, Kd, resident, parts, dev, g):
                 t8 = torch.randint(-127, 128, (512, 2), generator=g, device=dev, dtype=torch.int8)
             segs.append((w, t8, rs, o))
         prod = K.SmallProduct(segs, Ntot, resident=resident)
-        calls.append(lambda prod=prod: prod(q4, sc, parts))
+        calls.append(lambda prod=prod: prod(q4, sc, parts, dot))
         keep.append(prod)
     calls.keep = keep
     return calls, byts, S
@@ -742,8 +743,9 @@ def probe(kind, reps, dev):
     import torch
     from yanlongvla_amd import kernels as K
     g = torch.Generator(device=dev).manual_seed(1)
-    if kind in ('gate_up', 'qkv'):
-        calls, _, _ = product_sets([16384, 16384] if kind == 'gate_up' else [2048, 256, 256], 2048, False, 1, dev, g)
+    if kind in ('gate_up', 'qkv', 'gate_up_dot4', 'qkv_dot4'):
+        calls, _, _ = product_sets([16384, 16384] if kind.startswith('gate_up') else [2048, 256, 256], 2048, False, 1, dev, g,
+                                   dot=kind.endswith('dot4'))
     elif kind == 'mid2':
         N = 16384
         acc = torch.randn(1, 2 * N, generator=g, device=dev) * 0.01

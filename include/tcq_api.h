@@ -68,6 +68,12 @@ enum tcq_dtype { TCQ_F32 = 0, TCQ_BF16 = 1, TCQ_F16 = 2, TCQ_I32 = 3, TCQ_I8 = 4
  * finishes the middle from it. No reference counterpart: it splits tcq_mid2 (kernels.py:263-278) over many CUs. */
 #define TCQ_Z_W128T 0x1000
 
+/* One-token products on v_dot4c_i32_i8 (flag of out_dtype for tcq_gemm_tcq / tcq_gemm_w8, M == 1 only): each lane
+ * multiplies its 16 weights of a tile row with the token's 16 activations in four 4-byte dot products instead of
+ * a 16 x 16 x 64 MFMA whose 15 other token columns are zero; the sums are the same exact int32 values. Every plan and
+ * every other flag keeps its meaning. The reference's one-token products are dot products (__dp4a, kernels.py:365-382). */
+#define TCQ_DOT4 0x2000
+
 /* Library version string and the widest row the block-Walsh kernels take (16384). */
 const char* tcq_version(void);
 int tcq_max_width(void);

@@ -677,6 +677,76 @@ def test_gemm_k_parts(shapes, M, parts):
         K.gemm_tcq_segments([(wdevs[0], t8s[0][0], t8s[0][1], torch.empty(parts, M, ldz, device=DEV)[0])], qd, sd, ldz, parts)
 
 
+@pytest.mark.parametrize('shapes,parts', [([(2048, 1024)], 1), ([(4112, 1024), (2048, 1024)], 1), ([(48, 80), (32, 80)], 1),
+                                          ([(2048, 16384)], 1), ([(8192, 2048)] * 4, 1), ([(65536, 1024)], 1),
+                                          ([(2048, 2560)], 1), ([(2048, 16384)], 2), ([(2048, 2048)], 2), ([(256, 512)], 4)])
+def test_one_token_dot_products_bitexact(shapes, parts):
+    """One-token products on dot-product instructions (DOT4): the workgroup plan with one and two tile rows per workgroup,
+    the streaming plan at 16 / 4 / 1 waves per tile row, K parts on both plans, K = 80 (a partial chunk); fused decode
+    and INT8-resident weights; FP32 / BF16 / int32 outputs, row-major and token-block activations. Every output equals
+    the MFMA product's bits, and the FP32 / int32 ones the oracle's."""
+    from yanlongvla_amd import kernels as K
+    M = 1
+    layers, dev, t8s, q, s, ldz, ref = _small_product_case(shapes, M, 5 * len(shapes) + parts)
+    n = layers[0].n
+    qd, sd = T(q), T(s)
+    tb = K.token_blocks(M, n, DEV)
+    qp = torch.zeros(16, n, dtype=torch.int8, device=DEV)
+    qp[:M] = qd
+    tb.copy_(qp.view(1, 16, n // 16, 16).permute(0, 2, 1, 3))
+    exact = np.concatenate([O.int_matmul(q, L.w8_reference()) for L in layers], 1)
+    wdevs = [K.repack(d['bits'], L.m, n) for L, d in zip(layers, dev)]
+    w8s = []
+    for L, d, (t8, _) in zip(layers, dev, t8s):
+        w = torch.empty(L.m, n, dtype=torch.int8, device=DEV)
+        K.decode(d['bits'], t8, w)
+        w8s.append(w)
+    cols = np.cumsum([0] + [L.m for L in layers])[:-1]
+    dts = (torch.int32,) if parts > 1 else (torch.float32, torch.bfloat16, torch.int32)
+    for resident, ws in ((False, wdevs), (True, w8s)):
+        fn = K.gemm_w8_segments if resident else K.gemm_tcq_segments
+        for dt in dts:
+            for act in (qd, tb):
+                out = {}
+                for dot in (False, True):
+                    z = torch.full((parts, M, ldz), -7, dtype=torch.int32, device=DEV).view(dt) if dt != torch.bfloat16 else \
+                        torch.full((parts, M, ldz), float('nan'), dtype=dt, device=DEV)
+                    fn([(w, None if resident else t8, rs, z[0, :, c:]) for w, (t8, rs), c in zip(ws, t8s, cols)], act,
+                       None if (dt == torch.int32 and act is qd) else sd, ldz, parts, dot=dot)
+                    out[dot] = z.view(torch.int16 if dt == torch.bfloat16 else torch.int32).cpu().numpy()
+                case = (resident, dt, act is tb)
+                assert np.array_equal(out[True], out[False]), case
+                if dt == torch.int32:
+                    assert np.array_equal(out[True].astype(np.int64).sum(0), exact), case
+                elif dt == torch.float32:
+                    assert np.array_equal(out[True][0].view(np.uint32), ref.view(np.uint32)), case
+    with pytest.raises(ValueError):                                       # dot products take one token
+        K.gemm_tcq_segments([(wdevs[0], t8s[0][0], t8s[0][1], torch.empty(2, ldz, device=DEV))], T(np.repeat(q, 2, 0)),
+                            T(np.repeat(s, 2)), ldz, dot=True)
+
+
+def test_one_token_dot_stage_split_middle():
+    """The stage-split gated-MLP input (TCQ_Z_W128T) on dot-product instructions equals its MFMA form bit for bit."""
+    from yanlongvla_amd import kernels as K
+    N, n = 2048, 2048
+    layers = [O.random_layer(N, n, 90 + i) for i in range(2)]
+    dev = [dev_layer(L) for L in layers]
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, size=(1, n)).astype(np.int8)
+    s = (rng.random(1) * 0.02 + 1e-3).astype(np.float32)
+    segs = []
+    for L, d in zip(layers, dev):
+        t8, rs, _ = K.snap(d['tlut'], d['row_scale'])
+        segs.append((K.repack(d['bits'], L.m, n), t8, rs))
+    out = {}
+    for dot in (False, True):
+        zt = torch.full((2, 1, 128, N // 128), float('nan'), device=DEV)
+        K.gemm_tcq_w128t([(w, t8, rs, zt[i]) for i, (w, t8, rs) in enumerate(segs)], T(q), T(s), dot=dot)
+        out[dot] = zt.view(torch.int32).cpu().numpy()
+    assert np.array_equal(out[True], out[False])
+    assert not np.isnan(out[True].view(np.float32)).any()
+
+
 def test_gemm_small_rejects_bad_sizes():
     from yanlongvla_amd import kernels as K, _lib
     L = O.random_layer(32, 64, 1)

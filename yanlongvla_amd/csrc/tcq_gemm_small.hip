@@ -36,6 +36,28 @@ __device__ __forceinline__ void fill_table_i8(u32* tab, const i8* t8) {
     }
 }
 
+// acc + the dot product of the 16 INT8 weights a with the 16 INT8 activations b (four v_dot4c_i32_i8; exact int32).
+__device__ __forceinline__ int dot_product(int4v a, int4v b, int acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_sdot4(a[e], b[e], acc, false);
+    return acc;
+}
+
+// One-token dot products -> the MFMA result layout: v is lane (g, r)'s sum over k-block g of row r (token 0); the four
+// k-blocks are added (exact), and lane (g, 0) receives rows 4 g .. 4 g + 3 as the 16 x 16 x 64 MFMA leaves token 0
+// (every other lane: zeros, as the MFMA's empty token columns).
+__device__ __forceinline__ int4v dot_to_mfma_layout(int v, int lane) {
+    v += __float_as_int(lane_xor(__int_as_float(v), 16, lane));
+    v += __float_as_int(lane_xor(__int_as_float(v), 32, lane));
+    int4v o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int x = __builtin_amdgcn_ds_bpermute((4 * (lane >> 4) + e) << 2, v);
+        o[e] = (lane & 15) ? 0 : x;
+    }
+    return o;
+}
+
 }  // namespace
 
 struct SegPack {
@@ -51,10 +73,12 @@ enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
 // words (RB: from the reference word layout, 64 bytes per tile, tiles row-major); MODE 1: resident INT8 weights. ODT: output
 // dtype (F32 scaled, BF16 scaled, I32 accumulators). QL: activation layout (ldq only for QL_WORDS).
 // KS > 1 (I32 only): K parts, blockIdx.z = part p takes chunks [p * ceil(nch / KS), ...) and writes at out + p * M * ldz.
-template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1>
+// DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
+template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false>
 __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz,
                                                                     int ldq) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
+    static_assert(!DOT || (NB == 1 && QL != QL_WORDS), "dot products: one token, q rows or token blocks");
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
     const tcq_gemm_seg S = P.s[blockIdx.y];
@@ -104,7 +128,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const int t = 16 * b + lr, k = 256 * c + 64 * j + 16 * lg;
+                const int t = DOT ? 0 : 16 * b + lr, k = 256 * c + 64 * j + 16 * lg;   // DOT: every lane token 0
                 const bool in = t < M && k < K;
                 if (QL == QL_WORDS) {                                     // 4 words (k / 4 + i, t): 16 lanes read 64 bytes
 #pragma unroll
@@ -118,10 +142,13 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     };
 
     int4v acc[TR][NB];
+    int dacc[TR][2];                                                      // DOT: row lr, k-block lg, two chains
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
+    for (int r = 0; r < TR; ++r) {
+        dacc[r][0] = dacc[r][1] = 0;
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
+    }
     if (c0 + wave < nch) load(c0 + wave);
     // epilogue scales, loaded with the operands (wave 0 stores)
     float4_t rsv[TR];
@@ -160,10 +187,18 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
                 } else {
                     A = __builtin_bit_cast(int4v, wa[r][j]);
                 }
+                if constexpr (DOT) {
+                    dacc[r][j & 1] = dot_product(A, B[j][0], dacc[r][j & 1]);
+                } else {
 #pragma unroll
-                for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[r][b], 0, 0, 0);
+                    for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[r][b], 0, 0, 0);
+                }
             }
         }
+    }
+    if constexpr (DOT) {
+#pragma unroll
+        for (int r = 0; r < TR; ++r) acc[r][0] = dot_to_mfma_layout(dacc[r][0] + dacc[r][1], lane);
     }
     // sum the waves' partial accumulators (exact int32) through LDS, then scale and store
     if (wave > 0) {
@@ -221,7 +256,8 @@ constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table 
 // LO (TCQ_Z_W128T, FP32 scaled z, RPW = 8): the workgroup's 128 rows are one 128-row block of the segment; the first seven
 // stages of the block Walsh of the whole segment (h = 1 .. 64, which stay inside such a block) run here, in the reference's
 // stage order, and the block is stored transposed: zt[(t * 128 + o) * (m / 128) + blk] for row 128 blk + o of token t.
-template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false>
+// DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
+template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     static_assert(!LO || (ODT == TCQ_F32 && KS == 1 && NW / WPR == 8), "stage-split output: FP32 z, 8 tile rows per workgroup");
@@ -249,8 +285,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     auto loadB = [&](int c, int4v* B) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int k = 256 * c + 64 * j + 16 * lg;
-            const u32 off = (lr < M && k < K) ? (QB ? (u32)tb_offset(lr, k, K) : (u32)lr * (u32)K + (u32)k) : RSRC_OOB;
+            const int k = 256 * c + 64 * j + 16 * lg, t = DOT ? 0 : lr;              // DOT: every lane token 0
+            const u32 off = (t < M && k < K) ? (QB ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
             B[j] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
         }
     };
@@ -277,6 +313,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     }
     __syncthreads();
     int4v acc = int4v{0, 0, 0, 0};
+    int dacc[2] = {0, 0};                                                  // DOT: row lr, k-block lg, two chains
 #pragma unroll
     for (int i = 0; i < GV_CMAX; ++i) {
         const int c = c0 + part + WPR * i;
@@ -295,9 +332,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
             }
             const int4v A = int4v{__builtin_bit_cast(int, a[0]), __builtin_bit_cast(int, a[1]), __builtin_bit_cast(int, a[2]),
                                   __builtin_bit_cast(int, a[3])};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bf[i & 1][j], acc, 0, 0, 0);
+            if constexpr (DOT) dacc[j & 1] = dot_product(A, Bf[i & 1][j], dacc[j & 1]);
+            else acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bf[i & 1][j], acc, 0, 0, 0);
         }
     }
+    if constexpr (DOT) acc = dot_to_mfma_layout(dacc[0] + dacc[1], lane);
     if constexpr (WPR > 1) {
         int4v* red = (int4v*)tab;                                          // the table is dead once every wave is past here
         __syncthreads();
@@ -375,13 +414,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
 }
 
 // =========================================================================================================== C ABI
-template <int MODE, int NB, int TR, int QL, bool RB>
+template <int MODE, int NB, int TR, int QL, bool RB, bool DOT = false>
 static void launch_small_nb(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                             int ldo, int ldq, int odt) {
     switch (odt) {
-        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
-        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
-        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR, QL, RB>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
+        case TCQ_F32: launch_k(k_gemm_small<MODE, NB, TCQ_F32, TR, QL, RB, 1, DOT>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
+        case TCQ_BF16: launch_k(k_gemm_small<MODE, NB, TCQ_BF16, TR, QL, RB, 1, DOT>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
+        default: launch_k(k_gemm_small<MODE, NB, TCQ_I32, TR, QL, RB, 1, DOT>, grid, block, 0, st, P, q, s, M, K, ldo, ldq); break;
     }
 }
 template <int MODE, int TR, int QL, bool RB = false>
@@ -393,66 +432,74 @@ static void launch_small_qb(dim3 grid, dim3 block, hipStream_t st, const SegPack
 }
 template <int MODE, int TR>
 static void launch_small_tr(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
-                            int ldo, int odt, bool qb) {
-    if (qb) launch_small_qb<MODE, TR, QL_BLOCKS>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
+                            int ldo, int odt, bool qb, bool dot) {
+    if (dot && qb) launch_small_nb<MODE, 1, TR, QL_BLOCKS, false, true>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
+    else if (dot) launch_small_nb<MODE, 1, TR, QL_ROWS, false, true>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
+    else if (qb) launch_small_qb<MODE, TR, QL_BLOCKS>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
     else launch_small_qb<MODE, TR, QL_ROWS>(grid, block, st, P, q, s, M, K, ldo, 0, odt);
 }
 
-template <int ODT, bool QB>
+template <int ODT, bool QB, bool DOT>
 static void launch_gv(int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                       int ldo) {
     const int rpw = GV_NW / wpr;
     const dim3 grid((rows + rpw - 1) / rpw, nseg), block(64 * GV_NW);
     switch (wpr) {
-        case 1: launch_k(k_gemv_tcq<ODT, QB, 1, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 2: launch_k(k_gemv_tcq<ODT, QB, 2, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 4: launch_k(k_gemv_tcq<ODT, QB, 4, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 8: launch_k(k_gemv_tcq<ODT, QB, 8, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        default: launch_k(k_gemv_tcq<ODT, QB, 16, GV_NW>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 1: launch_k(k_gemv_tcq<ODT, QB, 1, GV_NW, 1, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 2: launch_k(k_gemv_tcq<ODT, QB, 2, GV_NW, 1, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 4: launch_k(k_gemv_tcq<ODT, QB, 4, GV_NW, 1, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 8: launch_k(k_gemv_tcq<ODT, QB, 8, GV_NW, 1, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemv_tcq<ODT, QB, 16, GV_NW, 1, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
     }
 }
 
 // K parts (int32 sums only): grid.z = KS parts
-template <int MODE, int KS, int QL>
+template <int MODE, int KS, int QL, bool DOT>
 static void launch_small_parts(dim3 grid, dim3 block, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                                int ldo) {
-    if (M <= 16) launch_k(k_gemm_small<MODE, 1, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
+    if (DOT || M <= 16) launch_k(k_gemm_small<MODE, 1, TCQ_I32, 1, QL, false, KS, DOT>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
     else if (M <= 32) launch_k(k_gemm_small<MODE, 2, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
     else launch_k(k_gemm_small<MODE, 4, TCQ_I32, 1, QL, false, KS>, grid, block, 0, st, P, q, s, M, K, ldo, 0);
 }
-template <bool QB, int KS>
+template <bool QB, int KS, bool DOT>
 static void launch_gv_parts(int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s, int M, int K,
                             int ldo) {
     const int rpw = GV_NW / wpr;
     const dim3 grid((rows + rpw - 1) / rpw, nseg, KS), block(64 * GV_NW);
     switch (wpr) {
-        case 1: launch_k(k_gemv_tcq<TCQ_I32, QB, 1, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 2: launch_k(k_gemv_tcq<TCQ_I32, QB, 2, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 4: launch_k(k_gemv_tcq<TCQ_I32, QB, 4, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        case 8: launch_k(k_gemv_tcq<TCQ_I32, QB, 8, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
-        default: launch_k(k_gemv_tcq<TCQ_I32, QB, 16, GV_NW, KS>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 1: launch_k(k_gemv_tcq<TCQ_I32, QB, 1, GV_NW, KS, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 2: launch_k(k_gemv_tcq<TCQ_I32, QB, 2, GV_NW, KS, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 4: launch_k(k_gemv_tcq<TCQ_I32, QB, 4, GV_NW, KS, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        case 8: launch_k(k_gemv_tcq<TCQ_I32, QB, 8, GV_NW, KS, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
+        default: launch_k(k_gemv_tcq<TCQ_I32, QB, 16, GV_NW, KS, false, DOT>, grid, block, 0, st, P, q, s, M, K, ldo); break;
     }
 }
-template <int MODE, int KS>
+template <int MODE, int KS, bool DOT>
 static void launch_parts(bool qb, int wpr, int rows, int nseg, int nw, hipStream_t st, const SegPack& P, const i8* q, const float* s,
                          int M, int K, int ldo) {
     if (MODE == 0 && wpr > 0) {
-        if (qb) launch_gv_parts<true, KS>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
-        else launch_gv_parts<false, KS>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
+        if (qb) launch_gv_parts<true, KS, DOT>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
+        else launch_gv_parts<false, KS, DOT>(wpr, rows, nseg, st, P, q, s, M, K, ldo);
         return;
     }
     const dim3 grid(rows, nseg, KS), block(64 * nw);
-    if (qb) launch_small_parts<MODE, KS, QL_BLOCKS>(grid, block, st, P, q, s, M, K, ldo);
-    else launch_small_parts<MODE, KS, QL_ROWS>(grid, block, st, P, q, s, M, K, ldo);
+    if (qb) launch_small_parts<MODE, KS, QL_BLOCKS, DOT>(grid, block, st, P, q, s, M, K, ldo);
+    else launch_small_parts<MODE, KS, QL_ROWS, DOT>(grid, block, st, P, q, s, M, K, ldo);
+}
+template <int MODE, int KS>
+static void launch_parts_dot(bool dot, bool qb, int wpr, int rows, int nseg, int nw, hipStream_t st, const SegPack& P, const i8* q,
+                             const float* s, int M, int K, int ldo) {
+    if (dot) launch_parts<MODE, KS, true>(qb, wpr, rows, nseg, nw, st, P, q, s, M, K, ldo);
+    else launch_parts<MODE, KS, false>(qb, wpr, rows, nseg, nw, st, P, q, s, M, K, ldo);
 }
 
-template <bool QB>
+template <bool QB, bool DOT>
 static void launch_gv_odt(int odt, int wpr, int rows, int nseg, hipStream_t st, const SegPack& P, const i8* q, const float* s,
                           int M, int K, int ldo) {
     switch (odt) {
-        case TCQ_F32: launch_gv<TCQ_F32, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
-        case TCQ_BF16: launch_gv<TCQ_BF16, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
-        default: launch_gv<TCQ_I32, QB>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+        case TCQ_F32: launch_gv<TCQ_F32, QB, DOT>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+        case TCQ_BF16: launch_gv<TCQ_BF16, QB, DOT>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
+        default: launch_gv<TCQ_I32, QB, DOT>(wpr, rows, nseg, st, P, q, s, M, K, ldo); break;
     }
 }
 
@@ -477,9 +524,10 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     const bool qb = odt & TCQ_Q_TOKEN_BLOCKS;                          // q in the token-block layout
     if ((odt & TCQ_K_PARTS2) && (odt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
     const int parts = (odt & TCQ_K_PARTS4) ? 4 : (odt & TCQ_K_PARTS2) ? 2 : 1;
-    const bool w128 = odt & TCQ_Z_W128T;
-    odt &= ~(TCQ_Q_TOKEN_BLOCKS | TCQ_K_PARTS2 | TCQ_K_PARTS4 | TCQ_Z_W128T);
+    const bool w128 = odt & TCQ_Z_W128T, dot = odt & TCQ_DOT4;
+    odt &= ~(TCQ_Q_TOKEN_BLOCKS | TCQ_K_PARTS2 | TCQ_K_PARTS4 | TCQ_Z_W128T | TCQ_DOT4);
     if (w128 && (MODE != 0 || odt != TCQ_F32 || parts > 1 || M > 16 || K > 256 * 2 * GV_CMAX)) return TCQ_ERR_UNSUPPORTED;
+    if (dot && M != 1) return TCQ_ERR_UNSUPPORTED;
     if (odt != TCQ_F32 && odt != TCQ_BF16 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (parts > 1 && odt != TCQ_I32) return TCQ_ERR_DTYPE;
     if (odt != TCQ_I32 && !s) return TCQ_ERR_ARG;
@@ -508,7 +556,9 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
         for (int i = 0; i < nseg; ++i)
             if (segs[i].m % 128 || (segs[i].rows_per_table > 0 && segs[i].rows_per_table % 128)) return TCQ_ERR_SHAPE;
         const dim3 grid(max_m / 128, nseg), block(64 * GV_NW);
-        if (qb) launch_k(k_gemv_tcq<TCQ_F32, true, 2, GV_NW, 1, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
+        if (dot && qb) launch_k(k_gemv_tcq<TCQ_F32, true, 2, GV_NW, 1, true, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
+        else if (dot) launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
+        else if (qb) launch_k(k_gemv_tcq<TCQ_F32, true, 2, GV_NW, 1, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
         else launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true>, grid, block, 0, st, P, qq, s, M, K, ldo);
         return launch_status();
     }
@@ -517,8 +567,8 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
         int tiles = 0;
         for (int i = 0; i < nseg; ++i) tiles += segs[i].m / 16;
         const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, M, nchp, tiles * parts) : 0;
-        if (parts == 2) launch_parts<MODE, 2>(qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
-        else launch_parts<MODE, 4>(qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
+        if (parts == 2) launch_parts_dot<MODE, 2>(dot, qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
+        else launch_parts_dot<MODE, 4>(dot, qb, wpr, max_m / 16, nseg, nwp, st, P, qq, s, M, K, ldo);
         return launch_status();
     }
     // two tile rows per workgroup when there are many (their activation fragments are then loaded once for both), at most 8
@@ -533,14 +583,16 @@ static int gemm_small(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const
     if (MODE == 0) {
         const int wpr = gv_waves_per_row(segs, nseg, M, nch, tiles);
         if (wpr > 0) {
-            if (qb) launch_gv_odt<true>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
-            else launch_gv_odt<false>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            if (dot && qb) launch_gv_odt<true, true>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            else if (dot) launch_gv_odt<false, true>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            else if (qb) launch_gv_odt<true, false>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
+            else launch_gv_odt<false, false>(odt, wpr, max_m / 16, nseg, st, P, qq, s, M, K, ldo);
             return launch_status();
         }
     }
     const dim3 block(64 * nw);
-    if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
-    else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt, qb);
+    if (pairs) launch_small_tr<MODE, 2>(dim3((max_m / 16 + 1) / 2, nseg), block, st, P, qq, s, M, K, ldo, odt, qb, dot);
+    else launch_small_tr<MODE, 1>(dim3(max_m / 16, nseg), block, st, P, qq, s, M, K, ldo, odt, qb, dot);
     return launch_status();
 }
 

@@ -446,6 +446,20 @@ def gelu_table(device):
 
 
 # ------------------------------------------------------------------------------------------------- small-M INT8 products
+DOT4 = 0x2000
+# One-token products (M == 1) on v_dot4c_i32_i8 instead of the 16 x 16 x 64 INT8 MFMA (TCQ_DOT4 in include/tcq_api.h);
+# the int32 sums are the same either way. The default is the faster of the two on MI355X.
+ONE_TOKEN_DOT = False
+
+
+def _dot_flag(M, dot):
+    if dot is None:
+        dot = ONE_TOKEN_DOT and M == 1
+    if dot and M != 1:
+        raise ValueError('dot-product products take one token')
+    return DOT4 if dot else 0
+
+
 class SmallProduct:
     """A prepared small-M product over 1..4 segments [(w, t8, rs, out), ...]: out is a view whose first element is the
     segment's first output column of an (M, ldo) buffer (FP32 / BF16 scaled, or int32 sums); rs (m,) FP32 gives m. The
@@ -480,15 +494,17 @@ class SmallProduct:
         self.n, self.ldo = len(segs), ldo
         self.fn = getattr(_lib.lib(), self.name)
 
-    def __call__(self, q, s, parts=1):
+    def __call__(self, q, s, parts=1, dot=None):
         """q (M, K) row-major, or a token-block tensor (M = s.numel() tokens; s is then required). parts 2 / 4: int32 outputs
-        only, K parts written at out + p * M * ldo (see K_PARTS)."""
+        only, K parts written at out + p * M * ldo (see K_PARTS). dot: one-token products on dot-product instructions
+        (DOT4); None = ONE_TOKEN_DOT at M == 1."""
         if q.dim() == 4:
             if s is None:
                 raise ValueError('token-block activations need s (their token count)')
             M, K, odt = s.numel(), q.shape[1] * 16, self.odt | Q_TOKEN_BLOCKS
         else:
             (M, K), odt = q.shape, self.odt
+        odt |= _dot_flag(M, dot)
         if parts != 1:
             if parts not in K_PARTS or self.odt != 3:
                 raise ValueError('K parts: 2 or 4, int32 outputs only')
@@ -505,25 +521,26 @@ class SmallProduct:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
 
-def gemm_tcq_segments(segs, q, s, ldo, parts=1):
+def gemm_tcq_segments(segs, q, s, ldo, parts=1, dot=None):
     """One-shot fused decode + product over segments (see SmallProduct)."""
     _contig(q, s)
-    SmallProduct(segs, ldo)(q, s, parts)
+    SmallProduct(segs, ldo)(q, s, parts, dot)
 
 
-def gemm_w8_segments(segs, q, s, ldo, parts=1):
+def gemm_w8_segments(segs, q, s, ldo, parts=1, dot=None):
     """One-shot INT8-resident product over segments (see SmallProduct)."""
     _contig(q, s)
-    SmallProduct(segs, ldo, resident=True)(q, s, parts)
+    SmallProduct(segs, ldo, resident=True)(q, s, parts, dot)
 
 
 Z_W128T = 0x1000
 
 
-def gemm_tcq_w128t(segs, q, s):
+def gemm_tcq_w128t(segs, q, s, dot=None):
     """Fused decode + product of up to 4 segments [(words, t8, rs, zt), ...] at M <= 16 tokens whose FP32 z leaves the
     kernel after the first seven block-Walsh stages of each segment, block-transposed: zt (M, 128, m / 128) float32
-    (TCQ_Z_W128T in include/tcq_api.h). q: token blocks (M = s.numel()) or (M, K) rows. No reference counterpart."""
+    (TCQ_Z_W128T in include/tcq_api.h). q: token blocks (M = s.numel()) or (M, K) rows; dot as SmallProduct. No reference
+    counterpart."""
     arr = (_lib.GemmSeg * len(segs))()
     M = s.numel()
     for i, (w, t8, rs, zt) in enumerate(segs):
@@ -535,7 +552,8 @@ def gemm_tcq_w128t(segs, q, s):
     blocks = q.dim() == 4
     K = q.shape[1] * 16 if blocks else q.shape[1]
     _contig(q, s)
-    call('tcq_gemm_tcq', arr, len(segs), ptr(q), ptr(s), M, K, 0 | Z_W128T | (Q_TOKEN_BLOCKS if blocks else 0), 128, stream())
+    call('tcq_gemm_tcq', arr, len(segs), ptr(q), ptr(s), M, K, 0 | Z_W128T | (Q_TOKEN_BLOCKS if blocks else 0) | _dot_flag(M, dot),
+         128, stream())
 
 
 def glu_split(zt, sv, gelu_lut, p):
