@@ -356,6 +356,35 @@ int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const floa
 int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                 tcq_stream_t stream);
 
+/* Decoder-layer prologue of a one-token product: the arguments of tcq_post_add_norm_pre for M = 1 with the norm (acc the
+ * previous product's int32 sums, acc_dtype TCQ_I32, optionally | TCQ_K_PARTS2 / TCQ_K_PARTS4 with part p at acc + p * lda;
+ * s, rs, sv, bias its epilogue; x, xout the residual; w, eps the RMSNorm; su the signs of the product that follows) and
+ * optional copies of the INT8 row (q, K bytes) and its scale. */
+typedef struct {
+    const void* acc;
+    int acc_dtype;
+    int lda, col0;
+    const float* s;
+    const float* rs;
+    const int8_t* sv;
+    const float* bias;
+    const void* x;
+    void* xout;
+    const void* w;
+    float eps;
+    const int8_t* su;
+    int8_t* q;
+    float* scale;
+} tcq_prologue;
+
+/* tcq_post_add_norm_pre(pro..., M = 1, N = K) followed by tcq_gemm_tcq / tcq_gemm_w8 of its INT8 row, in one launch: every
+ * workgroup computes the prologue's row itself (the same operations, bit for bit) and multiplies it, so the row never
+ * leaves the chip and the chain loses a launch. K = 2048 and bias NULL (TCQ_ERR_UNSUPPORTED otherwise), out_dtype TCQ_F32
+ * (tcq_gemm_tcq: optionally | TCQ_Z_W128T), 16-byte aligned operands. No reference counterpart: the reference runs the epilogue, the
+ * residual add, the norm and the quantizer as separate steps (kernels.py:208-230; the norm in PyTorch). */
+int tcq_gemm_tcq_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo, tcq_stream_t stream);
+int tcq_gemm_w8_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo, tcq_stream_t stream);
+
 /* kernels.gemm_w8 / k_gemm_w8 (deploy/tcq_kernels/kernels.py:365-382, 662-668), argument for argument: W (N, K) int8 resident
  * weights, q4 (K/4, ldq) int32 activation words (the reference passes q4 (K/4, M), ldq = M), s (M,) FP32 token scales, rs (N,)
  * FP32 row scales, z (M, N) FP32 = (float(acc) * s[t]) * rs[i], acc exact in int32. M <= 64, N and K multiples of 16; z and

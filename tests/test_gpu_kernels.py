@@ -517,6 +517,33 @@ def test_bf16_conversion_of_every_exponent_and_payload():
     assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), O.bf16_bits(u.view(np.float32)))
 
 
+def test_quantizer_at_rounding_ties():
+    """The INT8 quantizer's quotient v / s (reciprocal + two corrections for scales in [2^-90, 2^90], IEEE division
+    outside) against the oracle's FP32 division on rows built around the rounding ties: v = (k + 1/2) s moved by 0, +-1,
+    +-2 ulp for every k in -127 .. 126, with the row maximum 127 s fixing s; row scales from 1e-36 to 1e36, on both sides
+    of both ends of the reciprocal's range."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(17)
+    rows = []
+    for amax in (1e-36, 127 * 2.0 ** -90 * 0.999, 127 * 2.0 ** -90 * 1.001, 1e-20, 0.37, 1.0, 127.0, 3.3e11,
+                 127 * 2.0 ** 90 * 0.999, 127 * 2.0 ** 90 * 1.001, 1e36):
+        a = np.float32(amax)
+        s = a / np.float32(127)
+        k = np.arange(-127, 127, dtype=np.float32)
+        base = ((k + np.float32(0.5)) * s).astype(np.float32)
+        ties = np.concatenate([(base.view(np.int32) + d).view(np.float32) for d in (-2, -1, 0, 1, 2)])
+        ties = ties[np.abs(ties) <= a]
+        row = np.concatenate([[a], ties, (rng.uniform(-1, 1, 2048) * a).astype(np.float32)])[:2048]
+        rows.append(np.pad(row, (0, 2048 - row.size)))
+    x = np.stack(rows).astype(np.float32)
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    sc = torch.empty(x.shape[0], device=DEV)
+    K.quantize_rows(T(x), q, sc)
+    qr, sr = O.quantize_tokens(x)
+    assert np.array_equal(sc.cpu().numpy(), sr[:, 0])
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
 def test_rht_bf16_output_of_nan_and_inf_rows():
     """BF16 outputs of the rotation for rows holding a NaN (any payload), opposite infinities or one infinity, against the
     oracle: a NaN reaches every output of its row and converts to 0x7fc0 (the packed two-value conversion with its NaN

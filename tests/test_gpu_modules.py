@@ -216,6 +216,34 @@ def test_chained_prologues_bitexact(part):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize('runtime', ['fly', 'resident'])
+def test_layer_prologue_in_the_gate_up_product_bitexact(runtime):
+    """At one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
+    (FUSE['prologue']): a 3-layer backbone's decode steps give the hidden states and key / value rows of the separate
+    launch bit for bit, and the fused form is taken at every layer of every step on the fly runtime's spread middle (the
+    resident runtime keeps the separate launch)."""
+    from yanlongvla_amd import gemma, modules
+    model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
+    modules.install(model, runtime=runtime, layers=gemma.synthetic_layers(model, 15, DEV))
+    x = torch.randn(60, 2048, generator=torch.Generator(device=DEV).manual_seed(9), device=DEV).bfloat16()
+    _, ks, vs = model.prefill(x)
+    outs, taken = {}, {}
+    for fuse in (False, True):
+        modules.FUSE['prologue'] = fuse
+        try:
+            before = modules.STATS['layer_prologues']
+            k2, v2, outs[fuse] = ks, vs, []
+            for t in range(2):
+                h, k2, v2 = model.decode_step(x[t:t + 1], k2, v2)
+                outs[fuse] += [h] + list(k2) + list(v2)
+            taken[fuse] = modules.STATS['layer_prologues'] - before
+        finally:
+            modules.FUSE['prologue'] = True
+    assert taken == {False: 0, True: 2 * 3 if runtime == 'fly' else 0}
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize('runtime', ['reference', 'fly', 'resident'])
 def test_kv_cache_decode_matches_concatenation(runtime):
     """Decode steps on a KVCache (the new rows written in place: by the q/k/v epilogue on the fused layers, by a copy on

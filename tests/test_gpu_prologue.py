@@ -1,0 +1,136 @@
+"""GPU tests of the one-token products that run the decoder-layer prologue in their own launch (tcq_gemm_tcq_pro /
+tcq_gemm_w8_pro): every output equals, bit for bit, tcq_post_add_norm_pre followed by the plain product on its INT8 row
+(the residual output, the INT8 row and scale copies, the FP32 z or the stage-split zt). Plans: the workgroup plan with one
+and two tile rows per workgroup, the streaming plan at 8 / 4 / 2 / 1 waves per tile row, the stage-split gate | up output;
+the accumulators in one, two and four K parts. tcq_post_add_norm_pre itself is pinned against the oracle in
+test_gpu_norms.py and test_gpu_backbone_oracle.py."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+K = 2048
+
+
+@pytest.fixture(scope='module', autouse=True)
+def _lib():
+    from yanlongvla_amd import _lib
+    _lib.lib()
+    torch.cuda.init()
+
+
+def signs(g, n):
+    return (torch.randint(0, 2, (n,), generator=g, device=DEV) * 2 - 1).to(torch.int8)
+
+
+def prologue_inputs(parts, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    shape = (parts, 1, K) if parts > 1 else (1, K)
+    acc = torch.randint(-(1 << 20), 1 << 20, shape, generator=g, device=DEV, dtype=torch.int32)
+    return dict(acc=acc, s=torch.rand(1, generator=g, device=DEV) * 1e-3 + 1e-4, rs=torch.rand(K, generator=g, device=DEV) * 1e-3,
+                sv=signs(g, K), x=torch.randn(1, K, generator=g, device=DEV).bfloat16(),
+                w=(torch.randn(K, generator=g, device=DEV) * 0.1).bfloat16(), eps=1e-6, su=signs(g, K))
+
+
+def segments(widths, resident, seed, outs):
+    from yanlongvla_amd import kernels as Kn
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    segs = []
+    for m, o in zip(widths, outs):
+        rs = torch.rand(m, generator=g, device=DEV) * 1e-3
+        if resident:
+            w, t8 = torch.randint(-127, 128, (m, K), generator=g, device=DEV, dtype=torch.int8), None
+        else:
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (Kn.repack_words(m, K),), generator=g, device=DEV, dtype=torch.int32)
+            t8 = torch.randint(-127, 128, (512, 2), generator=g, device=DEV, dtype=torch.int8)
+        segs.append((w, t8, rs, o))
+    return segs
+
+
+def reference_row(a):
+    """tcq_post_add_norm_pre of the inputs: xout, the INT8 row and its scale."""
+    from yanlongvla_amd import kernels as Kn
+    xout = torch.empty_like(a['x'])
+    q = torch.empty(1, K, dtype=torch.int8, device=DEV)
+    sc = torch.empty(1, device=DEV)
+    Kn.post_add_norm_pre(a['acc'], a['s'], a['rs'], a['sv'], None, a['x'], xout, a['w'], a['eps'], a['su'], q=q, scale=sc)
+    return xout, q, sc
+
+
+def pro_of(a):
+    from yanlongvla_amd import kernels as Kn
+    xout = torch.full_like(a['x'], float('nan'))
+    q = torch.zeros(1, K, dtype=torch.int8, device=DEV)
+    sc = torch.zeros(1, device=DEV)
+    pro = Kn.prologue(a['acc'], a['s'], a['rs'], a['sv'], a['x'], xout, a['w'], a['eps'], a['su'], q=q, scale=sc)
+    return pro, xout, q, sc
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32 if t.element_size() == 4 else torch.int8).cpu()
+
+
+@pytest.mark.parametrize('widths,resident,parts', [
+    ([2048, 256, 256], False, 2),          # workgroup plan, one tile row per workgroup (the backbone's q / k / v)
+    ([2048, 256, 256], True, 1),
+    ([16384, 16384], True, 2),             # workgroup plan, two tile rows (resident gate | up)
+    ([16384, 16384], False, 4),            # streaming plan, 2 waves per tile row (fly gate | up)
+    ([8192], False, 2),                    # 8 waves per tile row
+    ([16384], False, 1),                   # 4
+    ([65536], False, 2),                   # 1
+])
+def test_product_with_prologue_equals_the_two_launches(widths, resident, parts):
+    from yanlongvla_amd import kernels as Kn
+    a = prologue_inputs(parts, sum(widths) + parts)
+    Ntot = sum(widths)
+    cols = np.cumsum([0] + widths)[:-1]
+    z_ref = torch.full((1, Ntot), float('nan'), device=DEV)
+    z_pro = torch.full((1, Ntot), float('nan'), device=DEV)
+    segs = segments(widths, resident, 7 + parts, [z_ref[:, c:] for c in cols])
+    xout, q, sc = reference_row(a)
+    Kn.SmallProduct(segs, Ntot, resident=resident)(q, sc)
+    pro, xo2, q2, sc2 = pro_of(a)
+    Kn.SmallProduct([(w, t8, rs, z_pro[:, c:]) for (w, t8, rs, _), c in zip(segs, cols)], Ntot, resident=resident).run_pro(pro)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(xo2), bits(xout))
+    assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(bits(sc2), bits(sc))
+    assert torch.equal(bits(z_pro), bits(z_ref))
+    assert not torch.isnan(z_pro).any()
+
+
+@pytest.mark.parametrize('parts', [1, 2])
+def test_stage_split_middle_with_prologue(parts):
+    """The gate | up product with the stage-split output (TCQ_Z_W128T) and the prologue: zt equals the two-launch form."""
+    from yanlongvla_amd import kernels as Kn
+    a = prologue_inputs(parts, 90 + parts)
+    zt = [torch.full((2, 1, 128, 128), float('nan'), device=DEV) for _ in range(2)]
+    segs = segments([16384, 16384], False, 11, [None, None])
+    xout, q, sc = reference_row(a)
+    Kn.gemm_tcq_w128t([(w, t8, rs, zt[0][i]) for i, (w, t8, rs, _) in enumerate(segs)], q, sc)
+    pro, xo2, q2, sc2 = pro_of(a)
+    Kn.gemm_tcq_w128t([(w, t8, rs, zt[1][i]) for i, (w, t8, rs, _) in enumerate(segs)], None, None, pro=pro)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(xo2), bits(xout)) and torch.equal(q2.cpu(), q.cpu())
+    assert torch.equal(bits(zt[1]), bits(zt[0]))
+    assert not torch.isnan(zt[1]).any()
+
+
+def test_prologue_refusals():
+    """Rows other than 2048 wide and non-FP32 outputs are refused before any launch."""
+    from yanlongvla_amd import kernels as Kn, _lib
+    a = prologue_inputs(2, 5)
+    z = torch.empty(1, 256, dtype=torch.int32, device=DEV)
+    segs = segments([256], False, 3, [z])
+    pro, _, _, _ = pro_of(a)
+    with pytest.raises(ValueError):                                   # int32 outputs
+        Kn.SmallProduct(segs, 256).run_pro(pro)
+    z = torch.empty(1, 256, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    x = torch.randn(1, 1024, generator=g, device=DEV).bfloat16()
+    pro1024 = Kn.prologue(a['acc'][:, :, :1024].contiguous(), a['s'], a['rs'][:1024].contiguous(), a['sv'][:1024].contiguous(), x,
+                          torch.empty_like(x), a['w'][:1024].contiguous(), 1e-6, a['su'][:1024].contiguous())
+    w = torch.randint(-127, 128, (256, 1024), generator=g, device=DEV, dtype=torch.int8)
+    with pytest.raises(_lib.TcqError):                                # K = 1024: no variant
+        Kn.SmallProduct([(w, None, segs[0][2], z)], 256, resident=True).run_pro(pro1024)

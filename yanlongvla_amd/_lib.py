@@ -69,6 +69,8 @@ SIGNATURES = {
     'tcq_gemmf_w8_hT': [_P, _P, _I, _P, _P, _I, _I, _I, _P],
     'tcq_gemmf_tcq_hT': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_glu_split': [_P, _I, _P, _P, _P, _I, _P],
+    'tcq_gemm_tcq_pro': [_P, _I, _P, _I, _I, _I, _P],
+    'tcq_gemm_w8_pro': [_P, _I, _P, _I, _I, _I, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 
@@ -86,6 +88,14 @@ class GemmSeg(ctypes.Structure):
     """tcq_gemm_seg (include/tcq_api.h)."""
     _fields_ = [('w', ctypes.c_void_p), ('t8', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('out', ctypes.c_void_p),
                 ('m', ctypes.c_int), ('rows_per_table', ctypes.c_int)]
+
+
+class Prologue(ctypes.Structure):
+    """tcq_prologue (include/tcq_api.h)."""
+    _fields_ = [('acc', ctypes.c_void_p), ('acc_dtype', ctypes.c_int), ('lda', ctypes.c_int), ('col0', ctypes.c_int),
+                ('s', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('sv', ctypes.c_void_p), ('bias', ctypes.c_void_p),
+                ('x', ctypes.c_void_p), ('xout', ctypes.c_void_p), ('w', ctypes.c_void_p), ('eps', ctypes.c_float),
+                ('su', ctypes.c_void_p), ('q', ctypes.c_void_p), ('scale', ctypes.c_void_p)]
 
 
 _state = {}

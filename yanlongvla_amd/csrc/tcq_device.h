@@ -23,16 +23,54 @@ typedef u16 u16x2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------------------------------------------------ conversions
 __device__ __forceinline__ float bf16_to_f32(u16 b) { return __uint_as_float(((u32)b) << 16); }
-// FP32 -> BF16, round to nearest even, every NaN -> 0x7fc0 (reference kernels.py:20-25). The rounded word is formed
-// unconditionally and replaced for NaN (an unordered compare and a select): fewer instructions than testing the bits first.
-__device__ __forceinline__ u32 bf16_round_word(float f) {
-    const u32 u = __float_as_uint(f);
-    const u32 r = u + 0x7fffu + ((u >> 16) & 1u);
-    return __builtin_isnan(f) ? 0x7fc00000u : r;                 // the BF16 value sits in the high half
+// FP32 -> BF16, round to nearest even, every NaN -> 0x7fc0 (reference kernels.py:20-25). gfx950's v_cvt_pk_bf16_f32
+// rounds to nearest even (subnormals kept: the kernels run with FP32 denormals on); only its NaN results differ (it keeps
+// the sign and payload), so NaN inputs are replaced after the conversion.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16 f32_to_bf16(float f) {
+    const u16 h = __builtin_bit_cast(u16, (__bf16)f);
+    return __builtin_isnan(f) ? (u16)0x7fc0 : h;
 }
-__device__ __forceinline__ u16 f32_to_bf16(float f) { return (u16)(bf16_round_word(f) >> 16); }
-// two values -> one word of two BF16 (a in the low half), the halves picked by one byte permute
-__device__ __forceinline__ u32 bf16x2(float a, float b) { return __builtin_amdgcn_perm(bf16_round_word(b), bf16_round_word(a), 0x07060302u); }
+__device__ __forceinline__ u32 bf16_cvt2(float a, float b) {
+    return __builtin_bit_cast(u32, __builtin_convertvector(float2_t{a, b}, bf16x2_t));
+}
+// the word of a converted pair with the half of each NaN input replaced by 0x7fc0 (one bitfield insert)
+__device__ __forceinline__ u32 bf16_nan_fix(u32 w, float a, float b) {
+    const u32 m = (__builtin_isnan(a) ? 0xffffu : 0u) | (__builtin_isnan(b) ? 0xffff0000u : 0u);
+    return (m & 0x7fc07fc0u) | (~m & w);
+}
+// two values -> one word of two BF16 (a in the low half)
+__device__ __forceinline__ u32 bf16x2(float a, float b) { return bf16_nan_fix(bf16_cvt2(a, b), a, b); }
+// 2 NP values -> NP words (value 2p in the low half of word p): one conversion per pair; one unordered compare per pair
+// into a wave-wide lane mask (scalar ORs) decides whether any lane of the wave holds a NaN, and only then does the wave run
+// the fix-up (a uniform branch).
+template <int NP>
+__device__ __forceinline__ void bf16_pack(const float* v, u32* w) {
+    u64 nan = 0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        w[p] = bf16_cvt2(v[2 * p], v[2 * p + 1]);
+        nan |= __builtin_amdgcn_ballot_w64(__builtin_isunordered(v[2 * p], v[2 * p + 1]));
+    }
+    if (__builtin_expect(nan != 0, false)) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) w[p] = bf16_nan_fix(w[p], v[2 * p], v[2 * p + 1]);
+    }
+}
+// 2 NP values rounded to BF16 in place (each replaced by its BF16 value as FP32), the BF16 halves in h
+template <int NP>
+__device__ __forceinline__ void bf16_round(float* v, u16* h) {
+    u32 w[NP];
+    bf16_pack<NP>(v, w);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        h[2 * p] = (u16)(w[p] & 0xffffu);
+        h[2 * p + 1] = (u16)(w[p] >> 16);
+        v[2 * p] = __uint_as_float(w[p] << 16);
+        v[2 * p + 1] = __uint_as_float(w[p] & 0xffff0000u);
+    }
+}
 __device__ __forceinline__ float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 // FP32 -> FP16 of an FP32 value. The value is pinned in a register first: otherwise the compiler may fuse a preceding multiply
 // and this conversion into one mixed-precision FMA (v_fma_mixlo_f16), a single rounding of the exact product, where the
@@ -403,9 +441,34 @@ __device__ __forceinline__ void tw_to_natural2(float (&a)[1 << LE], float (&b)[1
 }
 
 // ---------------------------------------------------------------------------------------------------- activation quantizer
-// Per-token symmetric INT8 of tcq_format.quantize_tokens (reference tcq_format.py:119-122): IEEE division, half-even, clamp.
-__device__ __forceinline__ int q8(float v, float s) {
-    float r = __builtin_rintf(v / s);
+// Per-token symmetric INT8 of tcq_format.quantize_tokens (reference tcq_format.py:119-122): the correctly rounded quotient
+// v / s, rounded half-even, clamped. The quotient: for a scale in [2^-90, 2^90] (every row whose largest magnitude is a
+// normal value far from overflow), q = v * (1 / s) with two Markstein corrections q += (v - q s) / s, the residuals exact
+// through fused multiply-adds: with a correctly rounded reciprocal, the first correction brings q within one ulp and the
+// second gives the correctly rounded quotient (Markstein's theorem) wherever nothing underflows, i.e. for every |v / s|
+// that can round to a nonzero integer (quotients below 2^-24 s / s may differ in their last bits and still round to 0).
+// Checked against IEEE division on the CPU over every FP32 v of a row at six scales and 2e7 near-tie pairs. Other scales
+// (tiny or huge rows, infinities) divide.
+struct QScale {
+    float s, rcp;
+    bool fast;
+};
+__device__ __forceinline__ QScale qscale(float s) {
+    const bool fast = s >= 0x1p-90f && s <= 0x1p90f;
+    return QScale{s, fast ? 1.f / s : 0.f, fast};
+}
+__device__ __forceinline__ int q8(float v, const QScale& S) {
+    float d;
+    if (S.fast) {
+        d = v * S.rcp;
+        float e = __builtin_fmaf(-d, S.s, v);
+        d = __builtin_fmaf(e, S.rcp, d);
+        e = __builtin_fmaf(-d, S.s, v);
+        d = __builtin_fmaf(e, S.rcp, d);
+    } else {
+        d = v / S.s;
+    }
+    float r = __builtin_rintf(d);
     r = fminf(fmaxf(r, -127.f), 127.f);
     return (int)r;
 }
@@ -418,7 +481,8 @@ __device__ __forceinline__ size_t tb_offset(int t, int k, int K) {
 
 // Quantize an LDS row (logical indices 0..K-1, K % 4 == 0) with scale s: q (K bytes, row-major) and / or the q4 layout
 // (K/4, ldq) int32 words (4 consecutive inputs per word, token = column), as reference kernels.py:170-184.
-__device__ __forceinline__ void quantize_row(const float* lds, float s, i8* q, int* q4, int tok, int K, int ldq) {
+__device__ __forceinline__ void quantize_row(const float* lds, float sc, i8* q, int* q4, int tok, int K, int ldq) {
+    const QScale s = qscale(sc);
     for (int j = threadIdx.x; j < (K >> 2); j += blockDim.x) {
         const u32 word = (u32)(q8(lds[lds_slot(4 * j)], s) & 0xff) | ((u32)(q8(lds[lds_slot(4 * j + 1)], s) & 0xff) << 8) |
                          ((u32)(q8(lds[lds_slot(4 * j + 2)], s) & 0xff) << 16) | ((u32)(q8(lds[lds_slot(4 * j + 3)], s) & 0xff) << 24);
@@ -523,11 +587,12 @@ __device__ __forceinline__ void reg_rotate_quantize(float (&v)[16], int N, float
     const float sc = token_scale(block_max(mx, red));
     if (t == 0) scale[tok] = sc;
     if (!on) return;
+    const QScale S = qscale(sc);
     u32 words[4];
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4)
-        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
-                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+        words[k4] = (u32)(q8(v[4 * k4], S) & 0xff) | ((u32)(q8(v[4 * k4 + 1], S) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], S) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], S) & 0xff) << 24);
     if (q) *gptr((uint4_t*)(q + (size_t)tok * N + 16 * t)) = uint4_t{words[0], words[1], words[2], words[3]};
     if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) {
         *gptr((uint4_t*)((i8*)q4 + tb_offset(tok, 16 * t, N))) = uint4_t{words[0], words[1], words[2], words[3]};
@@ -544,9 +609,11 @@ __device__ __forceinline__ float (&part16(float (&v)[E], int h))[16] { return *r
 // reg_rotate_quantize on the register + transpose engine: v holds the natural-layout values 2^LE t .. 2^LE t + 2^LE - 1 of
 // the row (N = 2^L); the same operations in the same order (Walsh, * c, row max, per-token INT8, q and / or q4 words).
 // Threads from 2^(L - LE) on (a workgroup wider than the row) hold no values: they meet the barriers and store nothing.
+// Any of q, q4, scale may be NULL; qs / scs (LDS, optional): the row's INT8 words (word j = inputs 4j .. 4j + 3) and its
+// scale are also left there.
 template <int L, int LE>
 __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* xs, float* red, i8* q, int* q4, int ldq,
-                                                   float* scale, int tok) {
+                                                   float* scale, int tok, u32* qs = nullptr, float* scs = nullptr) {
     constexpr int N = 1 << L, E = 1 << LE;
     const int t = threadIdx.x;
     const bool on = t < (N >> LE);
@@ -559,14 +626,21 @@ __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* x
         if (on) mx = fmaxf(mx, fabsf(v[k]));
     }
     const float sc = token_scale(block_max(mx, red));
-    if (t == 0) scale[tok] = sc;
+    if (t == 0 && scale) scale[tok] = sc;
+    if (t == 0 && scs) *scs = sc;
     tw_to_natural<L, LE>(v, xs);
     if (!on) return;
+    const QScale S = qscale(sc);
     u32 words[E / 4];
 #pragma unroll
     for (int k4 = 0; k4 < E / 4; ++k4)
-        words[k4] = (u32)(q8(v[4 * k4], sc) & 0xff) | ((u32)(q8(v[4 * k4 + 1], sc) & 0xff) << 8) |
-                    ((u32)(q8(v[4 * k4 + 2], sc) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], sc) & 0xff) << 24);
+        words[k4] = (u32)(q8(v[4 * k4], S) & 0xff) | ((u32)(q8(v[4 * k4 + 1], S) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], S) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], S) & 0xff) << 24);
+    if (qs) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h)
+            *(uint4_t*)(qs + (E / 4) * t + 4 * h) = uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+    }
     if (q) {
 #pragma unroll
         for (int h = 0; h < E / 16; ++h)
@@ -624,15 +698,26 @@ __device__ __forceinline__ void tw_span_store(void* row, float* xs) {
     constexpr int ESZ = YDT == TCQ_F32 ? 4 : 2;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint4_t* o = (uint4_t*)((char*)row + ((size_t)w << (LE + 6)) * ESZ);
+    constexpr int NJ = (1 << LE) * ESZ / 16;
+    if constexpr (YDT == TCQ_BF16) {                                     // every piece converted in one batch
+        float d[8 * NJ];
+        u32 w[4 * NJ];
 #pragma unroll
-    for (int j = 0; j < (1 << LE) * ESZ / 16; ++j) {
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[8 * j + e] = tw_piece_slot<LE, ESZ>(xs, j)[e];
+        bf16_pack<4 * NJ>(d, w);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) *gptr(o + 64 * j + lane) = uint4_t{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
         const float* d = tw_piece_slot<LE, ESZ>(xs, j);
         uint4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            v[e] = YDT == TCQ_F32 ? __float_as_uint(d[e])
-                 : YDT == TCQ_BF16 ? bf16x2(d[2 * e], d[2 * e + 1])
-                                   : (u32)f32_to_f16(d[2 * e]) | ((u32)f32_to_f16(d[2 * e + 1]) << 16);
+            v[e] = YDT == TCQ_F32 ? __float_as_uint(d[e]) : (u32)f32_to_f16(d[2 * e]) | ((u32)f32_to_f16(d[2 * e + 1]) << 16);
         *gptr(o + 64 * j + lane) = v;
     }
 }

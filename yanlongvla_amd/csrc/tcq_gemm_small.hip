@@ -15,6 +15,7 @@
 // workgroup costs one memory round trip. The partial int32 sums of the waves are added in LDS at the end (exact).
 #include "tcq_device.h"
 #include "tcq_launch.h"
+#include "tcq_rows.h"
 
 namespace {
 
@@ -64,6 +65,38 @@ struct SegPack {
     tcq_gemm_seg s[TCQ_MAX_SEGS];
 };
 
+// The segments plus the arguments of a one-token decoder-layer prologue (tcq_gemm_tcq_pro / tcq_gemm_w8_pro).
+struct SegPackPro {
+    tcq_gemm_seg s[TCQ_MAX_SEGS];
+    PanpArgs a;
+    i8* q;                   // optional copies of the prologue's INT8 row and token scale (written by workgroup 0)
+    float* scale;
+};
+template <int PL> struct PackOf { typedef SegPackPro type; };
+template <> struct PackOf<0> { typedef SegPack type; };
+
+// LDS of the prologue of a 2^PL-wide row: the Walsh engine's row, the chunk sums, the reduction slots, the INT8 row and its
+// scale (the product's activations).
+template <int PL>
+struct ProLds {
+    static constexpr int W = (1 << PL) + ((1 << PL) >> 5) + 1;           // lds_words(2^PL)
+    float xs[W + (1 << PL) / 16];
+    float red[16];
+    __attribute__((aligned(16))) u32 qs[(1 << PL) / 4];
+    float sc;
+};
+
+// Runs the prologue (tcq_post_add_norm_pre of token 0 with the norm; workgroup (0, 0, 0) stores xout and the optional
+// copies) and leaves the INT8 row and the scale in L. Every thread of the workgroup calls it; mid() issues the product's
+// weight loads once the prologue's accumulator registers are free, so their HBM latency runs under the prologue.
+template <int PL, class F>
+__device__ __forceinline__ void run_prologue(const SegPackPro& P, ProLds<PL>& L, F&& mid) {
+    const bool store = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+    float v[16];
+    panp_tw<TCQ_I32, PL, 4, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
+    tw_rotate_quantize<PL, 4>(v, L.xs, L.red, store ? P.q : nullptr, nullptr, 0, store ? P.scale : nullptr, 0, L.qs, &L.sc);
+}
+
 // Activation layouts of the small-M products: q (M, K) row-major, the token-block layout, or the reference's q4 (K/4, ldq)
 // int32 words (4 consecutive inputs of one token per word, token = column; deploy/tcq_kernels/kernels.py:170-184).
 enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
@@ -74,13 +107,17 @@ enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
 // dtype (F32 scaled, BF16 scaled, I32 accumulators). QL: activation layout (ldq only for QL_WORDS).
 // KS > 1 (I32 only): K parts, blockIdx.z = part p takes chunks [p * ceil(nch / KS), ...) and writes at out + p * M * ldz.
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
-template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false>
-__global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPack P, const i8* q, const float* s, int M, int K, int ldz,
-                                                                    int ldq) {
+// PL > 0 (M == 1, K = 2^PL, int32 K-part accumulators in): the activations come from the decoder-layer prologue run by
+// every workgroup (run_prologue) instead of q / s.
+template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false, int PL = 0>
+__global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typename PackOf<PL>::type P, const i8* q, const float* s,
+                                                                    int M, int K, int ldz, int ldq) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     static_assert(!DOT || (NB == 1 && QL != QL_WORDS), "dot products: one token, q rows or token blocks");
+    static_assert(PL == 0 || (NB == 1 && QL == QL_ROWS && !DOT), "prologue: one token");
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
+    __shared__ ProLds<PL ? PL : 4> pro;
     const tcq_gemm_seg S = P.s[blockIdx.y];
     const int tiles_m = S.m >> 4, nch_all = (K + 255) >> 8;
     const int c0 = KS > 1 ? (int)blockIdx.z * ((nch_all + KS - 1) / KS) : 0;
@@ -101,6 +138,13 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 
     uint4_t wa[TR][MODE == 0 ? 1 : 4];
     int4v B[4][NB];
+    auto loadB = [&](int c) {                                             // activations of chunk c from the prologue's row
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 256 * c + 64 * j + 16 * lg;
+            B[j][0] = (lr < M && k < K) ? *(const int4v*)((const char*)pro.qs + k) : int4v{0, 0, 0, 0};
+        }
+    };
     auto load = [&](int c) {                                              // words / weights and activations of chunk c
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
@@ -124,6 +168,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
                 }
             }
         }
+        if (PL) return;                                                   // activations: loadB after the prologue
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -149,7 +194,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
     }
-    if (c0 + wave < nch) load(c0 + wave);
+    if (!PL && c0 + wave < nch) load(c0 + wave);
     // epilogue scales, loaded with the operands (wave 0 stores)
     float4_t rsv[TR];
     float sv[NB];
@@ -160,13 +205,25 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const SegPa
     if (ODT != TCQ_I32 && wave == 0) {
 #pragma unroll
         for (int r = 0; r < TR; ++r) rsv[r] = gptr((const float4_t*)(S.rs + 16 * min(I0 + r, tiles_m - 1) + 4 * lg))[0];
+        if constexpr (!PL) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
+            for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
+        }
     }
     if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
+    if constexpr (PL > 0) run_prologue<PL>(P, pro, [&] {
+        if (c0 + wave < nch) load(c0 + wave);
+    });
     __syncthreads();
+    if constexpr (PL > 0) {
+        sv[0] = pro.sc;
+        if (c0 + wave < nch) loadB(c0 + wave);
+    }
     for (int c = c0 + wave; c < nch; c += nw) {
-        if (c != c0 + wave) load(c);
+        if (c != c0 + wave) {
+            load(c);
+            if constexpr (PL > 0) loadB(c);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -257,9 +314,13 @@ constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table 
 // stages of the block Walsh of the whole segment (h = 1 .. 64, which stay inside such a block) run here, in the reference's
 // stage order, and the block is stored transposed: zt[(t * 128 + o) * (m / 128) + blk] for row 128 blk + o of token t.
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
-template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false>
-__global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8* q, const float* s, int M, int K, int ldz) {
+// PL > 0: activations from the decoder-layer prologue, as k_gemm_small.
+template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false, int PL = 0>
+__global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>::type P, const i8* q, const float* s, int M, int K,
+                                                      int ldz) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
+    static_assert(PL == 0 || (!QB && !DOT), "prologue: one token");
+    __shared__ ProLds<PL ? PL : 4> pro;
     static_assert(!LO || (ODT == TCQ_F32 && KS == 1 && NW / WPR == 8), "stage-split output: FP32 z, 8 tile rows per workgroup");
     constexpr int RPW = NW / WPR;
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
@@ -276,27 +337,35 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
     const u32 cp4 = (u32)(lane & (GV_C - 1)) << 2;
     const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch_all) << 10);
     const rsrc_t Q = make_rsrc(q, QB ? 16u * (u32)K : (u32)M * (u32)K);
-    uint4_t wa[GV_CMAX];
+    constexpr int CM = PL ? ((1 << PL) / 256 + WPR - 1) / WPR : GV_CMAX;   // chunks per wave at most (K = 2^PL: known)
+    uint4_t wa[CM];
+    auto loadW = [&] {
 #pragma unroll
-    for (int i = 0; i < GV_CMAX; ++i) {
-        const int c = c0 + part + WPR * i;
-        if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
-    }
+        for (int i = 0; i < CM; ++i) {
+            const int c = c0 + part + WPR * i;
+            if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
+        }
+    };
+    if constexpr (!PL) loadW();
     auto loadB = [&](int c, int4v* B) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int k = 256 * c + 64 * j + 16 * lg, t = DOT ? 0 : lr;              // DOT: every lane token 0
-            const u32 off = (t < M && k < K) ? (QB ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
-            B[j] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
+            if constexpr (PL > 0) {                                        // the prologue's row (LDS)
+                B[j] = (t < M && k < K) ? *(const int4v*)((const char*)pro.qs + k) : int4v{0, 0, 0, 0};
+            } else {
+                const u32 off = (t < M && k < K) ? (QB ? (u32)tb_offset(t, k, K) : (u32)t * (u32)K + (u32)k) : RSRC_OOB;
+                B[j] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(Q, off, 0, 0));
+            }
         }
     };
     int4v Bf[2][4];                                                        // activation fragments, two chunks in turn
-    loadB(c0 + part, Bf[0]);
+    if constexpr (!PL) loadB(c0 + part, Bf[0]);
     float4_t rsv = float4_t{0.f, 0.f, 0.f, 0.f};
     float sv = 0.f;
     if (ODT != TCQ_I32 && part == 0) {
         rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
-        sv = gptr(s)[min(lr, M - 1)];
+        if constexpr (!PL) sv = gptr(s)[min(lr, M - 1)];
     }
     {
         const i8* t8 = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
@@ -311,14 +380,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const SegPack P, const i8*
             for (int c = 0; c < GV_C; c += 4) *(uint4_t*)(tab + e * GV_C + c) = uint4_t{vv, vv, vv, vv};
         }
     }
+    if constexpr (PL > 0) run_prologue<PL>(P, pro, loadW);
     __syncthreads();
+    if constexpr (PL > 0) {
+        if (ODT != TCQ_I32 && part == 0) sv = pro.sc;
+        loadB(c0 + part, Bf[0]);
+    }
     int4v acc = int4v{0, 0, 0, 0};
     int dacc[2] = {0, 0};                                                  // DOT: row lr, k-block lg, two chains
 #pragma unroll
-    for (int i = 0; i < GV_CMAX; ++i) {
+    for (int i = 0; i < CM; ++i) {
         const int c = c0 + part + WPR * i;
         if (c >= nch) continue;                                            // uniform
-        if (i + 1 < GV_CMAX && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
+        if (i + 1 < CM && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u32 hi = wa[i][j];
@@ -604,6 +678,96 @@ extern "C" int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q,
 extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                            tcq_stream_t stream) {
     return gemm_small<1>(segs, nseg, q, s, M, K, out_dtype, ldo, stream);
+}
+
+// ------------------------------------------------------------------------------------ products with the layer prologue
+// One token: every workgroup first runs tcq_post_add_norm_pre's operations on the previous product's int32 sums (the
+// register + transpose engine of its 2048-wide path, bit for bit), then its share of the product on the INT8 row it left in
+// LDS; workgroup (0, 0, 0) stores xout (and the optional q / scale copies). Plans as gemm_small picks them for M = 1:
+// the stage-split output (TCQ_Z_W128T), the streaming plan, or the workgroup plan with one or two tile rows.
+constexpr int PRO_L = 11;
+static bool pal16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int MODE>
+static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pr, int K, int odt, int ldo, tcq_stream_t stream) {
+    if (!segs || !pr || nseg <= 0 || ldo <= 0) return TCQ_ERR_ARG;
+    const bool w128 = odt & TCQ_Z_W128T;
+    odt &= ~TCQ_Z_W128T;
+    if (odt != TCQ_F32 || (w128 && MODE != 0)) return TCQ_ERR_UNSUPPORTED;
+    if (K != (1 << PRO_L)) return TCQ_ERR_UNSUPPORTED;
+    int adt = pr->acc_dtype;
+    if ((adt & TCQ_K_PARTS2) && (adt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
+    const int parts = (adt & TCQ_K_PARTS4) ? 4 : (adt & TCQ_K_PARTS2) ? 2 : 1;
+    adt &= ~(TCQ_K_PARTS2 | TCQ_K_PARTS4);
+    if (adt != TCQ_I32) return TCQ_ERR_DTYPE;
+    if (!pr->acc || !pr->s || !pr->rs || !pr->sv || !pr->x || !pr->xout || !pr->w || !pr->su || pr->col0 < 0 || pr->lda < pr->col0 + K)
+        return TCQ_ERR_ARG;
+    if (pr->bias) return TCQ_ERR_UNSUPPORTED;
+    if ((size_t)parts * pr->lda >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+    if (!pal16(pr->acc) || pr->lda % 4 || pr->col0 % 4 || !pal16(pr->rs) || !pal16(pr->sv) || !pal16(pr->x) || !pal16(pr->xout) ||
+        !pal16(pr->w) || !pal16(pr->su) || (pr->bias && !pal16(pr->bias)) || (pr->q && !pal16(pr->q)) || ldo % 4)
+        return TCQ_ERR_ALIGN;
+    SegPackPro P = {};
+    int max_m = 0, tiles = 0;
+    for (int i = 0; i < nseg && i < TCQ_MAX_SEGS; ++i) {
+        const tcq_gemm_seg& g = segs[i];
+        if (!g.w || !g.out || (MODE == 0 && !g.t8) || !g.rs || g.m <= 0) return TCQ_ERR_ARG;
+        if (g.m % 16) return TCQ_ERR_SHAPE;
+        if (g.rows_per_table < 0 || (g.rows_per_table > 0 && (g.rows_per_table % 16 || g.m % g.rows_per_table))) return TCQ_ERR_SHAPE;
+        if ((size_t)g.m * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+        if ((uintptr_t)g.out % 16 || (uintptr_t)g.rs % 16) return TCQ_ERR_ALIGN;
+        if (w128 && (g.m % 128 || (g.rows_per_table > 0 && g.rows_per_table % 128))) return TCQ_ERR_SHAPE;
+        P.s[i] = g;
+        max_m = g.m > max_m ? g.m : max_m;
+        tiles += g.m / 16;
+    }
+    if (nseg > TCQ_MAX_SEGS) return TCQ_ERR_UNSUPPORTED;
+    P.a = PanpArgs{pr->acc, pr->s, pr->rs, (const i8*)pr->sv, pr->bias, (const u16*)pr->x, (u16*)pr->xout, (const u16*)pr->w,
+                   (const i8*)pr->su, pr->lda, pr->col0, parts, (size_t)pr->lda, pr->eps};
+    P.q = (i8*)pr->q;
+    P.scale = pr->scale;
+    hipStream_t st = (hipStream_t)stream;
+    const int nch = K / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
+    if (w128) {
+        launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, PRO_L>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P,
+                 (const i8*)nullptr, (const float*)nullptr, 1, K, ldo);
+        return launch_status();
+    }
+    const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nch, tiles) : 0;
+    if (wpr > 0) {
+        const dim3 grid((max_m / 16 + GV_NW / wpr - 1) / (GV_NW / wpr), nseg), block(64 * GV_NW);
+#define GVP(W) launch_k(k_gemv_tcq<TCQ_F32, false, W, GV_NW, 1, false, false, PRO_L>, grid, block, 0, st, P, (const i8*)nullptr, \
+                        (const float*)nullptr, 1, K, ldo)
+        switch (wpr) {
+            case 1: GVP(1); break;
+            case 2: GVP(2); break;
+            case 4: GVP(4); break;
+            case 8: GVP(8); break;
+            default: GVP(16); break;
+        }
+#undef GVP
+        return launch_status();
+    }
+    bool pairs = nw <= 8 && tiles >= 384;
+    for (int i = 0; i < nseg; ++i)
+        if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
+    if (pairs)
+        launch_k(k_gemm_small<MODE, 1, TCQ_F32, 2, QL_ROWS, false, 1, false, PRO_L>, dim3((max_m / 16 + 1) / 2, nseg), dim3(64 * nw), 0,
+                 st, P, (const i8*)nullptr, (const float*)nullptr, 1, K, ldo, 0);
+    else
+        launch_k(k_gemm_small<MODE, 1, TCQ_F32, 1, QL_ROWS, false, 1, false, PRO_L>, dim3(max_m / 16, nseg), dim3(64 * nw), 0, st, P,
+                 (const i8*)nullptr, (const float*)nullptr, 1, K, ldo, 0);
+    return launch_status();
+}
+
+extern "C" int tcq_gemm_tcq_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo,
+                                tcq_stream_t stream) {
+    return gemm_small_pro<0>(segs, nseg, pro, K, out_dtype, ldo, stream);
+}
+
+extern "C" int tcq_gemm_w8_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo,
+                               tcq_stream_t stream) {
+    return gemm_small_pro<1>(segs, nseg, pro, K, out_dtype, ldo, stream);
 }
 
 // ------------------------------------------------------------------------------------------ reference-shaped helpers

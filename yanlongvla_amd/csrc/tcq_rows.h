@@ -1,0 +1,240 @@
+// Row helpers shared by the row kernels (tcq_walsh.hip) and the products that run a row kernel as their prologue
+// (tcq_gemm_small.hip): 16-element chunk loads / stores, the fixed-order sum of squares, accumulator chunks.
+#pragma once
+#include "tcq_device.h"
+
+// ------------------------------------------------------------------------------------------------ 16-element chunks
+// The row kernels keep every global access out of the Walsh passes: the passes read and write LDS only, and the
+// side vectors (signs, bias, residual, norm weight) are read per 16-element chunk with 16-byte loads (vec) or element by
+// element (rows whose base or length breaks the alignment), all loads of a chunk issued before any of them is used.
+__device__ __forceinline__ void c16_bf16(const u16* p, bool vec, float (&v)[16]) {
+    if (vec) {
+        const uint4_t a = gptr((const uint4_t*)p)[0], b = gptr((const uint4_t*)p)[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = bf16_to_f32((u16)(a[k] & 0xffffu)); v[2 * k + 1] = bf16_to_f32((u16)(a[k] >> 16));
+            v[8 + 2 * k] = bf16_to_f32((u16)(b[k] & 0xffffu)); v[9 + 2 * k] = bf16_to_f32((u16)(b[k] >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32(gptr(p)[k]);
+    }
+}
+__device__ __forceinline__ void c16_store_bf16(u16* p, bool vec, const u16 (&h)[16]) {
+    if (vec) {
+        uint4_t a, b;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[k] = (u32)h[2 * k] | ((u32)h[2 * k + 1] << 16);
+            b[k] = (u32)h[8 + 2 * k] | ((u32)h[9 + 2 * k] << 16);
+        }
+        gptr((uint4_t*)p)[0] = a;
+        gptr((uint4_t*)p)[1] = b;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) gptr(p)[k] = h[k];
+    }
+}
+__device__ __forceinline__ void c16_i8(const i8* p, bool vec, float (&v)[16]) {
+    if (vec) {
+        const uint4_t a = gptr((const uint4_t*)p)[0];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a[k >> 2] >> (8 * (k & 3)));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (float)gptr(p)[k];
+    }
+}
+__device__ __forceinline__ void c16_f32(const float* p, bool vec, float (&v)[16]) {
+    if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4_t a = gptr((const uint4_t*)p)[q];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * q + k] = __uint_as_float(a[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = gptr(p)[k];
+    }
+}
+
+// Sum of squares of a row in an order fixed by K alone: chunk sums of 16 consecutive values (sequential, part[j] for chunk
+// j), then a pairwise tree over the chunks, stage h adding chunk j + h into chunk j for j a multiple of 2h. Stages h < 64 run
+// in registers across the lanes of a wave (chunks past the end count as +0, which leaves every partial sum unchanged), the
+// rest over the per-wave results. part: the K / 16 chunk sums (LDS, complete on entry: the caller synchronises); red: >= 16
+// floats of LDS. Every thread gets the total. Ends with a barrier.
+__device__ __forceinline__ float chunk_sumsq(const float (&v)[16]) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a = a + v[k] * v[k];
+    return a;
+}
+__device__ __forceinline__ float tree_total(const float* part, float* red, int K) {
+    const int C = K >> 4, groups = (C + 63) >> 6;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int g = wid; g < groups; g += nw) {
+        const int j = (g << 6) + lane;
+        float v = j < C ? part[j] : 0.f;
+        // pairwise tree over the 64 lanes (stride 1, 2, 4, 8 inside the rows, then 16 and 32): lane l adds lane l + h for l
+        // a multiple of 2h; the other lanes compute values no kept lane reads
+        v = v + dpp<0x101>(v);
+        v = v + dpp<0x102>(v);
+        v = v + dpp<0x104>(v);
+        v = v + dpp<0x108>(v);
+        v = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+        if (lane == 0) red[g] = v;
+    }
+    __syncthreads();
+    float r[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) r[g] = g < groups ? red[g] : 0.f;
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+        for (int g = 0; g + h < 16; g += 2 * h) r[g] = r[g] + r[g + h];
+    __syncthreads();
+    return r[0];
+}
+
+// Accumulator chunk 16 t .. 16 t + 15 of a row (scaled as tcq_post scales it: int32 * s * rs, BF16 * rs, FP32 as is), loaded at kernel entry. int32 K parts (parts > 1,
+// part p at acc + p * pstride) are added in int32 first: the same sum as one part.
+template <int ADT>
+__device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st, const float* rs, float (&v)[16], int parts = 1,
+                                          size_t pstride = 0) {
+    if (ADT == TCQ_BF16) {
+        const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
+        const Raw16<4> r4 = raw16<4>(rs, true);
+        float r[16];
+        cv16(a, v);
+        cv16(r4, r);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
+    } else {
+        Raw16<4> a = raw16<4>((const u32*)acc + base, true);
+        if (ADT == TCQ_I32) {
+            Raw16<4> ap[3];
+#pragma unroll
+            for (int p = 1; p < 4; ++p)
+                if (p < parts) ap[p - 1] = raw16<4>((const u32*)acc + base + p * pstride, true);
+            const Raw16<4> r4 = raw16<4>(rs, true);
+#pragma unroll
+            for (int p = 1; p < 4; ++p)
+                if (p < parts) {
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) a.r[k >> 2][k & 3] = (u32)((int)a.r[k >> 2][k & 3] + (int)ap[p - 1].r[k >> 2][k & 3]);
+                }
+            float r[16];
+            cv16(r4, r);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = ((float)(int)a.r[k >> 2][k & 3] * st) * r[k];
+        } else {
+            cv16(a, v);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------ epilogue + residual + norm of a row
+// Arguments of tcq_post_add_norm_pre for one launch (device copies of its pointers).
+struct PanpArgs {
+    const void* acc;
+    const float* s;
+    const float* rs;
+    const i8* sv;
+    const float* bias;
+    const u16* x;
+    u16* xout;
+    const u16* w;
+    const i8* su;
+    int lda, col0, parts;
+    size_t pstride;          // elements between K parts of acc
+    float eps;
+};
+
+// tcq_post_add_norm_pre of token tok up to the rotate + quantize, on the register + transpose engine with 2^LE values per
+// thread: a = bf16((walsh(acc) * c) * sv (+ bias)), xout = bf16(x + a) (stored when `store`), then, when w is given,
+// v = bf16((xout * r) * (1 + w)) * su with r from the fixed-order sum of squares. v ends in natural layout (thread t holds
+// values 2^LE t ..), ready for tw_rotate_quantize. Threads from 2^(L - LE) on hold no values; they load and store nothing
+// but meet every barrier. xs: lds_words(2^L) floats, part: 2^L / 16 floats, red: 16 floats (LDS). Returns false (uniform)
+// when there is no norm (w NULL): v then holds xout. mid() runs once every thread's accumulator loads have been consumed
+// (a caller issues its own loads there, when the accumulator registers are free again).
+struct NoMid {
+    __device__ void operator()() const {}
+};
+// BIAS = false: A.bias is ignored (callers that have none save its registers).
+template <int ADT, int L, int LE, bool BIAS = true, class F = NoMid>
+__device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, float (&v)[1 << LE], float* xs, float* part,
+                                        float* red, F&& mid = NoMid{}) {
+    constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
+    const int t = threadIdx.x, i0 = E * t;
+    const bool on = t < (N >> LE);
+    const size_t row = (size_t)tok * N, base = (size_t)tok * A.lda + A.col0 + i0;
+    Raw16<1> sv0[NP], su0[NP];
+    Raw16<2> x0[NP], w0[NP];
+    Raw16<4> b0[NP];
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[16 * h + k] = 0.f;
+        if (on) {
+            sv0[h] = raw16<1>(A.sv + i0 + 16 * h, true);
+            x0[h] = raw16<2>(A.x + row + i0 + 16 * h, true);
+            if (BIAS && A.bias) b0[h] = raw16<4>(A.bias + i0 + 16 * h, true);
+            if (A.w) {
+                w0[h] = raw16<2>(A.w + i0 + 16 * h, true);
+                su0[h] = raw16<1>(A.su + i0 + 16 * h, true);
+            }
+        }
+    }
+    if (on) {
+#pragma unroll
+        for (int h = 0; h < NP; ++h)
+            acc_chunk<ADT>(A.acc, base + 16 * h, ADT == TCQ_I32 ? A.s[tok] : 1.f, A.rs ? A.rs + i0 + 16 * h : nullptr, part16(v, h),
+                           A.parts, A.pstride);
+    }
+    mid();
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh<L, LE>(v, xs);
+    tw_to_natural<L, LE>(v, xs);
+    if (on) {
+#pragma unroll
+        for (int h = 0; h < NP; ++h) {
+            float sg[16], b[16], xv[16], a[16];
+            u16 xn[16];
+            cv16(sv0[h], sg);
+            if (BIAS && A.bias) cv16(b0[h], b);
+            cv16(x0[h], xv);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                a[k] = (v[16 * h + k] * c) * sg[k];
+                if (BIAS && A.bias) a[k] = a[k] + b[k];
+            }
+            bf16_round<8>(a, xn);                                      // a = bf16(post output)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[16 * h + k] = xv[k] + a[k];
+            bf16_round<8>(&v[16 * h], xn);                             // xout = bf16(x + a)
+            if (store) c16_store_bf16(A.xout + row + i0 + 16 * h, true, xn);
+            if (A.w) part[NP * t + h] = chunk_sumsq(part16(v, h));
+        }
+    }
+    if (!A.w) return false;                                             // uniform
+    __syncthreads();
+    const float ss = tree_total(part, red, N);
+    const float r = 1.f / __builtin_sqrtf(ss / (float)N + A.eps);
+    if (on) {
+#pragma unroll
+        for (int h = 0; h < NP; ++h) {
+            float wv[16], sn[16];
+            cv16(w0[h], wv);
+            cv16(su0[h], sn);
+            float nv[16];
+            u16 nh[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) nv[k] = (v[16 * h + k] * r) * (1.f + wv[k]);
+            bf16_round<8>(nv, nh);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[16 * h + k] = nv[k] * sn[k];
+        }
+    }
+    return true;
+}

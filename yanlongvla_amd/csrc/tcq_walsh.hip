@@ -6,6 +6,7 @@
 // and the rows are 16-byte aligned, else element by element; the Walsh passes run in LDS between the two.
 #include "tcq_device.h"
 #include "tcq_launch.h"
+#include "tcq_rows.h"
 
 namespace {
 
@@ -38,10 +39,14 @@ template <int DT> struct Elem16 {
         for (int k = 0; k < 4; ++k) { v[2 * k] = cv((u16)(a[k] & 0xffffu)); v[2 * k + 1] = cv((u16)(a[k] >> 16)); }
     }
     static __device__ __forceinline__ void st8(void* p, size_t i, const float (&v)[8]) {
-        uint4_t a;
+        u32 a[4];
+        if constexpr (DT == TCQ_BF16) {
+            bf16_pack<4>(v, a);
+        } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a[k] = DT == TCQ_BF16 ? bf16x2(v[2 * k], v[2 * k + 1]) : (u32)cv(v[2 * k]) | ((u32)cv(v[2 * k + 1]) << 16);
-        gptr((uint4_t*)((u16*)p + i))[0] = a;
+            for (int k = 0; k < 4; ++k) a[k] = (u32)cv(v[2 * k]) | ((u32)cv(v[2 * k + 1]) << 16);
+        }
+        gptr((uint4_t*)((u16*)p + i))[0] = uint4_t{a[0], a[1], a[2], a[3]};
     }
 };
 template <> struct Elem<TCQ_BF16> : Elem16<TCQ_BF16> {};
@@ -511,100 +516,6 @@ __global__ void k_postg(SEGS segs, const float* s, const u16* gelu_lut, int maxN
     store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, S.gelu ? gelu_lut : nullptr, N, vec, has0, p0);
 }
 
-// ------------------------------------------------------------------------------------------------ 16-element chunks
-// The row kernels below keep every global access out of the Walsh passes: the passes read and write LDS only, and the
-// side vectors (signs, bias, residual, norm weight) are read per 16-element chunk with 16-byte loads (vec) or element by
-// element (rows whose base or length breaks the alignment), all loads of a chunk issued before any of them is used.
-__device__ __forceinline__ void c16_bf16(const u16* p, bool vec, float (&v)[16]) {
-    if (vec) {
-        const uint4_t a = gptr((const uint4_t*)p)[0], b = gptr((const uint4_t*)p)[1];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            v[2 * k] = bf16_to_f32((u16)(a[k] & 0xffffu)); v[2 * k + 1] = bf16_to_f32((u16)(a[k] >> 16));
-            v[8 + 2 * k] = bf16_to_f32((u16)(b[k] & 0xffffu)); v[9 + 2 * k] = bf16_to_f32((u16)(b[k] >> 16));
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = bf16_to_f32(gptr(p)[k]);
-    }
-}
-__device__ __forceinline__ void c16_store_bf16(u16* p, bool vec, const u16 (&h)[16]) {
-    if (vec) {
-        uint4_t a, b;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            a[k] = (u32)h[2 * k] | ((u32)h[2 * k + 1] << 16);
-            b[k] = (u32)h[8 + 2 * k] | ((u32)h[9 + 2 * k] << 16);
-        }
-        gptr((uint4_t*)p)[0] = a;
-        gptr((uint4_t*)p)[1] = b;
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) gptr(p)[k] = h[k];
-    }
-}
-__device__ __forceinline__ void c16_i8(const i8* p, bool vec, float (&v)[16]) {
-    if (vec) {
-        const uint4_t a = gptr((const uint4_t*)p)[0];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = (float)(i8)(a[k >> 2] >> (8 * (k & 3)));
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = (float)gptr(p)[k];
-    }
-}
-__device__ __forceinline__ void c16_f32(const float* p, bool vec, float (&v)[16]) {
-    if (vec) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint4_t a = gptr((const uint4_t*)p)[q];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[4 * q + k] = __uint_as_float(a[k]);
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = gptr(p)[k];
-    }
-}
-
-// Sum of squares of a row in an order fixed by K alone: chunk sums of 16 consecutive values (sequential, part[j] for chunk
-// j), then a pairwise tree over the chunks, stage h adding chunk j + h into chunk j for j a multiple of 2h. Stages h < 64 run
-// in registers across the lanes of a wave (chunks past the end count as +0, which leaves every partial sum unchanged), the
-// rest over the per-wave results. part: the K / 16 chunk sums (LDS, complete on entry: the caller synchronises); red: >= 16
-// floats of LDS. Every thread gets the total. Ends with a barrier.
-__device__ __forceinline__ float chunk_sumsq(const float (&v)[16]) {
-    float a = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) a = a + v[k] * v[k];
-    return a;
-}
-__device__ __forceinline__ float tree_total(const float* part, float* red, int K) {
-    const int C = K >> 4, groups = (C + 63) >> 6;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int g = wid; g < groups; g += nw) {
-        const int j = (g << 6) + lane;
-        float v = j < C ? part[j] : 0.f;
-        // pairwise tree over the 64 lanes (stride 1, 2, 4, 8 inside the rows, then 16 and 32): lane l adds lane l + h for l
-        // a multiple of 2h; the other lanes compute values no kept lane reads
-        v = v + dpp<0x101>(v);
-        v = v + dpp<0x102>(v);
-        v = v + dpp<0x104>(v);
-        v = v + dpp<0x108>(v);
-        v = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
-        if (lane == 0) red[g] = v;
-    }
-    __syncthreads();
-    float r[16];
-#pragma unroll
-    for (int g = 0; g < 16; ++g) r[g] = g < groups ? red[g] : 0.f;
-#pragma unroll
-    for (int h = 1; h < 16; h <<= 1)
-#pragma unroll
-        for (int g = 0; g + h < 16; g += 2 * h) r[g] = r[g] + r[g + h];
-    __syncthreads();
-    return r[0];
-}
-
 // RMSNorm of the LDS row (BF16 values as FP32) given its sum of squares: v <- bf16((v * r) * (1 + w[i])) * su[i] (su may be
 // NULL), r = 1 / sqrt(ss / K + eps). Ends with a barrier.
 // pre: w0 / su0 hold this thread's first chunk of w / su, loaded ahead.
@@ -852,43 +763,6 @@ __global__ __launch_bounds__(512) void k_post_add_norm_pre(const void* acc, int 
     if (!w) return;
     norm_apply(lds, tree_total(part, red, N), w, su, eps, N, svec, has0, w0, su0);
     rotate_quantize(lds, red, q, q4, ldq, scale, tok, N);
-}
-
-// Accumulator chunk 16 t .. 16 t + 15 of a row (scaled like load_acc_row), loaded at kernel entry. int32 K parts (parts > 1,
-// part p at acc + p * pstride) are added in int32 first: the same sum as one part.
-template <int ADT>
-__device__ __forceinline__ void acc_chunk(const void* acc, size_t base, float st, const float* rs, float (&v)[16], int parts = 1,
-                                          size_t pstride = 0) {
-    if (ADT == TCQ_BF16) {
-        const Raw16<2> a = raw16<2>((const u16*)acc + base, true);
-        const Raw16<4> r4 = raw16<4>(rs, true);
-        float r[16];
-        cv16(a, v);
-        cv16(r4, r);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = v[k] * r[k];
-    } else {
-        Raw16<4> a = raw16<4>((const u32*)acc + base, true);
-        if (ADT == TCQ_I32) {
-            Raw16<4> ap[3];
-#pragma unroll
-            for (int p = 1; p < 4; ++p)
-                if (p < parts) ap[p - 1] = raw16<4>((const u32*)acc + base + p * pstride, true);
-            const Raw16<4> r4 = raw16<4>(rs, true);
-#pragma unroll
-            for (int p = 1; p < 4; ++p)
-                if (p < parts) {
-#pragma unroll
-                    for (int k = 0; k < 16; ++k) a.r[k >> 2][k & 3] = (u32)((int)a.r[k >> 2][k & 3] + (int)ap[p - 1].r[k >> 2][k & 3]);
-                }
-            float r[16];
-            cv16(r4, r);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = ((float)(int)a.r[k >> 2][k & 3] * st) * r[k];
-        } else {
-            cv16(a, v);
-        }
-    }
 }
 
 // k_postg for power-of-two segments of 256 .. 4096 on the register + transpose engine (16 values per thread; the workgroup
@@ -1194,63 +1068,12 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_post_add_norm_pre_tw(const vo
                                                                        const float* rs, const i8* sv, const float* bias, const u16* x,
                                                                        u16* xout, const u16* w, float eps, const i8* su, i8* q,
                                                                        int* q4, int ldq, float* scale, int parts) {
-    constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
     extern __shared__ float xs[];                                      // lds_words(N) floats for the transposes, then N / 16 sums
-    float* part = xs + lds_words(N);
     __shared__ float red[16];
-    const int tok = blockIdx.x, t = threadIdx.x, i0 = E * t;
-    const size_t row = (size_t)tok * N, base = (size_t)tok * lda + col0 + i0;
-    Raw16<1> sv0[NP], su0[NP];
-    Raw16<2> x0[NP], w0[NP];
-    Raw16<4> b0[NP];
-#pragma unroll
-    for (int h = 0; h < NP; ++h) {
-        sv0[h] = raw16<1>(sv + i0 + 16 * h, true);
-        x0[h] = raw16<2>(x + row + i0 + 16 * h, true);
-        if (bias) b0[h] = raw16<4>(bias + i0 + 16 * h, true);
-        if (w) {
-            w0[h] = raw16<2>(w + i0 + 16 * h, true);
-            su0[h] = raw16<1>(su + i0 + 16 * h, true);
-        }
-    }
-    float v[E];
-#pragma unroll
-    for (int h = 0; h < NP; ++h)
-        acc_chunk<ADT>(acc, base + 16 * h, ADT == TCQ_I32 ? s[tok] : 1.f, rs ? rs + i0 + 16 * h : nullptr, part16(v, h), parts,
-                       (size_t)gridDim.x * lda);
-    const float c = (float)(1.0 / __builtin_sqrt((double)N));
-    tw_walsh<L, LE>(v, xs);
-    tw_to_natural<L, LE>(v, xs);
-#pragma unroll
-    for (int h = 0; h < NP; ++h) {
-        float sg[16], b[16], xv[16];
-        u16 xn[16];
-        cv16(sv0[h], sg);
-        if (bias) cv16(b0[h], b);
-        cv16(x0[h], xv);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            float a = (v[16 * h + k] * c) * sg[k];
-            if (bias) a = a + b[k];
-            xn[k] = f32_to_bf16(xv[k] + bf16_to_f32(f32_to_bf16(a)));
-            v[16 * h + k] = bf16_to_f32(xn[k]);
-        }
-        c16_store_bf16(xout + row + i0 + 16 * h, true, xn);
-        if (w) part[NP * t + h] = chunk_sumsq(part16(v, h));
-    }
-    if (!w) return;                                                    // uniform
-    __syncthreads();
-    const float ss = tree_total(part, red, N);
-    const float r = 1.f / __builtin_sqrtf(ss / (float)N + eps);
-#pragma unroll
-    for (int h = 0; h < NP; ++h) {
-        float wv[16], sn[16];
-        cv16(w0[h], wv);
-        cv16(su0[h], sn);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[16 * h + k] = bf16_to_f32(f32_to_bf16((v[16 * h + k] * r) * (1.f + wv[k]))) * sn[k];
-    }
-    tw_rotate_quantize<L, LE>(v, xs, red, q, q4, ldq, scale, tok);
+    const PanpArgs A{acc, s, rs, sv, bias, x, xout, w, su, lda, col0, parts, (size_t)gridDim.x * lda, eps};
+    float v[1 << LE];
+    if (!panp_tw<ADT, L, LE>(A, blockIdx.x, true, v, xs, xs + lds_words(1 << L), red)) return;   // uniform
+    tw_rotate_quantize<L, LE>(v, xs, red, q, q4, ldq, scale, blockIdx.x);
 }
 
 // =========================================================================================================== C ABI

@@ -2,6 +2,8 @@
 stream. Names and argument meaning follow the reference's launch helpers (deploy/tcq_kernels/kernels.py:572-696); the
 functions added here (rht, pre_h16, quantize_rows, repack, decode_f16, gemv_f16, ...) have no reference counterpart and say so.
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -520,6 +522,47 @@ class SmallProduct:
         if rc:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
+    def run_pro(self, pro):
+        """The product of one token whose INT8 activations come from the decoder-layer prologue `pro` (prologue()), run by
+        every workgroup of the same launch (tcq_gemm_tcq_pro / tcq_gemm_w8_pro); FP32 outputs only."""
+        if self.odt != 0:
+            raise ValueError('products with a prologue write FP32 z')
+        st, K = pro
+        if self.K is not None and K != self.K:
+            raise ValueError(f'the prologue row has {K} columns, the weights {self.K}')
+        for o, m in self.outs:
+            if o.storage_offset() + m > o.untyped_storage().nbytes() // o.element_size():
+                raise ValueError('an output buffer does not hold one row')
+        fn = getattr(_lib.lib(), self.name + '_pro')
+        rc = fn(self.arr, self.n, ctypes.byref(st), K, 0, self.ldo, stream())
+        if rc:
+            raise _lib.TcqError(f'{self.name}_pro failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
+
+
+def prologue(acc, s, rs, sv, x, xout, w, eps, su, q=None, scale=None, col0=0):
+    """The one-token decoder-layer prologue of a product (tcq_prologue in include/tcq_api.h): the arguments of
+    post_add_norm_pre for M = 1 with the norm and no bias. acc: the previous product's int32 sums, (1, lda) or K parts
+    (P, 1, lda); x, xout (1, K) BF16; q (1, K) int8 / scale (1,) FP32: optional copies of the INT8 row and its scale.
+    Returns (descriptor, K); keep the tensors alive until the launch has been issued."""
+    K = x.shape[1]
+    if x.shape[0] != 1 or xout.shape != x.shape:
+        raise ValueError('prologue: one token, x and xout (1, K)')
+    _bf16(x, 'prologue x'), _bf16(xout, 'prologue xout'), _bf16(w, 'prologue w')
+    _contig(acc, s, rs, sv, x, xout, w, su, q, scale)
+    if acc.dtype != torch.int32:
+        raise TypeError('prologue: int32 accumulators')
+    adt = 3
+    if acc.dim() == 3:
+        if acc.shape[0] not in K_PARTS or acc.shape[1] != 1:
+            raise ValueError(f'prologue: K parts must be (2 or 4, 1, lda), got {tuple(acc.shape)}')
+        adt |= K_PARTS[acc.shape[0]]
+    lda = acc.shape[-1]
+    if col0 < 0 or col0 + K > lda:
+        raise ValueError(f'prologue: columns {col0}..{col0 + K} exceed the accumulator width {lda}')
+    st = _lib.Prologue(ptr(acc), adt, lda, col0, ptr(s), ptr(rs), ptr(sv), None, ptr(x), ptr(xout), ptr(w), float(eps), ptr(su),
+                       ptr(q), ptr(scale))
+    return st, K
+
 
 def gemm_tcq_segments(segs, q, s, ldo, parts=1, dot=None):
     """One-shot fused decode + product over segments (see SmallProduct)."""
@@ -536,19 +579,23 @@ def gemm_w8_segments(segs, q, s, ldo, parts=1, dot=None):
 Z_W128T = 0x1000
 
 
-def gemm_tcq_w128t(segs, q, s, dot=None):
+def gemm_tcq_w128t(segs, q, s, dot=None, pro=None):
     """Fused decode + product of up to 4 segments [(words, t8, rs, zt), ...] at M <= 16 tokens whose FP32 z leaves the
     kernel after the first seven block-Walsh stages of each segment, block-transposed: zt (M, 128, m / 128) float32
-    (TCQ_Z_W128T in include/tcq_api.h). q: token blocks (M = s.numel()) or (M, K) rows; dot as SmallProduct. No reference
-    counterpart."""
+    (TCQ_Z_W128T in include/tcq_api.h). q: token blocks (M = s.numel()) or (M, K) rows; dot as SmallProduct. pro: one token
+    whose activations come from the decoder-layer prologue (prologue(); q and s unused). No reference counterpart."""
     arr = (_lib.GemmSeg * len(segs))()
-    M = s.numel()
+    M = 1 if pro is not None else s.numel()
     for i, (w, t8, rs, zt) in enumerate(segs):
         _contig(w, t8, rs, zt)
         m = rs.numel()
         if zt.dtype != torch.float32 or tuple(zt.shape) != (M, 128, m // 128):
             raise ValueError(f'segment {i}: zt must be ({M}, 128, {m // 128}) float32')
         arr[i] = _lib.GemmSeg(ptr(w), ptr(t8), ptr(rs), ptr(zt), m, 0 if _groups(t8) == 1 else m // _groups(t8))
+    if pro is not None:
+        st, K = pro
+        call('tcq_gemm_tcq_pro', arr, len(segs), ctypes.byref(st), K, 0 | Z_W128T, 128, stream())
+        return
     blocks = q.dim() == 4
     K = q.shape[1] * 16 if blocks else q.shape[1]
     _contig(q, s)

@@ -30,12 +30,14 @@ from . import tcq_format as F
 
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
-STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0)
+STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0,
+             layer_prologues=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
 # layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
-# (the first Walsh stages in the gate/up product, the rest in glu_split, then the down projection's pre) instead of mid2
-FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True)
+# (the first Walsh stages in the gate/up product, the rest in glu_split, then the down projection's pre) instead of mid2;
+# prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch
+FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -214,10 +216,20 @@ class Group:
             parts *= 2
         return parts
 
-    def product(self, b, parts=1):
+    def product(self, b, parts=1, pro=None):
         """INT8 activations -> FP32 z = (float(acc) * s) * rs (M, Ntot) of the exact int32 product acc: few tokens on the
         fused decode products, many tokens on the INT8 MFMA GEMM with the scaling in its epilogue (the order of tcq_post).
-        parts 2 / 4 (few tokens): the int32 K parts of acc instead, (parts, M, Ntot), for post_add_norm_pre."""
+        parts 2 / 4 (few tokens): the int32 K parts of acc instead, (parts, M, Ntot), for post_add_norm_pre. pro: one token
+        whose activations the decoder-layer prologue computes inside the product's launch (kernels.prologue; b unused)."""
+        if pro is not None:
+            dev = self.rs.device
+            z = torch.empty(1, self.Ntot, dtype=torch.float32, device=dev)
+            if self.W is not None:
+                segs = [(self.W[s.col0:s.col0 + s.width], None, s.rs, z[:, s.col0:]) for s in self.segments]
+            else:
+                segs = [(L.words(), L.t8, s.rs, z[:, s.col0:]) for L, s in zip(self.layers, self.segments)]
+            kernels.SmallProduct(segs, self.Ntot, resident=self.W is not None).run_pro(pro)
+            return z
         q = b['q'] if b['q'] is not None else b['q4']
         M, dev = b['scale'].numel(), q.device
         if parts > 1:
@@ -249,20 +261,23 @@ class Group:
         return (FUSE['spread'] and self.W is None and M <= 16 and self.K <= 4096 and self.N == [16384, 16384]
                 and not self.one_sided and self.col_scale is None and all(L.t8.dim() == 2 for L in self.layers))
 
-    def gated_middle(self, b, down, b2):
+    def gated_middle(self, b, down, b2, pro=None):
         """This gate | up group's product and the GeGLU middle (tcq_mid2's operations) into the down projection's quantized
-        input buffers b2: spread over many CUs when self.spreads(M), else one product launch and one mid2 launch."""
-        M, dev = b['scale'].numel(), b['scale'].device
+        input buffers b2: spread over many CUs when self.spreads(M), else one product launch and one mid2 launch. pro: one
+        token whose input the decoder-layer prologue computes inside the product (kernels.prologue; b None)."""
+        M, dev = (1, self.rs.device) if pro is not None else (b['scale'].numel(), b['scale'].device)
         if self.spreads(M):
-            q = b['q'] if b['q'] is not None else b['q4']
             zt = torch.empty(2, M, 128, 128, dtype=torch.float32, device=dev)
-            kernels.gemm_tcq_w128t([(L.words(), L.t8, s.rs, zt[i]) for i, (L, s) in enumerate(zip(self.layers, self.segments))],
-                                   q, b['scale'])
+            segs = [(L.words(), L.t8, s.rs, zt[i]) for i, (L, s) in enumerate(zip(self.layers, self.segments))]
+            if pro is not None:
+                kernels.gemm_tcq_w128t(segs, None, None, pro=pro)
+            else:
+                kernels.gemm_tcq_w128t(segs, b['q'] if b['q'] is not None else b['q4'], b['scale'])
             p = kernels.glu_split(zt, self.sv, kernels.gelu_table(dev), torch.empty(M, 16384, dtype=torch.bfloat16, device=dev))
             kernels.pre(p, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
             STATS['spread_middles'] += 1
             return
-        acc = self.product(b)
+        acc = self.product(b, pro=pro)
         s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], self.rs)
         kernels.mid2(acc, s_tok, rs, self.sv, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
 
@@ -449,6 +464,16 @@ class KDecoderLayer(torch.nn.Module):
         return b if (not x2.is_inference() and x2._version == ver) else None
 
     @staticmethod
+    def _prologue_fits(z, og, gu):
+        """Whether the o epilogue + residual + norm2 + rotate + quantize can run as the prologue of the gate | up product
+        (tcq_gemm_tcq_pro): one token, int32 sums, a two-sided o projection without bias, 2048-wide rows, and a gate | up
+        group on the spread middle (256 workgroups, one per CU, so each CU runs the prologue once). Measured on MI355X at
+        one token: fly 18.1 -> 17.2 us for the two launches' work; on the resident plan's 1024 workgroups the prologue
+        runs four times per CU and the pair gets slower (1.50 -> 1.72 ms per decode token), so it is not used there."""
+        return (FUSE['prologue'] and z.dtype == torch.int32 and z.shape[-2] == 1 and og.bias is None and not og.one_sided
+                and og.Ntot == 2048 and gu.K == 2048 and gu.a8 and gu.spreads(1))
+
+    @staticmethod
     def _unscaled(acc, b, group):
         """(token scales, row scales) the epilogue applies to acc: none for FP32 z, else the quantizer's and the group's."""
         return (None, None) if acc.dtype == torch.float32 else (b['scale'], group.rs)
@@ -476,11 +501,17 @@ class KDecoderLayer(torch.nn.Module):
             b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
         z = og.product(b2, og.k_parts(M))
         x3 = torch.empty_like(x2)
-        b3 = gu.buffers(M, dev)
-        kernels.post_add_norm_pre(z, *self._unscaled(z, b2, og), og.sv, og.bias, x2, x3, n2.weight, n2.eps, gu.su, q=b3['q'],
-                                  q4=b3['q4'], scale=b3['scale'])
         b4 = dn.buffers(M, dev)
-        gu.gated_middle(b3, dn, b4)
+        if self._prologue_fits(z, og, gu):
+            # one token: the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
+            pro = kernels.prologue(z, b2['scale'], og.rs, og.sv, x2, x3, n2.weight, n2.eps, gu.su)
+            gu.gated_middle(None, dn, b4, pro=pro)
+            STATS['layer_prologues'] += 1
+        else:
+            b3 = gu.buffers(M, dev)
+            kernels.post_add_norm_pre(z, *self._unscaled(z, b2, og), og.sv, og.bias, x2, x3, n2.weight, n2.eps, gu.su, q=b3['q'],
+                                      q4=b3['q4'], scale=b3['scale'])
+            gu.gated_middle(b3, dn, b4)
         z4 = dn.product(b4, dn.k_parts(M))
         x4 = torch.empty_like(x2)
         nxt = self._next[0] if (self._next and FUSE['chain']) else None
