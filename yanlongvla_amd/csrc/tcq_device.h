@@ -445,10 +445,10 @@ __device__ __forceinline__ void tw_to_natural2(float (&a)[1 << LE], float (&b)[1
 // v / s, rounded half-even, clamped. The quotient: for a scale in [2^-90, 2^90] (every row whose largest magnitude is a
 // normal value far from overflow), q = v * (1 / s) with two Markstein corrections q += (v - q s) / s, the residuals exact
 // through fused multiply-adds: with a correctly rounded reciprocal, the first correction brings q within one ulp and the
-// second gives the correctly rounded quotient (Markstein's theorem) wherever nothing underflows, i.e. for every |v / s|
-// that can round to a nonzero integer (quotients below 2^-24 s / s may differ in their last bits and still round to 0).
-// Checked against IEEE division on the CPU over every FP32 v of a row at six scales and 2e7 near-tie pairs. Other scales
-// (tiny or huge rows, infinities) divide.
+// second gives the correctly rounded quotient (Markstein's theorem) wherever nothing underflows; near the bottom of the
+// scale range the residual of a quotient below 2^-12 can underflow, and such a quotient rounds to 0 either way. Checked
+// against IEEE division on the host over every FP32 v of a row at six scales and 1.6e8 near-tie pairs (no rounded integer
+// differs; tests/native/quotient_check.c). Other scales (tiny or huge rows, infinities) divide.
 struct QScale {
     float s, rcp;
     bool fast;
