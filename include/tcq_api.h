@@ -356,10 +356,11 @@ int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const floa
 int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                 tcq_stream_t stream);
 
-/* Decoder-layer prologue of a one-token product: the arguments of tcq_post_add_norm_pre for M = 1 with the norm (acc the
- * previous product's int32 sums, acc_dtype TCQ_I32, optionally | TCQ_K_PARTS2 / TCQ_K_PARTS4 with part p at acc + p * lda;
- * s, rs, sv, bias its epilogue; x, xout the residual; w, eps the RMSNorm; su the signs of the product that follows) and
- * optional copies of the INT8 row (q, K bytes) and its scale. */
+/* Prologue of a one-token product, two forms. With acc: the arguments of tcq_post_add_norm_pre for M = 1 with the norm
+ * (acc the previous product's int32 sums, acc_dtype TCQ_I32, optionally | TCQ_K_PARTS2 / TCQ_K_PARTS4 with part p at
+ * acc + p * lda; s, rs, sv, bias its epilogue; x, xout the residual; w, eps the RMSNorm; su the signs of the product that
+ * follows). Without acc (NULL): tcq_pre of the BF16 row x with signs su (every other input unused). Both may write copies
+ * of the INT8 row (q, K bytes) and its scale (scale: the token scale a later epilogue of int32 sums needs). */
 typedef struct {
     const void* acc;
     int acc_dtype;
@@ -377,11 +378,13 @@ typedef struct {
     float* scale;
 } tcq_prologue;
 
-/* tcq_post_add_norm_pre(pro..., M = 1, N = K) followed by tcq_gemm_tcq / tcq_gemm_w8 of its INT8 row, in one launch: every
- * workgroup computes the prologue's row itself (the same operations, bit for bit) and multiplies it, so the row never
- * leaves the chip and the chain loses a launch. K = 2048 and bias NULL (TCQ_ERR_UNSUPPORTED otherwise), out_dtype TCQ_F32
- * (tcq_gemm_tcq: optionally | TCQ_Z_W128T), 16-byte aligned operands. No reference counterpart: the reference runs the epilogue, the
- * residual add, the norm and the quantizer as separate steps (kernels.py:208-230; the norm in PyTorch). */
+/* The prologue (tcq_post_add_norm_pre(pro..., M = 1, N = K), or tcq_pre(x, TCQ_BF16, su, ..., M = 1, K)) followed by
+ * tcq_gemm_tcq / tcq_gemm_w8 of its INT8 row, in one launch: every workgroup computes the row itself (the same operations,
+ * bit for bit) and multiplies it, so the row never leaves the chip and the chain loses a launch. Supported: with acc,
+ * K = 2048, bias NULL, out_dtype TCQ_F32 (tcq_gemm_tcq: optionally | TCQ_Z_W128T); without acc, K = 16384, out_dtype
+ * TCQ_I32 (optionally | TCQ_K_PARTS2); else TCQ_ERR_UNSUPPORTED. 16-byte aligned operands. No reference counterpart: the
+ * reference runs the epilogue, the residual add, the norm and the quantizer as separate steps (kernels.py:208-230; the
+ * norm in PyTorch). */
 int tcq_gemm_tcq_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo, tcq_stream_t stream);
 int tcq_gemm_w8_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo, tcq_stream_t stream);
 

@@ -217,11 +217,13 @@ def test_chained_prologues_bitexact(part):
 
 
 @pytest.mark.parametrize('runtime', ['fly', 'resident'])
-def test_layer_prologue_in_the_gate_up_product_bitexact(runtime):
+@pytest.mark.parametrize('flag,stat', [('prologue', 'layer_prologues'), ('pre_prologue', 'pre_prologues')])
+def test_prologues_in_the_mlp_products_bitexact(runtime, flag, stat):
     """At one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
-    (FUSE['prologue']): a 3-layer backbone's decode steps give the hidden states and key / value rows of the separate
-    launch bit for bit, and the fused form is taken at every layer of every step on the fly runtime's spread middle (the
-    resident runtime keeps the separate launch)."""
+    (FUSE['prologue']), and the down projection's rotate + quantize inside the down product's (FUSE['pre_prologue']): a
+    3-layer backbone's decode steps give the hidden states and key / value rows of the separate launches bit for bit, and
+    each fused form is taken at every layer of every step on the fly runtime's spread middle (the resident runtime keeps
+    the separate launches)."""
     from yanlongvla_amd import gemma, modules
     model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
     modules.install(model, runtime=runtime, layers=gemma.synthetic_layers(model, 15, DEV))
@@ -229,16 +231,16 @@ def test_layer_prologue_in_the_gate_up_product_bitexact(runtime):
     _, ks, vs = model.prefill(x)
     outs, taken = {}, {}
     for fuse in (False, True):
-        modules.FUSE['prologue'] = fuse
+        modules.FUSE[flag] = fuse
         try:
-            before = modules.STATS['layer_prologues']
+            before = modules.STATS[stat]
             k2, v2, outs[fuse] = ks, vs, []
             for t in range(2):
                 h, k2, v2 = model.decode_step(x[t:t + 1], k2, v2)
                 outs[fuse] += [h] + list(k2) + list(v2)
-            taken[fuse] = modules.STATS['layer_prologues'] - before
+            taken[fuse] = modules.STATS[stat] - before
         finally:
-            modules.FUSE['prologue'] = True
+            modules.FUSE[flag] = True
     assert taken == {False: 0, True: 2 * 3 if runtime == 'fly' else 0}
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)

@@ -1,9 +1,11 @@
-"""GPU tests of the one-token products that run the decoder-layer prologue in their own launch (tcq_gemm_tcq_pro /
-tcq_gemm_w8_pro): every output equals, bit for bit, tcq_post_add_norm_pre followed by the plain product on its INT8 row
-(the residual output, the INT8 row and scale copies, the FP32 z or the stage-split zt). Plans: the workgroup plan with one
-and two tile rows per workgroup, the streaming plan at 8 / 4 / 2 / 1 waves per tile row, the stage-split gate | up output;
-the accumulators in one, two and four K parts. tcq_post_add_norm_pre itself is pinned against the oracle in
-test_gpu_norms.py and test_gpu_backbone_oracle.py."""
+"""GPU tests of the one-token products that run their activations' prologue in their own launch (tcq_gemm_tcq_pro /
+tcq_gemm_w8_pro): every output equals, bit for bit, the standalone prologue kernel followed by the plain product on its
+INT8 row. The decoder-layer prologue (tcq_post_add_norm_pre, 2048 wide): the residual output, the INT8 row and scale
+copies, the FP32 z or the stage-split zt; the workgroup plan with one and two tile rows per workgroup, the streaming plan at
+8 / 4 / 2 / 1 waves per tile row, the stage-split gate | up output; accumulators in one, two and four K parts. The rotate +
+quantize prologue (tcq_pre, 16384 wide): int32 sums in one and two K parts on the streaming plan (fused decode) and the
+workgroup plan (INT8-resident weights). The standalone kernels are pinned against the oracle in test_gpu_norms.py,
+test_gpu_kernels.py and test_gpu_backbone_oracle.py."""
 import numpy as np
 import pytest
 import torch
@@ -118,14 +120,17 @@ def test_stage_split_middle_with_prologue(parts):
 
 
 def test_prologue_refusals():
-    """Rows other than 2048 wide and non-FP32 outputs are refused before any launch."""
+    """Layer prologues of rows other than 2048 wide or with int32 outputs, and rotate + quantize prologues of rows other
+    than 16384 wide, are refused before any launch."""
     from yanlongvla_amd import kernels as Kn, _lib
     a = prologue_inputs(2, 5)
     z = torch.empty(1, 256, dtype=torch.int32, device=DEV)
     segs = segments([256], False, 3, [z])
     pro, _, _, _ = pro_of(a)
-    with pytest.raises(ValueError):                                   # int32 outputs
+    with pytest.raises(_lib.TcqError):                                # int32 outputs after the layer prologue
         Kn.SmallProduct(segs, 256).run_pro(pro)
+    with pytest.raises(_lib.TcqError):                                # a 2048-wide rotate + quantize prologue
+        Kn.SmallProduct(segs, 256).run_pro(Kn.prologue_pre(a['x'], a['su']))
     z = torch.empty(1, 256, device=DEV)
     g = torch.Generator(device=DEV).manual_seed(1)
     x = torch.randn(1, 1024, generator=g, device=DEV).bfloat16()
@@ -134,3 +139,32 @@ def test_prologue_refusals():
     w = torch.randint(-127, 128, (256, 1024), generator=g, device=DEV, dtype=torch.int8)
     with pytest.raises(_lib.TcqError):                                # K = 1024: no variant
         Kn.SmallProduct([(w, None, segs[0][2], z)], 256, resident=True).run_pro(pro1024)
+
+
+@pytest.mark.parametrize('resident,parts', [(False, 2), (False, 1), (True, 2), (True, 1)])
+def test_product_with_rotate_quantize_prologue(resident, parts):
+    """tcq_pre of a 16384-wide BF16 row inside the down projection's one-token product (2048 x 16384): the int32 sums, the
+    INT8 row and the scale equal tcq_pre followed by the product."""
+    from yanlongvla_amd import kernels as Kn
+    Kd, m = 16384, 2048
+    g = torch.Generator(device=DEV).manual_seed(40 + parts + 2 * resident)
+    x = torch.randn(1, Kd, generator=g, device=DEV).bfloat16()
+    su = signs(g, Kd)
+    rs = torch.rand(m, generator=g, device=DEV) * 1e-3
+    if resident:
+        w, t8 = torch.randint(-127, 128, (m, Kd), generator=g, device=DEV, dtype=torch.int8), None
+    else:
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (Kn.repack_words(m, Kd),), generator=g, device=DEV, dtype=torch.int32)
+        t8 = torch.randint(-127, 128, (512, 2), generator=g, device=DEV, dtype=torch.int8)
+    q = torch.empty(1, Kd, dtype=torch.int8, device=DEV)
+    sc = torch.empty(1, device=DEV)
+    Kn.pre(x, su, q=q, scale=sc)
+    a_ref = torch.full((parts, 1, m), -5, dtype=torch.int32, device=DEV)
+    Kn.SmallProduct([(w, t8, rs, a_ref[0])], m, resident=resident)(q, sc, parts)
+    q2 = torch.zeros_like(q)
+    sc2 = torch.zeros_like(sc)
+    a_pro = torch.full((parts, 1, m), -7, dtype=torch.int32, device=DEV)
+    Kn.SmallProduct([(w, t8, rs, a_pro[0])], m, resident=resident).run_pro(Kn.prologue_pre(x, su, q=q2, scale=sc2), parts)
+    torch.cuda.synchronize()
+    assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(bits(sc2), bits(sc))
+    assert torch.equal(a_pro.cpu(), a_ref.cpu())

@@ -75,6 +75,14 @@ struct SegPackPro {
 template <int PL> struct PackOf { typedef SegPackPro type; };
 template <> struct PackOf<0> { typedef SegPack type; };
 
+// Prologues by row width 2^PL: PL = 11, the decoder-layer prologue of a 2048-wide row (tcq_post_add_norm_pre's
+// operations, 16 values per thread); PL = 14, the rotate + quantize of a 16384-wide BF16 row (tcq_pre's operations, 32
+// values per thread). Both on the register + transpose engine, as the standalone kernels run them.
+template <int PL> struct ProShape {
+    static_assert(PL == 11 || PL == 14, "prologue widths: 2048 (layer prologue), 16384 (rotate + quantize)");
+    static constexpr int LE = PL == 11 ? 4 : 5;
+};
+
 // LDS of the prologue of a 2^PL-wide row: the Walsh engine's row, the chunk sums, the reduction slots, the INT8 row and its
 // scale (the product's activations).
 template <int PL>
@@ -91,10 +99,12 @@ struct ProLds {
 // weight loads once the prologue's accumulator registers are free, so their HBM latency runs under the prologue.
 template <int PL, class F>
 __device__ __forceinline__ void run_prologue(const SegPackPro& P, ProLds<PL>& L, F&& mid) {
+    constexpr int LE = ProShape<PL>::LE;
     const bool store = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
-    float v[16];
-    panp_tw<TCQ_I32, PL, 4, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
-    tw_rotate_quantize<PL, 4>(v, L.xs, L.red, store ? P.q : nullptr, nullptr, 0, store ? P.scale : nullptr, 0, L.qs, &L.sc);
+    float v[1 << LE];
+    if constexpr (PL == 11) panp_tw<TCQ_I32, PL, LE, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
+    else pre_row_tw<PL, LE>(P.a.x, P.a.su, v, mid);
+    tw_rotate_quantize<PL, LE>(v, L.xs, L.red, store ? P.q : nullptr, nullptr, 0, store ? P.scale : nullptr, 0, L.qs, &L.sc);
 }
 
 // Activation layouts of the small-M products: q (M, K) row-major, the token-block layout, or the reference's q4 (K/4, ldq)
@@ -107,8 +117,8 @@ enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
 // dtype (F32 scaled, BF16 scaled, I32 accumulators). QL: activation layout (ldq only for QL_WORDS).
 // KS > 1 (I32 only): K parts, blockIdx.z = part p takes chunks [p * ceil(nch / KS), ...) and writes at out + p * M * ldz.
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
-// PL > 0 (M == 1, K = 2^PL, int32 K-part accumulators in): the activations come from the decoder-layer prologue run by
-// every workgroup (run_prologue) instead of q / s.
+// PL > 0 (M == 1, K = 2^PL): the activations come from the prologue run by every workgroup (run_prologue, ProShape)
+// instead of q / s.
 template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false, int PL = 0>
 __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typename PackOf<PL>::type P, const i8* q, const float* s,
                                                                     int M, int K, int ldz, int ldq) {
@@ -314,7 +324,7 @@ constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table 
 // stages of the block Walsh of the whole segment (h = 1 .. 64, which stay inside such a block) run here, in the reference's
 // stage order, and the block is stored transposed: zt[(t * 128 + o) * (m / 128) + blk] for row 128 blk + o of token t.
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
-// PL > 0: activations from the decoder-layer prologue, as k_gemm_small.
+// PL > 0: activations from the prologue, as k_gemm_small.
 template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false, int PL = 0>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>::type P, const i8* q, const float* s, int M, int K,
                                                       int ldz) {
@@ -337,7 +347,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
     const u32 cp4 = (u32)(lane & (GV_C - 1)) << 2;
     const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch_all) << 10);
     const rsrc_t Q = make_rsrc(q, QB ? 16u * (u32)K : (u32)M * (u32)K);
-    constexpr int CM = PL ? ((1 << PL) / 256 + WPR - 1) / WPR : GV_CMAX;   // chunks per wave at most (K = 2^PL: known)
+    constexpr int CM = PL ? (((1 << PL) / 256 + KS - 1) / KS + WPR - 1) / WPR : GV_CMAX;   // chunks per wave (K = 2^PL)
     uint4_t wa[CM];
     auto loadW = [&] {
 #pragma unroll
@@ -681,82 +691,115 @@ extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, 
 }
 
 // ------------------------------------------------------------------------------------ products with the layer prologue
-// One token: every workgroup first runs tcq_post_add_norm_pre's operations on the previous product's int32 sums (the
-// register + transpose engine of its 2048-wide path, bit for bit), then its share of the product on the INT8 row it left in
-// LDS; workgroup (0, 0, 0) stores xout (and the optional q / scale copies). Plans as gemm_small picks them for M = 1:
-// the stage-split output (TCQ_Z_W128T), the streaming plan, or the workgroup plan with one or two tile rows.
-constexpr int PRO_L = 11;
+// One token: every workgroup first computes the product's INT8 row itself, on the same register + transpose engine as the
+// standalone kernels and bit for bit, then its share of the product on that row (LDS); workgroup (0, 0, 0) stores the
+// row's side outputs (xout, and the optional q / scale copies). Two prologues (ProShape): with acc, tcq_post_add_norm_pre's
+// operations on a 2048-wide row (FP32 z out, optionally the stage-split TCQ_Z_W128T form); without acc, tcq_pre's on a
+// 16384-wide BF16 row x (int32 sums out, optionally in K parts). Plans as gemm_small picks them for M = 1.
 static bool pal16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int MODE, int PL, int ODT, int KS>
+static void launch_pro_small(int rows, int nseg, int nw, bool pairs, hipStream_t st, const SegPackPro& P, int K, int ldo) {
+    const i8* nq = nullptr;
+    const float* ns = nullptr;
+    if constexpr (PL == 11) {
+        if (pairs) {
+            launch_k(k_gemm_small<MODE, 1, ODT, 2, QL_ROWS, false, KS, false, PL>, dim3((rows + 1) / 2, nseg, KS), dim3(64 * nw), 0, st,
+                     P, nq, ns, 1, K, ldo, 0);
+            return;
+        }
+    }
+    launch_k(k_gemm_small<MODE, 1, ODT, 1, QL_ROWS, false, KS, false, PL>, dim3(rows, nseg, KS), dim3(64 * nw), 0, st, P, nq, ns, 1, K,
+             ldo, 0);
+}
 
 template <int MODE>
 static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pr, int K, int odt, int ldo, tcq_stream_t stream) {
     if (!segs || !pr || nseg <= 0 || ldo <= 0) return TCQ_ERR_ARG;
+    if (nseg > TCQ_MAX_SEGS) return TCQ_ERR_UNSUPPORTED;
+    const bool layer = pr->acc != nullptr;                             // the decoder-layer prologue, else rotate + quantize
     const bool w128 = odt & TCQ_Z_W128T;
-    odt &= ~TCQ_Z_W128T;
-    if (odt != TCQ_F32 || (w128 && MODE != 0)) return TCQ_ERR_UNSUPPORTED;
-    if (K != (1 << PRO_L)) return TCQ_ERR_UNSUPPORTED;
-    int adt = pr->acc_dtype;
-    if ((adt & TCQ_K_PARTS2) && (adt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
-    const int parts = (adt & TCQ_K_PARTS4) ? 4 : (adt & TCQ_K_PARTS2) ? 2 : 1;
-    adt &= ~(TCQ_K_PARTS2 | TCQ_K_PARTS4);
-    if (adt != TCQ_I32) return TCQ_ERR_DTYPE;
-    if (!pr->acc || !pr->s || !pr->rs || !pr->sv || !pr->x || !pr->xout || !pr->w || !pr->su || pr->col0 < 0 || pr->lda < pr->col0 + K)
-        return TCQ_ERR_ARG;
-    if (pr->bias) return TCQ_ERR_UNSUPPORTED;
-    if ((size_t)parts * pr->lda >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
-    if (!pal16(pr->acc) || pr->lda % 4 || pr->col0 % 4 || !pal16(pr->rs) || !pal16(pr->sv) || !pal16(pr->x) || !pal16(pr->xout) ||
-        !pal16(pr->w) || !pal16(pr->su) || (pr->bias && !pal16(pr->bias)) || (pr->q && !pal16(pr->q)) || ldo % 4)
-        return TCQ_ERR_ALIGN;
+    if ((odt & TCQ_K_PARTS2) && (odt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
+    const int parts = (odt & TCQ_K_PARTS4) ? 4 : (odt & TCQ_K_PARTS2) ? 2 : 1;
+    odt &= ~(TCQ_Z_W128T | TCQ_K_PARTS2 | TCQ_K_PARTS4);
+    if (layer ? (K != 2048 || odt != TCQ_F32 || parts > 1 || (w128 && MODE != 0))
+              : (K != 16384 || odt != TCQ_I32 || parts > 2 || w128))
+        return TCQ_ERR_UNSUPPORTED;
+    if (!pr->x || !pr->su) return TCQ_ERR_ARG;
+    int pparts = 1;
+    if (layer) {
+        int adt = pr->acc_dtype;
+        if ((adt & TCQ_K_PARTS2) && (adt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
+        pparts = (adt & TCQ_K_PARTS4) ? 4 : (adt & TCQ_K_PARTS2) ? 2 : 1;
+        adt &= ~(TCQ_K_PARTS2 | TCQ_K_PARTS4);
+        if (adt != TCQ_I32) return TCQ_ERR_DTYPE;
+        if (!pr->s || !pr->rs || !pr->sv || !pr->xout || !pr->w || pr->col0 < 0 || pr->lda < pr->col0 + K) return TCQ_ERR_ARG;
+        if (pr->bias) return TCQ_ERR_UNSUPPORTED;
+        if ((size_t)pparts * pr->lda >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
+        if (!pal16(pr->acc) || pr->lda % 4 || pr->col0 % 4 || !pal16(pr->rs) || !pal16(pr->sv) || !pal16(pr->xout) || !pal16(pr->w))
+            return TCQ_ERR_ALIGN;
+    }
+    if (!pal16(pr->x) || !pal16(pr->su) || (pr->q && !pal16(pr->q)) || ldo % 4) return TCQ_ERR_ALIGN;
+    if (parts > 1 && (size_t)parts * ldo >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     SegPackPro P = {};
     int max_m = 0, tiles = 0;
-    for (int i = 0; i < nseg && i < TCQ_MAX_SEGS; ++i) {
+    for (int i = 0; i < nseg; ++i) {
         const tcq_gemm_seg& g = segs[i];
-        if (!g.w || !g.out || (MODE == 0 && !g.t8) || !g.rs || g.m <= 0) return TCQ_ERR_ARG;
+        if (!g.w || !g.out || (MODE == 0 && !g.t8) || (odt != TCQ_I32 && !g.rs) || g.m <= 0) return TCQ_ERR_ARG;
         if (g.m % 16) return TCQ_ERR_SHAPE;
         if (g.rows_per_table < 0 || (g.rows_per_table > 0 && (g.rows_per_table % 16 || g.m % g.rows_per_table))) return TCQ_ERR_SHAPE;
         if ((size_t)g.m * K >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
-        if ((uintptr_t)g.out % 16 || (uintptr_t)g.rs % 16) return TCQ_ERR_ALIGN;
+        if ((uintptr_t)g.out % 16 || (g.rs && (uintptr_t)g.rs % 16)) return TCQ_ERR_ALIGN;
         if (w128 && (g.m % 128 || (g.rows_per_table > 0 && g.rows_per_table % 128))) return TCQ_ERR_SHAPE;
         P.s[i] = g;
         max_m = g.m > max_m ? g.m : max_m;
         tiles += g.m / 16;
     }
-    if (nseg > TCQ_MAX_SEGS) return TCQ_ERR_UNSUPPORTED;
-    P.a = PanpArgs{pr->acc, pr->s, pr->rs, (const i8*)pr->sv, pr->bias, (const u16*)pr->x, (u16*)pr->xout, (const u16*)pr->w,
-                   (const i8*)pr->su, pr->lda, pr->col0, parts, (size_t)pr->lda, pr->eps};
+    P.a = PanpArgs{pr->acc, pr->s, pr->rs, (const i8*)pr->sv, nullptr, (const u16*)pr->x, (u16*)pr->xout, (const u16*)pr->w,
+                   (const i8*)pr->su, pr->lda, pr->col0, pparts, (size_t)pr->lda, pr->eps};
     P.q = (i8*)pr->q;
     P.scale = pr->scale;
     hipStream_t st = (hipStream_t)stream;
-    const int nch = K / 256, nw = nch < SM_MAXW ? nch : SM_MAXW;
-    if (w128) {
-        launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, PRO_L>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P,
-                 (const i8*)nullptr, (const float*)nullptr, 1, K, ldo);
-        return launch_status();
-    }
-    const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nch, tiles) : 0;
-    if (wpr > 0) {
-        const dim3 grid((max_m / 16 + GV_NW / wpr - 1) / (GV_NW / wpr), nseg), block(64 * GV_NW);
-#define GVP(W) launch_k(k_gemv_tcq<TCQ_F32, false, W, GV_NW, 1, false, false, PRO_L>, grid, block, 0, st, P, (const i8*)nullptr, \
-                        (const float*)nullptr, 1, K, ldo)
-        switch (wpr) {
-            case 1: GVP(1); break;
-            case 2: GVP(2); break;
-            case 4: GVP(4); break;
-            case 8: GVP(8); break;
-            default: GVP(16); break;
+    const i8* nq = nullptr;
+    const float* ns = nullptr;
+    const int nch = K / 256, nchp = (nch + parts - 1) / parts, nw = nchp < SM_MAXW ? nchp : SM_MAXW;
+    if (layer) {
+        if (w128) {
+            launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, 11>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P, nq,
+                     ns, 1, K, ldo);
+            return launch_status();
         }
+        const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nch, tiles) : 0;
+        if (wpr > 0) {
+            const dim3 grid((max_m / 16 + GV_NW / wpr - 1) / (GV_NW / wpr), nseg), block(64 * GV_NW);
+#define GVP(W) launch_k(k_gemv_tcq<TCQ_F32, false, W, GV_NW, 1, false, false, 11>, grid, block, 0, st, P, nq, ns, 1, K, ldo)
+            switch (wpr) {
+                case 1: GVP(1); break;
+                case 2: GVP(2); break;
+                case 4: GVP(4); break;
+                case 8: GVP(8); break;
+                default: GVP(16); break;
+            }
 #undef GVP
+            return launch_status();
+        }
+        bool pairs = nw <= 8 && tiles >= 384;
+        for (int i = 0; i < nseg; ++i)
+            if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
+        launch_pro_small<MODE, 11, TCQ_F32, 1>(max_m / 16, nseg, nw, pairs, st, P, K, ldo);
         return launch_status();
     }
-    bool pairs = nw <= 8 && tiles >= 384;
-    for (int i = 0; i < nseg; ++i)
-        if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
-    if (pairs)
-        launch_k(k_gemm_small<MODE, 1, TCQ_F32, 2, QL_ROWS, false, 1, false, PRO_L>, dim3((max_m / 16 + 1) / 2, nseg), dim3(64 * nw), 0,
-                 st, P, (const i8*)nullptr, (const float*)nullptr, 1, K, ldo, 0);
-    else
-        launch_k(k_gemm_small<MODE, 1, TCQ_F32, 1, QL_ROWS, false, 1, false, PRO_L>, dim3(max_m / 16, nseg), dim3(64 * nw), 0, st, P,
-                 (const i8*)nullptr, (const float*)nullptr, 1, K, ldo, 0);
+    // rotate + quantize prologue, int32 sums: the streaming plan at 16 waves per tile row (the 2048 x 16384 down projection),
+    // else the workgroup plan with one tile row per workgroup
+    const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nchp, tiles * parts) : 0;
+    if (wpr == 16) {
+        const dim3 grid(max_m / 16, nseg, parts), block(64 * GV_NW);
+        if (parts == 2) launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 2, false, false, 14>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
+        else launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 1, false, false, 14>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
+        return launch_status();
+    }
+    if (parts == 2) launch_pro_small<MODE, 14, TCQ_I32, 2>(max_m / 16, nseg, nw, false, st, P, K, ldo);
+    else launch_pro_small<MODE, 14, TCQ_I32, 1>(max_m / 16, nseg, nw, false, st, P, K, ldo);
     return launch_status();
 }
 

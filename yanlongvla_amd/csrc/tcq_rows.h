@@ -238,3 +238,33 @@ __device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, 
     }
     return true;
 }
+
+// The rotate + quantize input of a BF16 row (tcq_pre's first steps): thread t's 2^LE contiguous values x[2^LE t ..] * su,
+// as FP32 in v (natural layout, ready for tw_rotate_quantize). Threads from 2^(L - LE) on hold no values (zeros). mid()
+// runs once the loaded words have been consumed.
+template <int L, int LE, class F = NoMid>
+__device__ __forceinline__ void pre_row_tw(const u16* x, const i8* su, float (&v)[1 << LE], F&& mid = NoMid{}) {
+    constexpr int E = 1 << LE;
+    const int t = threadIdx.x, i0 = E * t;
+    const bool on = t < (1 << (L - LE));
+    Raw16<1> s0[E / 16];
+    uint4_t raw[E / 8];
+    if (on) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) s0[h] = raw16<1>(su + i0 + 16 * h, true);
+#pragma unroll
+        for (int j = 0; j < E / 8; ++j) raw[j] = gptr((const uint4_t*)(x + i0))[j];
+    }
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = on ? bf16_to_f32((u16)(raw[k >> 3][(k & 7) >> 1] >> (16 * (k & 1)))) : 0.f;
+    if (on) {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h) {
+            float sg[16];
+            cv16(s0[h], sg);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[16 * h + k] = v[16 * h + k] * sg[k];
+        }
+    }
+    mid();
+}

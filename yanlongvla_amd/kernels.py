@@ -522,19 +522,20 @@ class SmallProduct:
         if rc:
             raise _lib.TcqError(f'{self.name} failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
-    def run_pro(self, pro):
-        """The product of one token whose INT8 activations come from the decoder-layer prologue `pro` (prologue()), run by
-        every workgroup of the same launch (tcq_gemm_tcq_pro / tcq_gemm_w8_pro); FP32 outputs only."""
-        if self.odt != 0:
-            raise ValueError('products with a prologue write FP32 z')
+    def run_pro(self, pro, parts=1):
+        """The product of one token whose INT8 activations come from the prologue `pro` (prologue() / prologue_pre()), run by
+        every workgroup of the same launch (tcq_gemm_tcq_pro / tcq_gemm_w8_pro): FP32 z after the layer prologue, int32
+        sums (optionally in K parts) after the rotate + quantize one."""
         st, K = pro
         if self.K is not None and K != self.K:
             raise ValueError(f'the prologue row has {K} columns, the weights {self.K}')
+        if parts != 1 and (parts not in K_PARTS or self.odt != 3):
+            raise ValueError('K parts: 2 or 4, int32 outputs only')
         for o, m in self.outs:
-            if o.storage_offset() + m > o.untyped_storage().nbytes() // o.element_size():
-                raise ValueError('an output buffer does not hold one row')
+            if o.storage_offset() + (parts - 1) * self.ldo + m > o.untyped_storage().nbytes() // o.element_size():
+                raise ValueError(f'an output buffer does not hold {parts} rows of stride {self.ldo}')
         fn = getattr(_lib.lib(), self.name + '_pro')
-        rc = fn(self.arr, self.n, ctypes.byref(st), K, 0, self.ldo, stream())
+        rc = fn(self.arr, self.n, ctypes.byref(st), K, self.odt | (K_PARTS[parts] if parts > 1 else 0), self.ldo, stream())
         if rc:
             raise _lib.TcqError(f'{self.name}_pro failed: {_lib.STATUS.get(rc, f"HIP error {rc}")} (status {rc})')
 
@@ -562,6 +563,17 @@ def prologue(acc, s, rs, sv, x, xout, w, eps, su, q=None, scale=None, col0=0):
     st = _lib.Prologue(ptr(acc), adt, lda, col0, ptr(s), ptr(rs), ptr(sv), None, ptr(x), ptr(xout), ptr(w), float(eps), ptr(su),
                        ptr(q), ptr(scale))
     return st, K
+
+
+def prologue_pre(x, su, q=None, scale=None):
+    """The rotate + quantize prologue of a one-token product (tcq_prologue without acc): tcq_pre of the (1, K) BF16 row x
+    with signs su; q (1, K) int8 / scale (1,) FP32: optional copies of the INT8 row and its scale. Returns (descriptor, K)."""
+    if x.dim() != 2 or x.shape[0] != 1:
+        raise ValueError('prologue_pre: one token, x (1, K)')
+    _bf16(x, 'prologue_pre x')
+    _contig(x, su, q, scale)
+    st = _lib.Prologue(None, 3, 0, 0, None, None, None, None, ptr(x), None, None, 0.0, ptr(su), ptr(q), ptr(scale))
+    return st, x.shape[1]
 
 
 def gemm_tcq_segments(segs, q, s, ldo, parts=1, dot=None):

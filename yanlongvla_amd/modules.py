@@ -31,13 +31,15 @@ from . import tcq_format as F
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
 STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0,
-             layer_prologues=0)
+             layer_prologues=0, pre_prologues=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
 # layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
 # (the first Walsh stages in the gate/up product, the rest in glu_split, then the down projection's pre) instead of mid2;
-# prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch
-FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True)
+# prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch;
+# pre_prologue: after the spread middle the down projection's rotate + quantize runs inside its product's launch
+FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True,
+            pre_prologue=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -221,15 +223,18 @@ class Group:
         fused decode products, many tokens on the INT8 MFMA GEMM with the scaling in its epilogue (the order of tcq_post).
         parts 2 / 4 (few tokens): the int32 K parts of acc instead, (parts, M, Ntot), for post_add_norm_pre. pro: one token
         whose activations the decoder-layer prologue computes inside the product's launch (kernels.prologue; b unused)."""
-        if pro is not None:
+        if pro is not None:                       # FP32 z after the layer prologue, int32 sums after the rotate + quantize one
             dev = self.rs.device
-            z = torch.empty(1, self.Ntot, dtype=torch.float32, device=dev)
+            layer = pro[0].acc is not None
+            z = torch.empty(1, self.Ntot, dtype=torch.float32, device=dev) if layer else \
+                torch.empty(parts, 1, self.Ntot, dtype=torch.int32, device=dev)
+            out = z if layer else z[0]
             if self.W is not None:
-                segs = [(self.W[s.col0:s.col0 + s.width], None, s.rs, z[:, s.col0:]) for s in self.segments]
+                segs = [(self.W[s.col0:s.col0 + s.width], None, s.rs, out[:, s.col0:]) for s in self.segments]
             else:
-                segs = [(L.words(), L.t8, s.rs, z[:, s.col0:]) for L, s in zip(self.layers, self.segments)]
-            kernels.SmallProduct(segs, self.Ntot, resident=self.W is not None).run_pro(pro)
-            return z
+                segs = [(L.words(), L.t8, s.rs, out[:, s.col0:]) for L, s in zip(self.layers, self.segments)]
+            kernels.SmallProduct(segs, self.Ntot, resident=self.W is not None).run_pro(pro, parts)
+            return z if (layer or parts > 1) else z[0]
         q = b['q'] if b['q'] is not None else b['q4']
         M, dev = b['scale'].numel(), q.device
         if parts > 1:
@@ -280,6 +285,35 @@ class Group:
         acc = self.product(b, pro=pro)
         s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], self.rs)
         kernels.mid2(acc, s_tok, rs, self.sv, down.su, q=b2['q'], q4=b2['q4'], scale=b2['scale'])
+
+    def pre_prologue_fits(self, M):
+        """Whether this group's product at M tokens can take a rotate + quantize prologue (tcq_gemm_*_pro without acc): one
+        token, 16384 input columns, plain signs (no column scale)."""
+        return FUSE['pre_prologue'] and M == 1 and self.a8 and self.K == 16384 and self.col_scale is None
+
+    def gated_down(self, b, down, parts=1, pro=None):
+        """This gate | up group's product, the GeGLU middle and the down projection's product: (z, b2) with z as
+        down.product(b2, parts) returns it and b2 the down input's buffers (its token scale for the epilogue). On the
+        spread middle at one token the down projection's rotate + quantize runs inside its product's launch (every
+        workgroup computes the INT8 row from glu_split's output); else gated_middle then down.product. pro: as in
+        gated_middle."""
+        M, dev = (1, self.rs.device) if pro is not None else (b['scale'].numel(), b['scale'].device)
+        if self.spreads(M) and down.pre_prologue_fits(M):
+            zt = torch.empty(2, M, 128, 128, dtype=torch.float32, device=dev)
+            segs = [(L.words(), L.t8, s.rs, zt[i]) for i, (L, s) in enumerate(zip(self.layers, self.segments))]
+            if pro is not None:
+                kernels.gemm_tcq_w128t(segs, None, None, pro=pro)
+            else:
+                kernels.gemm_tcq_w128t(segs, b['q'] if b['q'] is not None else b['q4'], b['scale'])
+            p = kernels.glu_split(zt, self.sv, kernels.gelu_table(dev), torch.empty(M, 16384, dtype=torch.bfloat16, device=dev))
+            b2 = dict(q=None, q4=None, scale=torch.empty(M, dtype=torch.float32, device=dev))
+            z = down.product(None, parts, pro=kernels.prologue_pre(p, down.su, scale=b2['scale']))
+            STATS['spread_middles'] += 1
+            STATS['pre_prologues'] += 1
+            return z, b2
+        b2 = down.buffers(M, dev)
+        self.gated_middle(b, down, b2, pro=pro)
+        return down.product(b2, parts), b2
 
     # ------------------------------------------------------------------------------------------------ epilogue
     def posts(self, acc, b, shape, gelu0=False, outs=None):
@@ -389,10 +423,9 @@ class KGatedMLP(torch.nn.Module):
         x2 = gu.prep(x)
         M, dev = x2.shape[0], x2.device
         if not FUSE['split'] and gu.spreads(M):
-            b, b2 = gu.quantize(x2), down.buffers(M, dev)
-            gu.gated_middle(b, down, b2)
+            z, b2 = gu.gated_down(gu.quantize(x2), down)
             STATS['fused_mlps'] += 1
-            return down.posts(down.product(b2), b2, x.shape)[0]
+            return down.posts(z, b2, x.shape)[0]
         acc, b = _first_half(gu, x)
         b2 = down.buffers(M, dev)
         s_tok, rs = (None, None) if acc.dtype == torch.float32 else (b['scale'], gu.rs)
@@ -501,18 +534,16 @@ class KDecoderLayer(torch.nn.Module):
             b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
         z = og.product(b2, og.k_parts(M))
         x3 = torch.empty_like(x2)
-        b4 = dn.buffers(M, dev)
         if self._prologue_fits(z, og, gu):
             # one token: the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
             pro = kernels.prologue(z, b2['scale'], og.rs, og.sv, x2, x3, n2.weight, n2.eps, gu.su)
-            gu.gated_middle(None, dn, b4, pro=pro)
+            z4, b4 = gu.gated_down(None, dn, dn.k_parts(M), pro=pro)
             STATS['layer_prologues'] += 1
         else:
             b3 = gu.buffers(M, dev)
             kernels.post_add_norm_pre(z, *self._unscaled(z, b2, og), og.sv, og.bias, x2, x3, n2.weight, n2.eps, gu.su, q=b3['q'],
                                       q4=b3['q4'], scale=b3['scale'])
-            gu.gated_middle(b3, dn, b4)
-        z4 = dn.product(b4, dn.k_parts(M))
+            z4, b4 = gu.gated_down(b3, dn, dn.k_parts(M))
         x4 = torch.empty_like(x2)
         nxt = self._next[0] if (self._next and FUSE['chain']) else None
         if nxt is None:
