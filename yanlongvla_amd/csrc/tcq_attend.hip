@@ -280,13 +280,14 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
 // chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
 // register engine) and quantized.
 constexpr int CW = 16;
-// rotate + quantize of the combined row (2^L values in xs, natural layout) on the register + transpose engine, 16 values per
-// thread on threads 0 .. 2^(L - 4) - 1; the rest of the workgroup meets the barriers
+// rotate + quantize of the combined row (2^L values in xs, natural layout) on the register + transpose engine, 8 values per
+// thread on threads 0 .. 2^(L - 3) - 1 (one row per workgroup: more threads per row shorten it); the rest of the
+// workgroup meets the barriers
 template <int L>
 __device__ __forceinline__ void combine_rotate_quantize(float* xs, float* red, i8* q8, int* q4, int ldq, float* scale, int t) {
-    float v[16];
-    tw_get<L, 4, 0>(v, xs);
-    tw_rotate_quantize<L, 4>(v, xs, red, q8, q4, ldq, scale, t);
+    float v[8];
+    tw_get<L, 3, 0>(v, xs);
+    tw_rotate_quantize<L, 3>(v, xs, red, q8, q4, ldq, scale, t);
 }
 __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su,
                                                         i8* q8, int* q4, int ldq, float* scale, int tw_ok) {

@@ -342,17 +342,33 @@ __device__ __forceinline__ void reg_walsh16_part(float (&v)[16], int K, float* x
 // ascending order, every stage is walsh_segment's butterfly in the same stage order and the sums are equal bit for bit.
 // The index parts of t and k use disjoint bits, so lds_slot(t part | k part) = lds_slot(t part) + lds_slot(k part) and
 // the k parts are compile-time offsets.
+//
+// Rows of 3 LE < L <= 4 LE take four passes instead (Tw::P4), each of LE index bits, with R = L - 3 LE for the last:
+//   A (natural):  (t << LE) | k
+//   B:            t bits [0, LE) -> [0, LE), the rest -> [2 LE, L); k -> [LE, 2 LE)
+//   C:            t bits [0, 2 LE) -> [0, 2 LE), the rest -> [3 LE, L); k -> [2 LE, 3 LE)
+//   D (last):     t -> [LE - R, 3 LE); k bits [0, R) -> [3 LE, L), k bits [R, LE) -> [0, LE - R) (bits whose stages are
+//                 done: the pass runs butterflies over k bits [0, R) only)
 template <int L, int LE>
 struct Tw {
     static constexpr int E = 1 << LE, T = 1 << (L - LE), H = L - LE, MB = L - 2 * LE;
-    static_assert(MB >= 0 && MB <= LE, "register + transpose Walsh needs 2 LE <= L <= 3 LE");
+    static constexpr bool P4 = L > 3 * LE;
+    static constexpr int R = L - 3 * LE, LAST = P4 ? 3 : 2;              // last pass: its bits, its layout
+    static_assert(MB >= 0 && L <= 4 * LE, "register + transpose Walsh needs 2 LE <= L <= 4 LE");
     template <int X>
     __device__ static int tpart(int t) {
-        return X == 0 ? t << LE : X == 1 ? (t & (E - 1)) | ((t >> LE) << H) : t;
+        if constexpr (P4)
+            return X == 0 ? t << LE : X == 1 ? (t & (E - 1)) | ((t >> LE) << (2 * LE))
+                 : X == 2 ? (t & (E * E - 1)) | ((t >> (2 * LE)) << (3 * LE)) : t << (LE - R);
+        else
+            return X == 0 ? t << LE : X == 1 ? (t & (E - 1)) | ((t >> LE) << H) : t;
     }
     template <int X>
     __host__ __device__ static constexpr int kpart(int k) {
-        return X == 0 ? k : X == 1 ? ((k & ((1 << MB) - 1)) << LE) | ((k >> MB) << (H + MB)) : k << H;
+        if constexpr (P4)
+            return X == 0 ? k : X == 1 ? k << LE : X == 2 ? k << (2 * LE) : ((k & ((1 << R) - 1)) << (3 * LE)) | (k >> R);
+        else
+            return X == 0 ? k : X == 1 ? ((k & ((1 << MB) - 1)) << LE) | ((k >> MB) << (H + MB)) : k << H;
     }
 };
 
@@ -384,6 +400,20 @@ __device__ __forceinline__ void tw_walsh(float (&v)[1 << LE], float* xs) {
     butterflies<LE>(v);
     tw_put<L, LE, 0>(v, xs);
     __syncthreads();
+    if constexpr (W::P4) {                                                 // four passes: B, C, then D
+        tw_get<L, LE, 1>(v, xs);
+        butterflies<LE>(v);
+        tw_put<L, LE, 1>(v, xs);
+        __syncthreads();
+        tw_get<L, LE, 2>(v, xs);
+        butterflies<LE>(v);
+        tw_put<L, LE, 2>(v, xs);
+        __syncthreads();
+        tw_get<L, LE, 3>(v, xs);
+#pragma unroll
+        for (int g = 0; g < (W::E >> W::R); ++g) butterflies<W::R>(v + (g << W::R));
+        return;
+    }
     if constexpr (W::MB > 0) {
         tw_get<L, LE, 1>(v, xs);
 #pragma unroll
@@ -400,6 +430,7 @@ __device__ __forceinline__ void tw_walsh(float (&v)[1 << LE], float* xs) {
 template <int L, int LE>
 __device__ __forceinline__ void tw_walsh2(float (&a)[1 << LE], float (&b)[1 << LE], float* xa, float* xb) {
     using W = Tw<L, LE>;
+    static_assert(!W::P4, "two rows at once: three-pass rows");
     butterflies<LE>(a);
     butterflies<LE>(b);
     tw_put<L, LE, 0>(a, xa);
@@ -423,10 +454,10 @@ __device__ __forceinline__ void tw_walsh2(float (&a)[1 << LE], float (&b)[1 << L
     butterflies<LE>(b);
 }
 
-// Layout C -> layout A through xs (own slots first, one barrier).
+// Last layout (C, or D for four passes) -> layout A through xs (own slots first, one barrier).
 template <int L, int LE>
 __device__ __forceinline__ void tw_to_natural(float (&v)[1 << LE], float* xs) {
-    tw_put<L, LE, 2>(v, xs);
+    tw_put<L, LE, Tw<L, LE>::LAST>(v, xs);
     __syncthreads();
     tw_get<L, LE, 0>(v, xs);
 }
@@ -636,23 +667,31 @@ __device__ __forceinline__ void tw_rotate_quantize(float (&v)[1 << LE], float* x
     for (int k4 = 0; k4 < E / 4; ++k4)
         words[k4] = (u32)(q8(v[4 * k4], S) & 0xff) | ((u32)(q8(v[4 * k4 + 1], S) & 0xff) << 8) |
                     ((u32)(q8(v[4 * k4 + 2], S) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], S) & 0xff) << 24);
-    if (qs) {
+    if constexpr (E == 8) {                                             // 8 bytes per thread: half a 16-byte group
+        const u64 d = (u64)words[0] | ((u64)words[1] << 32);
+        if (qs) *(u64*)(qs + 2 * t) = d;
+        if (q) *gptr((u64*)(q + (size_t)tok * N + 8 * t)) = d;
+        if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) *gptr((u64*)((i8*)q4 + tb_offset(tok, 8 * t, N))) = d;
+    } else {
+        if (qs) {
 #pragma unroll
-        for (int h = 0; h < E / 16; ++h)
-            *(uint4_t*)(qs + (E / 4) * t + 4 * h) = uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+            for (int h = 0; h < E / 16; ++h)
+                *(uint4_t*)(qs + (E / 4) * t + 4 * h) = uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+        }
+        if (q) {
+#pragma unroll
+            for (int h = 0; h < E / 16; ++h)
+                *gptr((uint4_t*)(q + (size_t)tok * N + E * t + 16 * h)) =
+                    uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+        }
+        if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) {
+#pragma unroll
+            for (int h = 0; h < E / 16; ++h)
+                *gptr((uint4_t*)((i8*)q4 + tb_offset(tok, E * t + 16 * h, N))) =
+                    uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
+        }
     }
-    if (q) {
-#pragma unroll
-        for (int h = 0; h < E / 16; ++h)
-            *gptr((uint4_t*)(q + (size_t)tok * N + E * t + 16 * h)) =
-                uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
-    }
-    if (q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS) {
-#pragma unroll
-        for (int h = 0; h < E / 16; ++h)
-            *gptr((uint4_t*)((i8*)q4 + tb_offset(tok, E * t + 16 * h, N))) =
-                uint4_t{words[4 * h], words[4 * h + 1], words[4 * h + 2], words[4 * h + 3]};
-    } else if (q4) {
+    if (q4 && ldq != TCQ_LDQ_TOKEN_BLOCKS) {
 #pragma unroll
         for (int k4 = 0; k4 < E / 4; ++k4) q4[(size_t)((E / 4) * t + k4) * ldq + tok] = (int)words[k4];
     }

@@ -76,11 +76,11 @@ template <int PL> struct PackOf { typedef SegPackPro type; };
 template <> struct PackOf<0> { typedef SegPack type; };
 
 // Prologues by row width 2^PL: PL = 11, the decoder-layer prologue of a 2048-wide row (tcq_post_add_norm_pre's
-// operations, 16 values per thread); PL = 14, the rotate + quantize of a 16384-wide BF16 row (tcq_pre's operations, 32
+// operations, 8 values per thread); PL = 14, the rotate + quantize of a 16384-wide BF16 row (tcq_pre's operations, 32
 // values per thread). Both on the register + transpose engine, as the standalone kernels run them.
 template <int PL> struct ProShape {
     static_assert(PL == 11 || PL == 14, "prologue widths: 2048 (layer prologue), 16384 (rotate + quantize)");
-    static constexpr int LE = PL == 11 ? 4 : 5;
+    static constexpr int LE = PL == 11 ? 3 : 5;
 };
 
 // LDS of the prologue of a 2^PL-wide row: the Walsh engine's row, the chunk sums, the reduction slots, the INT8 row and its

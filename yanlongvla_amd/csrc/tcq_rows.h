@@ -162,9 +162,134 @@ struct NoMid {
     __device__ void operator()() const {}
 };
 // BIAS = false: A.bias is ignored (callers that have none save its registers).
-template <int ADT, int L, int LE, bool BIAS = true, class F = NoMid>
-__device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, float (&v)[1 << LE], float* xs, float* part,
-                                        float* red, F&& mid = NoMid{}) {
+// 8-element pieces (the eight-values-per-thread engine): loads of 8 consecutive values as FP32.
+__device__ __forceinline__ void ld8_i8v(const i8* p, float (&v)[8]) {
+    const u64 w = *gptr((const u64*)p);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (float)(i8)(w >> (8 * k));
+}
+__device__ __forceinline__ void ld8_bf16v(const u16* p, float (&v)[8]) {
+    const uint4_t a = gptr((const uint4_t*)p)[0];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[2 * k] = __uint_as_float(a[k] << 16);
+        v[2 * k + 1] = __uint_as_float(a[k] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void ld8_f32v(const float* p, float (&v)[8]) {
+    const uint4_t a = gptr((const uint4_t*)p)[0], b = gptr((const uint4_t*)p)[1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k] = __uint_as_float(a[k]);
+        v[4 + k] = __uint_as_float(b[k]);
+    }
+}
+// acc_chunk for 8 values
+template <int ADT>
+__device__ __forceinline__ void acc_piece8(const void* acc, size_t base, float st, const float* rs, float (&v)[8], int parts,
+                                           size_t pstride) {
+    if (ADT == TCQ_BF16) {
+        float r[8];
+        ld8_bf16v((const u16*)acc + base, v);
+        ld8_f32v(rs, r);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = v[k] * r[k];
+    } else if (ADT == TCQ_I32) {
+        uint4_t a[2], ap[3][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) a[h] = gptr((const uint4_t*)((const u32*)acc + base))[h];
+#pragma unroll
+        for (int p = 1; p < 4; ++p)
+            if (p < parts) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) ap[p - 1][h] = gptr((const uint4_t*)((const u32*)acc + base + p * pstride))[h];
+            }
+        float r[8];
+        ld8_f32v(rs, r);
+#pragma unroll
+        for (int p = 1; p < 4; ++p)
+            if (p < parts) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) a[k >> 2][k & 3] = (u32)((int)a[k >> 2][k & 3] + (int)ap[p - 1][k >> 2][k & 3]);
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = ((float)(int)a[k >> 2][k & 3] * st) * r[k];
+    } else {
+        ld8_f32v((const float*)acc + base, v);
+    }
+}
+
+// panp_tw with 8 values per thread (rows of 2^L on 2^(L - 3) threads): the same operations in the same order. The sum of
+// squares keeps its 16-element chunks: the even thread of a pair sums its 8 squares from 0, the odd one continues from the
+// even one's partial sum (a DPP move from the lane below), so every chunk sum is the sequential one.
+template <int ADT, int L, bool BIAS, class F>
+__device__ __forceinline__ bool panp_tw8(const PanpArgs& A, int tok, bool store, float (&v)[8], float* xs, float* part,
+                                         float* red, F&& mid) {
+    constexpr int N = 1 << L;
+    const int t = threadIdx.x, i0 = 8 * t;
+    const bool on = t < (N >> 3);                                      // whole waves (N >= 512)
+    const size_t row = (size_t)tok * N, base = (size_t)tok * A.lda + A.col0 + i0;
+    float sg[8], xv[8], b[8], wv[8], sn[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = 0.f;
+    if (on) {
+        ld8_i8v(A.sv + i0, sg);
+        ld8_bf16v(A.x + row + i0, xv);
+        if (BIAS && A.bias) ld8_f32v(A.bias + i0, b);
+        if (A.w) {
+            ld8_bf16v(A.w + i0, wv);
+            ld8_i8v(A.su + i0, sn);
+        }
+        acc_piece8<ADT>(A.acc, base, ADT == TCQ_I32 ? A.s[tok] : 1.f, A.rs ? A.rs + i0 : nullptr, v, A.parts, A.pstride);
+    }
+    mid();
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    tw_walsh<L, 3>(v, xs);
+    tw_to_natural<L, 3>(v, xs);
+    if (on) {
+        float a[8];
+        u16 xn[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            a[k] = (v[k] * c) * sg[k];
+            if (BIAS && A.bias) a[k] = a[k] + b[k];
+        }
+        bf16_round<4>(a, xn);                                          // a = bf16(post output)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = xv[k] + a[k];
+        bf16_round<4>(v, xn);                                          // xout = bf16(x + a)
+        if (store)
+            *gptr((uint4_t*)(A.xout + row + i0)) = uint4_t{(u32)xn[0] | ((u32)xn[1] << 16), (u32)xn[2] | ((u32)xn[3] << 16),
+                                                           (u32)xn[4] | ((u32)xn[5] << 16), (u32)xn[6] | ((u32)xn[7] << 16)};
+        if (A.w) {
+            float s0 = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s0 = s0 + v[k] * v[k];
+            float s1 = dpp<0x111>(s0);                                 // row_shr:1: the even lane's partial sum
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s1 = s1 + v[k] * v[k];
+            if (t & 1) part[t >> 1] = s1;
+        }
+    }
+    if (!A.w) return false;                                             // uniform
+    __syncthreads();
+    const float ss = tree_total(part, red, N);
+    const float r = 1.f / __builtin_sqrtf(ss / (float)N + A.eps);
+    if (on) {
+        float nv[8];
+        u16 nh[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) nv[k] = (v[k] * r) * (1.f + wv[k]);
+        bf16_round<4>(nv, nh);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = nv[k] * sn[k];
+    }
+    return true;
+}
+
+template <int ADT, int L, int LE, bool BIAS, class F>
+__device__ __forceinline__ bool panp_tw16(const PanpArgs& A, int tok, bool store, float (&v)[1 << LE], float* xs, float* part,
+                                          float* red, F&& mid) {
     constexpr int N = 1 << L, E = 1 << LE, NP = E / 16;
     const int t = threadIdx.x, i0 = E * t;
     const bool on = t < (N >> LE);
@@ -237,6 +362,13 @@ __device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, 
         }
     }
     return true;
+}
+
+template <int ADT, int L, int LE, bool BIAS = true, class F = NoMid>
+__device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, float (&v)[1 << LE], float* xs, float* part,
+                                        float* red, F&& mid = NoMid{}) {
+    if constexpr (LE == 3) return panp_tw8<ADT, L, BIAS>(A, tok, store, v, xs, part, red, mid);
+    else return panp_tw16<ADT, L, LE, BIAS>(A, tok, store, v, xs, part, red, mid);
 }
 
 // The rotate + quantize input of a BF16 row (tcq_pre's first steps): thread t's 2^LE contiguous values x[2^LE t ..] * su,

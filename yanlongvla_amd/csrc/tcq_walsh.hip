@@ -1566,10 +1566,12 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
         case TCQ_BF16: PANT(TCQ_BF16, L, LE); break;     \
         default: return TCQ_ERR_DTYPE;                   \
     }
+        // few rows (latency): 8 values per thread, twice the threads per row (four register passes); many rows: 16
+        const bool wide = M <= 64;
         switch (N) {
-            case 1024: PANW(10, 4); break;
-            case 2048: PANW(11, 4); break;
-            default: PANW(12, 4); break;
+            case 1024: if (wide) { PANW(10, 3); } else { PANW(10, 4); } break;
+            case 2048: if (wide) { PANW(11, 3); } else { PANW(11, 4); } break;
+            default: if (wide) { PANW(12, 3); } else { PANW(12, 4); } break;
         }
 #undef PANW
 #undef PANT
