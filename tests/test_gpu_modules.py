@@ -201,14 +201,14 @@ def test_chained_prologues_bitexact(part):
                 model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
                 modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 14, DEV))
                 x = torch.randn(120, 2048, generator=torch.Generator(device=DEV).manual_seed(7), device=DEV).bfloat16()
-                before = modules.STATS['chained_prologues']
+                before = modules.STATS['chained_prologues'] + modules.STATS['deferred_outputs']
                 h, ks, vs = model.prefill(x)
                 outs[chain] = [h]
                 for t in range(2):
                     h, ks, vs = model.decode_step(x[t:t + 1], ks, vs)
                     outs[chain].append(h)
-                expect = 2 * 3
-            taken[chain] = modules.STATS['chained_prologues'] - before
+                expect = 2 * 3                               # decode steps: deferred outputs, counted alike
+            taken[chain] = modules.STATS['chained_prologues'] + modules.STATS['deferred_outputs'] - before
         finally:
             modules.FUSE['chain'] = True
     assert taken == {False: 0, True: expect}
@@ -217,13 +217,15 @@ def test_chained_prologues_bitexact(part):
 
 
 @pytest.mark.parametrize('runtime', ['fly', 'resident'])
-@pytest.mark.parametrize('flag,stat', [('prologue', 'layer_prologues'), ('pre_prologue', 'pre_prologues')])
+@pytest.mark.parametrize('flag,stat', [('prologue', 'layer_prologues'), ('pre_prologue', 'pre_prologues'),
+                                       ('defer', 'deferred_outputs')])
 def test_prologues_in_the_mlp_products_bitexact(runtime, flag, stat):
     """At one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
-    (FUSE['prologue']), and the down projection's rotate + quantize inside the down product's (FUSE['pre_prologue']): a
-    3-layer backbone's decode steps give the hidden states and key / value rows of the separate launches bit for bit, and
-    each fused form is taken at every layer of every step on the fly runtime's spread middle (the resident runtime keeps
-    the separate launches)."""
+    (FUSE['prologue']), the down projection's rotate + quantize inside the down product's (FUSE['pre_prologue']), and,
+    in the decode loop, a layer's down epilogue + residual + the next layer's norm1 prologue inside the next q/k/v
+    product's (FUSE['defer']): a 3-layer backbone's decode steps give the hidden states and key / value rows of the
+    separate launches bit for bit. The MLP forms are taken at every layer of every step on the fly runtime's spread middle
+    (the resident runtime keeps the separate launches); the deferred output at every layer boundary of both runtimes."""
     from yanlongvla_amd import gemma, modules
     model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
     modules.install(model, runtime=runtime, layers=gemma.synthetic_layers(model, 15, DEV))
@@ -241,9 +243,32 @@ def test_prologues_in_the_mlp_products_bitexact(runtime, flag, stat):
             taken[fuse] = modules.STATS[stat] - before
         finally:
             modules.FUSE[flag] = True
-    assert taken == {False: 0, True: 2 * 3 if runtime == 'fly' else 0}
+    expect = 2 * 2 if flag == 'defer' else (2 * 3 if runtime == 'fly' else 0)
+    assert taken == {False: 0, True: expect}
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)
+
+
+def test_deferred_output_completed_when_the_next_layer_takes_another_input():
+    """Inside deferred_outputs() a layer returns its output row uncomputed; when the next layer is called on a different
+    tensor, it writes that row first (as tcq_post_add_norm_pre would have), so the returned output holds the same bits as
+    without deferral, and the next layer runs its own norm prologue."""
+    from yanlongvla_amd import gemma, modules
+    model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=6, layers=2, vocab=512)
+    modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, 16, DEV))
+    g = torch.Generator(device=DEV).manual_seed(10)
+    x = torch.randn(40, 2048, generator=g, device=DEV).bfloat16()
+    _, ks, vs = model.prefill(x)
+    L0, L1 = model.stack.layers[0], model.stack.layers[1]
+    tok, other = x[5:6].clone(), torch.randn(1, 2048, generator=g, device=DEV).bfloat16()
+    ref0 = L0(tok, ks[0], vs[0])[0].clone()
+    ref1 = L1(other, ks[1], vs[1])[0].clone()
+    before = modules.STATS['deferred_outputs']
+    with modules.deferred_outputs():
+        out0 = L0(tok, ks[0], vs[0])[0]
+        out1 = L1(other, ks[1], vs[1])[0]
+    assert modules.STATS['deferred_outputs'] == before
+    assert torch.equal(out0, ref0) and torch.equal(out1, ref1)
 
 
 @pytest.mark.parametrize('runtime', ['reference', 'fly', 'resident'])

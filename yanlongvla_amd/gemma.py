@@ -221,20 +221,24 @@ class BackbonePolicy(nn.Module):
 
     def decode_step_cached(self, x, cache):
         """decode_step on a KVCache: the same hidden state, with this token's keys / values written into the cache."""
+        from . import modules
         h = x
-        for i, layer in enumerate(self.stack.layers):
-            ck, cv, out = cache.rows(i)
-            h, _, _ = layer(h, ck, cv, kv_out=out)
+        with modules.deferred_outputs():                 # each layer's output goes straight to the next layer
+            for i, layer in enumerate(self.stack.layers):
+                ck, cv, out = cache.rows(i)
+                h, _, _ = layer(h, ck, cv, kv_out=out)
         cache.length += 1
         return self.stack.norm(h)
 
     def decode_step(self, x, ks, vs):
         """One token x (1, width) against the caches; returns the hidden state and the caches grown by one row."""
+        from . import modules
         h, nk, nv = x, [], []
-        for i, layer in enumerate(self.stack.layers):
-            h, k, v = layer(h, ks[i], vs[i])
-            nk.append(torch.cat([ks[i], k.to(ks[i].dtype)], 0))
-            nv.append(torch.cat([vs[i], v.to(vs[i].dtype)], 0))
+        with modules.deferred_outputs():                 # each layer's output goes straight to the next layer
+            for i, layer in enumerate(self.stack.layers):
+                h, k, v = layer(h, ks[i], vs[i])
+                nk.append(torch.cat([ks[i], k.to(ks[i].dtype)], 0))
+                nv.append(torch.cat([vs[i], v.to(vs[i].dtype)], 0))
         return self.stack.norm(h), nk, nv
 
 

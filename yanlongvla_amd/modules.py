@@ -20,6 +20,7 @@ Layers that read the same tensor with the same input signs share one rotation + 
 gate/up): the group computes on the first member's call and the other members take their slice. Every launch goes to the
 HIP library; nothing here computes with PyTorch ops except the bookkeeping (views, empty outputs).
 """
+import contextlib
 from collections import Counter, namedtuple
 from itertools import accumulate
 
@@ -31,15 +32,16 @@ from . import tcq_format as F
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
 STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0,
-             layer_prologues=0, pre_prologues=0)
+             layer_prologues=0, pre_prologues=0, deferred_outputs=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
 # layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
 # (the first Walsh stages in the gate/up product, the rest in glu_split, then the down projection's pre) instead of mid2;
 # prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch;
-# pre_prologue: after the spread middle the down projection's rotate + quantize runs inside its product's launch
+# pre_prologue: after the spread middle the down projection's rotate + quantize runs inside its product's launch;
+# defer: inside deferred_outputs(), a layer's down epilogue + the next layer's norm1 prologue run in the next q/k/v product
 FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True,
-            pre_prologue=True)
+            pre_prologue=True, defer=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -459,6 +461,41 @@ class KPlainMLP(torch.nn.Module):
         return second.posts(second.product(b2), b2, x.shape)[0]
 
 
+_DEFER = {'on': False}
+
+
+@contextlib.contextmanager
+def deferred_outputs():
+    """Inside this context a chained decoder layer at one token may return its output row before it is computed: the next
+    layer's q/k/v product computes it (the down epilogue + residual) as part of its prologue and writes it before anything
+    later on the stream reads it. Only for callers that pass each layer's output straight to the next layer and read
+    nothing in between (the decode loops of gemma.BackbonePolicy); a layer whose input is not that output completes the
+    row first. The last layer of a stack always computes its own output."""
+    old = _DEFER['on']
+    _DEFER['on'] = True
+    try:
+        yield
+    finally:
+        _DEFER['on'] = old
+
+
+class Deferred:
+    """A decoder layer's output row left to the next layer: the down product's int32 K parts z, the token scale s, the
+    down group's row scales and output signs, the residual input x3 and the output x4 (not yet written)."""
+
+    def __init__(self, z, s, rs, sv, x3, x4):
+        self.z, self.s, self.rs, self.sv, self.x3, self.x4 = z, s, rs, sv, x3, x4
+
+    def prologue(self, x2, norm, su):
+        """The layer prologue of the next q/k/v product: writes x4 (= x2, the next layer's input) and computes the INT8 row
+        of fwht(RMSNorm(x4) * su)."""
+        return kernels.prologue(self.z, self.s, self.rs, self.sv, self.x3, x2, norm.weight, norm.eps, su)
+
+    def complete(self):
+        """Writes the output row alone (tcq_post_add_norm_pre without the norm)."""
+        kernels.post_add_norm_pre(self.z, self.s, self.rs, self.sv, None, self.x3, self.x4)
+
+
 class KDecoderLayer(torch.nn.Module):
     """Gemma decoder layer x + attn(norm1(x)) -> + mlp(norm2(.)) over the layer's groups with the norms and residual adds
     fused into the TCQ kernels: norm1 + rotate + quantize (tcq_norm_pre), q/k/v product, q/k/v epilogue, attention (the
@@ -484,17 +521,32 @@ class KDecoderLayer(torch.nn.Module):
         self._handoff = None     # (residual output, its version, q / scale buffers) left by the previous layer
 
     def _prologue(self, x, x2):
-        """The q/k/v input buffers the previous layer computed for exactly this input (x as passed, x2 its 2-D view), or
-        None."""
+        """What the previous layer left for exactly this input (x as passed, x2 its 2-D view): the q/k/v input buffers it
+        computed, a Deferred record (its output row still to be computed, by this layer's q/k/v product), or None. A
+        Deferred record that does not match the input is completed here, so the previous layer's output is valid."""
         h, self._handoff = self._handoff, None
         if h is None:
             return None
         xo, ver, ret, b = h
         if x2.data_ptr() != xo.data_ptr() or x2.shape != xo.shape or x2.dtype != xo.dtype:
-            return None
-        if ver is None:
-            return b if x is ret else None
-        return b if (not x2.is_inference() and x2._version == ver) else None
+            match = False
+        elif ver is None:
+            match = x is ret
+        else:
+            match = not x2.is_inference() and x2._version == ver
+        if match:
+            return b
+        if isinstance(b, Deferred):
+            b.complete()
+        return None
+
+    def _defers(self, M, z4, dn, nxt):
+        """Whether this layer may leave its output row to the next layer's q/k/v product (inside deferred_outputs() only):
+        one token, int32 sums of a two-sided down projection without bias, 2048-wide rows, a q/k/v group that takes the
+        layer prologue (tcq_gemm_*_pro)."""
+        nq = nxt.groups[0]
+        return (_DEFER['on'] and FUSE['defer'] and M == 1 and z4.dtype == torch.int32 and dn.bias is None and not dn.one_sided
+                and dn.Ntot == 2048 and nq.K == 2048 and nq.a8 and nq.col_scale is None)
 
     @staticmethod
     def _prologue_fits(z, og, gu):
@@ -521,12 +573,20 @@ class KDecoderLayer(torch.nn.Module):
         x2 = x.reshape(-1, shape[-1]).contiguous()
         M, dev = x2.shape[0], x2.device
         b = self._prologue(x, x2)
-        if b is None:
-            b = qkv.buffers(M, dev)
-            kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], q4=b['q4'], scale=b['scale'])
+        if isinstance(b, Deferred):
+            # the previous layer's down epilogue + residual (writing this layer's input x2) + norm1 + rotate + quantize run
+            # inside the q/k/v product's launch
+            z1 = qkv.product(None, pro=b.prologue(x2, n1, qkv.su))
+            b = None
+            STATS['deferred_outputs'] += 1
         else:
-            STATS['chained_prologues'] += 1
-        q, k, v = qkv.posts(qkv.product(b), b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
+            if b is None:
+                b = qkv.buffers(M, dev)
+                kernels.norm_pre(x2, n1.weight, n1.eps, qkv.su, q=b['q'], q4=b['q4'], scale=b['scale'])
+            else:
+                STATS['chained_prologues'] += 1
+            z1 = qkv.product(b)
+        q, k, v = qkv.posts(z1, b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
         if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
             b2 = og.buffers(M, dev)
             self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
@@ -548,6 +608,8 @@ class KDecoderLayer(torch.nn.Module):
         nxt = self._next[0] if (self._next and FUSE['chain']) else None
         if nxt is None:
             kernels.post_add_norm_pre(z4, *self._unscaled(z4, b4, dn), dn.sv, dn.bias, x3, x4)
+        elif self._defers(M, z4, dn, nxt):
+            bn = Deferred(z4, b4['scale'], dn.rs, dn.sv, x3, x4)        # x4 is written by the next layer's q/k/v product
         else:
             nq, nn1 = nxt.groups[0], nxt.input_layernorm
             bn = nq.buffers(M, dev)
