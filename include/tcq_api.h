@@ -256,6 +256,11 @@ int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, int col0, con
  * No reference counterpart: the reference policy's attention is PyTorch; this is the decoder layers' attention between
  * the TCQ projections, with the o-projection prologue (kernels.pre, deploy/tcq_kernels/kernels.py:208-219) fused in. */
 int tcq_attend_chunks(int P, int M);
+/* The first half of tcq_attend_q4: the chunk partials part ((M, tcq_attend_chunks(P, M), H, 260) FP32: o[256], m, l per
+ * token, chunk and head) without the merge, for a product that merges them in its prologue (tcq_prologue.part). No
+ * reference counterpart (the reference leaves attention to PyTorch). */
+int tcq_attend_parts(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
+                     int H, int D, int causal_offset, float* part, tcq_stream_t stream);
 int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
                int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale, tcq_stream_t stream);
 /* tcq_attend whose prologue also writes the q4 output of the quantizing entry points (q4, ldq as tcq_pre; q8 may then be
@@ -356,11 +361,14 @@ int tcq_gemm_tcq(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const floa
 int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, const float* s, int M, int K, int out_dtype, int ldo,
                 tcq_stream_t stream);
 
-/* Prologue of a one-token product, two forms. With acc: the arguments of tcq_post_add_norm_pre for M = 1 with the norm
+/* Prologue of a one-token product, three forms. With acc: the arguments of tcq_post_add_norm_pre for M = 1 with the norm
  * (acc the previous product's int32 sums, acc_dtype TCQ_I32, optionally | TCQ_K_PARTS2 / TCQ_K_PARTS4 with part p at
  * acc + p * lda; s, rs, sv, bias its epilogue; x, xout the residual; w, eps the RMSNorm; su the signs of the product that
- * follows). Without acc (NULL): tcq_pre of the BF16 row x with signs su (every other input unused). Both may write copies
- * of the INT8 row (q, K bytes) and its scale (scale: the token scale a later epilogue of int32 sums needs). */
+ * follows). Without acc, with part: the second half of tcq_attend_q4 for one token (the merge of the chunk partials part
+ * of tcq_attend_parts, chunks = tcq_attend_chunks(P, 1), keys = P + 1, causal the causal offset or -1, heads = 8), then the
+ * rotate + quantize of its BF16 row with signs su. Without acc and part: tcq_pre of the BF16 row x with signs su. Every
+ * form may write copies of the INT8 row (q, K bytes) and its scale (scale: the token scale a later epilogue of int32 sums
+ * needs). */
 typedef struct {
     const void* acc;
     int acc_dtype;
@@ -376,13 +384,16 @@ typedef struct {
     const int8_t* su;
     int8_t* q;
     float* scale;
+    const float* part;   /* attention partials of tcq_attend_parts (acc NULL): the merge of their chunks is the prologue */
+    int chunks, keys, causal, heads;
 } tcq_prologue;
 
 /* The prologue (tcq_post_add_norm_pre(pro..., M = 1, N = K), or tcq_pre(x, TCQ_BF16, su, ..., M = 1, K)) followed by
  * tcq_gemm_tcq / tcq_gemm_w8 of its INT8 row, in one launch: every workgroup computes the row itself (the same operations,
  * bit for bit) and multiplies it, so the row never leaves the chip and the chain loses a launch. Supported: with acc,
- * K = 2048, bias NULL, out_dtype TCQ_F32 (tcq_gemm_tcq: optionally | TCQ_Z_W128T); without acc, K = 16384, out_dtype
- * TCQ_I32 (optionally | TCQ_K_PARTS2); else TCQ_ERR_UNSUPPORTED. 16-byte aligned operands. No reference counterpart: the
+ * K = 2048, bias NULL, out_dtype TCQ_F32 (tcq_gemm_tcq: optionally | TCQ_Z_W128T); with part, K = 2048 (8 heads),
+ * out_dtype TCQ_I32 (optionally | TCQ_K_PARTS2); with neither, K = 16384, out_dtype TCQ_I32 (optionally | TCQ_K_PARTS2);
+ * else TCQ_ERR_UNSUPPORTED. 16-byte aligned operands. No reference counterpart: the
  * reference runs the epilogue, the residual add, the norm and the quantizer as separate steps (kernels.py:208-230; the
  * norm in PyTorch). */
 int tcq_gemm_tcq_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pro, int K, int out_dtype, int ldo, tcq_stream_t stream);

@@ -168,3 +168,34 @@ def test_product_with_rotate_quantize_prologue(resident, parts):
     torch.cuda.synchronize()
     assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(bits(sc2), bits(sc))
     assert torch.equal(a_pro.cpu(), a_ref.cpu())
+
+
+@pytest.mark.parametrize('resident,parts,P,causal', [(False, 2, 831, None), (True, 2, 831, None), (False, 1, 100, 100),
+                                                     (True, 1, 64, 64), (False, 2, 2000, 1500)])
+def test_product_with_attention_prologue(resident, parts, P, causal):
+    """The attention's chunk merge + rotate + quantize (8 heads, one token against P cached keys) inside the o projection's
+    product (2048 x 2048): the int32 sums, the INT8 row and the scale equal tcq_attend_q4's merge followed by the product;
+    causal offsets that hide the last chunks (1500 of 2001 keys) included."""
+    from yanlongvla_amd import kernels as Kn
+    H, D, m = 8, 256, 2048
+    g = torch.Generator(device=DEV).manual_seed(P + parts)
+    q = torch.randn(1, H * D, generator=g, device=DEV).bfloat16()
+    kc = torch.randn(P, D, generator=g, device=DEV).bfloat16()
+    vc = torch.randn(P, D, generator=g, device=DEV).bfloat16()
+    kn = torch.randn(1, D, generator=g, device=DEV).bfloat16()
+    vn = torch.randn(1, D, generator=g, device=DEV).bfloat16()
+    su = signs(g, H * D)
+    (w, t8, rs, _), = segments([m], resident, 21 + P, [None])
+    q8 = torch.empty(1, H * D, dtype=torch.int8, device=DEV)
+    sc = torch.empty(1, device=DEV)
+    Kn.attend(q, kc, vc, kn, vn, H, causal, su=su, q8=q8, scale=sc)
+    a_ref = torch.full((parts, 1, m), -5, dtype=torch.int32, device=DEV)
+    Kn.SmallProduct([(w, t8, rs, a_ref[0])], m, resident=resident)(q8, sc, parts)
+    q2 = torch.zeros_like(q8)
+    sc2 = torch.zeros_like(sc)
+    a_pro = torch.full((parts, 1, m), -7, dtype=torch.int32, device=DEV)
+    pro = Kn.prologue_attn(Kn.attend_parts(q, kc, vc, kn, vn, H, causal), H, su, q=q2, scale=sc2)
+    Kn.SmallProduct([(w, t8, rs, a_pro[0])], m, resident=resident).run_pro(pro, parts)
+    torch.cuda.synchronize()
+    assert torch.equal(q2.cpu(), q8.cpu()) and torch.equal(bits(sc2), bits(sc))
+    assert torch.equal(a_pro.cpu(), a_ref.cpu())

@@ -71,6 +71,7 @@ SIGNATURES = {
     'tcq_glu_split': [_P, _I, _P, _P, _P, _I, _P],
     'tcq_gemm_tcq_pro': [_P, _I, _P, _I, _I, _I, _P],
     'tcq_gemm_w8_pro': [_P, _I, _P, _I, _I, _I, _P],
+    'tcq_attend_parts': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 
@@ -95,7 +96,8 @@ class Prologue(ctypes.Structure):
     _fields_ = [('acc', ctypes.c_void_p), ('acc_dtype', ctypes.c_int), ('lda', ctypes.c_int), ('col0', ctypes.c_int),
                 ('s', ctypes.c_void_p), ('rs', ctypes.c_void_p), ('sv', ctypes.c_void_p), ('bias', ctypes.c_void_p),
                 ('x', ctypes.c_void_p), ('xout', ctypes.c_void_p), ('w', ctypes.c_void_p), ('eps', ctypes.c_float),
-                ('su', ctypes.c_void_p), ('q', ctypes.c_void_p), ('scale', ctypes.c_void_p)]
+                ('su', ctypes.c_void_p), ('q', ctypes.c_void_p), ('scale', ctypes.c_void_p), ('part', ctypes.c_void_p),
+                ('chunks', ctypes.c_int), ('keys', ctypes.c_int), ('causal', ctypes.c_int), ('heads', ctypes.c_int)]
 
 
 _state = {}

@@ -11,14 +11,11 @@
 // use fused multiply-adds (this attention is the decoder layers' own definition, not a reference rounding chain).
 #include "tcq_device.h"
 #include "tcq_launch.h"
+#include "tcq_attend.h"
 
 namespace {
 
-constexpr int AD = 256;          // head dim
-constexpr int AH = 8;            // most query heads
-constexpr int KC = 64;           // keys per chunk
 constexpr int AT = 256;          // threads of k_attn_part
-constexpr int PS = AD + 4;       // floats per (token, chunk, head) partial: o[AD], m, l and 2 pad words (16-byte rows)
 
 __device__ __forceinline__ const u16* key_row(const u16* cache, const u16* fresh, int P, int j) {
     return j < P ? cache + (size_t)j * AD : fresh + (size_t)(j - P) * AD;
@@ -173,18 +170,10 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     }
 }
 
-// Chunks of token t that hold a key it sees: the combine merges only these. A chunk past them has m = -inf, l = 0 and o = 0
-// for t (weight 0), and adding 0 * 0 to a sum that starts at +0 changes no bit, so skipping them gives the same result;
-// k_attn_part does not compute the chunks no token of its group sees.
-__device__ __forceinline__ int visible_chunks(int NC, int T, int causal, int t) {
-    return causal >= 0 ? min(NC, (min(T, causal + t + 1) + KC - 1) / KC) : NC;
-}
-
 // grid M, CT = 1024 threads: thread (d, g) = (tid % 256, tid / 256) sums dim d of every head over the chunks c = g (mod 4);
 // wave h < H first merges head h's chunk statistics (lane = chunk). The four partial sums of a head add in the fixed order
 // ((g0 + g1) + g2) + g3, so the result depends only on NC. With su set, the BF16 row (H x 256) is rotated and quantized
 // in place as the output projection's prologue.
-constexpr int MAXC = 256;        // most chunks a token may have in the combine (16384 keys)
 constexpr int CT = 1024, CG = CT / AD, CB = 4;   // threads, chunk groups, chunks per group held in registers per batch
 
 __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su, i8* q8,
@@ -273,13 +262,6 @@ __global__ __launch_bounds__(CT) void k_attn_combine(const float* part, int NC, 
     quantize_row(lds, sc, q8 ? q8 + (size_t)t * K : nullptr, q4, t, K, ldq);
 }
 
-// grid M, H * 64 threads (one wave per head, H <= 8): lane l of wave h owns dims 4 l .. 4 l + 3 of head h and loads them for
-// the first CW chunks together with the chunk statistics at entry, so a token of up to CW chunks costs one memory round trip
-// (k_attn_combine_reg holds 8 chunks and goes back to memory for the rest). Every 16-lane group repeats the statistics merge
-// of k_attn_combine_reg in its order (lane g: chunks g, g + 16, ...; butterfly over the 16 lanes), and the chunks add in
-// chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
-// register engine) and quantized.
-constexpr int CW = 16;
 // rotate + quantize of the combined row (2^L values in xs, natural layout) on the register + transpose engine, 8 values per
 // thread on threads 0 .. 2^(L - 3) - 1 (one row per workgroup: more threads per row shorten it); the rest of the
 // workgroup meets the barriers
@@ -289,65 +271,19 @@ __device__ __forceinline__ void combine_rotate_quantize(float* xs, float* red, i
     tw_get<L, 3, 0>(v, xs);
     tw_rotate_quantize<L, 3>(v, xs, red, q8, q4, ldq, scale, t);
 }
+// grid M, H * 64 threads (one wave per head, H <= 8): lane l of wave h owns dims 4 l .. 4 l + 3 of head h and loads them for
+// the first CW chunks together with the chunk statistics at entry, so a token of up to CW chunks costs one memory round trip
+// (k_attn_combine_reg holds 8 chunks and goes back to memory for the rest). Every 16-lane group repeats the statistics merge
+// of k_attn_combine_reg in its order (lane g: chunks g, g + 16, ...; butterfly over the 16 lanes), and the chunks add in
+// chunk order, so o is the same to the bit; with su the BF16 row is rotated on the LDS Walsh engine (the same values as the
+// register engine) and quantized.
 __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int NC, int T, int causal, int H, u16* o, const i8* su,
                                                         i8* q8, int* q4, int ldq, float* scale, int tw_ok) {
     extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
-    const int t = blockIdx.x, tid = threadIdx.x, h = tid >> 6, lane = tid & 63, g = lane & 15, d0 = 4 * lane, K = H * AD;
-    const size_t cs = (size_t)H * PS;
-    const float* hb = part + (size_t)t * NC * cs + (size_t)h * PS;      // head h of chunk 0
-    const int NV = visible_chunks(NC, T, causal, t);
-    constexpr int SC = MAXC / 16;
-    typedef float f2_t __attribute__((ext_vector_type(2)));
-    f2_t ml[SC];
-#pragma unroll
-    for (int r = 0; r < SC; ++r) {
-        const int c = g + 16 * r;
-        ml[r] = c < NV ? gptr((const f2_t*)(hb + c * cs + AD))[0] : f2_t{-__builtin_inff(), 0.f};
-    }
-    float4_t v[CW];
-#pragma unroll
-    for (int i = 0; i < CW; ++i) v[i] = i < NV ? gptr((const float4_t*)(hb + i * cs + d0))[0] : float4_t{0.f, 0.f, 0.f, 0.f};
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int r = 0; r < SC; ++r) mx = fmaxf(mx, ml[r].x);
-    mx = row16_max(mx);
-    float L = 0.f;
-#pragma unroll
-    for (int r = 0; r < SC; ++r) {
-        const int c = g + 16 * r;
-        if (c < NV) {
-            const float w = ml[r].x == -__builtin_inff() ? 0.f : expf(ml[r].x - mx);
-            if (lane < 16) wts[h][c] = w;                                // read back by this wave only: LDS keeps its order
-            L = __builtin_fmaf(w, ml[r].y, L);
-        }
-    }
-    L = row16_sum(L);
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < CW; ++i) {
-        if (i < NV) {
-            const float w = wts[h][i];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, v[i][k], acc[k]);
-        }
-    }
-    for (int c = CW; c < NV; ++c) {
-        const float4_t vc = gptr((const float4_t*)(hb + c * cs + d0))[0];
-        const float w = wts[h][c];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, vc[k], acc[k]);
-    }
-    u16 b[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) b[k] = f32_to_bf16(acc[k] / L);
-    if (o) *gptr((u64*)(o + (size_t)t * K + h * AD + d0)) = (u64)b[0] | ((u64)b[1] << 16) | ((u64)b[2] << 32) | ((u64)b[3] << 48);
-    if (!su) return;                                                     // uniform
-    const u32 sg = *gptr((const u32*)(su + h * AD + d0));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) xs[lds_slot(h * AD + d0 + k)] = bf16_to_f32(b[k]) * (float)(i8)(sg >> (8 * k));
-    __syncthreads();
+    const int t = blockIdx.x, tid = threadIdx.x, K = H * AD;
+    if (!combine_w_row(part, NC, T, causal, H, t, o, su, xs, wts, [] {})) return;   // uniform
     // power-of-two rows (H = 1, 2, 4, 8) and 16-byte aligned INT8 outputs: the register + transpose engine on the first K / 16
     // threads (16 values each, read from the LDS row in layout 0); the same stages in the same order as the LDS engine, so
     // the same bits
@@ -487,6 +423,19 @@ extern "C" int tcq_attend_q4(const void* q, const void* k_cache, const void* v_c
     else
         launch_k(k_attn_combine, dim3(M), dim3(CT), su ? (size_t)lds_words(H * AD) * sizeof(float) : 0, st, (const float*)part, NC,
                  P + M, causal_offset, H, (u16*)o, (const i8*)su, (i8*)q8, (int*)q4, ldq, scale);
+    return launch_status();
+}
+
+extern "C" int tcq_attend_parts(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new,
+                                int M, int H, int D, int causal_offset, float* part, tcq_stream_t stream) {
+    if (!q || !k_new || !v_new || !part || M <= 0 || H <= 0 || P < 0 || (P > 0 && (!k_cache || !v_cache))) return TCQ_ERR_ARG;
+    if (D != AD || H > AH) return TCQ_ERR_UNSUPPORTED;
+    if ((uintptr_t)k_new % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_new % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)part % 16)
+        return TCQ_ERR_ALIGN;
+    const int NC = tcq_attend_chunks(P, M);
+    if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
+    launch_k(k_attn_part<2>, dim3((M + 1) / 2, NC), dim3(AT), 0, (hipStream_t)stream, (const u16*)q, (const u16*)k_cache,
+             (const u16*)v_cache, P, (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
     return launch_status();
 }
 

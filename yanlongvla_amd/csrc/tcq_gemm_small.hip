@@ -16,6 +16,7 @@
 #include "tcq_device.h"
 #include "tcq_launch.h"
 #include "tcq_rows.h"
+#include "tcq_attend.h"
 
 namespace {
 
@@ -65,46 +66,59 @@ struct SegPack {
     tcq_gemm_seg s[TCQ_MAX_SEGS];
 };
 
-// The segments plus the arguments of a one-token decoder-layer prologue (tcq_gemm_tcq_pro / tcq_gemm_w8_pro).
+// The segments plus the arguments of a one-token prologue (tcq_gemm_tcq_pro / tcq_gemm_w8_pro).
 struct SegPackPro {
     tcq_gemm_seg s[TCQ_MAX_SEGS];
     PanpArgs a;
     i8* q;                   // optional copies of the prologue's INT8 row and token scale (written by workgroup 0)
     float* scale;
+    const float* part;       // attention partials (PRO_ATTN)
+    int nc, keys, causal, heads;
 };
+
+// Prologue kinds (the PL template argument of the product kernels): PRO_LAYER, the decoder-layer prologue of a 2048-wide
+// row (tcq_post_add_norm_pre's operations, 8 values per thread); PRO_PRE, the rotate + quantize of a 16384-wide BF16 row
+// (tcq_pre's, 32 values per thread); PRO_ATTN, the attention chunk merge of 8 heads (k_attn_combine_w's, one wave per head)
+// and the rotate + quantize of its 2048-wide row (8 values per thread). All on the register + transpose engine, as the
+// standalone kernels run them.
+enum { PRO_NONE = 0, PRO_LAYER = 1, PRO_PRE = 2, PRO_ATTN = 3 };
 template <int PL> struct PackOf { typedef SegPackPro type; };
-template <> struct PackOf<0> { typedef SegPack type; };
-
-// Prologues by row width 2^PL: PL = 11, the decoder-layer prologue of a 2048-wide row (tcq_post_add_norm_pre's
-// operations, 8 values per thread); PL = 14, the rotate + quantize of a 16384-wide BF16 row (tcq_pre's operations, 32
-// values per thread). Both on the register + transpose engine, as the standalone kernels run them.
+template <> struct PackOf<PRO_NONE> { typedef SegPack type; };
 template <int PL> struct ProShape {
-    static_assert(PL == 11 || PL == 14, "prologue widths: 2048 (layer prologue), 16384 (rotate + quantize)");
-    static constexpr int LE = PL == 11 ? 3 : 5;
+    static_assert(PL == PRO_LAYER || PL == PRO_PRE || PL == PRO_ATTN, "prologue kind");
+    static constexpr int L = PL == PRO_PRE ? 14 : 11, LE = PL == PRO_PRE ? 5 : 3;
 };
 
-// LDS of the prologue of a 2^PL-wide row: the Walsh engine's row, the chunk sums, the reduction slots, the INT8 row and its
-// scale (the product's activations).
+// LDS of a prologue: the Walsh engine's row, the chunk sums, the reduction slots, the INT8 row and its scale (the
+// product's activations), and the attention merge's chunk weights.
 template <int PL>
 struct ProLds {
-    static constexpr int W = (1 << PL) + ((1 << PL) >> 5) + 1;           // lds_words(2^PL)
-    float xs[W + (1 << PL) / 16];
+    static constexpr int N = 1 << ProShape<PL>::L;
+    static constexpr int W = N + (N >> 5) + 1;                           // lds_words(N)
+    float xs[W + N / 16];
     float red[16];
-    __attribute__((aligned(16))) u32 qs[(1 << PL) / 4];
+    __attribute__((aligned(16))) u32 qs[N / 4];
     float sc;
+    float wts[PL == PRO_ATTN ? AH : 1][MAXC];
 };
 
-// Runs the prologue (tcq_post_add_norm_pre of token 0 with the norm; workgroup (0, 0, 0) stores xout and the optional
-// copies) and leaves the INT8 row and the scale in L. Every thread of the workgroup calls it; mid() issues the product's
-// weight loads once the prologue's accumulator registers are free, so their HBM latency runs under the prologue.
+// Runs the prologue and leaves the INT8 row and the scale in L; workgroup (0, 0, 0) stores the side outputs (xout, the
+// optional q / scale copies). Every thread of the workgroup calls it; mid() issues the product's weight loads once the
+// prologue's entry loads have been consumed, so their HBM latency runs under the prologue.
 template <int PL, class F>
 __device__ __forceinline__ void run_prologue(const SegPackPro& P, ProLds<PL>& L, F&& mid) {
-    constexpr int LE = ProShape<PL>::LE;
+    constexpr int NL = ProShape<PL>::L, LE = ProShape<PL>::LE;
     const bool store = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
     float v[1 << LE];
-    if constexpr (PL == 11) panp_tw<TCQ_I32, PL, LE, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
-    else pre_row_tw<PL, LE>(P.a.x, P.a.su, v, mid);
-    tw_rotate_quantize<PL, LE>(v, L.xs, L.red, store ? P.q : nullptr, nullptr, 0, store ? P.scale : nullptr, 0, L.qs, &L.sc);
+    if constexpr (PL == PRO_LAYER) {
+        panp_tw<TCQ_I32, NL, LE, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
+    } else if constexpr (PL == PRO_PRE) {
+        pre_row_tw<NL, LE>(P.a.x, P.a.su, v, mid);
+    } else {
+        combine_w_row(P.part, P.nc, P.keys, P.causal, P.heads, 0, nullptr, P.a.su, L.xs, L.wts, mid);
+        tw_get<NL, LE, 0>(v, L.xs);
+    }
+    tw_rotate_quantize<NL, LE>(v, L.xs, L.red, store ? P.q : nullptr, nullptr, 0, store ? P.scale : nullptr, 0, L.qs, &L.sc);
 }
 
 // Activation layouts of the small-M products: q (M, K) row-major, the token-block layout, or the reference's q4 (K/4, ldq)
@@ -127,7 +141,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
     static_assert(PL == 0 || (NB == 1 && QL == QL_ROWS && !DOT), "prologue: one token");
     __shared__ __attribute__((aligned(16))) u32 tab[MODE == 0 ? 1024 * SM_C : 4];
     __shared__ __attribute__((aligned(16))) int4v red[(TR == 1 ? SM_MAXW - 1 : 7) * TR * NB * 64];
-    __shared__ ProLds<PL ? PL : 4> pro;
+    __shared__ ProLds<PL ? PL : PRO_LAYER> pro;
     const tcq_gemm_seg S = P.s[blockIdx.y];
     const int tiles_m = S.m >> 4, nch_all = (K + 255) >> 8;
     const int c0 = KS > 1 ? (int)blockIdx.z * ((nch_all + KS - 1) / KS) : 0;
@@ -330,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
                                                       int ldz) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     static_assert(PL == 0 || (!QB && !DOT), "prologue: one token");
-    __shared__ ProLds<PL ? PL : 4> pro;
+    __shared__ ProLds<PL ? PL : PRO_LAYER> pro;
     static_assert(!LO || (ODT == TCQ_F32 && KS == 1 && NW / WPR == 8), "stage-split output: FP32 z, 8 tile rows per workgroup");
     constexpr int RPW = NW / WPR;
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
@@ -347,7 +361,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
     const u32 cp4 = (u32)(lane & (GV_C - 1)) << 2;
     const rsrc_t Wr = make_rsrc(S.w, (u32)(tiles_m * nch_all) << 10);
     const rsrc_t Q = make_rsrc(q, QB ? 16u * (u32)K : (u32)M * (u32)K);
-    constexpr int CM = PL ? (((1 << PL) / 256 + KS - 1) / KS + WPR - 1) / WPR : GV_CMAX;   // chunks per wave (K = 2^PL)
+    constexpr int CM = PL ? (((1 << ProShape<PL ? PL : PRO_LAYER>::L) / 256 + KS - 1) / KS + WPR - 1) / WPR : GV_CMAX;   // chunks per wave
     uint4_t wa[CM];
     auto loadW = [&] {
 #pragma unroll
@@ -693,8 +707,9 @@ extern "C" int tcq_gemm_w8(const tcq_gemm_seg* segs, int nseg, const int8_t* q, 
 // ------------------------------------------------------------------------------------ products with the layer prologue
 // One token: every workgroup first computes the product's INT8 row itself, on the same register + transpose engine as the
 // standalone kernels and bit for bit, then its share of the product on that row (LDS); workgroup (0, 0, 0) stores the
-// row's side outputs (xout, and the optional q / scale copies). Two prologues (ProShape): with acc, tcq_post_add_norm_pre's
-// operations on a 2048-wide row (FP32 z out, optionally the stage-split TCQ_Z_W128T form); without acc, tcq_pre's on a
+// row's side outputs (xout, and the optional q / scale copies). Three prologues (ProShape): with acc, tcq_post_add_norm_pre's
+// operations on a 2048-wide row (FP32 z out, optionally the stage-split TCQ_Z_W128T form); with part, the attention merge
+// of 8 heads + rotate + quantize (int32 sums out, optionally in K parts; 8 waves, one per head); else tcq_pre's on a
 // 16384-wide BF16 row x (int32 sums out, optionally in K parts). Plans as gemm_small picks them for M = 1.
 static bool pal16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -702,7 +717,7 @@ template <int MODE, int PL, int ODT, int KS>
 static void launch_pro_small(int rows, int nseg, int nw, bool pairs, hipStream_t st, const SegPackPro& P, int K, int ldo) {
     const i8* nq = nullptr;
     const float* ns = nullptr;
-    if constexpr (PL == 11) {
+    if constexpr (PL == PRO_LAYER) {
         if (pairs) {
             launch_k(k_gemm_small<MODE, 1, ODT, 2, QL_ROWS, false, KS, false, PL>, dim3((rows + 1) / 2, nseg, KS), dim3(64 * nw), 0, st,
                      P, nq, ns, 1, K, ldo, 0);
@@ -717,15 +732,19 @@ template <int MODE>
 static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue* pr, int K, int odt, int ldo, tcq_stream_t stream) {
     if (!segs || !pr || nseg <= 0 || ldo <= 0) return TCQ_ERR_ARG;
     if (nseg > TCQ_MAX_SEGS) return TCQ_ERR_UNSUPPORTED;
-    const bool layer = pr->acc != nullptr;                             // the decoder-layer prologue, else rotate + quantize
+    const bool layer = pr->acc != nullptr, attn = !layer && pr->part != nullptr;   // else: rotate + quantize of x
     const bool w128 = odt & TCQ_Z_W128T;
     if ((odt & TCQ_K_PARTS2) && (odt & TCQ_K_PARTS4)) return TCQ_ERR_ARG;
     const int parts = (odt & TCQ_K_PARTS4) ? 4 : (odt & TCQ_K_PARTS2) ? 2 : 1;
     odt &= ~(TCQ_Z_W128T | TCQ_K_PARTS2 | TCQ_K_PARTS4);
     if (layer ? (K != 2048 || odt != TCQ_F32 || parts > 1 || (w128 && MODE != 0))
-              : (K != 16384 || odt != TCQ_I32 || parts > 2 || w128))
+              : (K != (attn ? 2048 : 16384) || odt != TCQ_I32 || parts > 2 || w128))
         return TCQ_ERR_UNSUPPORTED;
-    if (!pr->x || !pr->su) return TCQ_ERR_ARG;
+    if (!pr->su || (!attn && !pr->x)) return TCQ_ERR_ARG;
+    if (attn) {
+        if (pr->heads != 8 || pr->chunks <= 0 || pr->chunks > MAXC || pr->keys <= 0 || pr->keys > pr->chunks * KC) return TCQ_ERR_UNSUPPORTED;
+        if (!pal16(pr->part) || (uintptr_t)pr->su % 4) return TCQ_ERR_ALIGN;
+    }
     int pparts = 1;
     if (layer) {
         int adt = pr->acc_dtype;
@@ -739,7 +758,7 @@ static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue
         if (!pal16(pr->acc) || pr->lda % 4 || pr->col0 % 4 || !pal16(pr->rs) || !pal16(pr->sv) || !pal16(pr->xout) || !pal16(pr->w))
             return TCQ_ERR_ALIGN;
     }
-    if (!pal16(pr->x) || !pal16(pr->su) || (pr->q && !pal16(pr->q)) || ldo % 4) return TCQ_ERR_ALIGN;
+    if ((!attn && (!pal16(pr->x) || !pal16(pr->su))) || (pr->q && !pal16(pr->q)) || ldo % 4) return TCQ_ERR_ALIGN;
     if (parts > 1 && (size_t)parts * ldo >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
     SegPackPro P = {};
     int max_m = 0, tiles = 0;
@@ -759,20 +778,30 @@ static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue
                    (const i8*)pr->su, pr->lda, pr->col0, pparts, (size_t)pr->lda, pr->eps};
     P.q = (i8*)pr->q;
     P.scale = pr->scale;
+    P.part = pr->part;
+    P.nc = pr->chunks;
+    P.keys = pr->keys;
+    P.causal = pr->causal;
+    P.heads = pr->heads;
     hipStream_t st = (hipStream_t)stream;
     const i8* nq = nullptr;
     const float* ns = nullptr;
     const int nch = K / 256, nchp = (nch + parts - 1) / parts, nw = nchp < SM_MAXW ? nchp : SM_MAXW;
+    if (attn) {                                        // the workgroup plan on one wave per head (8), one tile row each
+        if (parts == 2) launch_pro_small<MODE, PRO_ATTN, TCQ_I32, 2>(max_m / 16, nseg, AH, false, st, P, K, ldo);
+        else launch_pro_small<MODE, PRO_ATTN, TCQ_I32, 1>(max_m / 16, nseg, AH, false, st, P, K, ldo);
+        return launch_status();
+    }
     if (layer) {
         if (w128) {
-            launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, 11>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P, nq,
+            launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, PRO_LAYER>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P, nq,
                      ns, 1, K, ldo);
             return launch_status();
         }
         const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nch, tiles) : 0;
         if (wpr > 0) {
             const dim3 grid((max_m / 16 + GV_NW / wpr - 1) / (GV_NW / wpr), nseg), block(64 * GV_NW);
-#define GVP(W) launch_k(k_gemv_tcq<TCQ_F32, false, W, GV_NW, 1, false, false, 11>, grid, block, 0, st, P, nq, ns, 1, K, ldo)
+#define GVP(W) launch_k(k_gemv_tcq<TCQ_F32, false, W, GV_NW, 1, false, false, PRO_LAYER>, grid, block, 0, st, P, nq, ns, 1, K, ldo)
             switch (wpr) {
                 case 1: GVP(1); break;
                 case 2: GVP(2); break;
@@ -786,7 +815,7 @@ static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue
         bool pairs = nw <= 8 && tiles >= 384;
         for (int i = 0; i < nseg; ++i)
             if (segs[i].rows_per_table > 0 && (segs[i].rows_per_table / 16) % 2) pairs = false;
-        launch_pro_small<MODE, 11, TCQ_F32, 1>(max_m / 16, nseg, nw, pairs, st, P, K, ldo);
+        launch_pro_small<MODE, PRO_LAYER, TCQ_F32, 1>(max_m / 16, nseg, nw, pairs, st, P, K, ldo);
         return launch_status();
     }
     // rotate + quantize prologue, int32 sums: the streaming plan at 16 waves per tile row (the 2048 x 16384 down projection),
@@ -794,12 +823,12 @@ static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue
     const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nchp, tiles * parts) : 0;
     if (wpr == 16) {
         const dim3 grid(max_m / 16, nseg, parts), block(64 * GV_NW);
-        if (parts == 2) launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 2, false, false, 14>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
-        else launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 1, false, false, 14>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
+        if (parts == 2) launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 2, false, false, PRO_PRE>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
+        else launch_k(k_gemv_tcq<TCQ_I32, false, 16, GV_NW, 1, false, false, PRO_PRE>, grid, block, 0, st, P, nq, ns, 1, K, ldo);
         return launch_status();
     }
-    if (parts == 2) launch_pro_small<MODE, 14, TCQ_I32, 2>(max_m / 16, nseg, nw, false, st, P, K, ldo);
-    else launch_pro_small<MODE, 14, TCQ_I32, 1>(max_m / 16, nseg, nw, false, st, P, K, ldo);
+    if (parts == 2) launch_pro_small<MODE, PRO_PRE, TCQ_I32, 2>(max_m / 16, nseg, nw, false, st, P, K, ldo);
+    else launch_pro_small<MODE, PRO_PRE, TCQ_I32, 1>(max_m / 16, nseg, nw, false, st, P, K, ldo);
     return launch_status();
 }
 

@@ -92,6 +92,12 @@ class GemmaAttention(nn.Module):
         kernels.attend(q.contiguous(), cache_k, cache_v, k.contiguous(), v.contiguous(), self.heads, causal_offset, su=su,
                        q8=q8, scale=scale, q4=q4)
 
+    def core_parts(self, q, k, v, cache_k, cache_v, causal_offset):
+        """The first half of core_quantized: the attention's chunk partials, merged later by the o_proj product's prologue
+        (kernels.prologue_attn). Device tensors only."""
+        from . import kernels
+        return kernels.attend_parts(q.contiguous(), cache_k, cache_v, k.contiguous(), v.contiguous(), self.heads, causal_offset)
+
     def forward(self, x, cache_k=None, cache_v=None, causal_offset=None):
         """x (M, width) -> (o_proj output, this call's k, v)."""
         q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)

@@ -259,6 +259,36 @@ def attend(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None,
     return o
 
 
+def attend_parts(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None):
+    """The first half of attend: the chunk partials of every token (tcq_attend_parts), without the merge. Returns
+    (part, chunks, keys, causal) for prologue_attn."""
+    M = q.shape[0]
+    P = 0 if k_cache is None else k_cache.shape[0]
+    for t in (q, k_cache, v_cache, k_new, v_new):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError('attend_parts: BF16 tensors only')
+    _contig(q, k_cache, v_cache, k_new, v_new)
+    D = k_new.shape[1]
+    nc = int(_lib.lib().tcq_attend_chunks(P, M))
+    part = torch.empty(M * nc * heads * (D + 4), dtype=torch.float32, device=q.device)
+    causal = -1 if causal_offset is None else int(causal_offset)
+    call('tcq_attend_parts', ptr(q), ptr(k_cache), ptr(v_cache), P, ptr(k_new), ptr(v_new), M, heads, D, causal, ptr(part), stream())
+    return part, nc, P + M, causal
+
+
+def prologue_attn(parts, heads, su, q=None, scale=None):
+    """The attention prologue of a one-token product (tcq_prologue with part): the merge of attend_parts' partials of 8
+    heads, then the rotate + quantize of the BF16 row with signs su; q / scale: optional copies of the INT8 row and its
+    scale. Returns (descriptor, K)."""
+    part, nc, keys, causal = parts
+    if part.numel() != nc * heads * (256 + 4):
+        raise ValueError('prologue_attn: the partials of one token')
+    _contig(part, su, q, scale)
+    st = _lib.Prologue(None, 3, 0, 0, None, None, None, None, None, None, None, 0.0, ptr(su), ptr(q), ptr(scale), ptr(part), nc, keys,
+                       causal, heads)
+    return st, heads * 256
+
+
 def attend_static(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None, o=None, su=None, q8=None, scale=None, q4=None):
     """attend without a workspace allocation: the library's own per-device scratch array (tcq_attend_q4_static). For code
     that must not allocate (e.g. under graph capture); calls that overlap on one device race."""

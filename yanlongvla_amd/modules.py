@@ -32,7 +32,7 @@ from . import tcq_format as F
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
 STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0,
-             layer_prologues=0, pre_prologues=0, deferred_outputs=0)
+             layer_prologues=0, pre_prologues=0, deferred_outputs=0, attn_prologues=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
 # layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
@@ -40,8 +40,9 @@ STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chain
 # prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch;
 # pre_prologue: after the spread middle the down projection's rotate + quantize runs inside its product's launch;
 # defer: inside deferred_outputs(), a layer's down epilogue + the next layer's norm1 prologue run in the next q/k/v product
+# attn_prologue: at one token the attention's chunk merge + o rotate + quantize run inside the o product's launch
 FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True,
-            pre_prologue=True, defer=True)
+            pre_prologue=True, defer=True, attn_prologue=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -558,6 +559,13 @@ class KDecoderLayer(torch.nn.Module):
         return (FUSE['prologue'] and z.dtype == torch.int32 and z.shape[-2] == 1 and og.bias is None and not og.one_sided
                 and og.Ntot == 2048 and gu.K == 2048 and gu.a8 and gu.spreads(1))
 
+    def _attn_prologue_fits(self, M, q, og):
+        """Whether the attention's merge + o rotate + quantize can run as the prologue of the o product (tcq_gemm_*_pro with
+        part): one token, a device attention with the split entry, 8 heads of 256 (2048-wide o input), plain signs."""
+        a = self.self_attn
+        return (FUSE['attn_prologue'] and M == 1 and hasattr(a, 'core_parts') and a._device(q) and getattr(a, 'heads', 0) == 8
+                and og.K == 2048 and og.a8 and og.col_scale is None and og.k_parts(M) <= 2)
+
     @staticmethod
     def _unscaled(acc, b, group):
         """(token scales, row scales) the epilogue applies to acc: none for FP32 z, else the quantizer's and the group's."""
@@ -587,12 +595,19 @@ class KDecoderLayer(torch.nn.Module):
                 STATS['chained_prologues'] += 1
             z1 = qkv.product(b)
         q, k, v = qkv.posts(z1, b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
-        if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
-            b2 = og.buffers(M, dev)
-            self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
+        if self._attn_prologue_fits(M, q, og):
+            # one token: the attention's chunk merge + o rotate + quantize run inside the o product's launch
+            parts = self.self_attn.core_parts(q, k, v, cache_k, cache_v, causal_offset)
+            b2 = dict(q=None, q4=None, scale=torch.empty(M, dtype=torch.float32, device=dev))
+            z = og.product(None, og.k_parts(M), pro=kernels.prologue_attn(parts, self.self_attn.heads, og.su, scale=b2['scale']))
+            STATS['attn_prologues'] += 1
         else:
-            b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
-        z = og.product(b2, og.k_parts(M))
+            if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
+                b2 = og.buffers(M, dev)
+                self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
+            else:
+                b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
+            z = og.product(b2, og.k_parts(M))
         x3 = torch.empty_like(x2)
         if self._prologue_fits(z, og, gu):
             # one token: the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
