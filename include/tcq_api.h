@@ -261,6 +261,16 @@ int tcq_attend_chunks(int P, int M);
  * reference counterpart (the reference leaves attention to PyTorch). */
 int tcq_attend_parts(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M,
                      int H, int D, int causal_offset, float* part, tcq_stream_t stream);
+/* tcq_post_group of a one-token q / k / v product with FP32 z (acc_dtype TCQ_F32, no bias, output rotations on) followed
+ * by tcq_attend_parts, in one launch: z_q (2048 = 8 heads x 256), z_k, z_v (256 each) the product's FP32 row segments
+ * (16-byte aligned), sv_q / sv_k / sv_v their signs (8-byte aligned); q_t = bf16((walsh(z_t) * c_t) * sv_t), c_t =
+ * 1 / sqrt(n_t), exactly as tcq_post_group. The new key and value rows are written to k_out / v_out (256 BF16 each, e.g.
+ * row P of a preallocated cache) and take part as key P; the query row exists only inside the launch. part as
+ * tcq_attend_parts with M = 1, H = 8, D = 256. No reference counterpart: it fuses the q / k / v epilogue
+ * (kernels.postg, deploy/tcq_kernels/kernels.py:249-261) into this library's attention. */
+int tcq_attend_post_parts(const float* z_q, const float* z_k, const float* z_v, const int8_t* sv_q, const int8_t* sv_k,
+                          const int8_t* sv_v, const void* k_cache, const void* v_cache, int P, void* k_out, void* v_out, int H, int D,
+                          int causal_offset, float* part, tcq_stream_t stream);
 int tcq_attend(const void* q, const void* k_cache, const void* v_cache, int P, const void* k_new, const void* v_new, int M, int H,
                int D, int causal_offset, float* part, void* o, const int8_t* su, int8_t* q8, float* scale, tcq_stream_t stream);
 /* tcq_attend whose prologue also writes the q4 output of the quantizing entry points (q4, ldq as tcq_pre; q8 may then be

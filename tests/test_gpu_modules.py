@@ -218,16 +218,18 @@ def test_chained_prologues_bitexact(part):
 
 @pytest.mark.parametrize('runtime', ['fly', 'resident'])
 @pytest.mark.parametrize('flag,stat', [('prologue', 'layer_prologues'), ('pre_prologue', 'pre_prologues'),
-                                       ('defer', 'deferred_outputs'), ('attn_prologue', 'attn_prologues')])
+                                       ('defer', 'deferred_outputs'), ('attn_prologue', 'attn_prologues'),
+                                       ('attn_post', 'attn_posts')])
 def test_prologues_in_the_mlp_products_bitexact(runtime, flag, stat):
     """At one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
     (FUSE['prologue']), the down projection's rotate + quantize inside the down product's (FUSE['pre_prologue']), and,
     in the decode loop, a layer's down epilogue + residual + the next layer's norm1 prologue inside the next q/k/v
     product's (FUSE['defer']), and the attention's chunk merge + o rotate + quantize inside the o product's
-    (FUSE['attn_prologue']): a 3-layer backbone's decode steps give the hidden states and key / value rows of the separate
+    (FUSE['attn_prologue']), with the q/k/v epilogue inside the attention's (FUSE['attn_post']): a 3-layer backbone's
+    decode steps give the hidden states and key / value rows of the separate
     launches bit for bit. The MLP forms are taken at every layer of every step on the fly runtime's spread middle (the
-    resident runtime keeps the separate launches); the deferred output at every layer boundary and the attention prologue
-    at every layer of both runtimes."""
+    resident runtime keeps the separate launches); the deferred output at every layer boundary and the attention forms at
+    every layer of both runtimes."""
     from yanlongvla_amd import gemma, modules
     model = gemma.make_policy(gemma.BackbonePolicy, DEV, seed=5, layers=3, vocab=512)
     modules.install(model, runtime=runtime, layers=gemma.synthetic_layers(model, 15, DEV))
@@ -245,7 +247,7 @@ def test_prologues_in_the_mlp_products_bitexact(runtime, flag, stat):
             taken[fuse] = modules.STATS[stat] - before
         finally:
             modules.FUSE[flag] = True
-    expect = 2 * 2 if flag == 'defer' else 2 * 3 if (flag == 'attn_prologue' or runtime == 'fly') else 0
+    expect = 2 * 2 if flag == 'defer' else 2 * 3 if (flag in ('attn_prologue', 'attn_post') or runtime == 'fly') else 0
     assert taken == {False: 0, True: expect}
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)

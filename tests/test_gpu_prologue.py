@@ -199,3 +199,35 @@ def test_product_with_attention_prologue(resident, parts, P, causal):
     torch.cuda.synchronize()
     assert torch.equal(q2.cpu(), q8.cpu()) and torch.equal(bits(sc2), bits(sc))
     assert torch.equal(a_pro.cpu(), a_ref.cpu())
+
+
+@pytest.mark.parametrize('P,causal', [(831, None), (831, 831), (64, 64), (127, 127), (0, None), (2000, 1500)])
+def test_attention_with_qkv_epilogue(P, causal):
+    """tcq_attend_post_parts: the q / k / v epilogue of one FP32 product row (output rotations 2048 / 256 / 256 wide, signs,
+    BF16) inside the attention's launch. The new key / value rows equal tcq_post_group's, and the chunk partials the merge
+    reads (o, m, l of every visible chunk and head) equal tcq_attend_parts' on tcq_post_group's q / k / v, bit for bit: the
+    new row first, last and inside its chunk, no cached rows, and a causal offset that hides the new row's chunk (its
+    workgroup still writes the rows)."""
+    from yanlongvla_amd import kernels as Kn
+    H, D = 8, 256
+    g = torch.Generator(device=DEV).manual_seed(P + 3)
+    z = torch.randn(1, H * D + 2 * D, generator=g, device=DEV) * 3
+    sv = signs(g, H * D + 2 * D)
+    kc = torch.randn(P, D, generator=g, device=DEV).bfloat16() if P else None
+    vc = torch.randn(P, D, generator=g, device=DEV).bfloat16() if P else None
+    cols = [(0, H * D), (H * D, D), (H * D + D, D)]
+    ys = [torch.empty(1, n, dtype=torch.bfloat16, device=DEV) for _, n in cols]
+    Kn.post_group([(z, c0, None, sv[c0:c0 + n], None, y, False) for (c0, n), y in zip(cols, ys)], torch.float32, torch.bfloat16,
+                  None, 1)
+    part, nc, keys, cz = Kn.attend_parts(ys[0], kc, vc, ys[1], ys[2], H, causal)
+    kn = torch.full((1, D), float('nan'), device=DEV).bfloat16()
+    vn = torch.full((1, D), float('nan'), device=DEV).bfloat16()
+    part2, nc2, keys2, cz2 = Kn.attend_post_parts(z, [(c0, sv[c0:c0 + n]) for c0, n in cols], kc, vc, kn, vn, H, causal)
+    torch.cuda.synchronize()
+    assert (nc2, keys2, cz2) == (nc, keys, cz)
+    assert torch.equal(bits(kn), bits(ys[1])) and torch.equal(bits(vn), bits(ys[2]))
+    T = P + 1
+    nv = nc if causal is None else min(nc, (min(T, causal + 1) + 63) // 64)
+    a = part.view(nc, H, D + 4)[:nv, :, :D + 2]
+    b = part2.view(nc, H, D + 4)[:nv, :, :D + 2]
+    assert torch.equal(bits(b), bits(a))

@@ -72,6 +72,7 @@ SIGNATURES = {
     'tcq_gemm_tcq_pro': [_P, _I, _P, _I, _I, _I, _P],
     'tcq_gemm_w8_pro': [_P, _I, _P, _I, _I, _I, _P],
     'tcq_attend_parts': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P],
+    'tcq_attend_post_parts': [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _P],
 }
 _RESTYPE = {'tcq_version': ctypes.c_char_p, 'tcq_repack_words': _L, 'tcq_attend_static_floats': ctypes.c_size_t}
 

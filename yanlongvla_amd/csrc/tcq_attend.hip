@@ -40,53 +40,140 @@ __device__ __forceinline__ float4_t mma_bf16(uint4_t a, uint4_t b, float4_t c) {
 // chunk's 64 keys. Outputs on the same MFMA: A = the exponentials e (BF16, rows x keys), B = 16 value columns x 32 keys
 // gathered from the LDS stage; each wave owns 4 of the 16 column tiles, 2 K steps. Element i of lane group lg in K step ks
 // is key 32 ks + lg + 4 i in both operands (any common order of the K index gives the same product).
-template <int TPB>
+// The q / k / v epilogue of a one-token FP32 product row, run by k_attn_part<2, true> instead of a separate launch: the
+// output rotations y = bf16((walsh(z) * c) * sv), c = 1 / sqrt(n), of the q segment (8 heads x 256, 2048 wide) in every
+// workgroup and of the new key / value rows (256 wide each) in the workgroup whose chunk holds key P, which also stores
+// them at k_out / v_out (the cache row P). The same stages in the same order as the epilogue kernel (k_postg_tw), so the
+// same bits.
+struct AttnPost {
+    const float* zq;
+    const float* zk;
+    const float* zv;
+    const i8* sq;
+    const i8* sk;
+    const i8* sv;
+    u16* k_out;
+    u16* v_out;
+};
+
+// POST (M = 1, H = 8): q, kn and vn are not read; the query row and the new key / value row come from AttnPost.
+template <int TPB, bool POST = false>
 __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, const u16* vc, int P, const u16* kn, const u16* vn,
-                                                  int M, int H, int causal, float* part) {
+                                                  int M, int H, int causal, float* part, AttnPost ap) {
     constexpr int AR = 8 * TPB, RB = AR / 16, QST = AD + 8;       // query rows, MFMA row blocks, padded row stride (u16)
+    constexpr int QW = 2048 + 64 + 1;                             // lds_words(2048): the q rotation's exchange row
     __shared__ float ps[AR][KC + 1];
     __shared__ __attribute__((aligned(16))) u16 vs[KC][VST];
     __shared__ __attribute__((aligned(16))) u16 qs[AR][QST];
+    __shared__ float xq[POST ? QW : 1];
+    __shared__ __attribute__((aligned(16))) u16 kns[POST ? AD : 8];
     const int t0 = TPB * blockIdx.x, c = blockIdx.y, NC = gridDim.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int T = P + M, j0 = c * KC;
     auto visible_end = [&](int t) { return min(T, causal >= 0 ? causal + t + 1 : T); };   // keys j < end are visible to t
     const int jend = visible_end(min(t0 + TPB, M) - 1);                 // the group's last token sees the most keys
     const float scl = 1.f / 16.f;                                       // 1 / sqrt(256), exact
-    if (j0 >= jend) return;                                             // no key of the chunk is visible to the group; the
+    const bool fresh = POST && j0 <= P && P < j0 + KC;                  // POST: this workgroup makes the new key / value row
+    if (j0 >= jend && !fresh) return;                                   // no key of the chunk is visible to the group; the
                                                                         // combine never reads its slots (visible_chunks)
-    // value stage (64 rows x 256 dims, 8 granules of 16 bytes per thread) and query rows (AR x 256), issued first
+    // POST: this thread's 8 values of the q segment and their signs, and (threads 0 .. 31 of the fresh workgroup) of the
+    // key and value segments, issued first
+    float zq[8] = {}, zk[8] = {}, zv[8] = {};
+    u64 gq = 0, gk = 0, gv = 0;
+    if constexpr (POST) {
+        const uint4_t* zp = (const uint4_t*)(ap.zq + 8 * tid);
+        const uint4_t a = gptr(zp)[0], b = gptr(zp)[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { zq[k] = __uint_as_float(a[k]); zq[4 + k] = __uint_as_float(b[k]); }
+        gq = gptr((const u64*)(ap.sq + 8 * tid))[0];
+        if (fresh && tid < AD / 8) {
+            const uint4_t* kp = (const uint4_t*)(ap.zk + 8 * tid);
+            const uint4_t* vp = (const uint4_t*)(ap.zv + 8 * tid);
+            const uint4_t ka = gptr(kp)[0], kb = gptr(kp)[1], va = gptr(vp)[0], vb = gptr(vp)[1];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                zk[k] = __uint_as_float(ka[k]); zk[4 + k] = __uint_as_float(kb[k]);
+                zv[k] = __uint_as_float(va[k]); zv[4 + k] = __uint_as_float(vb[k]);
+            }
+            gk = gptr((const u64*)(ap.sk + 8 * tid))[0];
+            gv = gptr((const u64*)(ap.sv + 8 * tid))[0];
+        }
+    }
+    // value stage (64 rows x 256 dims, 8 granules of 16 bytes per thread) and query rows (AR x 256), issued first (POST:
+    // the new row P is staged by its maker below)
     uint4_t vg[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int gi = u * AT + tid, row = gi >> 5, col = gi & 31, j = j0 + row;
-        vg[u] = j < jend ? gptr((const uint4_t*)(key_row(vc, vn, P, j) + 8 * col))[0] : uint4_t{0, 0, 0, 0};
+        vg[u] = j < jend && !(POST && j >= P) ? gptr((const uint4_t*)(key_row(vc, vn, P, j) + 8 * col))[0] : uint4_t{0, 0, 0, 0};
     }
     constexpr int QG = AR * 32 / AT;                                    // 16-byte query granules per thread
     uint4_t qg[QG];
 #pragma unroll
     for (int u = 0; u < QG; ++u) {
         const int gi = u * AT + tid, row = gi >> 5, col = gi & 31, t = t0 + (row >> 3), h = row & 7;
-        qg[u] = (h < H && t < M) ? gptr((const uint4_t*)(q + ((size_t)t * H + h) * AD + 8 * col))[0] : uint4_t{0, 0, 0, 0};
+        qg[u] = (!POST && h < H && t < M) ? gptr((const uint4_t*)(q + ((size_t)t * H + h) * AD + 8 * col))[0] : uint4_t{0, 0, 0, 0};
     }
-    // this lane's key (B column) for the scores: its 8 fragments straight into registers
+    // this lane's key (B column) for the scores: its 8 fragments straight into registers (POST: the new key from LDS later)
     const int jk = j0 + 16 * wave + lr;
     const bool kv = jk < jend;
-    const u16* kr = kv ? key_row(kc, kn, P, jk) : nullptr;
+    const bool kl = kv && !(POST && jk >= P);
+    const u16* kr = kl ? key_row(kc, kn, P, jk) : nullptr;
     uint4_t B[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) B[ks] = kv ? gptr((const uint4_t*)(kr + 32 * ks + 8 * lg))[0] : uint4_t{0, 0, 0, 0};
+    for (int ks = 0; ks < 8; ++ks) B[ks] = kl ? gptr((const uint4_t*)(kr + 32 * ks + 8 * lg))[0] : uint4_t{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < QG; ++u) {
         const int gi = u * AT + tid;
-        *(uint4_t*)&qs[gi >> 5][8 * (gi & 31)] = qg[u];
+        if (!POST || (gi >> 5) >= 8) *(uint4_t*)&qs[gi >> 5][8 * (gi & 31)] = qg[u];   // POST: rows 0 .. 7 made below
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int gi = u * AT + tid;
-        *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = vg[u];
+        if (!(fresh && j0 + (gi >> 5) == P)) *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = vg[u];
+    }
+    if constexpr (POST) {
+        if (fresh) {                                                    // uniform: the new key / value rows
+            float* xa = &ps[0][0];                                      // 2 x lds_words(256) floats, free until the scores
+            float* xb = xa + (AD + AD / 32 + 1);
+            tw_walsh2<8, 3>(zk, zv, xa, xb);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) { zk[k] = zk[k] * scl; zv[k] = zv[k] * scl; }   // c = 1 / sqrt(256)
+            tw_to_natural2<8, 3>(zk, zv, xa, xb);
+            if (tid < AD / 8) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    zk[k] = zk[k] * (float)(i8)(gk >> (8 * k));
+                    zv[k] = zv[k] * (float)(i8)(gv >> (8 * k));
+                }
+                u32 wk[4], wv[4];
+                bf16_pack<4>(zk, wk);
+                bf16_pack<4>(zv, wv);
+                const uint4_t kk = {wk[0], wk[1], wk[2], wk[3]}, vv = {wv[0], wv[1], wv[2], wv[3]};
+                gptr((uint4_t*)(ap.k_out + 8 * tid))[0] = kk;
+                gptr((uint4_t*)(ap.v_out + 8 * tid))[0] = vv;
+                *(uint4_t*)&kns[8 * tid] = kk;
+                *(uint4_t*)&vs[P - j0][8 * tid] = P < jend ? vv : uint4_t{0, 0, 0, 0};
+            }
+            if (j0 >= jend) return;                                     // uniform: no visible key in the chunk
+            // (xa / xb are next written as ps after the barriers of the q rotation below)
+        }
+        tw_walsh<11, 3>(zq, xq);
+        const float cq = (float)(1.0 / __builtin_sqrt(2048.0));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) zq[k] = zq[k] * cq;
+        tw_to_natural<11, 3>(zq, xq);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) zq[k] = zq[k] * (float)(i8)(gq >> (8 * k));
+        u32 w[4];
+        bf16_pack<4>(zq, w);
+        *(uint4_t*)&qs[tid >> 5][8 * (tid & 31)] = uint4_t{w[0], w[1], w[2], w[3]};   // head tid / 32, dims 8 (tid % 32) ..
     }
     __syncthreads();
+    if (POST && kv && jk >= P) {                                        // the new key's fragments, staged above
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) B[ks] = *(const uint4_t*)&kns[32 * ks + 8 * lg];
+    }
     // scores of every row block against this wave's 16 keys
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -409,7 +496,7 @@ extern "C" int tcq_attend_q4(const void* q, const void* k_cache, const void* v_c
     // token pairs (16 MFMA rows): measured on MI355X at 50 tokens x 850 keys, 2 tokens per group run 12.5 us, 4 run 13.6 us
     // and 8 run 20 us (fewer, longer groups); single tokens (8 rows, half the MFMA rows empty) match pairs
     launch_k(k_attn_part<2>, dim3((M + 1) / 2, NC), dim3(AT), 0, st, (const u16*)q, (const u16*)k_cache, (const u16*)v_cache, P,
-             (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
+             (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part, AttnPost{});
     // combine: one wave per head with every load at entry (8-byte aligned o, 4-byte aligned su), else the register path for
     // H * AD of 1024 / 2048 (16-byte aligned outputs), else 1024 threads over LDS
     const bool oal = (!o || (uintptr_t)o % 16 == 0) && (!su || ((uintptr_t)su % 16 == 0 && (uintptr_t)q8 % 16 == 0));
@@ -435,7 +522,25 @@ extern "C" int tcq_attend_parts(const void* q, const void* k_cache, const void* 
     const int NC = tcq_attend_chunks(P, M);
     if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
     launch_k(k_attn_part<2>, dim3((M + 1) / 2, NC), dim3(AT), 0, (hipStream_t)stream, (const u16*)q, (const u16*)k_cache,
-             (const u16*)v_cache, P, (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part);
+             (const u16*)v_cache, P, (const u16*)k_new, (const u16*)v_new, M, H, causal_offset, part, AttnPost{});
+    return launch_status();
+}
+
+extern "C" int tcq_attend_post_parts(const float* z_q, const float* z_k, const float* z_v, const int8_t* sv_q, const int8_t* sv_k,
+                                     const int8_t* sv_v, const void* k_cache, const void* v_cache, int P, void* k_out, void* v_out,
+                                     int H, int D, int causal_offset, float* part, tcq_stream_t stream) {
+    if (!z_q || !z_k || !z_v || !sv_q || !sv_k || !sv_v || !k_out || !v_out || !part || P < 0 || (P > 0 && (!k_cache || !v_cache)))
+        return TCQ_ERR_ARG;
+    if (D != AD || H != AH) return TCQ_ERR_UNSUPPORTED;
+    if ((uintptr_t)z_q % 16 || (uintptr_t)z_k % 16 || (uintptr_t)z_v % 16 || (uintptr_t)sv_q % 8 || (uintptr_t)sv_k % 8 ||
+        (uintptr_t)sv_v % 8 || (uintptr_t)k_out % 16 || (uintptr_t)v_out % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
+        (uintptr_t)part % 16)
+        return TCQ_ERR_ALIGN;
+    const int NC = tcq_attend_chunks(P, 1);
+    if (NC > MAXC) return TCQ_ERR_UNSUPPORTED;
+    const AttnPost ap = {z_q, z_k, z_v, (const i8*)sv_q, (const i8*)sv_k, (const i8*)sv_v, (u16*)k_out, (u16*)v_out};
+    launch_k(k_attn_part<2, true>, dim3(1, NC), dim3(AT), 0, (hipStream_t)stream, (const u16*)nullptr, (const u16*)k_cache,
+             (const u16*)v_cache, P, (const u16*)nullptr, (const u16*)nullptr, 1, H, causal_offset, part, ap);
     return launch_status();
 }
 

@@ -276,6 +276,27 @@ def attend_parts(q, k_cache, v_cache, k_new, v_new, heads, causal_offset=None):
     return part, nc, P + M, causal
 
 
+def attend_post_parts(z, segments, k_cache, v_cache, k_out, v_out, heads, causal_offset=None):
+    """The q / k / v epilogue of a one-token FP32 product row z (1, ldz) and attend_parts in one launch
+    (tcq_attend_post_parts): segments = ((col0, sv) of q, of k, of v); the new key / value rows go to k_out / v_out
+    ((1, 256) BF16, e.g. row P of a cache). Returns (part, chunks, keys, causal) for prologue_attn."""
+    if z.dtype != torch.float32 or z.dim() != 2 or z.shape[0] != 1:
+        raise TypeError('attend_post_parts: one FP32 row of z')
+    for t in (k_cache, v_cache, k_out, v_out):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError('attend_post_parts: BF16 cache and outputs')
+    _contig(z, k_cache, v_cache, k_out, v_out, *(sv for _, sv in segments))
+    P = 0 if k_cache is None else k_cache.shape[0]
+    D = k_out.shape[-1]
+    nc = int(_lib.lib().tcq_attend_chunks(P, 1))
+    part = torch.empty(nc * heads * (D + 4), dtype=torch.float32, device=z.device)
+    causal = -1 if causal_offset is None else int(causal_offset)
+    zp = [z.data_ptr() + 4 * c0 for c0, _ in segments]
+    call('tcq_attend_post_parts', *zp, *(ptr(sv) for _, sv in segments), ptr(k_cache), ptr(v_cache), P, ptr(k_out), ptr(v_out),
+         heads, D, causal, ptr(part), stream())
+    return part, nc, P + 1, causal
+
+
 def prologue_attn(parts, heads, su, q=None, scale=None):
     """The attention prologue of a one-token product (tcq_prologue with part): the merge of attend_parts' partials of 8
     heads, then the rotate + quantize of the BF16 row with signs su; q / scale: optional copies of the INT8 row and its

@@ -32,7 +32,7 @@ from . import tcq_format as F
 RUNTIMES = ('dense', 'reference', 'resident', 'fly', 'hybrid')
 GROUPS = (('q_proj', 'k_proj', 'v_proj'), ('gate_proj', 'up_proj'))
 STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chained_prologues=0, spread_middles=0,
-             layer_prologues=0, pre_prologues=0, deferred_outputs=0, attn_prologues=0)
+             layer_prologues=0, pre_prologues=0, deferred_outputs=0, attn_prologues=0, attn_posts=0)
 # mlp: KGatedMLP / KPlainMLP; split: gated-MLP middle as postg + pre2 instead of one mid2 launch; layer: KDecoderLayer (norms
 # and residual adds fused into the prologues / epilogues); chain: a decoder layer's last epilogue also computes the next
 # layer's norm + rotate + quantize prologue; spread: the 16384-wide gated-MLP middle of few tokens spread over many CUs
@@ -40,9 +40,10 @@ STATS = dict(group_runs=0, regroup_misses=0, fused_mlps=0, fused_layers=0, chain
 # prologue: at one token the o epilogue + residual + norm2 + rotate + quantize run inside the gate/up product's launch;
 # pre_prologue: after the spread middle the down projection's rotate + quantize runs inside its product's launch;
 # defer: inside deferred_outputs(), a layer's down epilogue + the next layer's norm1 prologue run in the next q/k/v product
-# attn_prologue: at one token the attention's chunk merge + o rotate + quantize run inside the o product's launch
+# attn_prologue: at one token the attention's chunk merge + o rotate + quantize run inside the o product's launch;
+# attn_post: with it, the q/k/v epilogue (output rotations, the new key / value rows) runs inside the attention's launch
 FUSE = dict(post3=True, mlp=True, split=False, layer=True, chain=True, k_parts=True, spread=True, prologue=True,
-            pre_prologue=True, defer=True, attn_prologue=True)
+            pre_prologue=True, defer=True, attn_prologue=True, attn_post=True)
 SMALL_M = 64                                         # most tokens of the small-M products
 
 
@@ -561,10 +562,25 @@ class KDecoderLayer(torch.nn.Module):
 
     def _attn_prologue_fits(self, M, q, og):
         """Whether the attention's merge + o rotate + quantize can run as the prologue of the o product (tcq_gemm_*_pro with
-        part): one token, a device attention with the split entry, 8 heads of 256 (2048-wide o input), plain signs."""
+        part): one token, a device attention with the split entry, 8 heads of 256 (2048-wide o input), plain signs. q: the
+        BF16 query rows (None: the device attention is taken as given)."""
         a = self.self_attn
-        return (FUSE['attn_prologue'] and M == 1 and hasattr(a, 'core_parts') and a._device(q) and getattr(a, 'heads', 0) == 8
+        return (FUSE['attn_prologue'] and M == 1 and hasattr(a, 'core_parts') and (q is None or a._device(q))
+                and getattr(a, 'heads', 0) == 8 and getattr(a, 'head_dim', 0) == 256
                 and og.K == 2048 and og.a8 and og.col_scale is None and og.k_parts(M) <= 2)
+
+    def _attn_post_fits(self, M, z1, qkv, og, cache_k, cache_v):
+        """Whether the q/k/v epilogue can run inside the attention's launch as well (tcq_attend_post_parts), with the merge in
+        the o product's prologue: the attention prologue's conditions, FP32 z of a two-sided q | k | v group of widths
+        2048, 256, 256 without biases, and a contiguous BF16 cache."""
+        if not (FUSE['attn_post'] and z1.is_cuda and z1.dtype == torch.float32 and z1.dim() == 2 and z1.is_contiguous()
+                and self._attn_prologue_fits(M, None, og) and not qkv.one_sided):
+            return False
+        segs = qkv.segments
+        if [s.width for s in segs] != [2048, 256, 256] or any(s.bias is not None for s in segs):
+            return False
+        return all(c is None or (c.dtype == torch.bfloat16 and c.is_contiguous() and c.dim() == 2 and c.shape[-1] == 256)
+                   for c in (cache_k, cache_v))
 
     @staticmethod
     def _unscaled(acc, b, group):
@@ -594,20 +610,35 @@ class KDecoderLayer(torch.nn.Module):
             else:
                 STATS['chained_prologues'] += 1
             z1 = qkv.product(b)
-        q, k, v = qkv.posts(z1, b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
-        if self._attn_prologue_fits(M, q, og):
-            # one token: the attention's chunk merge + o rotate + quantize run inside the o product's launch
-            parts = self.self_attn.core_parts(q, k, v, cache_k, cache_v, causal_offset)
+        if self._attn_post_fits(M, z1, qkv, og, cache_k, cache_v):
+            # one token: the q/k/v epilogue runs inside the attention's launch (the query row never leaves it; the new key /
+            # value rows go to kv_out), the chunk merge + o rotate + quantize inside the o product's launch
+            a = self.self_attn
+            kn, vn = kv_out if kv_out is not None else [torch.empty(M, s.width, dtype=torch.bfloat16, device=dev)
+                                                        for s in qkv.segments[1:]]
+            parts = kernels.attend_post_parts(z1, [(s.col0, s.sv) for s in qkv.segments], cache_k, cache_v, kn, vn, a.heads,
+                                              causal_offset)
+            k, v = kn.reshape(*shape[:-1], kn.shape[-1]), vn.reshape(*shape[:-1], vn.shape[-1])
             b2 = dict(q=None, q4=None, scale=torch.empty(M, dtype=torch.float32, device=dev))
-            z = og.product(None, og.k_parts(M), pro=kernels.prologue_attn(parts, self.self_attn.heads, og.su, scale=b2['scale']))
+            z = og.product(None, og.k_parts(M), pro=kernels.prologue_attn(parts, a.heads, og.su, scale=b2['scale']))
+            STATS['attn_posts'] += 1
             STATS['attn_prologues'] += 1
         else:
-            if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
-                b2 = og.buffers(M, dev)
-                self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'], q4=b2['q4'])
+            q, k, v = qkv.posts(z1, b, x2.shape, outs=None if kv_out is None else [None, kv_out[0], kv_out[1]])
+            if self._attn_prologue_fits(M, q, og):
+                # one token: the attention's chunk merge + o rotate + quantize run inside the o product's launch
+                parts = self.self_attn.core_parts(q, k, v, cache_k, cache_v, causal_offset)
+                b2 = dict(q=None, q4=None, scale=torch.empty(M, dtype=torch.float32, device=dev))
+                z = og.product(None, og.k_parts(M), pro=kernels.prologue_attn(parts, self.self_attn.heads, og.su, scale=b2['scale']))
+                STATS['attn_prologues'] += 1
             else:
-                b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
-            z = og.product(b2, og.k_parts(M))
+                if hasattr(self.self_attn, 'core_quantized') and self.self_attn._device(q):
+                    b2 = og.buffers(M, dev)
+                    self.self_attn.core_quantized(q, k, v, cache_k, cache_v, causal_offset, og.su, b2['q'], b2['scale'],
+                                                  q4=b2['q4'])
+                else:
+                    b2 = og.quantize(og.prep(self.self_attn.core(q, k, v, cache_k, cache_v, causal_offset)))
+                z = og.product(b2, og.k_parts(M))
         x3 = torch.empty_like(x2)
         if self._prologue_fits(z, og, gu):
             # one token: the o epilogue + residual + norm2 + rotate + quantize run inside the gate | up product's launch
