@@ -24,9 +24,10 @@ __device__ __forceinline__ int visible_chunks(int NC, int T, int causal, int t) 
 // BF16 row times su goes to xs (natural slots) for the rotate + quantize that follows, and the function ends with a
 // barrier; without su it returns false (uniform) and there is no barrier. Waves from H on take no part in the merge.
 // mid() runs once the entry loads have been consumed.
+// vr (H = 8): instead of xs, the thread's four values (dims 4 l .. of head h: row values 4 tid ..) go to vr, with no barrier.
 template <class F>
 __device__ __forceinline__ bool combine_w_row(const float* part, int NC, int T, int causal, int H, int t, u16* o, const i8* su,
-                                              float* xs, float (*wts)[MAXC], F&& mid) {
+                                              float* xs, float (*wts)[MAXC], F&& mid, float* vr = nullptr) {
     const int tid = threadIdx.x, h = tid >> 6, lane = tid & 63, g = lane & 15, d0 = 4 * lane, K = H * AD;
     const bool on = h < H;                                               // whole waves
     const size_t cs = (size_t)H * PS;
@@ -79,6 +80,12 @@ __device__ __forceinline__ bool combine_w_row(const float* part, int NC, int T, 
     for (int k = 0; k < 4; ++k) b[k] = f32_to_bf16(acc[k] / L);
     if (on && o) *gptr((u64*)(o + (size_t)t * K + h * AD + d0)) = (u64)b[0] | ((u64)b[1] << 16) | ((u64)b[2] << 32) | ((u64)b[3] << 48);
     if (!su) return false;                                               // uniform
+    if (vr) {                                                            // the caller's registers: values 4 tid .. 4 tid + 3
+        const u32 sg = on ? *gptr((const u32*)(su + h * AD + d0)) : 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) vr[k] = bf16_to_f32(b[k]) * (float)(i8)(sg >> (8 * k));
+        return true;
+    }
     if (on) {
         const u32 sg = *gptr((const u32*)(su + h * AD + d0));
 #pragma unroll

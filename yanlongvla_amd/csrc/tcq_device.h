@@ -19,6 +19,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef int int4_t __attribute__((ext_vector_type(4)));
 typedef u32 uint4_t __attribute__((ext_vector_type(4)));
+typedef u32 uint2_t __attribute__((ext_vector_type(2)));
 typedef u16 u16x2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------------------------------------------------ conversions
@@ -452,6 +453,53 @@ __device__ __forceinline__ void tw_walsh2(float (&a)[1 << LE], float (&b)[1 << L
     tw_get<L, LE, 2>(b, xb);
     butterflies<LE>(a);
     butterflies<LE>(b);
+}
+
+// Walsh of a row of 2^(LE + 6) * NWP values held 2^LE per thread by waves 0 .. NWP - 1 (NWP = 4 or 8; thread t = 64 w + l:
+// values 2^LE t .. in natural layout, which they keep): index bits [0, LE) inside the thread, [LE, LE + 6) across the
+// lanes (lane_xor), the last log2(NWP) across the waves through xs (2^LE * 64 * NWP floats of LDS, value k of thread (w, l)
+// at [(NWP k + w) * 64 + l]) after one sync() (a barrier these waves meet; a caller's other waves may meet it too). Each
+// wave evaluates the butterflies its own values need (wave-uniform choices). Every stage is the (a + b, a - b) butterfly in
+// ascending stage order, as in tw_walsh, so the sums are equal bit for bit. xs may be written again once every wave has
+// passed a later sync().
+template <int LE, int NWP, class SY>
+__device__ __forceinline__ void wave_walsh(float (&v)[1 << LE], float* xs, SY&& sync) {
+    static_assert(NWP == 4 || NWP == 8, "four or eight waves");
+    constexpr int E = 1 << LE;
+    butterflies<LE>(v);
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {
+        const int m = 1 << s;
+        const bool upper = lane & m;
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float p = lane_xor(v[k], m, lane);
+            v[k] = upper ? p - v[k] : v[k] + p;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < E; ++k) xs[(NWP * k + w) * 64 + lane] = v[k];
+    sync();
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        const float* xk = xs + NWP * k * 64 + lane;
+        // y1(j): stage 1 value at wave position j (lower keeps a + b, upper gets a - b of lower a, upper b)
+        auto y1 = [&](int j) {
+            const float a = xk[64 * (j & ~1)], b = xk[64 * (j | 1)];
+            return (j & 1) ? a - b : a + b;
+        };
+        auto y2 = [&](int j) {
+            const float a = y1(j & ~2), b = y1(j | 2);
+            return (j & 2) ? a - b : a + b;
+        };
+        if constexpr (NWP == 4) {
+            v[k] = y2(w);
+        } else {
+            const float a = y2(w & ~4), b = y2(w | 4);
+            v[k] = (w & 4) ? a - b : a + b;
+        }
+    }
 }
 
 // Last layout (C, or D for four passes) -> layout A through xs (own slots first, one barrier).

@@ -100,15 +100,30 @@ struct ProLds {
     __attribute__((aligned(16))) u32 qs[N / 4];
     float sc;
     float wts[PL == PRO_ATTN ? AH : 1][MAXC];
+    WavesLds wl[PL == PRO_PRE ? 0 : 1];                                  // the eight-wave engine's exchange (NWP = 8)
 };
 
 // Runs the prologue and leaves the INT8 row and the scale in L; workgroup (0, 0, 0) stores the side outputs (xout, the
 // optional q / scale copies). Every thread of the workgroup calls it; mid() issues the product's weight loads once the
 // prologue's entry loads have been consumed, so their HBM latency runs under the prologue.
-template <int PL, class F>
+// NWP = 8 (workgroups of exactly eight waves; the layer and attention prologues): the 2048-wide row on all eight waves,
+// four values per thread, on panp_waves / waves_rotate_quantize (no LDS transposes); the same row and scale.
+template <int PL, int NWP = 0, class F>
 __device__ __forceinline__ void run_prologue(const SegPackPro& P, ProLds<PL>& L, F&& mid) {
     constexpr int NL = ProShape<PL>::L, LE = ProShape<PL>::LE;
     const bool store = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+    if constexpr (NWP == 8) {
+        static_assert(PL == PRO_LAYER || PL == PRO_ATTN, "eight-wave prologue: 2048-wide rows");
+        const auto bar = [] { __syncthreads(); };
+        float v[4];
+        if constexpr (PL == PRO_LAYER) {
+            panp_waves<TCQ_I32, 8>(P.a, store, v, L.wl[0], mid, bar);
+        } else {
+            combine_w_row(P.part, P.nc, P.keys, P.causal, P.heads, 0, nullptr, P.a.su, L.xs, L.wts, mid, v);   // heads = 8
+        }
+        waves_rotate_quantize<8>(v, L.wl[0], L.qs, &L.sc, store ? P.q : nullptr, store ? P.scale : nullptr, bar);
+        return;
+    }
     float v[1 << LE];
     if constexpr (PL == PRO_LAYER) {
         panp_tw<TCQ_I32, NL, LE, false>(P.a, 0, store, v, L.xs, L.xs + ProLds<PL>::W, L.red, mid);
@@ -235,7 +250,7 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
         }
     }
     if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
-    if constexpr (PL > 0) run_prologue<PL>(P, pro, [&] {
+    if constexpr (PL > 0) run_prologue<PL, PL == PRO_PRE ? 0 : 8>(P, pro, [&] {
         if (c0 + wave < nch) load(c0 + wave);
     });
     __syncthreads();
@@ -339,12 +354,19 @@ constexpr int GV_NW = 16;              // waves per workgroup (one 64 KiB table 
 // stage order, and the block is stored transposed: zt[(t * 128 + o) * (m / 128) + blk] for row 128 blk + o of token t.
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
 // PL > 0: activations from the prologue, as k_gemm_small.
-template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false, int PL = 0>
+// OV (the layer prologue of a 2048-wide row): the prologue runs on waves 0 .. 3 from entry (panp_waves,
+// waves_rotate_quantize, at a raised issue priority) while the other waves fill the table and then decode the weight
+// fragments of their chunks into registers, one chunk after each of the prologue's WAVES_SYNCS barriers (the first of
+// which is also the table's); one more barrier hands the row to every wave for its products. The same row, sums and
+// outputs as without OV.
+template <int ODT, bool QB, int WPR, int NW, int KS = 1, bool LO = false, bool DOT = false, int PL = 0, bool OV = false>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>::type P, const i8* q, const float* s, int M, int K,
                                                       int ldz) {
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     static_assert(PL == 0 || (!QB && !DOT), "prologue: one token");
+    static_assert(!OV || (PL == PRO_LAYER && !DOT && NW >= 4), "overlapped prologue: the layer prologue on four waves");
     __shared__ ProLds<PL ? PL : PRO_LAYER> pro;
+    __shared__ WavesLds qd[1];                                            // OV only
     static_assert(!LO || (ODT == TCQ_F32 && KS == 1 && NW / WPR == 8), "stage-split output: FP32 z, 8 tile rows per workgroup");
     constexpr int RPW = NW / WPR;
     __shared__ __attribute__((aligned(16))) u32 tab[1024 * GV_C];
@@ -370,7 +392,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
             if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
         }
     };
-    if constexpr (!PL) loadW();
+    if constexpr (!PL || OV) loadW();
     auto loadB = [&](int c, int4v* B) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -391,9 +413,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
         rsv = gptr((const float4_t*)(S.rs + 16 * I + 4 * lg))[0];
         if constexpr (!PL) sv = gptr(s)[min(lr, M - 1)];
     }
-    {
+    // the table, filled by threads from t0 on (OV: the decode waves alone; the prologue waves start at once)
+    auto fill_table = [&](int t0) {
         const i8* t8 = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
-        for (int e = threadIdx.x; e < 1024; e += 64 * NW) {
+        for (int e = (int)threadIdx.x - t0; e < 1024; e += 64 * NW - t0) {
             const int h = e & 511;
             int v0 = gptr(t8)[2 * h];
             const int v1 = gptr(t8)[2 * h + 1];
@@ -403,35 +426,79 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
 #pragma unroll
             for (int c = 0; c < GV_C; c += 4) *(uint4_t*)(tab + e * GV_C + c) = uint4_t{vv, vv, vv, vv};
         }
+    };
+    if constexpr (!OV) {
+        fill_table(0);
+        if constexpr (PL > 0) run_prologue<PL>(P, pro, loadW);
+        __syncthreads();
     }
-    if constexpr (PL > 0) run_prologue<PL>(P, pro, loadW);
-    __syncthreads();
-    if constexpr (PL > 0) {
-        if (ODT != TCQ_I32 && part == 0) sv = pro.sc;
-        loadB(c0 + part, Bf[0]);
-    }
+    // the A fragment of one packed word: 16 weights of this lane's row, looked up in the table
+    auto frag = [&](u32 hi) {
+        const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+        u16x2_t a[4];                                                      // pairs p (a[0], a[1]) and p + 4 (a[2], a[3])
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+            a[p >> 1][p & 1] = *(const u16*)((const char*)tab + (((x >> 22) << 6) | cp4));
+            a[2 + (p >> 1)][p & 1] = *(const u16*)((const char*)tab + ((x & 0xFFC0u) | cp4));
+        }
+        return int4v{__builtin_bit_cast(int, a[0]), __builtin_bit_cast(int, a[1]), __builtin_bit_cast(int, a[2]),
+                     __builtin_bit_cast(int, a[3])};
+    };
     int4v acc = int4v{0, 0, 0, 0};
     int dacc[2] = {0, 0};                                                  // DOT: row lr, k-block lg, two chains
+    if constexpr (OV) {
+        int4v Af[CM][4];
+        auto decode = [&](int i) {
+            if (c0 + part + WPR * i < nch) {                               // uniform
 #pragma unroll
-    for (int i = 0; i < CM; ++i) {
-        const int c = c0 + part + WPR * i;
-        if (c >= nch) continue;                                            // uniform
-        if (i + 1 < CM && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32 hi = wa[i][j];
-            const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
-            u16x2_t a[4];                                                  // pairs p (a[0], a[1]) and p + 4 (a[2], a[3])
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
-                a[p >> 1][p & 1] = *(const u16*)((const char*)tab + (((x >> 22) << 6) | cp4));
-                a[2 + (p >> 1)][p & 1] = *(const u16*)((const char*)tab + ((x & 0xFFC0u) | cp4));
+                for (int j = 0; j < 4; ++j) Af[i][j] = frag(wa[i][j]);
             }
-            const int4v A = int4v{__builtin_bit_cast(int, a[0]), __builtin_bit_cast(int, a[1]), __builtin_bit_cast(int, a[2]),
-                                  __builtin_bit_cast(int, a[3])};
-            if constexpr (DOT) dacc[j & 1] = dot_product(A, Bf[i & 1][j], dacc[j & 1]);
-            else acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bf[i & 1][j], acc, 0, 0, 0);
+        };
+        if (wave < 4) {                                                    // uniform: the prologue waves
+            const bool store = blockIdx.x == 0 && blockIdx.y == 0;
+            const auto bar = [] { __syncthreads(); };
+            float v[8];
+            __builtin_amdgcn_s_setprio(2);
+            panp_waves<TCQ_I32, 4>(P.a, store, v, qd[0], NoMid{}, bar);
+            waves_rotate_quantize<4>(v, qd[0], pro.qs, &pro.sc, store ? P.q : nullptr, store ? P.scale : nullptr, bar);
+            __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+            for (int i = 0; i < CM; ++i) decode(i);
+        } else {                                                           // the others: the table, then a chunk per barrier
+            fill_table(256);
+#pragma unroll
+            for (int i = 0; i < (CM > WAVES_SYNCS ? CM : WAVES_SYNCS); ++i) {
+                if (i < WAVES_SYNCS) __syncthreads();
+                if (i < CM) decode(i);
+            }
+        }
+        __syncthreads();                                                   // the row is in pro.qs
+        if (ODT != TCQ_I32 && part == 0) sv = pro.sc;
+#pragma unroll
+        for (int i = 0; i < CM; ++i) {
+            const int c = c0 + part + WPR * i;
+            if (c >= nch) continue;                                        // uniform
+            loadB(c, Bf[0]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Af[i][j], Bf[0][j], acc, 0, 0, 0);
+        }
+    } else {
+        if constexpr (PL > 0) {
+            if (ODT != TCQ_I32 && part == 0) sv = pro.sc;
+            loadB(c0 + part, Bf[0]);
+        }
+#pragma unroll
+        for (int i = 0; i < CM; ++i) {
+            const int c = c0 + part + WPR * i;
+            if (c >= nch) continue;                                        // uniform
+            if (i + 1 < CM && c + WPR < nch) loadB(c + WPR, Bf[(i + 1) & 1]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int4v A = frag(wa[i][j]);
+                if constexpr (DOT) dacc[j & 1] = dot_product(A, Bf[i & 1][j], dacc[j & 1]);
+                else acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bf[i & 1][j], acc, 0, 0, 0);
+            }
         }
     }
     if constexpr (DOT) acc = dot_to_mfma_layout(dacc[0] + dacc[1], lane);
@@ -794,8 +861,8 @@ static int gemm_small_pro(const tcq_gemm_seg* segs, int nseg, const tcq_prologue
     }
     if (layer) {
         if (w128) {
-            launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, PRO_LAYER>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0, st, P, nq,
-                     ns, 1, K, ldo);
+            launch_k(k_gemv_tcq<TCQ_F32, false, 2, GV_NW, 1, true, false, PRO_LAYER, true>, dim3(max_m / 128, nseg), dim3(64 * GV_NW), 0,
+                     st, P, nq, ns, 1, K, ldo);
             return launch_status();
         }
         const int wpr = MODE == 0 ? gv_waves_per_row(segs, nseg, 1, nch, tiles) : 0;

@@ -371,6 +371,167 @@ __device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, 
     else return panp_tw16<ADT, L, LE, BIAS>(A, tok, store, v, xs, part, red, mid);
 }
 
+// ------------------------------------------------------------ the 2048-wide prologue on four or eight waves, no transposes
+// LDS of panp_waves / waves_rotate_quantize: the exchange rows of wave_walsh, the per-wave sums and maxima. The two take
+// WAVES_SYNCS calls of sync() together (two each).
+struct WavesLds {
+    float xs[2048];
+    float red[16];
+};
+constexpr int WAVES_SYNCS = 4;
+
+// panp_tw8 for one 2048-wide token with the norm (A.w set, no bias) on waves 0 .. NWP - 1 (NWP = 4 or 8: E = 8 or 4 values
+// per thread), with two sync() points (barriers that a caller's other waves may meet while they do other work): the Walsh
+// on wave_walsh; the chunk sums of squares in order, each chunk's 16 values over 16 / E consecutive lanes (each lane
+// continues the sum of the lane below, a DPP move), so the last lane of the group holds the sequential sum; their pairwise
+// tree over the lanes of a wave by DPP inside the 16-lane rows, then across the rows, and over the waves through LDS. The
+// tree is tree_total's (chunk j + h into chunk j at level h), so every value equals panp_tw8's bit for bit. Threads of
+// waves < NWP call it; v ends in natural layout for waves_rotate_quantize. mid() runs once the accumulator loads have
+// been consumed.
+template <int ADT, int NWP, class F, class SY>
+__device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float (&v)[2048 / 64 / NWP], WavesLds& Q, F&& mid,
+                                           SY&& sync) {
+    constexpr int N = 2048, E = N / 64 / NWP, LE = E == 8 ? 3 : 2, LPC = 16 / E;
+    const int t = threadIdx.x, i0 = E * t, lane = t & 63, w = t >> 6;
+    float sg[E], xv[E], wv[E], sn[E];
+    auto ld_i8 = [&](const i8* p, float (&o)[E]) {
+        if constexpr (E == 8) {
+            ld8_i8v(p, o);
+        } else {
+            const u32 x = *gptr((const u32*)p);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = (float)(i8)(x >> (8 * k));
+        }
+    };
+    auto ld_bf16 = [&](const u16* p, float (&o)[E]) {
+        if constexpr (E == 8) {
+            ld8_bf16v(p, o);
+        } else {
+            const uint2_t x = *gptr((const uint2_t*)p);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                o[2 * k] = __uint_as_float(x[k] << 16);
+                o[2 * k + 1] = __uint_as_float(x[k] & 0xffff0000u);
+            }
+        }
+    };
+    ld_i8(A.sv + i0, sg);
+    ld_bf16(A.x + i0, xv);
+    ld_bf16(A.w + i0, wv);
+    ld_i8(A.su + i0, sn);
+    if constexpr (E == 8) {
+        acc_piece8<ADT>(A.acc, (size_t)A.col0 + i0, ADT == TCQ_I32 ? A.s[0] : 1.f, A.rs ? A.rs + i0 : nullptr, v, A.parts, A.pstride);
+    } else {
+        static_assert(ADT == TCQ_I32, "four values per thread: int32 sums");
+        uint4_t a = *gptr((const uint4_t*)((const u32*)A.acc + A.col0 + i0));
+        uint4_t ap[3];
+#pragma unroll
+        for (int p = 1; p < 4; ++p)
+            if (p < A.parts) ap[p - 1] = *gptr((const uint4_t*)((const u32*)A.acc + A.col0 + i0 + p * A.pstride));
+        const float4_t r = *gptr((const float4_t*)(A.rs + i0));
+        const float st = A.s[0];
+#pragma unroll
+        for (int p = 1; p < 4; ++p)
+            if (p < A.parts) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) a[k] = (u32)((int)a[k] + (int)ap[p - 1][k]);
+            }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = ((float)(int)a[k] * st) * r[k];
+    }
+    mid();
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    wave_walsh<LE, NWP>(v, Q.xs, sync);
+    float a[E];
+    u16 xn[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) a[k] = (v[k] * c) * sg[k];
+    bf16_round<E / 2>(a, xn);                                          // a = bf16(post output)
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = xv[k] + a[k];
+    bf16_round<E / 2>(v, xn);                                          // xout = bf16(x + a)
+    if (store) {
+        u32 x2[E / 2];
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) x2[k] = (u32)xn[2 * k] | ((u32)xn[2 * k + 1] << 16);
+        if constexpr (E == 8) *gptr((uint4_t*)(A.xout + i0)) = uint4_t{x2[0], x2[1], x2[2], x2[3]};
+        else *gptr((uint2_t*)(A.xout + i0)) = uint2_t{x2[0], x2[1]};
+    }
+    // chunk sums: lane l continues lane l - 1's partial sum (row_shr:1), LPC lanes per chunk
+    float cs = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; ++k) cs = cs + v[k] * v[k];
+#pragma unroll
+    for (int g = 1; g < LPC; ++g) {
+        float p = dpp<0x111>(cs);
+#pragma unroll
+        for (int k = 0; k < E; ++k) p = p + v[k] * v[k];
+        cs = p;
+    }
+    // lane LPC j + LPC - 1 now holds chunk j of the wave; the tree inside the rows (row_shl by LPC, 2 LPC, .. 8)
+#pragma unroll
+    for (int h = LPC; h < 16; h *= 2) cs = cs + (h == 2 ? dpp<0x102>(cs) : h == 4 ? dpp<0x104>(cs) : dpp<0x108>(cs));
+    const float ws = (lane_value(cs, LPC - 1) + lane_value(cs, 16 + LPC - 1)) +
+                     (lane_value(cs, 32 + LPC - 1) + lane_value(cs, 48 + LPC - 1));
+    if (lane == 0) Q.red[w] = ws;
+    sync();
+    float ss;
+    if constexpr (NWP == 4) ss = (Q.red[0] + Q.red[1]) + (Q.red[2] + Q.red[3]);
+    else ss = ((Q.red[0] + Q.red[1]) + (Q.red[2] + Q.red[3])) + ((Q.red[4] + Q.red[5]) + (Q.red[6] + Q.red[7]));
+    const float r = 1.f / __builtin_sqrtf(ss / (float)N + A.eps);
+    float nv[E];
+    u16 nh[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) nv[k] = (v[k] * r) * (1.f + wv[k]);
+    bf16_round<E / 2>(nv, nh);
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = nv[k] * sn[k];
+}
+
+// tw_rotate_quantize of a 2048-wide row on waves 0 .. NWP - 1 (v: E = 2048 / 64 / NWP values per thread, natural layout),
+// with two sync() points: wave_walsh, the row maximum over the waves through LDS, the INT8 row into qs (LDS, E bytes per
+// thread) and, when given, q (global); the scale into *scs and, when given, scale[0]. The same values as
+// tw_rotate_quantize<11, 3>.
+template <int NWP, class SY>
+__device__ __forceinline__ void waves_rotate_quantize(float (&v)[2048 / 64 / NWP], WavesLds& Q, u32* qs, float* scs, i8* q, float* scale,
+                                                      SY&& sync) {
+    constexpr int E = 2048 / 64 / NWP, LE = E == 8 ? 3 : 2;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const float c = (float)(1.0 / __builtin_sqrt(2048.0));
+    wave_walsh<LE, NWP>(v, Q.xs, sync);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) Q.red[8 + w] = mx;
+    sync();
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWP; ++i) m = fmaxf(m, Q.red[8 + i]);
+    const float sc = token_scale(m);
+    if (t == 0) {
+        *scs = sc;
+        if (scale) scale[0] = sc;
+    }
+    const QScale S = qscale(sc);
+    u32 words[E / 4];
+#pragma unroll
+    for (int k4 = 0; k4 < E / 4; ++k4)
+        words[k4] = (u32)(q8(v[4 * k4], S) & 0xff) | ((u32)(q8(v[4 * k4 + 1], S) & 0xff) << 8) |
+                    ((u32)(q8(v[4 * k4 + 2], S) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], S) & 0xff) << 24);
+    if constexpr (E == 8) {
+        const u64 d = (u64)words[0] | ((u64)words[1] << 32);
+        *(u64*)(qs + 2 * t) = d;
+        if (q) *gptr((u64*)(q + 8 * t)) = d;
+    } else {
+        qs[t] = words[0];
+        if (q) *gptr((u32*)(q + 4 * t)) = words[0];
+    }
+}
+
 // The rotate + quantize input of a BF16 row (tcq_pre's first steps): thread t's 2^LE contiguous values x[2^LE t ..] * su,
 // as FP32 in v (natural layout, ready for tw_rotate_quantize). Threads from 2^(L - LE) on hold no values (zeros). mid()
 // runs once the loaded words have been consumed.
