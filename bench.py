@@ -58,6 +58,8 @@ def parse():
                         'k_mid2_tw2), the W8A8 GEMM 800 x 2048 x 16384 (k_gemm_i8, int32 out) over distinct weights, or '
                         'the backbone\'s 800-token prefill (fly) or its 32 decode steps as one graph')
     p.add_argument('--probe-reps', type=int, default=10)
+    p.add_argument('--classes', choices=('chunk', 'backbone'), default=None,
+                   help='child mode of the bench: print the kernel classes of the fly stages of one workload as JSON')
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device-to-device copy 8 times (the reference kernel for scaling the '
                         'FETCH_SIZE / WRITE_SIZE counters into bytes)')
@@ -399,23 +401,30 @@ def blas_threads():
 
 def rht_cpu_baseline(seed, seconds):
     """The oracle's fwht (tcq_format.py:44-55 restated in numpy) of x * su over BF16 rows [800, 16384] (the largest
-    RHT shape), FP32 butterflies and BF16 output, as many repeats as fit in about `seconds` (at least 3, median)."""
+    RHT shape), FP32 butterflies and BF16 output, as many repeats as fit in about `seconds` (at least 3, median). The rows
+    are split into one slice per host core, each transformed by its own thread (numpy's element-wise loops release the
+    interpreter lock), so every core of the box works."""
     import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import tcq_oracle as O
     rng = np.random.default_rng(seed + 5)
     M, n = 800, 16384
     x = O.bf16_to_f32(O.bf16_bits(rng.standard_normal((M, n)).astype(np.float32)))
     su = np.where(rng.integers(0, 2, n) > 0, 1, -1).astype(np.float32)
+    cores = max(1, len(os.sched_getaffinity(0)))
+    bounds = np.linspace(0, M, cores + 1).astype(int)
+    slices = [(int(a), int(b)) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
     ts, t0 = [], time.perf_counter()
-    while len(ts) < 3 or (time.perf_counter() - t0 < seconds and len(ts) < 20):
-        t1 = time.perf_counter()
-        O.bf16_bits(O.fwht(x * su))
-        ts.append(time.perf_counter() - t1)
+    with ThreadPoolExecutor(max_workers=len(slices)) as ex:
+        while len(ts) < 3 or (time.perf_counter() - t0 < seconds and len(ts) < 20):
+            t1 = time.perf_counter()
+            list(ex.map(lambda ab: O.bf16_bits(O.fwht(x[ab[0]:ab[1]] * su)), slices))
+            ts.append(time.perf_counter() - t1)
     med = float(np.median(ts))
     byts = 4 * M * n + n
-    return dict(value=round(byts / med / 1e9, 4), unit='GB/s', cores=1, kind='port',
+    return dict(value=round(byts / med / 1e9, 4), unit='GB/s', cores=len(slices), kind='port',
                 sample=f'{len(ts)} transforms of BF16 [{M}, {n}] through the numpy oracle (fwht of x * su, BF16 out), median '
-                       f'{med * 1e3:.1f} ms; numpy elementwise (one thread)')
+                       f'{med * 1e3:.1f} ms; rows split over {len(slices)} threads, one per host core')
 
 
 def gemm_cpu_baseline(seed, seconds):
@@ -491,8 +500,7 @@ def action_chunk(args, dev):
                 med, p95 = graph_latency(chunk, replays=args.chunk_replays, warmup=10)
                 res[runtime] = {'median': round(med, 4), 'p95': round(p95, 4)}
             if runtime == 'fly':
-                from yanlongvla_amd import harness
-                keep = dict(model=model, layers=layers, classes=harness.kernel_classes(harness.capture(chunk), chunk))
+                keep = dict(model=model, layers=layers, classes=traced_classes('chunk', args.seed))
             else:
                 del model, layers
             torch.cuda.synchronize()
@@ -611,10 +619,7 @@ def backbone(args, dev):
                                 'total_ms': round(p_med + d_med, 3), 'decode_ms_per_token': round(d_med / BB_DECODE, 4)}
                 products[runtime] = decode_products(model, runtime, dev, args.seed)
             if runtime == 'fly':
-                from yanlongvla_amd import harness
-                prefill()
-                classes['prefill'] = harness.kernel_classes(harness.capture(prefill), prefill)
-                classes['decode_32_tokens'] = harness.kernel_classes(harness.capture(decode), decode)
+                classes = traced_classes('backbone', args.seed)
                 if not args.no_cpu:
                     prefill()
                     cpu = backbone_cpu_baseline(model, layers, x, state, [model.embed(dec[t]) for t in range(2)])
@@ -785,6 +790,60 @@ def probe(kind, reps, dev):
     note(f'probe {kind}: {reps} x {len(calls)} calls')
 
 
+def traced_classes(kind, seed):
+    """harness.kernel_classes of the fly stages of `kind` ('chunk': one action chunk; 'backbone': the prefill and the 32
+    decode steps), traced in a child process (`bench.py --classes kind`) on the same seeded setup: the device tracer then
+    runs apart from the measurements, and a failure inside it costs only this record."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), '--classes', kind, '--seed', str(seed)]
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return dict(error='tracer child timed out after 300 s')
+    lines = [line for line in r.stdout.splitlines() if line.startswith('{')]
+    if r.returncode != 0 or not lines:
+        return dict(error=f'tracer child exited with status {r.returncode}')
+    return json.loads(lines[-1])
+
+
+def classes_child(kind, seed, dev):
+    """--classes: the kernel classes of the fly stages of `kind`, as one JSON line on stdout."""
+    import torch
+    from yanlongvla_amd import gemma, harness, modules
+    with torch.inference_mode():
+        if kind == 'chunk':
+            ks, vs, noise = expert_setup(seed, dev)
+            model, _ = expert_policy('fly', seed, dev, ks, vs)
+
+            def chunk():
+                return model.sample_chunk(noise, CHUNK_STEPS)
+            chunk()
+            out = harness.kernel_classes(harness.capture(chunk), chunk)
+        else:
+            img, ids, dec = backbone_setup(seed, dev)
+            model = gemma.make_policy(gemma.BackbonePolicy, dev, seed=seed + 1)
+            modules.install(model, runtime='fly', layers=gemma.synthetic_layers(model, seed + 9, dev))
+            x = torch.cat([img, model.embed(ids)], 0)
+            state = {}
+
+            def prefill():
+                h, ks, vs = model.prefill(x)
+                state.update(ks=ks, vs=vs)
+                return h
+            prefill()
+            cache = gemma.KVCache(state['ks'], state['vs'], BB_DECODE)
+
+            def decode():
+                cache.rewind()
+                return torch.cat([model.decode_step_cached(model.embed(dec[t]), cache) for t in range(BB_DECODE)], 0)
+            out = {'prefill': harness.kernel_classes(harness.capture(prefill), prefill)}
+            prefill()
+            out['decode_32_tokens'] = harness.kernel_classes(harness.capture(decode), decode)
+    torch.cuda.synchronize()
+    note(f'kernel classes of the {kind} traced')
+    print(json.dumps(out), flush=True)
+
+
 def note(msg):
     """Progress line of a finished stage, on stderr (the JSON result line stays alone on stdout)."""
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
@@ -805,6 +864,13 @@ def main():
         _lib.lib()
         torch.cuda.set_device(0)
         probe(args.probe, args.probe_reps, torch.device('cuda:0'))
+        return
+    if args.classes:
+        import torch
+        from yanlongvla_amd import _lib
+        _lib.lib()
+        torch.cuda.set_device(0)
+        classes_child(args.classes, args.seed, torch.device('cuda:0'))
         return
     import torch
     from yanlongvla_amd import _lib

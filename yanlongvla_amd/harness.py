@@ -125,7 +125,9 @@ def _kernel_totals(run):
     run()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+    # device activity only: the kernels are all that is read back, and without host activity the tracer links no host
+    # launches to device records (that linking warned of duplicate flow starts on ROCm)
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
         start.record()
         run()
         end.record()
