@@ -76,27 +76,23 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
     const bool fresh = POST && j0 <= P && P < j0 + KC;                  // POST: this workgroup makes the new key / value row
     if (j0 >= jend && !fresh) return;                                   // no key of the chunk is visible to the group; the
                                                                         // combine never reads its slots (visible_chunks)
-    // POST: this thread's 8 values of the q segment and their signs, and (threads 0 .. 31 of the fresh workgroup) of the
-    // key and value segments, issued first
-    float zq[8] = {}, zk[8] = {}, zv[8] = {};
-    u64 gq = 0, gk = 0, gv = 0;
+    // POST: this thread's 8 values of the q segment and their signs, and (waves 0 and 1 of the fresh workgroup) 4 values of
+    // the key (wave 0) or value (wave 1) segment per lane, issued first
+    float zq[8] = {}, zr[4] = {};
+    u64 gq = 0;
+    u32 gr = 0;
+    const bool kvw = fresh && wave < 2;                                 // wave-uniform
     if constexpr (POST) {
         const uint4_t* zp = (const uint4_t*)(ap.zq + 8 * tid);
         const uint4_t a = gptr(zp)[0], b = gptr(zp)[1];
 #pragma unroll
         for (int k = 0; k < 4; ++k) { zq[k] = __uint_as_float(a[k]); zq[4 + k] = __uint_as_float(b[k]); }
         gq = gptr((const u64*)(ap.sq + 8 * tid))[0];
-        if (fresh && tid < AD / 8) {
-            const uint4_t* kp = (const uint4_t*)(ap.zk + 8 * tid);
-            const uint4_t* vp = (const uint4_t*)(ap.zv + 8 * tid);
-            const uint4_t ka = gptr(kp)[0], kb = gptr(kp)[1], va = gptr(vp)[0], vb = gptr(vp)[1];
+        if (kvw) {
+            const float4_t r = gptr((const float4_t*)((wave ? ap.zv : ap.zk) + 4 * lane))[0];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                zk[k] = __uint_as_float(ka[k]); zk[4 + k] = __uint_as_float(kb[k]);
-                zv[k] = __uint_as_float(va[k]); zv[4 + k] = __uint_as_float(vb[k]);
-            }
-            gk = gptr((const u64*)(ap.sk + 8 * tid))[0];
-            gv = gptr((const u64*)(ap.sv + 8 * tid))[0];
+            for (int k = 0; k < 4; ++k) zr[k] = r[k];
+            gr = gptr((const u32*)((wave ? ap.sv : ap.sk) + 4 * lane))[0];
         }
     }
     // value stage (64 rows x 256 dims, 8 granules of 16 bytes per thread) and query rows (AR x 256), issued first (POST:
@@ -133,36 +129,33 @@ __global__ __launch_bounds__(AT) void k_attn_part(const u16* q, const u16* kc, c
         if (!(fresh && j0 + (gi >> 5) == P)) *(uint4_t*)&vs[gi >> 5][8 * (gi & 31)] = vg[u];
     }
     if constexpr (POST) {
-        if (fresh) {                                                    // uniform: the new key / value rows
-            float* xa = &ps[0][0];                                      // 2 x lds_words(256) floats, free until the scores
-            float* xb = xa + (AD + AD / 32 + 1);
-            tw_walsh2<8, 3>(zk, zv, xa, xb);
+        if (kvw) {                                                      // the new key (wave 0) / value (wave 1) row, in the wave:
+            butterflies<2>(zr);                                         // h = 1, 2 in the lane, h = 4 .. 128 across the lanes
 #pragma unroll
-            for (int k = 0; k < 8; ++k) { zk[k] = zk[k] * scl; zv[k] = zv[k] * scl; }   // c = 1 / sqrt(256)
-            tw_to_natural2<8, 3>(zk, zv, xa, xb);
-            if (tid < AD / 8) {
+            for (int s = 0; s < 6; ++s) {
+                const int m = 1 << s;
+                const bool upper = lane & m;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    zk[k] = zk[k] * (float)(i8)(gk >> (8 * k));
-                    zv[k] = zv[k] * (float)(i8)(gv >> (8 * k));
+                for (int k = 0; k < 4; ++k) {
+                    const float pv = lane_xor(zr[k], m, lane);
+                    zr[k] = upper ? pv - zr[k] : zr[k] + pv;
                 }
-                u32 wk[4], wv[4];
-                bf16_pack<4>(zk, wk);
-                bf16_pack<4>(zv, wv);
-                const uint4_t kk = {wk[0], wk[1], wk[2], wk[3]}, vv = {wv[0], wv[1], wv[2], wv[3]};
-                gptr((uint4_t*)(ap.k_out + 8 * tid))[0] = kk;
-                gptr((uint4_t*)(ap.v_out + 8 * tid))[0] = vv;
-                *(uint4_t*)&kns[8 * tid] = kk;
-                *(uint4_t*)&vs[P - j0][8 * tid] = P < jend ? vv : uint4_t{0, 0, 0, 0};
             }
-            if (j0 >= jend) return;                                     // uniform: no visible key in the chunk
-            // (xa / xb are next written as ps after the barriers of the q rotation below)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) zr[k] = (zr[k] * scl) * (float)(i8)(gr >> (8 * k));   // c = 1 / sqrt(256)
+            u32 w2[2];
+            bf16_pack<2>(zr, w2);
+            const u64 d = (u64)w2[0] | ((u64)w2[1] << 32);
+            gptr((u64*)((wave ? ap.v_out : ap.k_out) + 4 * lane))[0] = d;
+            if (wave == 0) *(u64*)&kns[4 * lane] = d;
+            else *(u64*)&vs[P - j0][4 * lane] = P < jend ? d : 0ull;
         }
-        tw_walsh<11, 3>(zq, xq);
+        if (fresh && j0 >= jend) return;                                // uniform: no visible key in the chunk
+        // the query row on the no-transpose engine: index bits inside the thread, across the lanes, across the 4 waves
+        wave_walsh<3, 4>(zq, xq, [] { __syncthreads(); });
         const float cq = (float)(1.0 / __builtin_sqrt(2048.0));
 #pragma unroll
         for (int k = 0; k < 8; ++k) zq[k] = zq[k] * cq;
-        tw_to_natural<11, 3>(zq, xq);
 #pragma unroll
         for (int k = 0; k < 8; ++k) zq[k] = zq[k] * (float)(i8)(gq >> (8 * k));
         u32 w[4];
