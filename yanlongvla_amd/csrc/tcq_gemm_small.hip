@@ -117,7 +117,7 @@ __device__ __forceinline__ void run_prologue(const SegPackPro& P, ProLds<PL>& L,
         const auto bar = [] { __syncthreads(); };
         float v[4];
         if constexpr (PL == PRO_LAYER) {
-            panp_waves<TCQ_I32, 8>(P.a, store, v, L.wl[0], mid, bar);
+            panp_waves<TCQ_I32, 8>(P.a, 0, store, v, L.wl[0], mid, bar);
         } else {
             combine_w_row(P.part, P.nc, P.keys, P.causal, P.heads, 0, nullptr, P.a.su, L.xs, L.wts, mid, v);   // heads = 8
         }
@@ -460,7 +460,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
             const auto bar = [] { __syncthreads(); };
             float v[8];
             __builtin_amdgcn_s_setprio(2);
-            panp_waves<TCQ_I32, 4>(P.a, store, v, qd[0], NoMid{}, bar);
+            panp_waves<TCQ_I32, 4>(P.a, 0, store, v, qd[0], NoMid{}, bar);
             waves_rotate_quantize<4>(v, qd[0], pro.qs, &pro.sc, store ? P.q : nullptr, store ? P.scale : nullptr, bar);
             __builtin_amdgcn_s_setprio(0);
 #pragma unroll

@@ -371,7 +371,7 @@ __device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, 
     else return panp_tw16<ADT, L, LE, BIAS>(A, tok, store, v, xs, part, red, mid);
 }
 
-// ------------------------------------------------------------ the 2048-wide prologue on four or eight waves, no transposes
+// --------------------------------------------------------- rows of 1024 / 2048 on four or eight waves, no transposes
 // LDS of panp_waves / waves_rotate_quantize: the exchange rows of wave_walsh, the per-wave sums and maxima. The two take
 // WAVES_SYNCS calls of sync() together (two each).
 struct WavesLds {
@@ -380,19 +380,21 @@ struct WavesLds {
 };
 constexpr int WAVES_SYNCS = 4;
 
-// panp_tw8 for one 2048-wide token with the norm (A.w set, no bias) on waves 0 .. NWP - 1 (NWP = 4 or 8: E = 8 or 4 values
-// per thread), with two sync() points (barriers that a caller's other waves may meet while they do other work): the Walsh
-// on wave_walsh; the chunk sums of squares in order, each chunk's 16 values over 16 / E consecutive lanes (each lane
-// continues the sum of the lane below, a DPP move), so the last lane of the group holds the sequential sum; their pairwise
-// tree over the lanes of a wave by DPP inside the 16-lane rows, then across the rows, and over the waves through LDS. The
-// tree is tree_total's (chunk j + h into chunk j at level h), so every value equals panp_tw8's bit for bit. Threads of
-// waves < NWP call it; v ends in natural layout for waves_rotate_quantize. mid() runs once the accumulator loads have
-// been consumed.
-template <int ADT, int NWP, class F, class SY>
-__device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float (&v)[2048 / 64 / NWP], WavesLds& Q, F&& mid,
-                                           SY&& sync) {
-    constexpr int N = 2048, E = N / 64 / NWP, LE = E == 8 ? 3 : 2, LPC = 16 / E;
+// panp_tw for token tok of a 2^L-wide row (L = 10 or 11) with the norm (A.w set, no bias) on waves 0 .. NWP - 1 (NWP = 4
+// or 8: E = 2^L / 64 / NWP = 4 or 8 values per thread), with two sync() points (barriers that a caller's other waves may
+// meet while they do other work): the Walsh on wave_walsh; the chunk sums of squares in order, each chunk's 16 values
+// over 16 / E consecutive lanes (each lane continues the sum of the lane below, a DPP move), so the last lane of the
+// group holds the sequential sum; their pairwise tree over the lanes of a wave by DPP inside the 16-lane rows, then
+// across the rows, and over the waves through LDS. The tree is tree_total's (chunk j + h into chunk j at level h), so
+// every value equals panp_tw's bit for bit. Threads of waves < NWP call it; v ends in natural layout for
+// waves_rotate_quantize. mid() runs once the accumulator loads have been consumed. xout is stored when `store`.
+template <int ADT, int NWP, int L = 11, class F, class SY>
+__device__ __forceinline__ void panp_waves(const PanpArgs& A, int tok, bool store, float (&v)[(1 << L) / 64 / NWP], WavesLds& Q,
+                                           F&& mid, SY&& sync) {
+    constexpr int N = 1 << L, E = N / 64 / NWP, LE = E == 8 ? 3 : 2, LPC = 16 / E;
+    static_assert((L == 10 || L == 11) && (E == 4 || E == 8), "rows of 1024 or 2048, 4 or 8 values per thread");
     const int t = threadIdx.x, i0 = E * t, lane = t & 63, w = t >> 6;
+    const size_t row = (size_t)tok * N, base = (size_t)tok * A.lda + A.col0 + i0;
     float sg[E], xv[E], wv[E], sn[E];
     auto ld_i8 = [&](const i8* p, float (&o)[E]) {
         if constexpr (E == 8) {
@@ -416,20 +418,19 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float 
         }
     };
     ld_i8(A.sv + i0, sg);
-    ld_bf16(A.x + i0, xv);
+    ld_bf16(A.x + row + i0, xv);
     ld_bf16(A.w + i0, wv);
     ld_i8(A.su + i0, sn);
+    const float st = ADT == TCQ_I32 ? A.s[tok] : 1.f;
     if constexpr (E == 8) {
-        acc_piece8<ADT>(A.acc, (size_t)A.col0 + i0, ADT == TCQ_I32 ? A.s[0] : 1.f, A.rs ? A.rs + i0 : nullptr, v, A.parts, A.pstride);
-    } else {
-        static_assert(ADT == TCQ_I32, "four values per thread: int32 sums");
-        uint4_t a = *gptr((const uint4_t*)((const u32*)A.acc + A.col0 + i0));
+        acc_piece8<ADT>(A.acc, base, st, A.rs ? A.rs + i0 : nullptr, v, A.parts, A.pstride);
+    } else if constexpr (ADT == TCQ_I32) {
+        uint4_t a = *gptr((const uint4_t*)((const u32*)A.acc + base));
         uint4_t ap[3];
 #pragma unroll
         for (int p = 1; p < 4; ++p)
-            if (p < A.parts) ap[p - 1] = *gptr((const uint4_t*)((const u32*)A.acc + A.col0 + i0 + p * A.pstride));
+            if (p < A.parts) ap[p - 1] = *gptr((const uint4_t*)((const u32*)A.acc + base + p * A.pstride));
         const float4_t r = *gptr((const float4_t*)(A.rs + i0));
-        const float st = A.s[0];
 #pragma unroll
         for (int p = 1; p < 4; ++p)
             if (p < A.parts) {
@@ -438,6 +439,15 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float 
             }
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = ((float)(int)a[k] * st) * r[k];
+    } else if constexpr (ADT == TCQ_BF16) {
+        ld_bf16((const u16*)A.acc + base, v);
+        const float4_t r = *gptr((const float4_t*)(A.rs + i0));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = v[k] * r[k];
+    } else {
+        const float4_t a = *gptr((const float4_t*)((const float*)A.acc + base));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = a[k];
     }
     mid();
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
@@ -454,8 +464,8 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float 
         u32 x2[E / 2];
 #pragma unroll
         for (int k = 0; k < E / 2; ++k) x2[k] = (u32)xn[2 * k] | ((u32)xn[2 * k + 1] << 16);
-        if constexpr (E == 8) *gptr((uint4_t*)(A.xout + i0)) = uint4_t{x2[0], x2[1], x2[2], x2[3]};
-        else *gptr((uint2_t*)(A.xout + i0)) = uint2_t{x2[0], x2[1]};
+        if constexpr (E == 8) *gptr((uint4_t*)(A.xout + row + i0)) = uint4_t{x2[0], x2[1], x2[2], x2[3]};
+        else *gptr((uint2_t*)(A.xout + row + i0)) = uint2_t{x2[0], x2[1]};
     }
     // chunk sums: lane l continues lane l - 1's partial sum (row_shr:1), LPC lanes per chunk
     float cs = 0.f;
@@ -475,6 +485,7 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float 
                      (lane_value(cs, 32 + LPC - 1) + lane_value(cs, 48 + LPC - 1));
     if (lane == 0) Q.red[w] = ws;
     sync();
+    // the waves' sums: levels 16 / 32 chunks (E = 4 / 8) and up, in tree_total's pairing for 2^L / 16 chunks
     float ss;
     if constexpr (NWP == 4) ss = (Q.red[0] + Q.red[1]) + (Q.red[2] + Q.red[3]);
     else ss = ((Q.red[0] + Q.red[1]) + (Q.red[2] + Q.red[3])) + ((Q.red[4] + Q.red[5]) + (Q.red[6] + Q.red[7]));
@@ -488,16 +499,16 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, bool store, float 
     for (int k = 0; k < E; ++k) v[k] = nv[k] * sn[k];
 }
 
-// tw_rotate_quantize of a 2048-wide row on waves 0 .. NWP - 1 (v: E = 2048 / 64 / NWP values per thread, natural layout),
-// with two sync() points: wave_walsh, the row maximum over the waves through LDS, the INT8 row into qs (LDS, E bytes per
-// thread) and, when given, q (global); the scale into *scs and, when given, scale[0]. The same values as
-// tw_rotate_quantize<11, 3>.
-template <int NWP, class SY>
-__device__ __forceinline__ void waves_rotate_quantize(float (&v)[2048 / 64 / NWP], WavesLds& Q, u32* qs, float* scs, i8* q, float* scale,
-                                                      SY&& sync) {
-    constexpr int E = 2048 / 64 / NWP, LE = E == 8 ? 3 : 2;
+// tw_rotate_quantize of a 2^L-wide row (token tok) on waves 0 .. NWP - 1 (v: E = 2^L / 64 / NWP values per thread, natural
+// layout), with two sync() points: wave_walsh, the row maximum over the waves through LDS, the INT8 row into qs (LDS, E
+// bytes per thread), q (row tok), q4 (the word layout, or token blocks when ldq is TCQ_LDQ_TOKEN_BLOCKS) as given; the
+// scale into *scs and scale[tok] as given. The same values as tw_rotate_quantize<L, LE>.
+template <int NWP, int L = 11, class SY>
+__device__ __forceinline__ void waves_rotate_quantize(float (&v)[(1 << L) / 64 / NWP], WavesLds& Q, u32* qs, float* scs, i8* q,
+                                                      float* scale, SY&& sync, int tok = 0, int* q4 = nullptr, int ldq = 0) {
+    constexpr int N = 1 << L, E = N / 64 / NWP, LE = E == 8 ? 3 : 2;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const float c = (float)(1.0 / __builtin_sqrt(2048.0));
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
     wave_walsh<LE, NWP>(v, Q.xs, sync);
     float mx = 0.f;
 #pragma unroll
@@ -513,8 +524,8 @@ __device__ __forceinline__ void waves_rotate_quantize(float (&v)[2048 / 64 / NWP
     for (int i = 0; i < NWP; ++i) m = fmaxf(m, Q.red[8 + i]);
     const float sc = token_scale(m);
     if (t == 0) {
-        *scs = sc;
-        if (scale) scale[0] = sc;
+        if (scs) *scs = sc;
+        if (scale) scale[tok] = sc;
     }
     const QScale S = qscale(sc);
     u32 words[E / 4];
@@ -522,13 +533,20 @@ __device__ __forceinline__ void waves_rotate_quantize(float (&v)[2048 / 64 / NWP
     for (int k4 = 0; k4 < E / 4; ++k4)
         words[k4] = (u32)(q8(v[4 * k4], S) & 0xff) | ((u32)(q8(v[4 * k4 + 1], S) & 0xff) << 8) |
                     ((u32)(q8(v[4 * k4 + 2], S) & 0xff) << 16) | ((u32)(q8(v[4 * k4 + 3], S) & 0xff) << 24);
+    const bool tb = q4 && ldq == TCQ_LDQ_TOKEN_BLOCKS;
     if constexpr (E == 8) {
         const u64 d = (u64)words[0] | ((u64)words[1] << 32);
-        *(u64*)(qs + 2 * t) = d;
-        if (q) *gptr((u64*)(q + 8 * t)) = d;
+        if (qs) *(u64*)(qs + 2 * t) = d;
+        if (q) *gptr((u64*)(q + (size_t)tok * N + 8 * t)) = d;
+        if (tb) *gptr((u64*)((i8*)q4 + tb_offset(tok, 8 * t, N))) = d;
     } else {
-        qs[t] = words[0];
-        if (q) *gptr((u32*)(q + 4 * t)) = words[0];
+        if (qs) qs[t] = words[0];
+        if (q) *gptr((u32*)(q + (size_t)tok * N + 4 * t)) = words[0];
+        if (tb) *gptr((u32*)((i8*)q4 + tb_offset(tok, 4 * t, N))) = words[0];
+    }
+    if (q4 && !tb) {
+#pragma unroll
+        for (int k4 = 0; k4 < E / 4; ++k4) q4[(size_t)((E / 4) * t + k4) * ldq + tok] = (int)words[k4];
     }
 }
 

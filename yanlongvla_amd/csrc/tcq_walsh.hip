@@ -1076,6 +1076,22 @@ __global__ __launch_bounds__(1 << (L - LE)) void k_post_add_norm_pre_tw(const vo
     tw_rotate_quantize<L, LE>(v, xs, red, q, q4, ldq, scale, blockIdx.x);
 }
 
+// k_post_add_norm_pre_tw for few rows of 1024 or 2048 with the norm and without bias, on the no-transpose engine
+// (panp_waves, waves_rotate_quantize): NWP waves per row, 4 values per thread, one LDS exchange per transform; the same
+// values as k_post_add_norm_pre_tw.
+template <int ADT, int L, int NWP>
+__global__ __launch_bounds__(64 * NWP) void k_post_add_norm_pre_wv(const void* acc, int lda, int col0, const float* s,
+                                                                  const float* rs, const i8* sv, const u16* x, u16* xout,
+                                                                  const u16* w, float eps, const i8* su, i8* q, int* q4, int ldq,
+                                                                  float* scale, int parts) {
+    __shared__ WavesLds Q;
+    const PanpArgs A{acc, s, rs, sv, nullptr, x, xout, w, su, lda, col0, parts, (size_t)gridDim.x * lda, eps};
+    float v[(1 << L) / 64 / NWP];
+    const auto bar = [] { __syncthreads(); };
+    panp_waves<ADT, NWP, L>(A, blockIdx.x, true, v, Q, NoMid{}, bar);
+    waves_rotate_quantize<NWP, L>(v, Q, nullptr, nullptr, q, scale, bar, blockIdx.x, q4, ldq);
+}
+
 // =========================================================================================================== C ABI
 // Threads per row: few rows (latency) -> about one 8-element vector per thread (up to 1024 threads when there are fewer
 // rows than CUs); many rows (throughput) -> four vectors per thread so more rows share a CU. Every row kernel's result is
@@ -1555,6 +1571,22 @@ extern "C" int tcq_post_add_norm_pre(const void* acc, int acc_dtype, int lda, in
     // register + transpose engine, 16 values per thread: power-of-two rows of 1024 .. 4096, aligned (measured on MI355X
     // against the register path: 50 x 1024 5.4 us against 6.9, 1 x 2048 5.7 against 7.5, 800 x 4096 13.7 against 19.5; with
     // 32 values per thread 2048-wide rows of few tokens run slower than the register path)
+    // few rows of 1024 / 2048 with the norm: the no-transpose engine, 4 values per thread on 4 / 8 waves
+    if (M <= 64 && w && !bias && (N == 1024 || N == 2048) && vec && svec && (!q || al16(q))) {
+#define PANV(AD, L, NWP) launch_k(k_post_add_norm_pre_wv<AD, L, NWP>, dim3(M), dim3(64 * NWP), 0, st, acc, lda, col0, s, rs,   \
+                                  (const i8*)sv, xp, (u16*)xout, wp, eps, (const i8*)su, (i8*)q, (int*)q4, ldq, scale, parts)
+#define PANVW(L, NWP)                                    \
+    switch (acc_dtype) {                                 \
+        case TCQ_I32: PANV(TCQ_I32, L, NWP); break;      \
+        case TCQ_F32: PANV(TCQ_F32, L, NWP); break;      \
+        case TCQ_BF16: PANV(TCQ_BF16, L, NWP); break;    \
+        default: return TCQ_ERR_DTYPE;                   \
+    }
+        if (N == 1024) { PANVW(10, 4); } else { PANVW(11, 8); }
+#undef PANVW
+#undef PANV
+        return launch_status();
+    }
     if ((N == 1024 || N == 2048 || N == 4096) && vec && svec && (!q || al16(q))) {
         const size_t tsh = (size_t)(lds_words(N) + N / 16) * sizeof(float);
 #define PANT(AD, L, LE) launch_k(k_post_add_norm_pre_tw<AD, L, LE>, dim3(M), dim3(1 << (L - LE)), tsh, st, acc, lda, col0, s, rs, \
