@@ -12,6 +12,7 @@
 #include "tcq_device.h"
 #include "tcq_launch.h"
 #include "tcq_attend.h"
+#include "tcq_rows.h"
 
 namespace {
 
@@ -362,7 +363,14 @@ __global__ __launch_bounds__(512) void k_attn_combine_w(const float* part, int N
     extern __shared__ float xs[];                                        // lds_words(H * AD) floats: the row to rotate
     __shared__ float wts[AH][MAXC];
     __shared__ float red[16];
+    __shared__ WavesLds wl;
     const int t = blockIdx.x, tid = threadIdx.x, K = H * AD;
+    if (H == AH && tw_ok) {                                              // uniform: 8 heads, the row stays in registers (each
+        float v[4];                                                      // lane holds 4 consecutive values) and is rotated and
+        if (!combine_w_row(part, NC, T, causal, H, t, o, su, xs, wts, [] {}, v)) return;   // quantized on all 8 waves
+        waves_rotate_quantize<8, 11>(v, wl, nullptr, nullptr, q8, scale, [] { __syncthreads(); }, t, q4, ldq);
+        return;
+    }
     if (!combine_w_row(part, NC, T, causal, H, t, o, su, xs, wts, [] {})) return;   // uniform
     // power-of-two rows (H = 1, 2, 4, 8) and 16-byte aligned INT8 outputs: the register + transpose engine on the first K / 16
     // threads (16 values each, read from the LDS row in layout 0); the same stages in the same order as the LDS engine, so

@@ -462,12 +462,11 @@ __device__ __forceinline__ void tw_walsh2(float (&a)[1 << LE], float (&b)[1 << L
 // wave evaluates the butterflies its own values need (wave-uniform choices). Every stage is the (a + b, a - b) butterfly in
 // ascending stage order, as in tw_walsh, so the sums are equal bit for bit. xs may be written again once every wave has
 // passed a later sync().
-template <int LE, int NWP, class SY>
-__device__ __forceinline__ void wave_walsh(float (&v)[1 << LE], float* xs, SY&& sync) {
-    static_assert(NWP == 4 || NWP == 8, "four or eight waves");
+template <int LE>
+__device__ __forceinline__ void wave_walsh_lanes(float (&v)[1 << LE]) {
     constexpr int E = 1 << LE;
     butterflies<LE>(v);
-    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int s = 0; s < 6; ++s) {
         const int m = 1 << s;
@@ -478,11 +477,19 @@ __device__ __forceinline__ void wave_walsh(float (&v)[1 << LE], float* xs, SY&& 
             v[k] = upper ? p - v[k] : v[k] + p;
         }
     }
+}
+template <int LE, int NWP>
+__device__ __forceinline__ void wave_walsh_put(const float (&v)[1 << LE], float* xs) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int k = 0; k < E; ++k) xs[(NWP * k + w) * 64 + lane] = v[k];
-    sync();
+    for (int k = 0; k < (1 << LE); ++k) xs[(NWP * k + w) * 64 + lane] = v[k];
+}
+template <int LE, int NWP>
+__device__ __forceinline__ void wave_walsh_get(float (&v)[1 << LE], const float* xs) {
+    static_assert(NWP == 4 || NWP == 8, "four or eight waves");
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int k = 0; k < E; ++k) {
+    for (int k = 0; k < (1 << LE); ++k) {
         const float* xk = xs + NWP * k * 64 + lane;
         // y1(j): stage 1 value at wave position j (lower keeps a + b, upper gets a - b of lower a, upper b)
         auto y1 = [&](int j) {
@@ -500,6 +507,24 @@ __device__ __forceinline__ void wave_walsh(float (&v)[1 << LE], float* xs, SY&& 
             v[k] = (w & 4) ? a - b : a + b;
         }
     }
+}
+template <int LE, int NWP, class SY>
+__device__ __forceinline__ void wave_walsh(float (&v)[1 << LE], float* xs, SY&& sync) {
+    wave_walsh_lanes<LE>(v);
+    wave_walsh_put<LE, NWP>(v, xs);
+    sync();
+    wave_walsh_get<LE, NWP>(v, xs);
+}
+// two rows at once (a through xa, b through xb), one sync() for both
+template <int LE, int NWP, class SY>
+__device__ __forceinline__ void wave_walsh2(float (&a)[1 << LE], float (&b)[1 << LE], float* xa, float* xb, SY&& sync) {
+    wave_walsh_lanes<LE>(a);
+    wave_walsh_lanes<LE>(b);
+    wave_walsh_put<LE, NWP>(a, xa);
+    wave_walsh_put<LE, NWP>(b, xb);
+    sync();
+    wave_walsh_get<LE, NWP>(a, xa);
+    wave_walsh_get<LE, NWP>(b, xb);
 }
 
 // Last layout (C, or D for four passes) -> layout A through xs (own slots first, one barrier).

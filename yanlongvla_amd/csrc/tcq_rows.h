@@ -374,10 +374,12 @@ __device__ __forceinline__ bool panp_tw(const PanpArgs& A, int tok, bool store, 
 // --------------------------------------------------------- rows of 1024 / 2048 on four or eight waves, no transposes
 // LDS of panp_waves / waves_rotate_quantize: the exchange rows of wave_walsh, the per-wave sums and maxima. The two take
 // WAVES_SYNCS calls of sync() together (two each).
-struct WavesLds {
-    float xs[2048];
+template <int N>
+struct WavesLdsN {
+    float xs[N];
     float red[16];
 };
+typedef WavesLdsN<2048> WavesLds;
 constexpr int WAVES_SYNCS = 4;
 
 // panp_tw for token tok of a 2^L-wide row (L = 10 or 11) with the norm (A.w set, no bias) on waves 0 .. NWP - 1 (NWP = 4
@@ -503,10 +505,11 @@ __device__ __forceinline__ void panp_waves(const PanpArgs& A, int tok, bool stor
 // layout), with two sync() points: wave_walsh, the row maximum over the waves through LDS, the INT8 row into qs (LDS, E
 // bytes per thread), q (row tok), q4 (the word layout, or token blocks when ldq is TCQ_LDQ_TOKEN_BLOCKS) as given; the
 // scale into *scs and scale[tok] as given. The same values as tw_rotate_quantize<L, LE>.
-template <int NWP, int L = 11, class SY>
-__device__ __forceinline__ void waves_rotate_quantize(float (&v)[(1 << L) / 64 / NWP], WavesLds& Q, u32* qs, float* scs, i8* q,
-                                                      float* scale, SY&& sync, int tok = 0, int* q4 = nullptr, int ldq = 0) {
+template <int NWP, int L = 11, class QL, class SY>
+__device__ __forceinline__ void waves_rotate_quantize(float (&v)[(1 << L) / 64 / NWP], QL& Q, u32* qs, float* scs, i8* q, float* scale,
+                                                      SY&& sync, int tok = 0, int* q4 = nullptr, int ldq = 0) {
     constexpr int N = 1 << L, E = N / 64 / NWP, LE = E == 8 ? 3 : 2;
+    static_assert((E == 4 || E == 8) && sizeof(Q.xs) >= N * sizeof(float), "4 or 8 values per thread, an exchange row of N");
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const float c = (float)(1.0 / __builtin_sqrt((double)N));
     wave_walsh<LE, NWP>(v, Q.xs, sync);

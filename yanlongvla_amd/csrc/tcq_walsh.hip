@@ -929,6 +929,138 @@ __global__ __launch_bounds__(1 << (L - LE), 4) void k_mid2_tw(const void* acc, i
     tw_rotate_quantize<L, LE>(u, xs, red, q, q4, ldq, scale, tok);
 }
 
+// k_postg_tw for groups whose segments are all 256 or 2048 wide, on the no-transpose engine with 4 values per thread:
+// a 2048-wide segment on all 8 waves (one LDS exchange), a 256-wide one inside wave 0 (index bits inside the thread and
+// across the lanes only). The same operations in the same order, y = conv(((walsh(acc) * c) * sv) (+ bias), GELU).
+template <int ADT, int YDT, int L, int NWP>
+__device__ __forceinline__ void postg_wv_seg(const tcq_post_seg& S, int tok, float st, const u16* gelu, float* xs) {
+    constexpr int N = 1 << L;
+    const int i0 = 4 * threadIdx.x;
+    float v[4];
+    const size_t base = (size_t)tok * S.lda + S.col0 + i0;
+    if (ADT == TCQ_I32) {
+        const uint4_t a = *gptr((const uint4_t*)((const u32*)S.acc + base));
+        const float4_t r = *gptr((const float4_t*)(S.rs + i0));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = ((float)(int)a[k] * st) * r[k];
+    } else if (ADT == TCQ_BF16) {
+        const uint2_t a = *gptr((const uint2_t*)((const u16*)S.acc + base));
+        const float4_t r = *gptr((const float4_t*)(S.rs + i0));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            v[2 * k] = __uint_as_float(a[k] << 16) * r[2 * k];
+            v[2 * k + 1] = __uint_as_float(a[k] & 0xffff0000u) * r[2 * k + 1];
+        }
+    } else {
+        const float4_t a = *gptr((const float4_t*)((const float*)S.acc + base));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = a[k];
+    }
+    const u32 sg = *gptr((const u32*)(S.sv + i0));
+    float4_t b = {0.f, 0.f, 0.f, 0.f};
+    if (S.bias) b = *gptr((const float4_t*)(S.bias + i0));
+    wave_walsh_lanes<2>(v);
+    if constexpr (NWP > 1) {
+        wave_walsh_put<2, NWP>(v, xs);
+        __syncthreads();
+        wave_walsh_get<2, NWP>(v, xs);
+    }
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k] = (v[k] * c) * (float)(i8)(sg >> (8 * k));
+        if (S.bias) v[k] = v[k] + b[k];
+        if (YDT == TCQ_BF16 && gelu) v[k] = bf16_to_f32(gptr(gelu)[f32_to_bf16(v[k])]);
+    }
+    const size_t o = (size_t)tok * N + i0;
+    if constexpr (YDT == TCQ_F32) {
+        *gptr((float4_t*)((float*)S.y + o)) = float4_t{v[0], v[1], v[2], v[3]};
+    } else if constexpr (YDT == TCQ_BF16) {
+        u32 w2[2];
+        bf16_pack<2>(v, w2);
+        *gptr((uint2_t*)((u16*)S.y + o)) = uint2_t{w2[0], w2[1]};
+    } else {
+        *gptr((uint2_t*)((u16*)S.y + o)) = uint2_t{(u32)f32_to_f16(v[0]) | ((u32)f32_to_f16(v[1]) << 16),
+                                                   (u32)f32_to_f16(v[2]) | ((u32)f32_to_f16(v[3]) << 16)};
+    }
+}
+template <int ADT, int YDT, class SEGS>
+__global__ __launch_bounds__(512) void k_postg_wv(SEGS segs, const float* s, const u16* gelu_lut) {
+    __shared__ float xs[2048];
+    const tcq_post_seg S = segs[blockIdx.y];
+    const int tok = blockIdx.x;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    const u16* gl = S.gelu ? gelu_lut : nullptr;
+    if (S.N == 2048) postg_wv_seg<ADT, YDT, 11, 8>(S, tok, st, gl, xs);   // uniform
+    else if (threadIdx.x < 64) postg_wv_seg<ADT, YDT, 8, 1>(S, tok, st, gl, xs);
+}
+
+// k_mid2 for few rows of 2^L = 1024 .. 4096 on the no-transpose engine: NWP waves, E = 2^L / 64 / NWP = 4 or 8 values of
+// each half per thread (natural layout, loaded straight from the accumulators); the gate and up transforms share one LDS
+// exchange (wave_walsh2), GELU, product and signs follow in the thread, then waves_rotate_quantize with its own exchange
+// row. The same operations on each value in the same order as k_mid2_tw2.
+template <int ADT, int L, int NWP>
+__global__ __launch_bounds__(64 * NWP) void k_mid2_wv(const void* acc, int lda, const float* s, const float* rs, const i8* sv,
+                                                      const u16* lut, const i8* su, i8* q, int* q4, int ldq, float* scale) {
+    constexpr int N = 1 << L, E = N / 64 / NWP, LE = E == 8 ? 3 : 2;
+    static_assert(E == 4 || E == 8, "4 or 8 values per thread");
+    __shared__ float xg[N], xu[N];
+    __shared__ WavesLdsN<N> Qr;
+    const int tok = blockIdx.x, t = threadIdx.x, i0 = E * t;
+    const size_t base = (size_t)tok * lda + i0;
+    const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
+    auto ld_i8 = [&](const i8* p, float (&o)[E]) {
+        if constexpr (E == 8) {
+            ld8_i8v(p, o);
+        } else {
+            const u32 x = *gptr((const u32*)p);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = (float)(i8)(x >> (8 * k));
+        }
+    };
+    // accumulator values i0 .. i0 + E - 1 of the half at column offset h (scaled as acc_chunk scales them)
+    auto ld_acc = [&](size_t off, const float* r, float (&o)[E]) {
+        if constexpr (E == 8) {
+            acc_piece8<ADT>(acc, base + off, st, r ? r + i0 : nullptr, o, 1, 0);
+        } else if constexpr (ADT == TCQ_I32) {
+            const uint4_t a = *gptr((const uint4_t*)((const u32*)acc + base + off));
+            const float4_t rv = *gptr((const float4_t*)(r + i0));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = ((float)(int)a[k] * st) * rv[k];
+        } else if constexpr (ADT == TCQ_BF16) {
+            const uint2_t a = *gptr((const uint2_t*)((const u16*)acc + base + off));
+            const float4_t rv = *gptr((const float4_t*)(r + i0));
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                o[2 * k] = __uint_as_float(a[k] << 16) * rv[2 * k];
+                o[2 * k + 1] = __uint_as_float(a[k] & 0xffff0000u) * rv[2 * k + 1];
+            }
+        } else {
+            const float4_t a = *gptr((const float4_t*)((const float*)acc + base + off));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = a[k];
+        }
+    };
+    float g[E], u[E], sg[E], sgu[E], sn[E];
+    ld_i8(sv + i0, sg);
+    ld_i8(sv + N + i0, sgu);
+    ld_i8(su + i0, sn);
+    ld_acc(0, rs, g);
+    ld_acc(N, rs ? rs + N : nullptr, u);
+    const auto bar = [] { __syncthreads(); };
+    const float c = (float)(1.0 / __builtin_sqrt((double)N));
+    wave_walsh2<LE, NWP>(g, u, xg, xu, bar);
+    u16 gv[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) gv[k] = gptr(lut)[f32_to_bf16(g[k] * c * sg[k])];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        const float uu = bf16_to_f32(f32_to_bf16((u[k] * c) * sgu[k]));
+        u[k] = bf16_to_f32(f32_to_bf16(bf16_to_f32(gv[k]) * uu)) * sn[k];
+    }
+    waves_rotate_quantize<NWP, L>(u, Qr, nullptr, nullptr, q, scale, bar, tok, q4, ldq);
+}
+
 // k_mid2_tw with the gate and up transforms side by side (tw_walsh2: one barrier per pass for both rows; LDS for two rows,
 // so it serves as many rows as fit one wave of workgroups): the same operations on each row in the same order.
 template <int ADT, int L, int LE>
@@ -1384,6 +1516,23 @@ extern "C" int tcq_mid2(const void* acc, int acc_dtype, int lda, const float* s,
                                 (i8*)q, (int*)q4, ldq, scale); break;                                                         \
         default: return TCQ_ERR_DTYPE;                                                                                        \
     }
+        if (M <= 64 && N <= 4096) {                       // few rows: the no-transpose engine on 4 (1024) or 8 waves
+#define MID2_WV(L, NWP)                                                                                                     \
+    switch (acc_dtype) {                                                                                                      \
+        case TCQ_I32: launch_k(k_mid2_wv<TCQ_I32, L, NWP>, grid, dim3(64 * NWP), 0, st, acc, lda, s, rs, svp, gelu_lut, sup,     \
+                               (i8*)q, (int*)q4, ldq, scale); break;                                                          \
+        case TCQ_F32: launch_k(k_mid2_wv<TCQ_F32, L, NWP>, grid, dim3(64 * NWP), 0, st, acc, lda, s, rs, svp, gelu_lut, sup,     \
+                               (i8*)q, (int*)q4, ldq, scale); break;                                                          \
+        case TCQ_BF16: launch_k(k_mid2_wv<TCQ_BF16, L, NWP>, grid, dim3(64 * NWP), 0, st, acc, lda, s, rs, svp, gelu_lut, sup,   \
+                                (i8*)q, (int*)q4, ldq, scale); break;                                                         \
+        default: return TCQ_ERR_DTYPE;                                                                                        \
+    }
+            if (N == 1024) MID2_WV(10, 4)
+            else if (N == 2048) MID2_WV(11, 8)
+            else MID2_WV(12, 8)
+#undef MID2_WV
+            return launch_status();
+        }
         if (M <= 256) {                                   // gate and up side by side (two LDS rows per workgroup)
 #undef MID2_TW
 #define MID2_TW(L, LE) MID2_TWK(k_mid2_tw2, L, LE, 2 * tsh)
@@ -1471,11 +1620,20 @@ extern "C" int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype,
     // widest segment a power of two of 256 .. 4096: the register + transpose engine (16 values per thread) for the
     // power-of-two segments; measured on MI355X for q / k / v of 2048 / 256 / 256 at 50 tokens: 3.5 us against 4.1 on LDS
     const bool tw = (maxN & (maxN - 1)) == 0 && maxN >= 256 && maxN <= 4096;
-    const dim3 grid(M, nseg), block(tw ? maxN / 16 : row_threads(M * nseg, maxN));
-    const size_t sh = row_lds(maxN);
+    // few tokens and segments of 256 / 2048 only, 16-byte aligned: the no-transpose engine (k_postg_wv)
+    const int esz = dsize(acc_dtype), ysz = dsize(y_dtype);
+    bool wv = M <= 64;
+    for (int i = 0; i < nseg; ++i) {
+        const tcq_post_seg& g = segs[i];
+        wv = wv && (g.N == 256 || g.N == 2048) && al16(g.acc) && ((size_t)g.lda * esz) % 16 == 0 && ((size_t)g.col0 * esz) % 16 == 0 &&
+             al16(g.y) && al16(g.sv) && (!g.rs || al16(g.rs)) && (!g.bias || al16(g.bias)) && ysz >= 2;
+    }
+    const dim3 grid(M, nseg), block(wv ? 512 : tw ? maxN / 16 : row_threads(M * nseg, maxN));
+    const size_t sh = wv ? 0 : row_lds(maxN);
     hipStream_t st = (hipStream_t)stream;
 #define POSTV_Y(AD, YD)                                                                                                    \
-    if (tw) launch_k(k_postg_tw<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN);                \
+    if (wv) launch_k(k_postg_wv<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut);                      \
+    else if (tw) launch_k(k_postg_tw<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN);           \
     else launch_k(k_postg<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN)
 #define POSTV_A(AD)                                          \
     switch (y_dtype) {                                       \
