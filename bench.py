@@ -51,13 +51,15 @@ def parse():
     p.add_argument('--no-ops', action='store_true', help='skip the RHT and W8A8 GEMM measurements')
     p.add_argument('--no-backbone', action='store_true', help='skip the Gemma-2B-shaped backbone measurement')
     p.add_argument('--backbone-replays', type=int, default=10)
-    p.add_argument('--probe', choices=('gate_up', 'qkv', 'gate_up_dot4', 'qkv_dot4', 'mid2', 'gemm', 'prefill', 'decode', 'chunk'),
+    p.add_argument('--probe', choices=('gate_up', 'qkv', 'gate_up_dot4', 'qkv_dot4', 'mid2', 'gemm', 'prefill', 'decode', 'chunk',
+                                       'layer'),
                    help='only run one kernel kind --probe-reps times (for rocprofv3 counter passes): the fused decode '
                         'product of one token at the backbone gate/up (32768 x 2048, k_gemv_tcq) or q/k/v (2560 x 2048, '
                         'k_gemm_small) shape over distinct weight sets, the one-token GeGLU middle (16384 wide, '
                         'k_mid2_tw2), the W8A8 GEMM 800 x 2048 x 16384 (k_gemm_i8, int32 out) over distinct weights, or '
                         'the backbone\'s 800-token prefill (fly) or its 32 decode steps as one graph, or one action chunk '
-                        '(fly) as one graph')
+                        '(fly) as one graph, or 100 steps of the single 2048 x 2048 FP16-table layer (three launches each) '
+                        'as one graph')
     p.add_argument('--probe-reps', type=int, default=10)
     p.add_argument('--classes', choices=('chunk', 'backbone'), default=None,
                    help='child mode of the bench: print the kernel classes of the fly stages of one workload as JSON')
@@ -759,6 +761,17 @@ def probe(kind, reps, dev):
         su = (torch.randint(0, 2, (N,), generator=g, device=dev) * 2 - 1).to(torch.int8)
         q4, sc, lut = K.token_blocks(1, N, dev), torch.empty(1, device=dev), K.gelu_table(dev)
         calls = [lambda: K.mid2(acc, None, None, sv, su, q4=q4, scale=sc, gelu_lut=lut)] * 64
+    elif kind == 'layer':
+        from yanlongvla_amd import harness
+        L = make_stream(1, 0, dev)
+        x = torch.randn(1, N_DIM, generator=g, device=dev).half()
+        S1 = Stream(L, x, fused=False)
+
+        def steps():
+            for _ in range(100):
+                S1.step()
+        g = harness.capture(steps)
+        calls = [g.replay]
     elif kind == 'chunk':
         from yanlongvla_amd import harness
         with torch.inference_mode():

@@ -369,9 +369,11 @@ def test_layer_f16_graph_replays():
 
 
 @pytest.mark.parametrize('K,M,xdt', [(256, 1, torch.float16), (1024, 3, torch.bfloat16), (2048, 1, torch.float16),
-                                     (16384, 2, torch.float32), (1152, 2, torch.float16), (2048, 5, torch.bfloat16)])
+                                     (16384, 2, torch.float32), (1152, 2, torch.float16), (2048, 5, torch.bfloat16),
+                                     (1024, 64, torch.float32), (2048, 65, torch.float16)])
 def test_pre_h16_bitexact(K, M, xdt):
-    """The float path's input rotation (register engine for power-of-two rows, LDS engine otherwise) against the oracle:
+    """The float path's input rotation (no-transpose engine for up to 64 rows of 1024 / 2048, register engine for other
+    power-of-two rows, LDS engine otherwise) against the oracle:
     h = fwht(x * su), hscale = 2^e with amax / 2^e in [2^14, 2^15), h16 = FP16(h / hscale), bit for bit."""
     from yanlongvla_amd import kernels as K_
     rng = np.random.default_rng(K + M)
@@ -501,6 +503,33 @@ def test_postg_matches_post_and_oracle(M):
     for z, v, y in zip(zs, svs, outs):
         ref = O.fwht(z.cpu().numpy()) * v.astype(np.float32)
         assert np.array_equal(bits_of(y), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize('M', [1, 7])
+def test_postg_few_tokens_mixed_widths(M):
+    """Device descriptors with a 2048-wide segment beside segments of other widths and an unaligned column offset: the
+    few-token kernel rotates the aligned 2048 / 256 segments on its own engine and the rest on the LDS engine; every output
+    equals the oracle's epilogue bit for bit."""
+    from yanlongvla_amd import kernels as K
+    rng = np.random.default_rng(100 + M)
+    widths, col0s, lda = [2048, 256, 1024, 300, 256], [0, 2048, 2304, 3328, 3629], 3900
+    acc = (rng.standard_normal((M, lda)) * 0.3).astype(np.float32)
+    sv = np.where(rng.integers(0, 2, lda) > 0, 1, -1).astype(np.int8)
+    bias = (rng.standard_normal(lda) * 0.1).astype(np.float32)
+    accd, segs, ys = T(acc), [], []
+    for i, (w, c0) in enumerate(zip(widths, col0s)):
+        y = torch.empty(M, w, dtype=torch.bfloat16, device=DEV)
+        segs.append((accd, c0, None, T(sv[c0:c0 + w].copy()), T(bias[c0:c0 + w].copy()) if i % 2 else None, y, i == 2))
+        ys.append(y)
+    lut = K.gelu_table(DEV)
+    desc = K.post_segments(segs, DEV)
+    K.post_batched(desc, len(segs), torch.float32, torch.bfloat16, None, M, 2048, gelu_lut=lut)
+    lut_np = lut.view(torch.int16).cpu().numpy().view(np.uint16)
+    for i, (w, c0, y) in enumerate(zip(widths, col0s, ys)):
+        ref = O.post_bf16(acc[:, c0:c0 + w], sv[c0:c0 + w], bias[c0:c0 + w] if i % 2 else None)
+        if i == 2:
+            ref = lut_np[ref]
+        assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), ref), i
 
 
 def test_bf16_conversion_of_every_exponent_and_payload():

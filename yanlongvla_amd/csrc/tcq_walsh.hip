@@ -281,6 +281,54 @@ __global__ void k_pre_h16(const void* x, const i8* su, u16* h16, float* hscale, 
     }, [&](int, float v) { return ldexpf(v, -e); });
 }
 
+// k_pre_h16 for few rows of 2^L = 1024 / 2048 on the no-transpose engine (NWP = 2^L / 256 waves, 4 values per thread): the
+// same sign products, butterflies, constant, maximum and scaling as k_pre_h16.
+template <int XDT, int L, int NWP>
+__global__ __launch_bounds__(64 * NWP) void k_pre_h16_wv(const void* x, const i8* su, u16* h16, float* hscale) {
+    constexpr int K = 1 << L;
+    __shared__ float xs[K];
+    __shared__ float red[NWP];
+    const int tok = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const size_t i0 = (size_t)tok * K + 4 * t;
+    float v[4];
+    if constexpr (XDT == TCQ_F32) {
+        const float4_t a = *gptr((const float4_t*)((const float*)x + i0));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = a[k];
+    } else {
+        const uint2_t a = *gptr((const uint2_t*)((const u16*)x + i0));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = Elem16<XDT>::cv((u16)(a[k >> 1] >> (16 * (k & 1))));
+    }
+    if (su) {
+        const u32 sg = *gptr((const u32*)(su + 4 * t));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = v[k] * (float)(i8)(sg >> (8 * k));
+    }
+    wave_walsh<2, NWP>(v, xs, [] { __syncthreads(); });
+    const float c = (float)(1.0 / __builtin_sqrt((double)K));
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k] = v[k] * c;
+        mx = fmaxf(mx, fabsf(v[k]));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWP; ++i) amax = fmaxf(amax, red[i]);
+    int e = 0;
+    if (amax > 0.f && amax < __builtin_inff()) {
+        frexpf(amax, &e);
+        e -= 15;
+    }
+    if (t == 0) hscale[tok] = ldexpf(1.f, e);
+    *gptr((uint2_t*)(h16 + i0)) = uint2_t{(u32)f32_to_f16(ldexpf(v[0], -e)) | ((u32)f32_to_f16(ldexpf(v[1], -e)) << 16),
+                                         (u32)f32_to_f16(ldexpf(v[2], -e)) | ((u32)f32_to_f16(ldexpf(v[3], -e)) << 16)};
+}
+
 // k_pre_h16 on the register engine for power-of-two rows of 256 .. 16384 (thread t < K / 16 owns elements [16 t, 16 t + 16),
 // 16-byte loads and stores): the same sign products, butterflies, constant, maximum and scaling as k_pre_h16.
 template <int XDT>
@@ -984,15 +1032,32 @@ __device__ __forceinline__ void postg_wv_seg(const tcq_post_seg& S, int tok, flo
                                                    (u32)f32_to_f16(v[2]) | ((u32)f32_to_f16(v[3]) << 16)};
     }
 }
+// Segments of other widths or alignments (device descriptors, which the host cannot inspect) take the LDS engine of
+// k_postg (dynamic LDS of lds_words(maxN) floats).
 template <int ADT, int YDT, class SEGS>
-__global__ __launch_bounds__(512) void k_postg_wv(SEGS segs, const float* s, const u16* gelu_lut) {
+__global__ __launch_bounds__(512) void k_postg_wv(SEGS segs, const float* s, const u16* gelu_lut, int maxN) {
+    extern __shared__ float lds[];
     __shared__ float xs[2048];
     const tcq_post_seg S = segs[blockIdx.y];
-    const int tok = blockIdx.x;
+    const int tok = blockIdx.x, N = S.N;
+    if (N <= 0 || N > maxN || (ADT != TCQ_F32 && !S.rs)) return;    // uniform
     const float st = ADT == TCQ_I32 ? s[tok] : 1.f;
     const u16* gl = S.gelu ? gelu_lut : nullptr;
-    if (S.N == 2048) postg_wv_seg<ADT, YDT, 11, 8>(S, tok, st, gl, xs);   // uniform
-    else if (threadIdx.x < 64) postg_wv_seg<ADT, YDT, 8, 1>(S, tok, st, gl, xs);
+    const int esz = ADT == TCQ_BF16 ? 2 : 4, ysz = YDT == TCQ_F32 ? 4 : 2;
+    const bool al = aligned16(S.acc) && ((size_t)S.lda * esz) % 16 == 0 && ((size_t)S.col0 * esz) % 16 == 0 && aligned16(S.y) &&
+                    aligned16(S.sv) && (!S.rs || aligned16(S.rs)) && (!S.bias || aligned16(S.bias));
+    if (al && N == 2048) {                                           // uniform
+        postg_wv_seg<ADT, YDT, 11, 8>(S, tok, st, gl, xs);
+        return;
+    }
+    if (al && N == 256) {
+        if (threadIdx.x < 64) postg_wv_seg<ADT, YDT, 8, 1>(S, tok, st, gl, xs);
+        return;
+    }
+    const bool vec = N % 8 == 0 && al && ((size_t)N * ysz) % 16 == 0 && ((uintptr_t)S.sv & 7) == 0;
+    load_acc_row<ADT>(lds, S.acc, (size_t)tok * S.lda + S.col0, st, S.rs, N, vec);
+    walsh_inplace(lds, N);
+    store_post_row<YDT>(lds, S.y, (size_t)tok * N, S.sv, S.bias, gl, N, vec);
 }
 
 // k_mid2 for few rows of 2^L = 1024 .. 4096 on the no-transpose engine: NWP waves, E = 2^L / 64 / NWP = 4 or 8 values of
@@ -1365,6 +1430,13 @@ extern "C" int tcq_pre_h16(const void* x, int x_dtype, const int8_t* su, void* h
     const size_t sh = row_lds(K);
     const int vec = K % 8 == 0 && al16(x) && al16(h16) && ((size_t)K * dsize(x_dtype)) % 16 == 0 && (!su || al8(su));
     hipStream_t st = (hipStream_t)stream;
+    if (M <= 64 && (K == 1024 || K == 2048) && vec && (!su || al16(su))) {   // few rows: the no-transpose engine
+#define PREHW(XD, _) if (K == 1024) launch_k(k_pre_h16_wv<XD, 10, 4>, grid, dim3(256), 0, st, x, (const i8*)su, (u16*)h16, hscale); \
+                     else launch_k(k_pre_h16_wv<XD, 11, 8>, grid, dim3(512), 0, st, x, (const i8*)su, (u16*)h16, hscale)
+        DISPATCH_X(x_dtype, PREHW, 0)
+#undef PREHW
+        return launch_status();
+    }
     if ((K & (K - 1)) == 0 && K >= 256 && vec && (!su || al16(su))) {     // register engine
         const int nt = K / 16 < 64 ? 64 : K / 16;
 #define PREHR(XD, _) launch_k(k_pre_h16_reg<XD>, grid, dim3(nt), (size_t)K * sizeof(float), st, x, (const i8*)su, (u16*)h16, hscale, K)
@@ -1464,11 +1536,13 @@ extern "C" int tcq_postg(const tcq_post_seg* segs, int nseg, int acc_dtype, cons
     if (maxN > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     if (nseg > 65535) return TCQ_ERR_UNSUPPORTED;
     const bool tw = (maxN & (maxN - 1)) == 0 && maxN >= 256 && maxN <= 4096;
-    const dim3 grid(M, nseg), block(tw ? maxN / 16 : row_threads(M * nseg, maxN));
+    const bool wv = M <= 64 && maxN == 2048;                 // few tokens: 2048 / 256-wide segments on the no-transpose engine
+    const dim3 grid(M, nseg), block(wv ? 512 : tw ? maxN / 16 : row_threads(M * nseg, maxN));
     const size_t sh = row_lds(maxN);
     hipStream_t st = (hipStream_t)stream;
 #define POSTG_Y(AD, YD)                                                                                                    \
-    if (tw) launch_k(k_postg_tw<AD, YD, const tcq_post_seg*>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN);   \
+    if (wv) launch_k(k_postg_wv<AD, YD, const tcq_post_seg*>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN);   \
+    else if (tw) launch_k(k_postg_tw<AD, YD, const tcq_post_seg*>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN); \
     else launch_k(k_postg<AD, YD, const tcq_post_seg*>, grid, block, sh, st, segs, s, (const u16*)gelu_lut, maxN)
 #define POSTG_A(AD)                                          \
     switch (y_dtype) {                                       \
@@ -1629,10 +1703,11 @@ extern "C" int tcq_post_group(const tcq_post_seg* segs, int nseg, int acc_dtype,
              al16(g.y) && al16(g.sv) && (!g.rs || al16(g.rs)) && (!g.bias || al16(g.bias)) && ysz >= 2;
     }
     const dim3 grid(M, nseg), block(wv ? 512 : tw ? maxN / 16 : row_threads(M * nseg, maxN));
+    // no dynamic LDS for k_postg_wv here: its own checks equal the ones above, so it never takes its LDS fallback
     const size_t sh = wv ? 0 : row_lds(maxN);
     hipStream_t st = (hipStream_t)stream;
 #define POSTV_Y(AD, YD)                                                                                                    \
-    if (wv) launch_k(k_postg_wv<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut);                      \
+    if (wv) launch_k(k_postg_wv<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN);                \
     else if (tw) launch_k(k_postg_tw<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN);           \
     else launch_k(k_postg<AD, YD, PostPack>, grid, block, sh, st, pk, s, (const u16*)gelu_lut, maxN)
 #define POSTV_A(AD)                                          \
