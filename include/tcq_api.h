@@ -346,6 +346,14 @@ int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev
                   const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
                   tcq_stream_t stream);
 
+/* The first two steps of that layer in one launch: z (M, m) FP32 = walsh(x * su) Q^T * row_scale, i.e. tcq_pre_h16 +
+ * tcq_gemv_f16 (its latency plan) step for step, so z equals that two-launch chain bit for bit; tcq_post(z, ...) then gives
+ * tcq_layer_f16's y. For one layer, the input rotation and the FP16-table product of tcq_format.reference_linear(table='fp16',
+ * a8=False) (tcq_format.py:139-144); the reference's kernel counterparts are kernels.pre_h + kernels.gemmf_tcq
+ * (kernels.py:309-317, 465-489). Arguments as tcq_layer_f16 (no workspace: z is the output). */
+int tcq_pre_gemv_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                     int M, int m, int n, float* z, tcq_stream_t stream);
+
 /* One layer (segment) of a small-M INT8 product. The output of the segment starts at its first column: out[t * ldo + i] for
  * token t and output row i < m (the layers of a q/k/v or gate/up group write side by side into one (M, ldo) buffer). */
 typedef struct tcq_gemm_seg {

@@ -305,11 +305,12 @@ def test_gemv_f16_layer(m, n, M, nl):
 @pytest.mark.parametrize('m,n,M,xdt,ydt', [(2048, 2048, 1, torch.float16, torch.float16), (2048, 2048, 4, torch.bfloat16, torch.float32),
                                            (1024, 4096, 1, torch.float32, torch.bfloat16), (4096, 1024, 2, torch.float16, torch.float16),
                                            (64, 1152, 3, torch.float16, torch.float32), (1536, 512, 1, torch.bfloat16, torch.bfloat16),
-                                           (256, 16384, 1, torch.float16, torch.float16)])
+                                           (256, 16384, 1, torch.float16, torch.float16), (1024, 1024, 16, torch.float32, torch.bfloat16),
+                                           (2048, 2048, 16, torch.bfloat16, torch.float16)])
 def test_layer_f16_one_launch(m, n, M, xdt, ydt):
     """tcq_layer_f16 equals the three-launch chain pre_h16 -> gemv_f16 -> post bit for bit (y and z), twice in a row on
     different inputs (the second call finds the counter the first left at zero), and is within 2e-3 of the oracle's
-    reference_linear(table='fp16', a8=False)."""
+    reference_linear(table='fp16', a8=False); tcq_pre_gemv_f16 gives the same z."""
     from yanlongvla_amd import kernels as K
     L = O.random_layer(m, n, 300 + m + M)
     d = dev_layer(L)
@@ -330,6 +331,9 @@ def test_layer_f16_one_launch(m, n, M, xdt, ydt):
         y3 = torch.empty(M, m, dtype=ydt, device=DEV)
         K.post(z3, None, None, d['sv'], bias, y3)
         assert torch.equal(z, z3), call
+        z2 = torch.full((M, m), float('nan'), dtype=torch.float32, device=DEV)
+        K.pre_gemv_f16(x, d['su'], wdev, d['tlut'], d['row_scale'], z2)
+        assert torch.equal(z2, z3), call
         assert torch.equal(y.view(torch.int16) if ydt != torch.float32 else y, y3.view(torch.int16) if ydt != torch.float32 else y3), call
         assert int(counter.item()) == 0
         ref = O.reference_linear(x.float().cpu().numpy(), L, a8=False, table='fp16', out_dtype='f32') + bias.cpu().numpy()

@@ -43,6 +43,7 @@ SIGNATURES = {
     'tcq_gemv_f16_groups': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_gemv_f16_post': [_P, _I, _P, _P, _I, _I, _I, _I, _P],
     'tcq_layer_f16': [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
+    'tcq_pre_gemv_f16': [_P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P],
     'tcq_gemm_bf16': [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     'tcq_attend': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     'tcq_attend_q4': [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P, _P],

@@ -428,23 +428,50 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
     const u32 cp4 = (u32)(lane & (C - 1)) << 2;
     const int nchw = wave < nch ? (nch - 1 - wave) / KS + 1 : 0;
     const rsrc_t W = make_rsrc(A.wdev, (u32)(tiles_m * nch) << 10);
-    uint4_t buf[LAYER_MAXCW];
+    // the codebook's halves first (fill_table's entries: tid + 64 KS j), so the table fill waits for them alone
+    constexpr int TPT = NE / (64 * KS);
+    u16 tl0[TPT], tl1[TPT];
 #pragma unroll
-    for (int j = 0; j < LAYER_MAXCW; ++j)
-        if (j < nchw)
-            buf[j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, (u32)lane << 4, (u32)(I * nch + wave + j * KS) << 10, 2));
-    const bool rin = vec && reg_row(n), rout = vec && reg_row(m);
+    for (int j = 0; j < TPT; ++j) {
+        const int h = (tid + 64 * KS * j) & 511;
+        tl0[j] = gptr(A.tlut)[2 * h];
+        tl1[j] = gptr(A.tlut)[2 * h + 1];
+    }
+    // rows of 256 KS = 64 KS x 4 values (KS = 4 or 8 waves): the no-transpose engine (wave_walsh), thread t holding
+    // elements [4 t, 4 t + 4); other power-of-two rows: registers (16 values per thread); the rest: the LDS block Walsh
+    constexpr int WL = KS == 4 ? 10 : KS == 8 ? 11 : 0;
+    const bool win = WL != 0 && vec && n == 1 << WL, wout = WL != 0 && vec && m == 1 << WL;
+    const bool rin = !win && vec && reg_row(n), rout = !wout && vec && reg_row(m);
     const bool on_in = tid < (n >> 4), on_out = tid < (m >> 4);
-    // token 0's input, the input signs and the output signs / bias of the final rotation (used only by the workgroup that
-    // completes the count), all issued before the table fill
+    // token 0's input and the input signs, then the words, then the output signs / bias of the final rotation (used only
+    // by the workgroup that completes the count), all issued before the table fill (the no-transpose engine keeps them in
+    // xr[0], s4[0], sv4[0], b4[0])
     uint4_t xr[4], s4 = {0, 0, 0, 0}, sv4 = {0, 0, 0, 0};
     float4_t b4[4];
+    if (win) {
+        if constexpr (XDT == TCQ_F32) {
+            xr[0] = gptr((const uint4_t*)((const float*)A.x + 4 * tid))[0];
+        } else {
+            const uint2_t a = gptr((const uint2_t*)((const u16*)A.x + 4 * tid))[0];
+            xr[0] = uint4_t{a[0], a[1], 0, 0};
+        }
+        s4[0] = gptr((const u32*)(A.su + 4 * tid))[0];
+    }
     if (rin && on_in) {
 #pragma unroll
         for (int h = 0; h < (XDT == TCQ_F32 ? 4 : 2); ++h) xr[h] = gptr((const uint4_t*)((const char*)A.x + (size_t)16 * tid * (XDT == TCQ_F32 ? 4 : 2)))[h];
         s4 = gptr((const uint4_t*)(A.su + 16 * tid))[0];
     }
-    if (rout && on_out) {
+    uint4_t buf[LAYER_MAXCW];
+#pragma unroll
+    for (int j = 0; j < LAYER_MAXCW; ++j)
+        if (j < nchw)
+            buf[j] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, (u32)lane << 4, (u32)(I * nch + wave + j * KS) << 10, 2));
+    if (wout && A.counter) {
+        sv4[0] = gptr((const u32*)(A.sv + 4 * tid))[0];
+        if (A.bias) b4[0] = gptr((const float4_t*)(A.bias + 4 * tid))[0];
+    }
+    if (rout && on_out && A.counter) {
         sv4 = gptr((const uint4_t*)(A.sv + 16 * tid))[0];
         if (A.bias) {
 #pragma unroll
@@ -456,11 +483,71 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
     u16* hl = (u16*)dyn;                                          // h16 rows (M, np), zero from n on
     float* row = (float*)(dyn + (M * np >> 1));                   // one FP32 row (input rotation, then output rotation)
     float4_t* part = (float4_t*)(row + lds_words(max(n, m)));     // the KS waves' partial sums
-    fill_table<C, NE>(tab, A.tlut);
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {                               // fill_table's entries from the loaded halves
+        const int e = tid + 64 * KS * j;
+        const u32 v = ((u32)tl0[j] ^ ((u32)(e >> 9) << 15)) | ((u32)tl1[j] << 16);
+        if constexpr (C % 4 == 0) {
+#pragma unroll
+            for (int c = 0; c < C; c += 4) *(uint4_t*)(tab + e * C + c) = uint4_t{v, v, v, v};
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; ++c) tab[e * C + c] = v;
+        }
+    }
     // input rotation of every token row, as tcq_pre_h16: h = walsh(x * su), hscale = 2^e with amax / 2^e in [2^14, 2^15)
+    float hsw = 0.f;                                              // no-transpose engine: the lane's token's hscale
     for (int t = 0; t < M; ++t) {
         float mx = 0.f;
-        if (rin) {
+        if (win) {
+            if constexpr (WL != 0) {
+                float v[4];
+                uint4_t a = xr[0];
+                if (t > 0) {
+                    const size_t i = (size_t)t * n + 4 * tid;
+                    if constexpr (XDT == TCQ_F32) {
+                        a = gptr((const uint4_t*)((const float*)A.x + i))[0];
+                    } else {
+                        const uint2_t b = gptr((const uint2_t*)((const u16*)A.x + i))[0];
+                        a = uint4_t{b[0], b[1], 0, 0};
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const u32 w = XDT == TCQ_F32 ? a[k] : a[k >> 1] >> (16 * (k & 1));
+                    const float xv = XDT == TCQ_F32 ? __uint_as_float(w) : XDT == TCQ_BF16 ? bf16_to_f32((u16)w) : f16_to_f32((u16)w);
+                    v[k] = xv * (float)(i8)(s4[0] >> (8 * k));
+                }
+                wave_walsh<2, KS>(v, row, [] { __syncthreads(); });
+                const float c = (float)(1.0 / __builtin_sqrt((double)n));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[k] = v[k] * c;
+                    mx = fmaxf(mx, fabsf(v[k]));
+                }
+                // the row maximum through one barrier (red is written again only after the next token's Walsh
+                // barrier, which every wave reaches after reading it here)
+                mx = wave_max(mx);
+                if (lane == 0) red[wave] = mx;
+                __syncthreads();
+                float amax = 0.f;
+#pragma unroll
+                for (int i = 0; i < KS; ++i) amax = fmaxf(amax, red[i]);
+                int e = 0;
+                if (amax > 0.f && amax < __builtin_inff()) {
+                    frexpf(amax, &e);
+                    e -= 15;
+                }
+                if (lr == t) hsw = ldexpf(1.f, e);
+                // wave w holds elements [256 w, 256 w + 256), chunk w: the only h16 it multiplies (nch = KS), so
+                // no barrier follows the store, only the wave's own ordering of its LDS accesses
+                *(uint2_t*)(hl + t * np + 4 * tid) = uint2_t{(u32)f32_to_f16(ldexpf(v[0], -e)) | ((u32)f32_to_f16(ldexpf(v[1], -e)) << 16),
+                                                       (u32)f32_to_f16(ldexpf(v[2], -e)) | ((u32)f32_to_f16(ldexpf(v[3], -e)) << 16)};
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        } else if (rin) {
             float v[16];
             if (t > 0 && on_in) {
                 layer_x16<XDT>(A.x, (size_t)t * n + 16 * tid, v);
@@ -507,9 +594,9 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
             if (tid == 0) hsl[t] = ldexpf(1.f, e);
             for (int i = tid; i < np; i += blockDim.x) hl[t * np + i] = i < n ? f32_to_f16(ldexpf(row[lds_slot(i)], -e)) : (u16)0;
         }
-        __syncthreads();
+        if (!win) __syncthreads();
     }
-    const float hs = hsl[tok ? lr : 0];
+    const float hs = win ? hsw : hsl[tok ? lr : 0];
     const char* hb = (const char*)hl + (size_t)(lr * np + 16 * lg) * 2;
 
     float4_t acc[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
@@ -551,6 +638,7 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
         for (int e = 0; e < 4; ++e) o[e] = __float_as_uint((a[e] * hs) * f16_to_f32((u16)(rs4 >> (16 * e))));
         gptr((uint4_t*)(A.z + (size_t)lr * m + r0))[0] = o;
     }
+    if (!A.counter) return;                                       // tcq_pre_gemv_f16: z is the output
     // hand-off: the barrier orders the workgroup's z stores before the count; the count is an agent-scope release (the
     // stores reach the level every XCD reads) and acquire; the workgroup that completes it reads every z row after an
     // agent-scope acquire fence
@@ -563,7 +651,30 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
     // output rotation of every token row, as tcq_post: y = walsh(z) * sv (+ bias)
     const rsrc_t Z = make_rsrc(A.z, (u32)(M * m) * 4);
     for (int t = 0; t < M; ++t) {
-        if (rout) {
+        if (wout) {
+            if constexpr (WL != 0) {
+                float v[4];
+                const uint4_t a = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Z, (u32)(t * m + 4 * tid) * 4, 0, 16));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = __uint_as_float(a[k]);
+                wave_walsh<2, KS>(v, row, [] { __syncthreads(); });
+                const float c = (float)(1.0 / __builtin_sqrt((double)m));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[k] = (v[k] * c) * (float)(i8)(sv4[0] >> (8 * k));
+                    if (A.bias) v[k] = v[k] + b4[0][k];
+                }
+                const size_t o = (size_t)t * m + 4 * tid;
+                if constexpr (YDT == TCQ_F32) {
+                    gptr((float4_t*)((float*)A.y + o))[0] = float4_t{v[0], v[1], v[2], v[3]};
+                } else {
+                    u32 h[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) h[k] = YDT == TCQ_BF16 ? f32_to_bf16(v[k]) : f32_to_f16(v[k]);
+                    gptr((uint2_t*)((u16*)A.y + o))[0] = uint2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+                }
+            }
+        } else if (rout) {
             float v[16];
             if (on_out) {
 #pragma unroll
@@ -616,10 +727,10 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
     }
 }
 
-extern "C" int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
-                             const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
-                             tcq_stream_t stream) {
-    if (!x || !su || !wdev || !tlut || !row_scale || !sv || !y || !z || !counter || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+// counter NULL: the launch stops after z (tcq_pre_gemv_f16; sv, bias and y unused)
+static int layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                     const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
+                     tcq_stream_t stream) {
     if (m % 16 || n % 16 || m > TCQ_MAX_WIDTH || n > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
     if (M > 16 || m / 16 > 65535) return TCQ_ERR_UNSUPPORTED;
     if ((size_t)(m / 16) * ((n + 255) / 256) * 1024 >= ((size_t)1 << 31)) return TCQ_ERR_SHAPE;
@@ -658,4 +769,17 @@ extern "C" int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const
 #undef LAYER_Y
 #undef LAYER_K
     return launch_status();
+}
+
+extern "C" int tcq_layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                             const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
+                             tcq_stream_t stream) {
+    if (!x || !su || !wdev || !tlut || !row_scale || !sv || !y || !z || !counter || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+    return layer_f16(x, x_dtype, su, wdev, tlut, row_scale, sv, bias, y, y_dtype, M, m, n, z, counter, stream);
+}
+
+extern "C" int tcq_pre_gemv_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
+                                int M, int m, int n, float* z, tcq_stream_t stream) {
+    if (!x || !su || !wdev || !tlut || !row_scale || !z || M <= 0 || m <= 0 || n <= 0) return TCQ_ERR_ARG;
+    return layer_f16(x, x_dtype, su, wdev, tlut, row_scale, nullptr, nullptr, nullptr, TCQ_F16, M, m, n, z, nullptr, stream);
 }

@@ -391,6 +391,20 @@ def layer_f16(x, su, wdev, tlut, row_scale, sv, bias, y, z, counter):
          ptr(bias), ptr(y), DTYPE[y.dtype], M, m, n, ptr(z), ptr(counter), stream())
 
 
+def pre_gemv_f16(x, su, wdev, tlut, row_scale, z):
+    """Input rotation and decode-GEMV of an FP16-table layer in one launch (tcq_pre_gemv_f16): z (M, m) float32 =
+    walsh(x * su) Q^T * row_scale, bit-identical to pre_h16 -> gemv_f16; post(z, ...) completes the layer."""
+    M, n = x.shape
+    m = row_scale.numel()
+    _contig(x, su, wdev, tlut, row_scale, z)
+    if z.dtype != torch.float32 or tuple(z.shape) != (M, m):
+        raise ValueError(f'pre_gemv_f16: z must be ({M}, {m}) float32')
+    if su.numel() != n or _groups(tlut) != 1:
+        raise ValueError('pre_gemv_f16: su (n,) and one (512, 2) table')
+    call('tcq_pre_gemv_f16', ptr(x), _dt(x, (0, 1, 2), 'pre_gemv_f16 x'), ptr(su), ptr(wdev), ptr(tlut), ptr(row_scale), M, m, n,
+         ptr(z), stream())
+
+
 _SEG = None
 
 
