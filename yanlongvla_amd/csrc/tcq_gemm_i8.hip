@@ -130,8 +130,9 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const 
             for (int i = 0; i < BN; ++i) B[i] = frag(st, (wn * BN + i) * 2, kk);
 #pragma unroll
             for (int j = 0; j < BM; ++j)
+                if (m0 + (wm * BM + j) * 32 < M)                         // blocks of padding rows only: no MFMA work
 #pragma unroll
-                for (int i = 0; i < BN; ++i) acc[i][j] = MfmaOf<ESZ>::mma(A[j], B[i], acc[i][j]);
+                    for (int i = 0; i < BN; ++i) acc[i][j] = MfmaOf<ESZ>::mma(A[j], B[i], acc[i][j]);
         }
     }
 
