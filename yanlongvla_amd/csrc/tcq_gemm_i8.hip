@@ -130,7 +130,9 @@ __global__ __launch_bounds__(64 * WN * WM) void k_gemm_i8(const void* a_, const 
             for (int i = 0; i < BN; ++i) B[i] = frag(st, (wn * BN + i) * 2, kk);
 #pragma unroll
             for (int j = 0; j < BM; ++j)
-                if (m0 + (wm * BM + j) * 32 < M)                         // blocks of padding rows only: no MFMA work
+                // blocks of padding rows only: no MFMA work (with one wave row, where a tile always holds rows, the test is
+                // left out: the branch changed the code of the narrow tiles and slowed them)
+                if (WM == 1 || m0 + (wm * BM + j) * 32 < M)
 #pragma unroll
                     for (int i = 0; i < BN; ++i) acc[i][j] = MfmaOf<ESZ>::mma(A[j], B[i], acc[i][j]);
         }
