@@ -727,6 +727,149 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
     }
 }
 
+// tcq_pre_gemv_f16 for rows of n = 256 NWP (NWP = 4 or 8: n = 1024 or 2048) with 16-byte aligned operands: one tile row
+// per workgroup of 2 NWP waves. Waves 0 .. NWP - 1 rotate the token rows on the no-transpose engine (4 values per thread,
+// the steps of k_layer_f16's) while waves NWP .. 2 NWP - 1 decode the tile row's NWP chunks, one each, into registers
+// between the rotation's two barriers; after the last row's FP16 store the decode waves multiply, and the partial sums add
+// in chunk order with k_layer_f16's epilogue, so z is the same bit for bit.
+template <int XDT, int NWP>
+__global__ __launch_bounds__(128 * NWP) void k_pre_gemv_wv(LayerArgs A, int M, int m) {
+    constexpr int C = LAT_C, NE = 1024, ESH = 2 + ilog2(C), N = 256 * NWP, NT = 128 * NWP, TPT = NE / NT;
+    __shared__ __attribute__((aligned(16))) u32 tab[NE * C];
+    __shared__ __attribute__((aligned(16))) float row[N];
+    __shared__ __attribute__((aligned(16))) float4_t part[NWP * 64];
+    __shared__ float red[NWP], hsl[16];
+    extern __shared__ __attribute__((aligned(16))) u32 dyn[];
+    u16* hl = (u16*)dyn;                                          // h16 rows (M, N)
+    const int tiles_m = m >> 4, I = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const bool rot = wave < NWP;                                  // uniform: a rotation wave, else the decoder of chunk c
+    const int c = wave - NWP;
+    const u32 cp4 = (u32)(lane & (C - 1)) << 2;
+    const rsrc_t W = make_rsrc(A.wdev, (u32)(tiles_m * NWP) << 10);
+    u16 tl0[TPT], tl1[TPT];                                       // the codebook's halves first
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int h = (tid + NT * j) & 511;
+        tl0[j] = gptr(A.tlut)[2 * h];
+        tl1[j] = gptr(A.tlut)[2 * h + 1];
+    }
+    uint4_t xw = {0, 0, 0, 0}, wd = {0, 0, 0, 0};
+    u32 sg = 0;
+    if (rot) {                                                    // token 0's four values and their signs
+        if constexpr (XDT == TCQ_F32) {
+            xw = gptr((const uint4_t*)((const float*)A.x + 4 * tid))[0];
+        } else {
+            const uint2_t a = gptr((const uint2_t*)((const u16*)A.x + 4 * tid))[0];
+            xw = uint4_t{a[0], a[1], 0, 0};
+        }
+        sg = gptr((const u32*)(A.su + 4 * tid))[0];
+    } else {                                                      // the chunk's words
+        wd = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(W, (u32)lane << 4, (u32)(I * NWP + c) << 10, 2));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {                               // fill_table's entries from the loaded halves
+        const int e = tid + NT * j;
+        const u32 v = ((u32)tl0[j] ^ ((u32)(e >> 9) << 15)) | ((u32)tl1[j] << 16);
+#pragma unroll
+        for (int cc = 0; cc < C; cc += 4) *(uint4_t*)(tab + e * C + cc) = uint4_t{v, v, v, v};
+    }
+    uint4_t Aq[4][2];
+    for (int t = 0; t < M; ++t) {
+        float v[4];
+        if (rot) {
+            uint4_t a = xw;
+            if (t > 0) {
+                const size_t i = (size_t)t * N + 4 * tid;
+                if constexpr (XDT == TCQ_F32) {
+                    a = gptr((const uint4_t*)((const float*)A.x + i))[0];
+                } else {
+                    const uint2_t b = gptr((const uint2_t*)((const u16*)A.x + i))[0];
+                    a = uint4_t{b[0], b[1], 0, 0};
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32 w = XDT == TCQ_F32 ? a[k] : a[k >> 1] >> (16 * (k & 1));
+                const float xv = XDT == TCQ_F32 ? __uint_as_float(w) : XDT == TCQ_BF16 ? bf16_to_f32((u16)w) : f16_to_f32((u16)w);
+                v[k] = xv * (float)(i8)(sg >> (8 * k));
+            }
+            wave_walsh_lanes<2>(v);
+            wave_walsh_put<2, NWP>(v, row);
+        }
+        __syncthreads();                                          // the exchange row (at t = 0 also the table)
+        if (rot) {
+            wave_walsh_get<2, NWP>(v, row);
+            const float cn = (float)(1.0 / __builtin_sqrt((double)N));
+            float mx = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[k] = v[k] * cn;
+                mx = fmaxf(mx, fabsf(v[k]));
+            }
+            mx = wave_max(mx);
+            if (lane == 0) red[wave] = mx;
+        } else if (t == 0) {                                      // the decode waves' work, beside the rotation
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32 hi = wd[q];
+                const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+                u32 vv[8];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                    vv[p] = *(const u32*)((const char*)tab + ((((x >> 22) & (NE - 1)) << ESH) | cp4));
+                    vv[4 + p] = *(const u32*)((const char*)tab + ((((x >> 6) & (NE - 1)) << ESH) | cp4));
+                }
+                Aq[q][0] = uint4_t{vv[0], vv[1], vv[2], vv[3]};
+                Aq[q][1] = uint4_t{vv[4], vv[5], vv[6], vv[7]};
+            }
+        }
+        __syncthreads();                                          // the row maximum (red is rewritten only after the next
+        if (rot) {                                                // token's first barrier, which follows every read here)
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < NWP; ++i) amax = fmaxf(amax, red[i]);
+            int e = 0;
+            if (amax > 0.f && amax < __builtin_inff()) {
+                frexpf(amax, &e);
+                e -= 15;
+            }
+            if (tid == 0) hsl[t] = ldexpf(1.f, e);
+            *(uint2_t*)(hl + t * N + 4 * tid) = uint2_t{(u32)f32_to_f16(ldexpf(v[0], -e)) | ((u32)f32_to_f16(ldexpf(v[1], -e)) << 16),
+                                                      (u32)f32_to_f16(ldexpf(v[2], -e)) | ((u32)f32_to_f16(ldexpf(v[3], -e)) << 16)};
+        }
+    }
+    __syncthreads();                                              // every FP16 row and scale
+    const bool tok = lr < M;
+    if (!rot) {
+        const char* hb = (const char*)hl + (size_t)(lr * N + 16 * lg) * 2;
+        float4_t acc[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const half8_t B0 = tok ? *(const half8_t*)(hb + 512 * c + 128 * q) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            const half8_t B1 = tok ? *(const half8_t*)(hb + 512 * c + 128 * q + 16) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, Aq[q][0]), B0, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, Aq[q][1]), B1, acc[1], 0, 0, 0);
+        }
+        part[c * 64 + lane] = acc[0] + acc[1];
+    }
+    __syncthreads();
+    if (wave == 0 && tok) {                                       // the chunk sums in chunk order, then k_layer_f16's epilogue
+        float4_t a = part[lane];
+        for (int k = 1; k < NWP; ++k) a += part[k * 64 + lane];
+        const float hs = hsl[lr];
+        const int r0 = 16 * I + 4 * lg;
+        const u64 rs4 = *gptr((const u64*)(A.row_scale + r0));
+        uint4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = __float_as_uint((a[e] * hs) * f16_to_f32((u16)(rs4 >> (16 * e))));
+        gptr((uint4_t*)(A.z + (size_t)lr * m + r0))[0] = o;
+    }
+}
+
 // counter NULL: the launch stops after z (tcq_pre_gemv_f16; sv, bias and y unused)
 static int layer_f16(const void* x, int x_dtype, const int8_t* su, const void* wdev, const void* tlut, const void* row_scale,
                      const int8_t* sv, const float* bias, void* y, int y_dtype, int M, int m, int n, float* z, int* counter,
@@ -745,6 +888,20 @@ static int layer_f16(const void* x, int x_dtype, const int8_t* su, const void* w
                     (uintptr_t)z % 16 == 0 && (uintptr_t)bias % 16 == 0 && (size_t)n * xs % 16 == 0 && (size_t)m * ys % 16 == 0;
     const dim3 grid(m / 16), block(64 * ks);
     const hipStream_t st = (hipStream_t)stream;
+    if (!counter && vec && (n == 1024 || n == 2048)) {            // rotation and decode on separate waves
+        const size_t hb = (size_t)M * n * 2;
+#define PGW(XD)                                                                                                            \
+    if (n == 1024) launch_k(k_pre_gemv_wv<XD, 4>, grid, dim3(512), hb, st, a, M, m);                                       \
+    else launch_k(k_pre_gemv_wv<XD, 8>, grid, dim3(1024), hb, st, a, M, m)
+        switch (x_dtype) {
+            case TCQ_F16: PGW(TCQ_F16); break;
+            case TCQ_BF16: PGW(TCQ_BF16); break;
+            case TCQ_F32: PGW(TCQ_F32); break;
+            default: return TCQ_ERR_DTYPE;
+        }
+#undef PGW
+        return launch_status();
+    }
 #define LAYER_K(KS, XD, YD) launch_k(k_layer_f16<KS, XD, YD>, grid, block, dyn, st, a, M, m, n, vec)
 #define LAYER_Y(KS, XD)                                      \
     switch (y_dtype) {                                       \
