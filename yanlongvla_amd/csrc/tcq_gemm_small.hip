@@ -148,9 +148,14 @@ enum { QL_ROWS = 0, QL_BLOCKS = 1, QL_WORDS = 2 };
 // DOT (M == 1): the product on v_dot4c_i32_i8 (dot_product) instead of the MFMA; the epilogues are shared.
 // PL > 0 (M == 1, K = 2^PL): the activations come from the prologue run by every workgroup (run_prologue, ProShape)
 // instead of q / s.
-template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false, int PL = 0>
+// OVS (the layer or attention prologue, one tile row, one chunk per product wave): the prologue runs on waves 0 .. 7
+// while waves 8 .. NW - 1 fill the table and decode the weight fragments of their chunks (chunk c0 + wave - 8) into
+// registers, meeting the prologue's barriers; after the row is in LDS they multiply, and their partial sums add in chunk
+// order as without OVS (the same sums and outputs).
+template <int MODE, int NB, int ODT, int TR, int QL, bool RB = false, int KS = 1, bool DOT = false, int PL = 0, bool OVS = false>
 __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typename PackOf<PL>::type P, const i8* q, const float* s,
                                                                     int M, int K, int ldz, int ldq) {
+    static_assert(!OVS || ((PL == PRO_LAYER || PL == PRO_ATTN) && MODE == 0 && TR == 1 && !RB), "overlapped prologue");
     static_assert(KS == 1 || ODT == TCQ_I32, "K parts are int32 sums");
     static_assert(!DOT || (NB == 1 && QL != QL_WORDS), "dot products: one token, q rows or token blocks");
     static_assert(PL == 0 || (NB == 1 && QL == QL_ROWS && !DOT), "prologue: one token");
@@ -165,6 +170,8 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
     if (I0 >= tiles_m) return;                                            // uniform
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // OVS: the product's waves are 8 .. nw - 1 (pw = wave - 8 of npw); otherwise every wave
+    const int pw = OVS ? wave - 8 : wave, npw = OVS ? nw - 8 : nw;
     const int lr = lane & 15, lg = lane >> 4;
     const u32 cp4 = (u32)(lane & (SM_C - 1)) << 2;
     constexpr int ESH = SM_C == 16 ? 6 : SM_C == 8 ? 5 : SM_C == 4 ? 4 : 2;
@@ -234,14 +241,15 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
         for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
     }
     if (!PL && c0 + wave < nch) load(c0 + wave);
-    // epilogue scales, loaded with the operands (wave 0 stores)
+    if (OVS && pw >= 0 && c0 + pw < nch) load(c0 + pw);
+    // epilogue scales, loaded with the operands (wave 0 stores; OVS: wave 8)
     float4_t rsv[TR];
     float sv[NB];
 #pragma unroll
     for (int r = 0; r < TR; ++r) rsv[r] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NB; ++b) sv[b] = 0.f;
-    if (ODT != TCQ_I32 && wave == 0) {
+    if (ODT != TCQ_I32 && pw == 0) {
 #pragma unroll
         for (int r = 0; r < TR; ++r) rsv[r] = gptr((const float4_t*)(S.rs + 16 * min(I0 + r, tiles_m - 1) + 4 * lg))[0];
         if constexpr (!PL) {
@@ -249,45 +257,84 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
             for (int b = 0; b < NB; ++b) sv[b] = gptr(s)[min(16 * b + lr, M - 1)];
         }
     }
-    if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
-    if constexpr (PL > 0) run_prologue<PL, PL == PRO_PRE ? 0 : 8>(P, pro, [&] {
-        if (c0 + wave < nch) load(c0 + wave);
-    });
-    __syncthreads();
-    if constexpr (PL > 0) {
-        sv[0] = pro.sc;
-        if (c0 + wave < nch) loadB(c0 + wave);
-    }
-    for (int c = c0 + wave; c < nch; c += nw) {
-        if (c != c0 + wave) {
-            load(c);
-            if constexpr (PL > 0) loadB(c);
+    // the A fragment of packed word hi (16 weights of this lane's row, looked up in the table)
+    auto frag = [&](u32 hi) {
+        const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+        u32 e0[4], e1[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+            e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << ESH) | cp4));             // pair p
+            e1[p] = *(const u16*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));    // pair p + 4
         }
+        return int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
+                     (int)(e1[2] | (e1[3] << 16))};
+    };
+    if constexpr (OVS) {
+        constexpr int SY = PL == PRO_LAYER ? WAVES_SYNCS : WAVES_SYNCS / 2;   // the prologue's barriers
+        const bool on = pw >= 0 && c0 + pw < nch;                         // uniform
+        int4v Af[4];
+        if (pw < 0) {                                                     // the prologue waves
+            run_prologue<PL, 8>(P, pro, [] {});
+        } else {                                                          // the table, then the fragments, beside the prologue
+            const i8* t8 = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
+            for (int e = (int)threadIdx.x - 512; e < 1024; e += 64 * npw) {
+                const int h = e & 511;
+                int v0 = gptr(t8)[2 * h];
+                const int v1 = gptr(t8)[2 * h + 1];
+                if (e >> 9) v0 = -v0;
+                const u32 v = (u32)(v0 & 0xff) | ((u32)(v1 & 0xff) << 8);
+                const u32 vv = v | (v << 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+                for (int cc = 0; cc < SM_C; cc += 4) *(uint4_t*)(tab + e * SM_C + cc) = uint4_t{vv, vv, vv, vv};
+            }
 #pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                int4v A;
-                if (MODE == 0) {
-                    const u32 hi = wa[r][0][j];
-                    const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
-                    u32 e0[4], e1[4];
+            for (int i = 0; i < SY; ++i) {
+                __syncthreads();
+                if (i == 0 && on) {
 #pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
-                        e0[p] = *(const u16*)((const char*)tab + (((x >> 22) << ESH) | cp4));             // pair p
-                        e1[p] = *(const u16*)((const char*)tab + ((((x >> 6) & 1023u) << ESH) | cp4));    // pair p + 4
-                    }
-                    A = int4v{(int)(e0[0] | (e0[1] << 16)), (int)(e0[2] | (e0[3] << 16)), (int)(e1[0] | (e1[1] << 16)),
-                              (int)(e1[2] | (e1[3] << 16))};
-                } else {
-                    A = __builtin_bit_cast(int4v, wa[r][j]);
+                    for (int j = 0; j < 4; ++j) Af[j] = frag(wa[0][0][j]);
                 }
-                if constexpr (DOT) {
-                    dacc[r][j & 1] = dot_product(A, B[j][0], dacc[r][j & 1]);
-                } else {
+            }
+        }
+        __syncthreads();                                                  // the row is in pro.qs
+        if (pw == 0) sv[0] = pro.sc;
+        if (on) {
+            loadB(c0 + pw);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[r][b], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Af[j], B[j][0], acc[0][0], 0, 0, 0);
+        }
+    } else {
+        if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
+        if constexpr (PL > 0) run_prologue<PL, PL == PRO_PRE ? 0 : 8>(P, pro, [&] {
+            if (c0 + wave < nch) load(c0 + wave);
+        });
+        __syncthreads();
+        if constexpr (PL > 0) {
+            sv[0] = pro.sc;
+            if (c0 + wave < nch) loadB(c0 + wave);
+        }
+        for (int c = c0 + wave; c < nch; c += nw) {
+            if (c != c0 + wave) {
+                load(c);
+                if constexpr (PL > 0) loadB(c);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int r = 0; r < TR; ++r) {
+                    int4v A;
+                    if (MODE == 0) {
+                        A = frag(wa[r][0][j]);
+                    } else {
+                        A = __builtin_bit_cast(int4v, wa[r][j]);
+                    }
+                    if constexpr (DOT) {
+                        dacc[r][j & 1] = dot_product(A, B[j][0], dacc[r][j & 1]);
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < NB; ++b) acc[r][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[j][b], acc[r][b], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -297,15 +344,15 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
         for (int r = 0; r < TR; ++r) acc[r][0] = dot_to_mfma_layout(dacc[r][0] + dacc[r][1], lane);
     }
     // sum the waves' partial accumulators (exact int32) through LDS, then scale and store
-    if (wave > 0) {
+    if (pw > 0) {
 #pragma unroll
         for (int r = 0; r < TR; ++r)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) red[(((wave - 1) * TR + r) * NB + b) * 64 + lane] = acc[r][b];
+            for (int b = 0; b < NB; ++b) red[(((pw - 1) * TR + r) * NB + b) * 64 + lane] = acc[r][b];
     }
     __syncthreads();
-    if (wave != 0) return;
-    for (int w = 0; w < nw - 1; ++w)
+    if (pw != 0) return;
+    for (int w = 0; w < npw - 1; ++w)
 #pragma unroll
         for (int r = 0; r < TR; ++r)
 #pragma unroll
@@ -784,6 +831,14 @@ template <int MODE, int PL, int ODT, int KS>
 static void launch_pro_small(int rows, int nseg, int nw, bool pairs, hipStream_t st, const SegPackPro& P, int K, int ldo) {
     const i8* nq = nullptr;
     const float* ns = nullptr;
+    if constexpr (MODE == 0 && (PL == PRO_LAYER || PL == PRO_ATTN)) {
+        const int nchp = (K / 256 + KS - 1) / KS;                      // one product wave per chunk beside 8 prologue waves
+        if (!pairs && nchp <= 8) {
+            launch_k(k_gemm_small<MODE, 1, ODT, 1, QL_ROWS, false, KS, false, PL, true>, dim3(rows, nseg, KS), dim3(64 * (8 + nchp)), 0,
+                     st, P, nq, ns, 1, K, ldo, 0);
+            return;
+        }
+    }
     if constexpr (PL == PRO_LAYER) {
         if (pairs) {
             launch_k(k_gemm_small<MODE, 1, ODT, 2, QL_ROWS, false, KS, false, PL>, dim3((rows + 1) / 2, nseg, KS), dim3(64 * nw), 0, st,
