@@ -240,6 +240,19 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[r][b] = int4v{0, 0, 0, 0};
     }
+    // without a prologue, the codebook's entries are loaded first (fill_table_i8's split, entry tid + blockDim j), so the
+    // table fill waits for them alone while the words and activations are still on their way
+    constexpr int TE = 4;
+    u32 t8w[TE];
+    const bool early = MODE == 0 && !PL && blockDim.x >= 1024 / TE;     // uniform
+    const i8* t8p = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
+    if (early) {
+#pragma unroll
+        for (int j = 0; j < TE; ++j) {
+            const int e = (int)threadIdx.x + (int)blockDim.x * j;
+            if (e < 1024) t8w[j] = gptr((const u16*)t8p)[e & 511];
+        }
+    }
     if (!PL && c0 + wave < nch) load(c0 + wave);
     if (OVS && pw >= 0 && c0 + pw < nch) load(c0 + pw);
     // epilogue scales, loaded with the operands (wave 0 stores; OVS: wave 8)
@@ -305,7 +318,23 @@ __global__ __launch_bounds__(TR == 1 ? 1024 : 512) void k_gemm_small(const typen
             for (int j = 0; j < 4; ++j) acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Af[j], B[j][0], acc[0][0], 0, 0, 0);
         }
     } else {
-        if (MODE == 0) fill_table_i8(tab, S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0));
+        if (early) {
+#pragma unroll
+            for (int j = 0; j < TE; ++j) {
+                const int e = (int)threadIdx.x + (int)blockDim.x * j;
+                if (e < 1024) {                                            // fill_table_i8's entry e from its loaded pair
+                    int v0 = (int)(i8)(t8w[j] & 0xff);
+                    const int v1 = (int)(i8)(t8w[j] >> 8);
+                    if (e >> 9) v0 = -v0;
+                    const u32 v = (u32)(v0 & 0xff) | ((u32)(v1 & 0xff) << 8);
+                    const u32 vv = v | (v << 16);
+#pragma unroll
+                    for (int c = 0; c < SM_C; c += 4) *(uint4_t*)(tab + e * SM_C + c) = uint4_t{vv, vv, vv, vv};
+                }
+            }
+        } else if (MODE == 0) {
+            fill_table_i8(tab, t8p);
+        }
         if constexpr (PL > 0) run_prologue<PL, PL == PRO_PRE ? 0 : 8>(P, pro, [&] {
             if (c0 + wave < nch) load(c0 + wave);
         });
