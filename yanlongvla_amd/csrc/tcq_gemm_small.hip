@@ -468,6 +468,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
             if (c < nch) wa[i] = __builtin_bit_cast(uint4_t, __builtin_amdgcn_raw_buffer_load_b128(Wr, (u32)lane << 4, (u32)(I * nch_all + c) << 10, 2));
         }
     };
+    // the codebook's entries first (the table fill's split: entry tid - t0 + (64 NW - t0) j, t0 = the first filling thread:
+    // 0, or 256 past the four prologue waves with OV), so the fill waits for them alone
+    constexpr int FT0 = OV ? 256 : 0;
+    static_assert(2 * (64 * NW - FT0) >= 1024, "two table entries per filling thread");
+    u32 t8w[2];
+    const i8* t8p = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int e = (int)threadIdx.x - FT0 + (64 * NW - FT0) * j;
+        if (e >= 0 && e < 1024) t8w[j] = gptr((const u16*)t8p)[e & 511];
+    }
     if constexpr (!PL || OV) loadW();
     auto loadB = [&](int c, int4v* B) {
 #pragma unroll
@@ -490,12 +501,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tcq(const typename PackOf<PL>:
         if constexpr (!PL) sv = gptr(s)[min(lr, M - 1)];
     }
     // the table, filled by threads from t0 on (OV: the decode waves alone; the prologue waves start at once)
-    auto fill_table = [&](int t0) {
-        const i8* t8 = S.t8 + (S.rows_per_table > 0 ? (size_t)(16 * I0 / S.rows_per_table) * 1024 : 0);
-        for (int e = (int)threadIdx.x - t0; e < 1024; e += 64 * NW - t0) {
-            const int h = e & 511;
-            int v0 = gptr(t8)[2 * h];
-            const int v1 = gptr(t8)[2 * h + 1];
+    auto fill_table = [&](int t0) {                                        // t0 = FT0: from the loaded pairs
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int e = (int)threadIdx.x - t0 + (64 * NW - t0) * j;
+            if (e < 0 || e >= 1024) continue;
+            int v0 = (int)(i8)(t8w[j] & 0xff);
+            const int v1 = (int)(i8)(t8w[j] >> 8);
             if (e >> 9) v0 = -v0;
             const u32 v = (u32)(v0 & 0xff) | ((u32)(v1 & 0xff) << 8);
             const u32 vv = v | (v << 16);
