@@ -811,9 +811,9 @@ __global__ __launch_bounds__(128 * NWP) void k_pre_gemv_wv(LayerArgs A, int M, i
             }
             mx = wave_max(mx);
             if (lane == 0) red[wave] = mx;
-        } else if (t == 0) {                                      // the decode waves' work, beside the rotation
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
+        } else if (t == 0) {                                      // the decode waves' work, beside the rotation: steps 0, 1
+#pragma unroll                                                    // here, 2 and 3 beside the FP16 store
+            for (int q = 0; q < 2; ++q) {
                 const u32 hi = wd[q];
                 const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
                 u32 vv[8];
@@ -828,7 +828,23 @@ __global__ __launch_bounds__(128 * NWP) void k_pre_gemv_wv(LayerArgs A, int M, i
             }
         }
         __syncthreads();                                          // the row maximum (red is rewritten only after the next
-        if (rot) {                                                // token's first barrier, which follows every read here)
+        if (!rot && t == 0) {                                     // token's first barrier, which follows every read here)
+#pragma unroll
+            for (int q = 2; q < 4; ++q) {
+                const u32 hi = wd[q];
+                const u32 hn = (u32)__builtin_amdgcn_mov_dpp((int)hi, 0x12F, 0xf, 0xf, false);
+                u32 vv[8];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const u32 x = pk_code(p == 0 ? hi : __builtin_amdgcn_alignbit(hi, hn, 32 - 4 * p));
+                    vv[p] = *(const u32*)((const char*)tab + ((((x >> 22) & (NE - 1)) << ESH) | cp4));
+                    vv[4 + p] = *(const u32*)((const char*)tab + ((((x >> 6) & (NE - 1)) << ESH) | cp4));
+                }
+                Aq[q][0] = uint4_t{vv[0], vv[1], vv[2], vv[3]};
+                Aq[q][1] = uint4_t{vv[4], vv[5], vv[6], vv[7]};
+            }
+        }
+        if (rot) {
             float amax = 0.f;
 #pragma unroll
             for (int i = 0; i < NWP; ++i) amax = fmaxf(amax, red[i]);
