@@ -730,8 +730,9 @@ __global__ __launch_bounds__(64 * KS) void k_layer_f16(LayerArgs A, int M, int m
 // tcq_pre_gemv_f16 for rows of n = 256 NWP (NWP = 4 or 8: n = 1024 or 2048) with 16-byte aligned operands: one tile row
 // per workgroup of 2 NWP waves. Waves 0 .. NWP - 1 rotate the token rows on the no-transpose engine (4 values per thread,
 // the steps of k_layer_f16's) while waves NWP .. 2 NWP - 1 decode the tile row's NWP chunks, one each, into registers
-// between the rotation's two barriers; after the last row's FP16 store the decode waves multiply, and the partial sums add
-// in chunk order with k_layer_f16's epilogue, so z is the same bit for bit.
+// (steps 0 and 1 between the first token's two barriers, steps 2 and 3 beside its FP16 store); after the last row's FP16
+// store the decode waves multiply, and the partial sums add in chunk order with k_layer_f16's epilogue, so z is the same
+// bit for bit.
 template <int XDT, int NWP>
 __global__ __launch_bounds__(128 * NWP) void k_pre_gemv_wv(LayerArgs A, int M, int m) {
     constexpr int C = LAT_C, NE = 1024, ESH = 2 + ilog2(C), N = 256 * NWP, NT = 128 * NWP, TPT = NE / NT;
