@@ -63,6 +63,16 @@ def test_argument_errors_are_reported_before_launch():
     assert lib.tcq_gemmf_tcq_hT(P(16), P(16), P(16), 1, P(16), P(16), 1, 24, 16, 0, 0, None) == -2
     assert lib.tcq_gemmf_tcq_hT(P(16), P(16), P(16), 1, P(16), P(8), 1, 16, 16, 0, 0, None) == -5
     assert lib.tcq_gemmf_tcq(P(16), 1, P(16), 1, 16, 3, 16, None) == -3               # int32 out: not a float product
+    # one-layer entry points: tcq_pre_gemv_f16(x, x_dtype, su, wdev, tlut, row_scale, M, m, n, z, stream)
+    assert lib.tcq_pre_gemv_f16(None, 2, P(16), P(16), P(16), P(16), 1, 2048, 2048, P(16), None) == -1
+    assert lib.tcq_pre_gemv_f16(P(16), 2, P(16), P(16), P(16), P(16), 17, 2048, 2048, P(16), None) == -4   # M > 16
+    assert lib.tcq_pre_gemv_f16(P(16), 2, P(16), P(16), P(16), P(16), 1, 2056, 2048, P(16), None) == -2   # m % 16
+    assert lib.tcq_pre_gemv_f16(P(16), 2, P(16), P(16), P(16), P(16), 1, 2048, 2048, P(8), None) == -5    # z alignment
+    assert lib.tcq_pre_gemv_f16(P(16), 2, P(16), P(16), P(16), P(4), 1, 2048, 2048, P(16), None) == -5    # row scales
+    assert lib.tcq_pre_gemv_f16(P(16), 7, P(16), P(16), P(16), P(16), 1, 2048, 2048, P(16), None) == -3   # x dtype
+    # tcq_layer_f16 needs its counter and output
+    assert lib.tcq_layer_f16(P(16), 2, P(16), P(16), P(16), P(16), P(16), None, P(16), 2, 1, 2048, 2048, P(16), None,
+                             None) == -1
 
 
 @pytest.mark.skipif(not LIB.exists(), reason='libtcq.so not built')
