@@ -770,7 +770,7 @@ def probe(kind, reps, dev):
         def steps():                              # the two-launch layer: rotation + decode-GEMV, output rotation
             for _ in range(100):
                 K.pre_gemv_f16(x, L['su'], L['wdev'], L['tlut'][0], L['row_scale'][0], S1.z[0])
-                S1.rotate_out()
+                K.post(S1.z[0], None, None, L['sv'][0], None, S1.y[0])
         g = harness.capture(steps)
         calls = [g.replay]
     elif kind == 'chunk':
@@ -937,10 +937,10 @@ def main():
     one_med, one_p95 = graph_latency(one_launch)
     one_am_med, one_am_p95 = graph_latency(one_launch, replays=50, warmup=5, per_graph=100)
 
-    # and in two launches (tcq_pre_gemv_f16: input rotation and decode-GEMV in one kernel; then the output rotation)
+    # and in two launches (tcq_pre_gemv_f16: input rotation and decode-GEMV in one kernel; then the output rotation, tcq_post)
     def two_launch():
         K.pre_gemv_f16(x, L1['su'], L1['wdev'], L1['tlut'][0], L1['row_scale'][0], S1.z[0])
-        S1.rotate_out()
+        K.post(S1.z[0], None, None, L1['sv'][0], None, S1.y[0])
     S1.y.zero_()
     two_launch()
     torch.cuda.synchronize()
@@ -987,7 +987,7 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': 'k_gemv_f16<16, 4, 1, 2, 1, 1024, true, tcq_gemv_post_layer, 2> (layer stream, output rotation fused)', 'achieved': round(achieved, 2), 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_from_profile(nl),
                      'ms_per_launch': round(ms_gemv, 5), 'bytes_per_launch': byts},
-        'single_layer_ms': {'kernels': 'tcq_pre_gemv_f16 + tcq_postg (two launches: input rotation and decode-GEMV, '
+        'single_layer_ms': {'kernels': 'tcq_pre_gemv_f16 + tcq_post (two launches: input rotation and decode-GEMV, '
                                        'then the output rotation)',
                             'graph_replay_median': round(two_med, 5), 'graph_replay_p95': round(two_p95, 5),
                             'per_step_in_100_step_graph_median': round(two_am_med, 5),

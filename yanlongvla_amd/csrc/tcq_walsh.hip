@@ -1032,6 +1032,17 @@ __device__ __forceinline__ void postg_wv_seg(const tcq_post_seg& S, int tok, flo
                                                    (u32)f32_to_f16(v[2]) | ((u32)f32_to_f16(v[3]) << 16)};
     }
 }
+// tcq_post of few rows 256 / 1024 / 2048 wide with 16-byte aligned operands on the no-transpose engine: one workgroup of
+// 2^L / 256 waves per token (postg_wv_seg's steps).
+template <int ADT, int YDT, int L, int NWP>
+__global__ __launch_bounds__(64 * NWP) void k_post_wv(const void* acc, int lda, int col0, const float* s, const float* rs, const i8* sv,
+                                                      const float* bias, void* y) {
+    __shared__ float xs[NWP > 1 ? (1 << L) : 1];
+    const tcq_post_seg S{acc, rs, sv, bias, y, lda, col0, 1 << L, 0};
+    const int tok = blockIdx.x;
+    postg_wv_seg<ADT, YDT, L, NWP>(S, tok, ADT == TCQ_I32 ? s[tok] : 1.f, nullptr, xs);
+}
+
 // Segments of other widths or alignments (device descriptors, which the host cannot inspect) take the LDS engine of
 // k_postg (dynamic LDS of lds_words(maxN) floats).
 template <int ADT, int YDT, class SEGS>
@@ -1506,9 +1517,35 @@ extern "C" int tcq_post(const void* acc, int acc_dtype, int lda, int col0, const
         return launch_status();
     }
     if (N > TCQ_MAX_WIDTH) return TCQ_ERR_SHAPE;
+    const int asz = dsize(acc_dtype);
+    if (M <= 64 && (N == 256 || N == 1024 || N == 2048) && al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 &&
+        al16(y) && al16(sv) && (!rs || al16(rs)) && (!bias || al16(bias))) {   // few rows: the no-transpose engine
+        hipStream_t st = (hipStream_t)stream;
+#define POSTW_K(AD, YD, L, NWP) launch_k(k_post_wv<AD, YD, L, NWP>, dim3(M), dim3(64 * NWP), 0, st, acc, lda, col0, s, rs, (const i8*)sv, bias, y)
+#define POSTW_Y(AD, YD)                                                                                                    \
+    if (N == 2048) POSTW_K(AD, YD, 11, 8);                                                                                 \
+    else if (N == 1024) POSTW_K(AD, YD, 10, 4);                                                                            \
+    else POSTW_K(AD, YD, 8, 1)
+#define POSTW_A(AD)                                          \
+    switch (y_dtype) {                                       \
+        case TCQ_F32: POSTW_Y(AD, TCQ_F32); break;           \
+        case TCQ_BF16: POSTW_Y(AD, TCQ_BF16); break;         \
+        case TCQ_F16: POSTW_Y(AD, TCQ_F16); break;           \
+        default: return TCQ_ERR_DTYPE;                       \
+    }
+        switch (acc_dtype) {
+            case TCQ_I32: POSTW_A(TCQ_I32); break;
+            case TCQ_F32: POSTW_A(TCQ_F32); break;
+            case TCQ_BF16: POSTW_A(TCQ_BF16); break;
+            default: return TCQ_ERR_DTYPE;
+        }
+#undef POSTW_A
+#undef POSTW_Y
+#undef POSTW_K
+        return launch_status();
+    }
     const dim3 grid(M), block(row_threads(M, N));
     const size_t sh = row_lds(N);
-    const int asz = dsize(acc_dtype);
     const int vec = N % 8 == 0 && al16(acc) && ((size_t)lda * asz) % 16 == 0 && ((size_t)col0 * asz) % 16 == 0 && al16(y) &&
                     ((size_t)N * dsize(y_dtype)) % 16 == 0 && al8(sv) && (!rs || al16(rs)) && (!bias || al16(bias));
     hipStream_t st = (hipStream_t)stream;
