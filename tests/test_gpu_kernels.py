@@ -205,7 +205,7 @@ def test_pre_bitexact(M, K, xdt):
 
 
 @pytest.mark.parametrize('M,N', [(1, 16), (3, 48), (2, 20), (10, 256), (16, 2048), (50, 4096), (5, 16384), (300, 1024),
-                                 (2, 4304), (800, 2048)])
+                                 (2, 4304), (800, 2048), (7, 1024), (64, 256), (1, 2048)])
 def test_post_bitexact(M, N):
     from yanlongvla_amd import kernels as K
     rng = np.random.default_rng(M * N)
@@ -231,6 +231,12 @@ def test_post_bitexact(M, N):
             assert np.array_equal(bits_of(y), ref.view(np.uint32))
         else:
             assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    # BF16 accumulators (scaled by the row scale only), BF16 output
+    ab = torch.from_numpy((rng.standard_normal((M, N)) * 100).astype(np.float32)).bfloat16()
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    K.post(ab.to(DEV), None, T(rs[:N].copy()), T(sv[:N].copy()), None, y)
+    ref = O.post_bf16(ab.float().numpy() * rs[None, :N], sv[:N])
+    assert np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
 @pytest.mark.parametrize('tag', ['l0', 'l1', 'l2', 'l3'])
